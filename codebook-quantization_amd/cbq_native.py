@@ -1,0 +1,89 @@
+"""ctypes binding of libcbq_hip.so, the gfx950 C ABI (include/cbq_hip.h).
+
+The library is loaded after torch so that it binds to the HIP runtime torch
+already loaded (same SONAME), which makes torch's device pointers and
+streams valid inside it.  Loading fails loudly: there is no CPU fallback
+behind these calls.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch  # noqa: F401  (must be loaded first: shares its HIP runtime)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+SO_PATH = os.path.join(HERE, "libcbq_hip.so")
+
+CK_SUCCESS, CK_ERR_HIP, CK_ERR_ARG = 0, 1, 2
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_i64 = ctypes.c_int64
+
+
+class HuffStream(ctypes.Structure):
+    """struct cbq_huff_stream (include/cbq_hip.h)."""
+    _fields_ = [
+        ("words", _vp), ("n_words", _i64),
+        ("chunk_off", _vp), ("sub_len", _vp),
+        ("lut1", _vp), ("lut2", _vp), ("n_lut2", ctypes.c_int32),
+        ("canon", _vp), ("canon_pay", _vp),
+        ("value_cb", _vp), ("C", ctypes.c_int32),
+        ("stage_words", ctypes.c_int32),
+    ]
+
+
+# name -> (restype, argtypes); every symbol declared in include/cbq_hip.h
+SIGNATURES = {
+    "ck_error_string": (ctypes.c_char_p, [_i]),
+    "cbq_version": (ctypes.c_char_p, []),
+    "ck_linear_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "ck_linear_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "ck_embedding_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "cbq_embedding_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "huff_decode_to_i32": (_i, [_vp] * 8 + [_i, _i, _i, _vp]),
+    "huff_i32_linear_f32": (_i, [_vp] * 4 + [_i] * 4 + [_vp]),
+    "huff_i32_embedding_f32": (_i, [_vp] * 4 + [_i] * 3 + [_vp]),
+    "cbq_huff_build_luts": (_i, [_vp, _i, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    "cbq_huff_index_stream": (_i, [_vp, _i64, _vp, _i, _vp, _i, _i, _vp, _vp, _i]),
+    "cbq_huff_linear_f32": (_i, [_vp, ctypes.POINTER(HuffStream), _vp, _i, _i, _i, _vp]),
+    "cbq_huff_embedding_f32": (_i, [_vp, ctypes.POINTER(HuffStream), _vp, _i, _i, _i, _vp]),
+    "cbq_huff_decode_indices": (_i, [ctypes.POINTER(HuffStream), _vp, _i64, _vp]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load(path: str = SO_PATH) -> ctypes.CDLL:
+    """Load (once) and type the library; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"{path} is not built: run `python codebook-quantization_amd/build_native.py` "
+            "(or __graft_entry__.build()); the compressed path has no CPU fallback")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != CK_SUCCESS:
+        msg = load().ck_error_string(rc).decode()
+        raise RuntimeError(f"{what} returned error {rc} ({msg})")
+
+
+def stream_ptr(device: Optional[torch.device] = None) -> int:
+    """Raw hipStream_t of torch's current stream on `device`."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()

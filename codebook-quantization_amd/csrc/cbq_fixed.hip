@@ -1,0 +1,410 @@
+// Fixed-width codebook GEMV / skinny GEMM and embedding gather for gfx950.
+//
+// Index stream: b-bit indices, LSB-first; index i occupies stream bits
+// [i*b, (i+1)*b) (src/bitpack.py:32-95, src/compressed_matmul.c:334-347).
+// When K % 32 == 0 every run of 32 consecutive indices of a row starts on a
+// 32-bit word boundary and fills exactly b words, so one lane loads b words
+// with wide loads and unpacks its 32 indices with compile-time shifts
+// (v_alignbit for the fields that straddle words).  The codebook sits in LDS,
+// padded reads never leave the row's own words, and each wave owns whole
+// rows, reducing its lanes' partial dots with a butterfly.
+//
+// Output semantics follow ck_linear_f32 / ck_embedding_f32
+// (rocm/compressed_kernel.hip:58-120): fp32 accumulate, index clamped to C-1,
+// output written.
+#include "cbq_device.h"
+
+#include <algorithm>
+
+namespace {
+
+constexpr int kBlock = 512;                 // 8 waves share one LDS codebook
+constexpr int kWavesPerBlock = kBlock / CBQ_WAVE;
+constexpr int kMaxLdsBytes = 64 * 1024;     // per-workgroup budget we allow
+constexpr int kMaxLdsCodebook = 16384;      // entries of fp32 codebook in LDS
+
+template <typename XT>
+__device__ __forceinline__ void load_x32(const XT *__restrict__ p, float xv[32]);
+
+template <>
+__device__ __forceinline__ void load_x32<float>(const float *__restrict__ p, float xv[32])
+{
+    __builtin_memcpy(xv, p, 32 * sizeof(float));
+}
+
+template <>
+__device__ __forceinline__ void load_x32<uint16_t>(const uint16_t *__restrict__ p, float xv[32])
+{
+    uint32_t h[16];
+    __builtin_memcpy(h, p, 32 * sizeof(uint16_t));
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        xv[2 * i] = __uint_as_float(h[i] << 16);
+        xv[2 * i + 1] = __uint_as_float(h[i] & 0xffff0000u);
+    }
+}
+
+// Indices of group `g` of the 32-index groups of a row, already clamped and
+// turned into weights (the codebook gather).
+template <int BITS>
+__device__ __forceinline__ void gather_weights(const uint32_t w[BITS],
+                                               const float *__restrict__ s_cb,
+                                               uint32_t cmax, float wv[32])
+{
+    constexpr uint32_t mask = (1u << BITS) - 1u;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        const int o = j * BITS;
+        const int q = o >> 5;
+        const int s = o & 31;
+        uint32_t v;
+        if (s + BITS <= 32)
+            v = w[q] >> s;
+        else
+            v = funnel(w[q + 1], w[q], (uint32_t)s);
+        v &= mask;
+        v = v < cmax ? v : cmax;
+        wv[j] = s_cb[v];
+    }
+}
+
+// One wave per row (grid-stride over rows); codebook (and x when it fits) in
+// LDS.  Each lane walks its (row, group) items with a one-deep software
+// pipeline: the words of the next item are in flight while the current one
+// is unpacked, and the very first load is issued before the LDS staging
+// barrier so HBM latency overlaps the codebook copy.  T <= TMAX tokens.
+template <int BITS, int TMAX, bool XLDS, typename XT, typename OT>
+__global__ __launch_bounds__(kBlock) void fixed_gemv_kernel(
+    const XT *__restrict__ x, const uint32_t *__restrict__ words,
+    const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C)
+{
+    extern __shared__ float lds[];
+    float *s_cb = lds;
+    float *s_x = lds + ((C + 3) & ~3);
+    const int tid = threadIdx.x;
+    const int lane = tid & (CBQ_WAVE - 1);
+    const int wave = tid / CBQ_WAVE;
+    const int G = K >> 5;                       // 32-index groups per row
+    const int NG = (G + CBQ_WAVE - 1) / CBQ_WAVE;  // items per lane per row (wave-uniform)
+    const int stride = gridDim.x * kWavesPerBlock;
+    const uint32_t cmax = (uint32_t)(C - 1);
+
+    int row = blockIdx.x * kWavesPerBlock + wave;
+    uint32_t cur[BITS];
+    if (row < M && lane < G)
+        __builtin_memcpy(cur, words + ((size_t)row * G + lane) * BITS, sizeof(cur));
+
+    for (int i = tid; i < C; i += kBlock) s_cb[i] = cb[i];
+    if (XLDS)
+        for (int i = tid; i < T * K; i += kBlock) s_x[i] = to_f32<XT>(x[i]);
+    __syncthreads();
+
+    while (row < M) {
+        float acc[TMAX];
+#pragma unroll
+        for (int t = 0; t < TMAX; t++) acc[t] = 0.f;
+        for (int it = 0; it < NG; it++) {
+            const int g = lane + it * CBQ_WAVE;
+            // next item of this lane: next group of the row, else first of next row
+            int g2 = g + CBQ_WAVE, row2 = row;
+            if (it + 1 == NG) { g2 = lane; row2 = row + stride; }
+            uint32_t nxt[BITS];
+            if (row2 < M && g2 < G)
+                __builtin_memcpy(nxt, words + ((size_t)row2 * G + g2) * BITS, sizeof(nxt));
+            if (g < G) {
+                float wv[32];
+                gather_weights<BITS>(cur, s_cb, cmax, wv);
+#pragma unroll
+                for (int t = 0; t < TMAX; t++) {
+                    if (t < T) {
+                        float xv[32];
+                        if (XLDS)
+                            __builtin_memcpy(xv, s_x + t * K + g * 32, sizeof(xv));
+                        else
+                            load_x32<XT>(x + (size_t)t * K + g * 32, xv);
+                        float a = acc[t];
+#pragma unroll
+                        for (int j = 0; j < 32; j++) a = fmaf(xv[j], wv[j], a);
+                        acc[t] = a;
+                    }
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < BITS; b++) cur[b] = nxt[b];
+        }
+#pragma unroll
+        for (int t = 0; t < TMAX; t++) {
+            if (t < T) {
+                const float s = wave_sum(acc[t]);
+                if (lane == 0) out[(size_t)t * M + row] = from_f32<OT>(s);
+            }
+        }
+        row += stride;
+    }
+}
+
+// Any width, any K, codebook read through the cache: per-element 4-byte
+// window like the reference (reads at most 3 bytes past the last index).
+template <int TMAX, typename XT, typename OT>
+__global__ __launch_bounds__(kBlock) void fixed_gemv_generic_kernel(
+    const XT *__restrict__ x, const uint8_t *__restrict__ packed,
+    const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C,
+    int bits)
+{
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int wave = threadIdx.x / CBQ_WAVE;
+    const uint32_t mask = (1u << bits) - 1u;
+    const uint32_t cmax = (uint32_t)(C - 1);
+    for (int row = blockIdx.x * kWavesPerBlock + wave; row < M;
+         row += gridDim.x * kWavesPerBlock) {
+        float acc[TMAX];
+#pragma unroll
+        for (int t = 0; t < TMAX; t++) acc[t] = 0.f;
+        for (int k = lane; k < K; k += CBQ_WAVE) {
+            const int64_t bit = ((int64_t)row * K + k) * bits;
+            const uint8_t *p = packed + (bit >> 3);
+            uint32_t win = (uint32_t)p[0] | ((uint32_t)p[1] << 8) |
+                           ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+            uint32_t v = (win >> (bit & 7)) & mask;
+            v = v < cmax ? v : cmax;
+            const float w = cb[v];
+#pragma unroll
+            for (int t = 0; t < TMAX; t++)
+                if (t < T) acc[t] = fmaf(to_f32<XT>(x[(size_t)t * K + k]), w, acc[t]);
+        }
+#pragma unroll
+        for (int t = 0; t < TMAX; t++) {
+            if (t < T) {
+                const float s = wave_sum(acc[t]);
+                if (lane == 0) out[(size_t)t * M + row] = from_f32<OT>(s);
+            }
+        }
+    }
+}
+
+// Embedding: one thread per 32-index group of a requested row (H % 32 == 0).
+template <int BITS>
+__global__ __launch_bounds__(kBlock) void fixed_embedding_kernel(
+    const int32_t *__restrict__ ids, const uint32_t *__restrict__ words,
+    const float *__restrict__ cb, float *__restrict__ out, int T, int vocab, int H,
+    int C)
+{
+    const int G = H >> 5;
+    const int g = blockIdx.x * kBlock + threadIdx.x;
+    const int t = blockIdx.y;
+    if (g >= G || t >= T) return;
+    int id = ids[t];
+    if (vocab > 0) id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+    uint32_t w[BITS];
+    __builtin_memcpy(w, words + ((size_t)id * G + g) * BITS, BITS * sizeof(uint32_t));
+    constexpr uint32_t mask = (1u << BITS) - 1u;
+    const uint32_t cmax = (uint32_t)(C - 1);
+    float v32[32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        const int o = j * BITS, q = o >> 5, s = o & 31;
+        uint32_t v = (s + BITS <= 32) ? (w[q] >> s) : funnel(w[q + 1], w[q], (uint32_t)s);
+        v &= mask;
+        v = v < cmax ? v : cmax;
+        v32[j] = cb[v];
+    }
+    __builtin_memcpy(out + (size_t)t * H + (size_t)g * 32, v32, sizeof(v32));
+}
+
+__global__ __launch_bounds__(kBlock) void fixed_embedding_generic_kernel(
+    const int32_t *__restrict__ ids, const uint8_t *__restrict__ packed,
+    const float *__restrict__ cb, float *__restrict__ out, int T, int vocab, int H,
+    int C, int bits)
+{
+    const int h = blockIdx.x * kBlock + threadIdx.x;
+    const int t = blockIdx.y;
+    if (h >= H || t >= T) return;
+    int id = ids[t];
+    if (vocab > 0) id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+    const int64_t bit = ((int64_t)id * H + h) * bits;
+    const uint8_t *p = packed + (bit >> 3);
+    uint32_t win = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
+                   ((uint32_t)p[3] << 24);
+    uint32_t v = (win >> (bit & 7)) & ((1u << bits) - 1u);
+    const uint32_t cmax = (uint32_t)(C - 1);
+    out[(size_t)t * H + h] = cb[v < cmax ? v : cmax];
+}
+
+// ---- launch plumbing -------------------------------------------------------
+
+template <int BITS, int TMAX, bool XLDS, typename XT, typename OT>
+int launch_fast(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T,
+                int M, int K, int C, hipStream_t st)
+{
+    const size_t lds = (size_t)((C + 3) & ~3) * 4 + (XLDS ? (size_t)T * K * 4 : 0);
+    // Two 8-wave blocks per CU: each block stages its own codebook copy, so
+    // more blocks would only add L2->LDS traffic.
+    const int per_cu = std::max(1, std::min(2, (int)(160 * 1024 / std::max<size_t>(lds, 1))));
+    const int blocks = std::max(1, std::min((M + kWavesPerBlock - 1) / kWavesPerBlock,
+                                            cbq_num_cus() * per_cu));
+    hipLaunchKernelGGL((fixed_gemv_kernel<BITS, TMAX, XLDS, XT, OT>), dim3(blocks),
+                       dim3(kBlock), lds, st, x, (const uint32_t *)packed, cb, out, T, M,
+                       K, C);
+    return cbq_launch_status("fixed_gemv_kernel");
+}
+
+template <int BITS, int TMAX, typename XT, typename OT>
+int dispatch_x(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T,
+               int M, int K, int C, hipStream_t st)
+{
+    const size_t cb_bytes = (size_t)((C + 3) & ~3) * 4;
+    if (cb_bytes + (size_t)T * K * 4 <= (size_t)kMaxLdsBytes)
+        return launch_fast<BITS, TMAX, true>(x, packed, cb, out, T, M, K, C, st);
+    return launch_fast<BITS, TMAX, false>(x, packed, cb, out, T, M, K, C, st);
+}
+
+template <int BITS, typename XT, typename OT>
+int dispatch_t(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T,
+               int M, int K, int C, hipStream_t st)
+{
+    if (T == 1) return dispatch_x<BITS, 1>(x, packed, cb, out, T, M, K, C, st);
+    if (T <= 4) return dispatch_x<BITS, 4>(x, packed, cb, out, T, M, K, C, st);
+    return dispatch_x<BITS, 16>(x, packed, cb, out, T, M, K, C, st);
+}
+
+template <int TMAX, typename XT, typename OT>
+int launch_generic(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T,
+                   int M, int K, int C, int bits, hipStream_t st)
+{
+    const int blocks = std::max(1, std::min((M + kWavesPerBlock - 1) / kWavesPerBlock,
+                                            cbq_num_cus() * 8));
+    hipLaunchKernelGGL((fixed_gemv_generic_kernel<TMAX, XT, OT>), dim3(blocks),
+                       dim3(kBlock), 0, st, x, packed, cb, out, T, M, K, C, bits);
+    return cbq_launch_status("fixed_gemv_generic_kernel");
+}
+
+// One token tile (T <= 16).
+template <typename XT, typename OT>
+int linear_tile(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T,
+                int M, int K, int C, int bits, hipStream_t st)
+{
+    const bool fast = (K % 32 == 0) && C <= kMaxLdsCodebook &&
+                      ((uintptr_t)packed & 3) == 0;
+    if (fast) {
+        switch (bits) {
+        case 8: return dispatch_t<8>(x, packed, cb, out, T, M, K, C, st);
+        case 10: return dispatch_t<10>(x, packed, cb, out, T, M, K, C, st);
+        case 11: return dispatch_t<11>(x, packed, cb, out, T, M, K, C, st);
+        case 12: return dispatch_t<12>(x, packed, cb, out, T, M, K, C, st);
+        case 13: return dispatch_t<13>(x, packed, cb, out, T, M, K, C, st);
+        case 14: return dispatch_t<14>(x, packed, cb, out, T, M, K, C, st);
+        case 16: return dispatch_t<16>(x, packed, cb, out, T, M, K, C, st);
+        default: break;
+        }
+    }
+    if (T == 1) return launch_generic<1>(x, packed, cb, out, T, M, K, C, bits, st);
+    if (T <= 4) return launch_generic<4>(x, packed, cb, out, T, M, K, C, bits, st);
+    return launch_generic<16>(x, packed, cb, out, T, M, K, C, bits, st);
+}
+
+template <typename XT, typename OT>
+int linear_any_t(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T,
+                 int M, int K, int C, int bits, hipStream_t st)
+{
+    if (!x || !packed || !cb || !out) return CK_ERR_ARG;
+    if (T <= 0 || M <= 0 || K <= 0 || C <= 0 || bits < 1 || bits > 16) return CK_ERR_ARG;
+    for (int t0 = 0; t0 < T; t0 += 16) {
+        const int tt = std::min(16, T - t0);
+        int rc = linear_tile<XT, OT>(x + (size_t)t0 * K, packed, cb, out + (size_t)t0 * M,
+                                     tt, M, K, C, bits, st);
+        if (rc) return rc;
+    }
+    return CK_SUCCESS;
+}
+
+template <int BITS>
+int launch_emb_fast(const int32_t *ids, const uint8_t *packed, const float *cb, float *out,
+                    int T, int vocab, int H, int C, hipStream_t st)
+{
+    dim3 grid((unsigned)((H / 32 + kBlock - 1) / kBlock), (unsigned)T);
+    hipLaunchKernelGGL((fixed_embedding_kernel<BITS>), grid, dim3(kBlock), 0, st, ids,
+                       (const uint32_t *)packed, cb, out, T, vocab, H, C);
+    return cbq_launch_status("fixed_embedding_kernel");
+}
+
+int embedding_impl(const int32_t *ids, const uint8_t *packed, const float *cb, float *out,
+                   int T, int vocab, int H, int C, int bits, hipStream_t st)
+{
+    if (!ids || !packed || !cb || !out) return CK_ERR_ARG;
+    if (T <= 0 || H <= 0 || C <= 0 || bits < 1 || bits > 16) return CK_ERR_ARG;
+    if (T > 65535) return CK_ERR_ARG;
+    if (H % 32 == 0) {
+        switch (bits) {
+        case 8: return launch_emb_fast<8>(ids, packed, cb, out, T, vocab, H, C, st);
+        case 12: return launch_emb_fast<12>(ids, packed, cb, out, T, vocab, H, C, st);
+        case 13: return launch_emb_fast<13>(ids, packed, cb, out, T, vocab, H, C, st);
+        case 14: return launch_emb_fast<14>(ids, packed, cb, out, T, vocab, H, C, st);
+        case 16: return launch_emb_fast<16>(ids, packed, cb, out, T, vocab, H, C, st);
+        default: break;
+        }
+    }
+    dim3 grid((unsigned)((H + kBlock - 1) / kBlock), (unsigned)T);
+    hipLaunchKernelGGL(fixed_embedding_generic_kernel, grid, dim3(kBlock), 0, st, ids,
+                       packed, cb, out, T, vocab, H, C, bits);
+    return cbq_launch_status("fixed_embedding_generic_kernel");
+}
+
+}  // namespace
+
+int cbq_num_cus()
+{
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cache[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
+extern "C" {
+
+const char *ck_error_string(int err)
+{
+    switch (err) {
+    case CK_SUCCESS: return "success";
+    case CK_ERR_HIP: return "HIP runtime error";
+    case CK_ERR_ARG: return "invalid argument";
+    default: return "unknown error";
+    }
+}
+
+const char *cbq_version(void) { return "cbq_hip 0.1 gfx950"; }
+
+int ck_linear_f32(const float *x, const uint8_t *packed, const float *codebook, float *out,
+                  int T, int M, int K, int C, int bits, hipStream_t stream)
+{
+    return linear_any_t<float, float>(x, packed, codebook, out, T, M, K, C, bits, stream);
+}
+
+int ck_linear_bf16(const void *x_bf16, const uint8_t *packed, const float *codebook,
+                   void *out_bf16, int T, int M, int K, int C, int bits, hipStream_t stream)
+{
+    return linear_any_t<uint16_t, uint16_t>((const uint16_t *)x_bf16, packed, codebook,
+                                            (uint16_t *)out_bf16, T, M, K, C, bits, stream);
+}
+
+int ck_embedding_f32(const int32_t *token_ids, const uint8_t *packed, const float *codebook,
+                     float *out, int T, int H, int C, int bits, hipStream_t stream)
+{
+    return embedding_impl(token_ids, packed, codebook, out, T, 0, H, C, bits, stream);
+}
+
+int cbq_embedding_f32(const int32_t *token_ids, const uint8_t *packed, const float *codebook,
+                      float *out, int T, int vocab, int H, int C, int bits,
+                      hipStream_t stream)
+{
+    if (vocab <= 0) return CK_ERR_ARG;
+    return embedding_impl(token_ids, packed, codebook, out, T, vocab, H, C, bits, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,882 @@
+// Canonical-Huffman compressed GEMV / embedding / decode for gfx950.
+//
+// Stream semantics are those of the reference decoder
+// (src/compressed_matmul.c:121-186, rocm/huffman_kernel.hip:78-115): codes
+// are canonical (RFC 1951), MSB-first in the byte stream; a 12-bit table
+// resolves codes <= 12 bits, longer codes are matched length by length, and
+// a prefix that matches no code yields symbol 0 and advances one bit.
+//
+// Device format (built once at load, see cbq_hip.h): the bits of each stream
+// byte are reversed so the stream reads LSB-first from little-endian 32-bit
+// words; `window = alignbit(w[d+1], w[d], pos)` then holds the next 32 stream
+// bits with the first one in bit 0, and a code's first 12 bits are
+// `window & 0xfff` (bit-reversed).  Decode tables:
+//   lut1[4096]  leaf: len (bits 0-5) | payload << 16, or pointer: len 0,
+//               nb (bits 6-10) extra bits, base (bits 11-31) into lut2;
+//   lut2        leaf entries of the per-prefix subtables (2^nb each); 0
+//               marks "longer than 24 bits": resolved from canon tables.
+// payload = bf16 value of codebook[min(sym, C-1)], or the symbol itself.
+//
+// Work decomposition of the fused GEMV: flat symbols are cut into 64-symbol
+// sub-blocks (one per lane) and 4096-symbol chunks (one per wave step); a
+// sub-block's start bit is chunk_off[c] + the wave's exclusive scan of the
+// chunk's sub_len[].  A wave owns a row group (the least number of whole rows
+// that is also a whole number of chunks), stages each chunk's words in LDS,
+// decodes 64 symbols per lane straight into the dot product and reduces per
+// row with masked wave sums, carrying the one row that spans two chunks.
+#include "cbq_device.h"
+
+#include <algorithm>
+#include <thread>
+#include <vector>
+
+namespace {
+
+constexpr int kLutBits = 12;
+constexpr int kLutSize = 1 << kLutBits;
+constexpr int kChunk = 4096;
+constexpr int kSub = 64;
+constexpr int kMaxLen = 32;
+constexpr int kCanonInts = 3 * (kMaxLen + 1) + 1;   // first | count | base | invalid payload
+constexpr int kHBlock = 512;                        // 8 waves
+constexpr int kHWaves = kHBlock / CBQ_WAVE;
+constexpr int kLut2LdsMax = 8192;                   // lut2 entries kept in LDS
+constexpr int kStageMaxWords = 4096;                // per-wave staging cap (16 KB)
+
+// ---------------------------------------------------------------------------
+// Host: canonical codes and tables
+// ---------------------------------------------------------------------------
+
+uint32_t bitrev(uint32_t v, int n)
+{
+    uint32_t r = 0;
+    for (int i = 0; i < n; i++) r |= ((v >> i) & 1u) << (n - 1 - i);
+    return r;
+}
+
+struct Canon {
+    int max_len = 0;
+    int64_t first[kMaxLen + 2];
+    int32_t count[kMaxLen + 2];
+    int32_t base[kMaxLen + 2];
+    std::vector<uint32_t> code;     // per symbol
+    std::vector<int32_t> order;     // symbols in canonical order
+};
+
+// RFC 1951 section 3.2.2 code assignment; false when the lengths over-fill
+// the code space (Kraft sum > 1) or exceed 32.
+bool make_canon(const uint8_t *lengths, int n, Canon &cn)
+{
+    for (int L = 0; L <= kMaxLen + 1; L++) { cn.first[L] = -1; cn.count[L] = 0; cn.base[L] = 0; }
+    uint64_t kraft = 0;
+    for (int s = 0; s < n; s++) {
+        int L = lengths[s];
+        if (L > kMaxLen) return false;
+        if (L) { cn.count[L]++; kraft += 1ull << (kMaxLen - L); cn.max_len = std::max(cn.max_len, L); }
+    }
+    if (kraft > (1ull << kMaxLen)) return false;
+    int64_t next[kMaxLen + 2];
+    int64_t code = 0;
+    next[0] = 0;
+    for (int L = 1; L <= kMaxLen; L++) {
+        code = (code + (L > 1 ? cn.count[L - 1] : 0)) << 1;
+        next[L] = code;
+        if (cn.count[L]) cn.first[L] = code;
+    }
+    int acc = 0;
+    for (int L = 1; L <= kMaxLen; L++) { cn.base[L] = acc; acc += cn.count[L]; }
+    cn.base[kMaxLen + 1] = acc;
+    cn.code.assign(n, 0);
+    cn.order.assign(acc, 0);
+    int fill[kMaxLen + 2];
+    for (int L = 0; L <= kMaxLen + 1; L++) fill[L] = cn.base[L];
+    for (int s = 0; s < n; s++) {
+        int L = lengths[s];
+        if (!L) continue;
+        cn.code[s] = (uint32_t)next[L]++;
+        cn.order[fill[L]++] = s;
+    }
+    return true;
+}
+
+inline uint32_t leaf(int len, uint32_t payload) { return (uint32_t)len | (payload << 16); }
+
+// ---------------------------------------------------------------------------
+// Host: decoder used by the indexer (MSB-first, reference semantics)
+// ---------------------------------------------------------------------------
+
+struct HostDecoder {
+    Canon cn;
+    uint8_t lut_len[kLutSize];      // 0: no code of <= 12 bits has this prefix
+
+    bool init(const uint8_t *lengths, int n)
+    {
+        if (!make_canon(lengths, n, cn)) return false;
+        std::fill(lut_len, lut_len + kLutSize, 0);
+        for (int s = 0; s < n; s++) {
+            int L = lengths[s];
+            if (!L || L > kLutBits) continue;
+            uint32_t lo = cn.code[s] << (kLutBits - L), cnt = 1u << (kLutBits - L);
+            for (uint32_t i = 0; i < cnt; i++) lut_len[lo + i] = (uint8_t)L;
+        }
+        return true;
+    }
+
+    // 32 stream bits at `pos`, first one in the MSB (stream has >= 4 pad bytes
+    // beyond the last code byte; reads at most 5 bytes).
+    static uint32_t peek32(const uint8_t *s, int64_t nbytes, int64_t pos)
+    {
+        int64_t b = pos >> 3;
+        uint64_t w = 0;
+        for (int i = 0; i < 5; i++) w = (w << 8) | (b + i < nbytes ? s[b + i] : 0);
+        return (uint32_t)(w >> (8 - (pos & 7)));
+    }
+
+    int length_at(const uint8_t *s, int64_t nbytes, int64_t pos) const
+    {
+        uint32_t w = peek32(s, nbytes, pos);
+        int L = lut_len[w >> (32 - kLutBits)];
+        if (L) return L;
+        for (L = kLutBits + 1; L <= cn.max_len; L++) {
+            if (!cn.count[L]) continue;
+            int64_t d = (int64_t)(w >> (32 - L)) - cn.first[L];
+            if (d >= 0 && d < cn.count[L]) return L;
+        }
+        return 1;   // corrupt prefix: symbol 0, one bit
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Device: decode tables in LDS and the per-symbol step
+// ---------------------------------------------------------------------------
+
+struct Tabs {
+    const uint32_t *lut1;       // LDS
+    const uint32_t *lut2;       // LDS or global
+    uint32_t n_lut2;
+    const int32_t *canon;       // global
+    const int32_t *canon_pay;   // global
+};
+
+// Codes longer than 24 bits (and their corrupt neighbours): length by length
+// over the canonical first codes, as the reference's slow path.
+__device__ __noinline__ uint32_t decode_canon(uint32_t w, const int32_t *__restrict__ canon,
+                                              const int32_t *__restrict__ pay)
+{
+    const uint32_t msb = __brev(w);
+    for (int L = kLutBits + 1; L <= kMaxLen; L++) {
+        const int32_t cnt = canon[(kMaxLen + 1) + L];
+        if (!cnt) continue;
+        const uint32_t code = msb >> (32 - L);
+        const uint32_t first = (uint32_t)canon[L];   // < 2^L, stored as raw bits
+        if (code >= first && code - first < (uint32_t)cnt)
+            return (uint32_t)L | ((uint32_t)pay[canon[2 * (kMaxLen + 1) + L] + (code - first)] << 16);
+    }
+    return 1u | ((uint32_t)canon[3 * (kMaxLen + 1)] << 16);
+}
+
+__device__ __forceinline__ uint32_t decode_entry(uint32_t w, const Tabs &tb)
+{
+    uint32_t e = tb.lut1[w & (kLutSize - 1)];
+    if ((e & 63u) == 0u) {
+        const uint32_t nb = (e >> 6) & 31u;
+        uint32_t i = (e >> 11) + ((w >> kLutBits) & ((1u << nb) - 1u));
+        i = i < tb.n_lut2 ? i : tb.n_lut2 - 1u;
+        e = tb.lut2[i];
+        if ((e & 63u) == 0u) e = decode_canon(w, tb.canon, tb.canon_pay);
+    }
+    return e;
+}
+
+// Stage the words of bit range [b0, b1) (plus one word of look-ahead) into a
+// wave's LDS slot.  Returns false when the range does not fit (the caller
+// then reads windows from global memory).
+__device__ __forceinline__ bool stage_words(uint32_t *__restrict__ stg, int stg_words,
+                                            const uint32_t *__restrict__ words,
+                                            int64_t n_words, uint64_t b0, uint64_t b1,
+                                            int lane)
+{
+    const int64_t w0 = (int64_t)(b0 >> 5);
+    const int64_t nw = (int64_t)((b1 + 31) >> 5) - w0 + 2;
+    if (nw > stg_words) return false;
+    for (int64_t i = lane; i < nw; i += CBQ_WAVE) {
+        const int64_t src = w0 + i;
+        stg[i] = src < n_words ? words[src] : 0u;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    return true;
+}
+
+__device__ __forceinline__ void wave_sync_lds()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// 32 stream bits at relative bit `pos` of a staged range (staged) or of the
+// global stream starting at word w0 (fallback; word index clamped).
+__device__ __forceinline__ uint32_t window_lds(const uint32_t *__restrict__ stg, uint32_t pos)
+{
+    const uint32_t d = pos >> 5;
+    return funnel(stg[d + 1], stg[d], pos);
+}
+
+__device__ __forceinline__ uint32_t window_global(const uint32_t *__restrict__ words,
+                                                  int64_t n_words, int64_t w0, uint32_t pos)
+{
+    int64_t d = w0 + (pos >> 5);
+    d = d < n_words - 1 ? d : n_words - 2;
+    d = d < 0 ? 0 : d;
+    return funnel(words[d + 1], words[d], pos);
+}
+
+// Load the block-shared decode tables into LDS.
+__device__ __forceinline__ void load_tables(uint32_t *s_lut1, uint32_t *s_lut2,
+                                            const uint32_t *__restrict__ lut1,
+                                            const uint32_t *__restrict__ lut2, int n_lut2,
+                                            bool lut2_lds, float *s_cb,
+                                            const float *__restrict__ cb, int n_cb)
+{
+    for (int i = threadIdx.x; i < kLutSize; i += blockDim.x) s_lut1[i] = lut1[i];
+    if (lut2_lds)
+        for (int i = threadIdx.x; i < n_lut2; i += blockDim.x) s_lut2[i] = lut2[i];
+    for (int i = threadIdx.x; i < n_cb; i += blockDim.x) s_cb[i] = cb[i];
+}
+
+// Payload -> weight.  VALUE_MODE: bf16 bits in the payload; else symbol
+// index into the (clamped-at-build-time) LDS codebook.
+template <bool VALUE_MODE>
+__device__ __forceinline__ float payload_value(uint32_t e, const float *__restrict__ s_cb)
+{
+    if (VALUE_MODE) return __uint_as_float(e & 0xffff0000u);
+    return s_cb[e >> 16];
+}
+
+struct HuffArgs {
+    const uint32_t *words;
+    int64_t n_words;
+    const uint64_t *chunk_off;
+    const uint16_t *sub_len;
+    const uint32_t *lut1;
+    const uint32_t *lut2;
+    int n_lut2;
+    const int32_t *canon;
+    const int32_t *canon_pay;
+    const float *value_cb;
+    int C;
+    int64_t n_sym;      // flat symbols
+    int64_t n_chunks;
+    int64_t n_sub;
+};
+
+// Start bit (absolute) of sub-block c*64 + lane, via a wave scan of the
+// chunk's sub-block lengths.  Lanes past the last sub-block get length 0.
+__device__ __forceinline__ uint64_t subblock_start(const HuffArgs &a, int64_t c, int lane,
+                                                   uint32_t &my_len)
+{
+    const int64_t s = c * kSub + lane;
+    my_len = s < a.n_sub ? (uint32_t)a.sub_len[s] : 0u;
+    const uint32_t incl = wave_incl_scan(my_len);
+    return a.chunk_off[c] + (uint64_t)(incl - my_len);
+}
+
+// ---------------------------------------------------------------------------
+// Fused GEMV
+// ---------------------------------------------------------------------------
+
+template <int TMAX, bool VALUE_MODE>
+__global__ __launch_bounds__(kHBlock) void huff_gemv_kernel(
+    const float *__restrict__ x, float *__restrict__ out, HuffArgs a, int T, int M, int K,
+    int RW, int SPL, int stg_words, int lut2_lds, int n_cb)
+{
+    extern __shared__ uint32_t hlds[];
+    uint32_t *s_lut1 = hlds;
+    uint32_t *s_lut2 = s_lut1 + kLutSize;
+    const int lut2_slots = lut2_lds ? ((a.n_lut2 + 3) & ~3) : 0;
+    float *s_cb = (float *)(s_lut2 + lut2_slots);
+    uint32_t *s_stg = (uint32_t *)(s_cb + ((n_cb + 3) & ~3));
+    load_tables(s_lut1, s_lut2, a.lut1, a.lut2, a.n_lut2, lut2_lds, s_cb, a.value_cb, n_cb);
+    __syncthreads();
+
+    const Tabs tb{s_lut1, lut2_lds ? s_lut2 : a.lut2, (uint32_t)a.n_lut2, a.canon, a.canon_pay};
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int wave = threadIdx.x / CBQ_WAVE;
+    uint32_t *stg = s_stg + wave * stg_words;
+    const int64_t n_groups = ((int64_t)M + RW - 1) / RW;
+
+    for (int64_t grp = (int64_t)blockIdx.x * kHWaves + wave; grp < n_groups;
+         grp += (int64_t)gridDim.x * kHWaves) {
+        float carry[TMAX];
+#pragma unroll
+        for (int t = 0; t < TMAX; t++) carry[t] = 0.f;
+        int64_t carry_row = -1;
+        for (int ci = 0; ci < SPL; ci++) {
+            const int64_t c = grp * SPL + ci;
+            if (c >= a.n_chunks) break;
+            uint32_t my_len;
+            const uint64_t start = subblock_start(a, c, lane, my_len);
+            const uint64_t cbeg = a.chunk_off[c], cend = a.chunk_off[c + 1];
+            const bool staged = stage_words(stg, stg_words, a.words, a.n_words, cbeg, cend, lane);
+            const int64_t w0 = (int64_t)(cbeg >> 5);
+            uint32_t pos = (uint32_t)(start - ((uint64_t)w0 << 5));
+
+            const int64_t s = c * kSub + lane;
+            const int64_t sym0 = s * kSub;
+            const bool active = s < a.n_sub;
+            const int64_t row = active ? sym0 / K : -1;
+            const int k0 = active ? (int)(sym0 - row * K) : 0;
+            float acc[TMAX];
+#pragma unroll
+            for (int t = 0; t < TMAX; t++) acc[t] = 0.f;
+            if (active) {
+                const float *xr = x + k0;
+#pragma unroll 4
+                for (int i = 0; i < kSub; i += 4) {
+                    float wv[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const uint32_t w = staged ? window_lds(stg, pos)
+                                                  : window_global(a.words, a.n_words, w0, pos);
+                        const uint32_t e = decode_entry(w, tb);
+                        pos += e & 63u;
+                        wv[j] = payload_value<VALUE_MODE>(e, s_cb);
+                    }
+#pragma unroll
+                    for (int t = 0; t < TMAX; t++) {
+                        if (t < T) {
+                            float xv[4];
+                            __builtin_memcpy(xv, xr + (size_t)t * K + i, sizeof(xv));
+                            float v = acc[t];
+#pragma unroll
+                            for (int j = 0; j < 4; j++) v = fmaf(xv[j], wv[j], v);
+                            acc[t] = v;
+                        }
+                    }
+                }
+            }
+            // per-row reduction of this chunk's lanes; rows are contiguous lane runs
+            const int64_t first_row = (c * kChunk) / K;
+            int64_t last_row = (std::min<int64_t>(c * kChunk + kChunk, a.n_sym) - 1) / K;
+            for (int64_t r = first_row; r <= last_row; r++) {
+                const bool mine = row == r;
+                const bool row_ends_here = (r + 1) * (int64_t)K <= std::min<int64_t>(c * kChunk + kChunk, a.n_sym);
+#pragma unroll
+                for (int t = 0; t < TMAX; t++) {
+                    if (t < T) {
+                        float v = wave_sum(mine ? acc[t] : 0.f);
+                        if (r == carry_row) v += carry[t];
+                        if (row_ends_here) {
+                            if (lane == 0 && r < M) out[(size_t)t * M + r] = v;
+                        } else {
+                            carry[t] = v;
+                        }
+                    }
+                }
+                if (!row_ends_here) carry_row = r;
+            }
+            wave_sync_lds();   // staging slot is rewritten by the next chunk
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Embedding: one wave per requested row (H % 64 == 0)
+// ---------------------------------------------------------------------------
+
+template <bool VALUE_MODE>
+__global__ __launch_bounds__(kHBlock) void huff_embedding_kernel(
+    const int32_t *__restrict__ ids, float *__restrict__ out, HuffArgs a, int T, int vocab,
+    int H, int stg_words, int lut2_lds, int n_cb)
+{
+    extern __shared__ uint32_t hlds[];
+    uint32_t *s_lut1 = hlds;
+    uint32_t *s_lut2 = s_lut1 + kLutSize;
+    const int lut2_slots = lut2_lds ? ((a.n_lut2 + 3) & ~3) : 0;
+    float *s_cb = (float *)(s_lut2 + lut2_slots);
+    uint32_t *s_stg = (uint32_t *)(s_cb + ((n_cb + 3) & ~3));
+    load_tables(s_lut1, s_lut2, a.lut1, a.lut2, a.n_lut2, lut2_lds, s_cb, a.value_cb, n_cb);
+    __syncthreads();
+
+    const Tabs tb{s_lut1, lut2_lds ? s_lut2 : a.lut2, (uint32_t)a.n_lut2, a.canon, a.canon_pay};
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int wave = threadIdx.x / CBQ_WAVE;
+    uint32_t *stg = s_stg + wave * stg_words;
+    const int KS = H / kSub;                 // sub-blocks per row
+
+    for (int t = blockIdx.x * kHWaves + wave; t < T; t += gridDim.x * kHWaves) {
+        int id = ids[t];
+        id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);
+        const int64_t s_first = (int64_t)id * KS;
+        for (int r0 = 0; r0 < KS; r0 += CBQ_WAVE) {
+            // sub-blocks s_first + r0 + lane lie in at most two chunks: scan both
+            const int64_t sA = s_first + r0;
+            const int64_t cA = sA / kSub;
+            uint32_t lenA, lenB = 0;
+            const uint64_t startA = subblock_start(a, cA, lane, lenA);
+            const uint64_t startB = cA + 1 < a.n_chunks ? subblock_start(a, cA + 1, lane, lenB) : 0;
+            const int64_t s = sA + lane;
+            const bool active = (r0 + lane) < KS && s < a.n_sub;
+            const int src = (int)(s & (kSub - 1));
+            const bool inA = (s / kSub) == cA;
+            const uint64_t my_start = inA ? __shfl(startA, src, CBQ_WAVE) : __shfl(startB, src, CBQ_WAVE);
+            const uint32_t my_len = inA ? __shfl(lenA, src, CBQ_WAVE) : __shfl(lenB, src, CBQ_WAVE);
+            const int n_act = std::min(CBQ_WAVE, KS - r0);
+            const uint64_t lo = __shfl(my_start, 0, CBQ_WAVE);
+            const uint64_t hi = __shfl(my_start + my_len, n_act - 1, CBQ_WAVE);
+            const bool staged = stage_words(stg, stg_words, a.words, a.n_words, lo, hi, lane);
+            const int64_t w0 = (int64_t)(lo >> 5);
+            uint32_t pos = (uint32_t)(my_start - ((uint64_t)w0 << 5));
+            if (active) {
+                float *dst = out + (size_t)t * H + (size_t)(r0 + lane) * kSub;
+#pragma unroll 4
+                for (int i = 0; i < kSub; i += 4) {
+                    float v[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const uint32_t w = staged ? window_lds(stg, pos)
+                                                  : window_global(a.words, a.n_words, w0, pos);
+                        const uint32_t e = decode_entry(w, tb);
+                        pos += e & 63u;
+                        v[j] = payload_value<VALUE_MODE>(e, s_cb);
+                    }
+                    __builtin_memcpy(dst + i, v, sizeof(v));
+                }
+            }
+            wave_sync_lds();
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode to indices: one wave per chunk (payload = symbol)
+// ---------------------------------------------------------------------------
+
+__global__ __launch_bounds__(kHBlock) void huff_decode_kernel(int32_t *__restrict__ out,
+                                                            HuffArgs a, int stg_words,
+                                                            int lut2_lds)
+{
+    extern __shared__ uint32_t hlds[];
+    uint32_t *s_lut1 = hlds;
+    uint32_t *s_lut2 = s_lut1 + kLutSize;
+    const int lut2_slots = lut2_lds ? ((a.n_lut2 + 3) & ~3) : 0;
+    uint32_t *s_stg = s_lut2 + lut2_slots;
+    load_tables(s_lut1, s_lut2, a.lut1, a.lut2, a.n_lut2, lut2_lds, nullptr, nullptr, 0);
+    __syncthreads();
+
+    const Tabs tb{s_lut1, lut2_lds ? s_lut2 : a.lut2, (uint32_t)a.n_lut2, a.canon, a.canon_pay};
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int wave = threadIdx.x / CBQ_WAVE;
+    uint32_t *stg = s_stg + wave * stg_words;
+    for (int64_t c = (int64_t)blockIdx.x * kHWaves + wave; c < a.n_chunks;
+         c += (int64_t)gridDim.x * kHWaves) {
+        uint32_t my_len;
+        const uint64_t start = subblock_start(a, c, lane, my_len);
+        const uint64_t cbeg = a.chunk_off[c], cend = a.chunk_off[c + 1];
+        const bool staged = stage_words(stg, stg_words, a.words, a.n_words, cbeg, cend, lane);
+        const int64_t w0 = (int64_t)(cbeg >> 5);
+        uint32_t pos = (uint32_t)(start - ((uint64_t)w0 << 5));
+        const int64_t sym0 = (c * kSub + lane) * kSub;
+        const int nsym = (int)std::max<int64_t>(0, std::min<int64_t>(kSub, a.n_sym - sym0));
+        for (int i = 0; i < nsym; i++) {
+            const uint32_t w = staged ? window_lds(stg, pos)
+                                      : window_global(a.words, a.n_words, w0, pos);
+            const uint32_t e = decode_entry(w, tb);
+            pos += e & 63u;
+            out[sym0 + i] = (int32_t)(e >> 16);
+        }
+        wave_sync_lds();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Reference-format kernels (huff_decode_to_i32 & co.)
+// ---------------------------------------------------------------------------
+
+// One thread per row over the reference's tables: MSB-first 32-bit peek,
+// 12-bit LUT (-1 = miss), then lengths 13..max_len; corrupt -> 0, +1 bit.
+__global__ void ref_decode_rows_kernel(const uint8_t *__restrict__ stream,
+                                       const int64_t *__restrict__ rbs,
+                                       const int32_t *__restrict__ lut_sym,
+                                       const int32_t *__restrict__ lut_len,
+                                       const int32_t *__restrict__ sl_first,
+                                       const int32_t *__restrict__ sl_base,
+                                       const int32_t *__restrict__ sl_sym,
+                                       int32_t *__restrict__ out, int M, int K, int max_len)
+{
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= M) return;
+    int64_t pos = rbs[r];
+    int32_t *dst = out + (int64_t)r * K;
+    for (int k = 0; k < K; k++) {
+        // 40-bit big-endian window; the stream carries >= 4 pad bytes, so the
+        // 5th byte after the byte holding the symbol's first bit is readable.
+        const uint8_t *p = stream + (pos >> 3);
+        uint64_t w40 = 0;
+        for (int i = 0; i < 5; i++) w40 = (w40 << 8) | p[i];
+        const uint32_t w = (uint32_t)(w40 >> (8 - (pos & 7)));   // 32 bits, first in MSB
+        const uint32_t key = w >> (32 - kLutBits);
+        const int32_t sym = lut_sym[key];
+        if (sym != -1) {
+            dst[k] = sym;
+            pos += lut_len[key];
+            continue;
+        }
+        int32_t out_sym = 0, out_len = 1;
+        for (int L = kLutBits + 1; L <= max_len; L++) {
+            const int32_t fc = sl_first[L];
+            if (fc < 0) continue;
+            const int64_t d = (int64_t)(w >> (32 - L)) - fc;
+            if (d >= 0 && d < sl_base[L + 1] - sl_base[L]) {
+                out_sym = sl_sym[sl_base[L] + d];
+                out_len = L;
+                break;
+            }
+        }
+        dst[k] = out_sym;
+        pos += out_len;
+    }
+}
+
+__global__ void i32_linear_kernel(const float *__restrict__ x, const int32_t *__restrict__ idx,
+                                  const float *__restrict__ cb, float *__restrict__ out, int T,
+                                  int M, int K, int C)
+{
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int row = blockIdx.x * (blockDim.x / CBQ_WAVE) + threadIdx.x / CBQ_WAVE;
+    if (row >= M) return;
+    const int32_t *wi = idx + (int64_t)row * K;
+    for (int t = 0; t < T; t++) {
+        float acc = 0.f;
+        for (int k = lane; k < K; k += CBQ_WAVE) {
+            int32_t v = wi[k];
+            v = (v < 0 || v >= C) ? C - 1 : v;
+            acc = fmaf(x[(int64_t)t * K + k], cb[v], acc);
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) out[(int64_t)t * M + row] = acc;
+    }
+}
+
+__global__ void i32_embedding_kernel(const int32_t *__restrict__ ids,
+                                     const int32_t *__restrict__ idx,
+                                     const float *__restrict__ cb, float *__restrict__ out,
+                                     int T, int H, int C)
+{
+    const int h = blockIdx.x * blockDim.x + threadIdx.x;
+    const int t = blockIdx.y;
+    if (h >= H || t >= T) return;
+    int32_t v = idx[(int64_t)ids[t] * H + h];
+    v = (v < 0 || v >= C) ? C - 1 : v;
+    out[(int64_t)t * H + h] = cb[v];
+}
+
+// ---------------------------------------------------------------------------
+// Launch helpers
+// ---------------------------------------------------------------------------
+
+bool fill_args(HuffArgs &a, const cbq_huff_stream *hs, int64_t n_sym)
+{
+    if (!hs || !hs->words || hs->n_words < 2 || !hs->chunk_off || !hs->sub_len || !hs->lut1 ||
+        !hs->lut2 || hs->n_lut2 < 1 || !hs->canon || !hs->canon_pay || n_sym <= 0)
+        return false;
+    a.words = hs->words; a.n_words = hs->n_words; a.chunk_off = hs->chunk_off;
+    a.sub_len = hs->sub_len; a.lut1 = hs->lut1; a.lut2 = hs->lut2; a.n_lut2 = hs->n_lut2;
+    a.canon = hs->canon; a.canon_pay = hs->canon_pay; a.value_cb = hs->value_cb; a.C = hs->C;
+    a.n_sym = n_sym;
+    a.n_chunks = (n_sym + kChunk - 1) / kChunk;
+    a.n_sub = (n_sym + kSub - 1) / kSub;
+    return true;
+}
+
+int stage_words_of(const cbq_huff_stream *hs)
+{
+    int w = hs->stage_words > 0 ? hs->stage_words : 1536;
+    return std::max(8, std::min(w, kStageMaxWords));
+}
+
+struct LdsPlan {
+    size_t bytes;
+    int lut2_lds;
+    int stg_words;
+    int n_cb;
+};
+
+// Staging slot size: from the chunk sizes known at load we only know the cap
+// here, so use the cap that keeps two blocks per CU when possible.
+LdsPlan plan_lds(int n_lut2, int n_cb, int stg_words)
+{
+    LdsPlan p;
+    p.lut2_lds = n_lut2 <= kLut2LdsMax;
+    p.n_cb = n_cb;
+    p.stg_words = stg_words;
+    p.bytes = (size_t)kLutSize * 4 + (p.lut2_lds ? (size_t)((n_lut2 + 3) & ~3) * 4 : 0) +
+              (size_t)((n_cb + 3) & ~3) * 4 + (size_t)kHWaves * stg_words * 4;
+    return p;
+}
+
+template <int TMAX, bool VM>
+int launch_gemv(const float *x, float *out, const HuffArgs &a, int T, int M, int K, int RW,
+                int SPL, const LdsPlan &p, hipStream_t st)
+{
+    const int64_t n_groups = ((int64_t)M + RW - 1) / RW;
+    const int per_cu = std::max(1, std::min(2, (int)(160 * 1024 / p.bytes)));
+    const int64_t want = (n_groups + kHWaves - 1) / kHWaves;
+    const int blocks = (int)std::max<int64_t>(1, std::min<int64_t>(want, (int64_t)cbq_num_cus() * per_cu));
+    hipLaunchKernelGGL((huff_gemv_kernel<TMAX, VM>), dim3(blocks), dim3(kHBlock), p.bytes, st, x,
+                       out, a, T, M, K, RW, SPL, p.stg_words, p.lut2_lds, p.n_cb);
+    return cbq_launch_status("huff_gemv_kernel");
+}
+
+int64_t gcd64(int64_t a, int64_t b) { while (b) { int64_t t = a % b; a = b; b = t; } return a; }
+
+}  // namespace
+
+extern "C" {
+
+int cbq_huff_build_luts(const uint8_t *lengths, int n_alpha, const float *codebook, int C,
+                        int payload_is_value, int clamp_to, uint32_t *lut1, uint32_t *lut2,
+                        int *n_lut2, int32_t *canon, int32_t *canon_pay)
+{
+    if (!lengths || n_alpha <= 0 || n_alpha > 65536 || !n_lut2) return CK_ERR_ARG;
+    if (payload_is_value && (!codebook || C <= 0)) return CK_ERR_ARG;
+    if (clamp_to && C <= 0) return CK_ERR_ARG;
+    Canon cn;
+    if (!make_canon(lengths, n_alpha, cn)) return CK_ERR_ARG;
+
+    auto payload = [&](int sym) -> uint32_t {
+        int s = sym;
+        if (payload_is_value || clamp_to) s = std::min(s, C - 1);
+        if (payload_is_value) {
+            uint32_t u;
+            __builtin_memcpy(&u, &codebook[s], 4);
+            return u >> 16;
+        }
+        return (uint32_t)s;
+    };
+    const uint32_t invalid = leaf(1, payload(0));
+
+    // Long-code prefixes: key = reversed first 12 code bits; subtable width.
+    std::vector<int> maxlen(kLutSize, 0);
+    for (int s = 0; s < n_alpha; s++) {
+        int L = lengths[s];
+        if (L <= kLutBits) continue;
+        uint32_t key = bitrev(cn.code[s] >> (L - kLutBits), kLutBits);
+        maxlen[key] = std::max(maxlen[key], L);
+    }
+    std::vector<uint32_t> base(kLutSize, 0), nbits(kLutSize, 0);
+    int64_t total = 0;
+    for (int k = 0; k < kLutSize; k++) {
+        if (!maxlen[k]) continue;
+        nbits[k] = (uint32_t)std::min(maxlen[k] - kLutBits, kLutBits);
+        base[k] = (uint32_t)total;
+        total += 1ll << nbits[k];
+    }
+    if (total == 0) total = 1;     // keep one (unused) entry so the array is never empty
+    if (total >= (1 << 21)) return CK_ERR_ARG;
+    *n_lut2 = (int)total;
+    if (canon) {
+        for (int L = 0; L <= kMaxLen; L++) {
+            canon[L] = (int32_t)cn.first[L];
+            canon[(kMaxLen + 1) + L] = cn.count[L];
+            canon[2 * (kMaxLen + 1) + L] = cn.base[L];
+        }
+        canon[3 * (kMaxLen + 1)] = (int32_t)payload(0);
+    }
+    if (canon_pay)
+        for (size_t i = 0; i < cn.order.size(); i++) canon_pay[i] = (int32_t)payload(cn.order[i]);
+    if (!lut1 || !lut2) return CK_SUCCESS;
+
+    for (int k = 0; k < kLutSize; k++) lut1[k] = invalid;
+    for (int64_t i = 0; i < total; i++) lut2[i] = invalid;
+    for (int k = 0; k < kLutSize; k++) {
+        if (!maxlen[k]) continue;
+        lut1[k] = (nbits[k] << 6) | (base[k] << 11);
+        if (maxlen[k] > 2 * kLutBits)   // codes beyond 24 bits: unresolved -> canon stage
+            for (uint32_t i = 0; i < (1u << nbits[k]); i++) lut2[base[k] + i] = 0u;
+    }
+    for (int s = 0; s < n_alpha; s++) {
+        const int L = lengths[s];
+        if (!L) continue;
+        const uint32_t e = leaf(L, payload(s));
+        if (L <= kLutBits) {
+            const uint32_t r = bitrev(cn.code[s], L);
+            for (uint32_t hi = 0; hi < (1u << (kLutBits - L)); hi++) lut1[r | (hi << L)] = e;
+        } else {
+            const uint32_t key = bitrev(cn.code[s] >> (L - kLutBits), kLutBits);
+            const int rest = L - kLutBits;
+            if (rest > (int)nbits[key]) continue;     // resolved by the canon stage
+            const uint32_t suf = bitrev(cn.code[s] & ((1u << rest) - 1u), rest);
+            for (uint32_t hi = 0; hi < (1u << (nbits[key] - rest)); hi++)
+                lut2[base[key] + (suf | (hi << rest))] = e;
+        }
+    }
+    return CK_SUCCESS;
+}
+
+int cbq_huff_index_stream(const uint8_t *stream_msb, int64_t stream_bytes,
+                          const uint8_t *lengths, int n_alpha, const int64_t *row_bit_starts,
+                          int M, int K, uint64_t *chunk_off, uint16_t *sub_len, int threads)
+{
+    if (!stream_msb || stream_bytes <= 0 || !lengths || n_alpha <= 0 || M <= 0 || K <= 0 ||
+        !chunk_off || !sub_len)
+        return CK_ERR_ARG;
+    HostDecoder dec;
+    if (!dec.init(lengths, n_alpha)) return CK_ERR_ARG;
+    const int64_t N = (int64_t)M * K;
+    const int64_t n_sub = (N + kSub - 1) / kSub;
+    const int64_t n_chunks = (N + kChunk - 1) / kChunk;
+    std::vector<int64_t> sub_start(n_sub + 1, -1);
+    const int64_t total_bits = stream_bytes * 8;
+    if (!row_bit_starts) threads = 1;
+    threads = std::max(1, std::min(threads, M));
+    std::vector<int> ok(threads, 1);
+    std::vector<int64_t> end_pos(threads, 0);
+
+    auto work = [&](int ti) {
+        const int ra = (int)((int64_t)M * ti / threads), rb = (int)((int64_t)M * (ti + 1) / threads);
+        int64_t pos = ti == 0 ? 0 : row_bit_starts[ra];
+        if (row_bit_starts && row_bit_starts[ra] != pos) { ok[ti] = 0; return; }
+        int64_t sym = (int64_t)ra * K, sym_end = (int64_t)rb * K;
+        // own the sub-blocks whose first symbol lies in [ra*K, rb*K)
+        while (sym < sym_end || (sym % kSub) != 0) {
+            if (sym >= N) break;
+            if (sym % kSub == 0) sub_start[sym / kSub] = pos;
+            if (row_bit_starts && sym % K == 0 && sym < sym_end && row_bit_starts[sym / K] != pos) {
+                ok[ti] = 0;
+                return;
+            }
+            if (pos >= total_bits) { ok[ti] = 0; return; }
+            pos += dec.length_at(stream_msb, stream_bytes, pos);
+            sym++;
+        }
+        end_pos[ti] = pos;
+    };
+    if (threads == 1) {
+        work(0);
+    } else {
+        std::vector<std::thread> pool;
+        for (int ti = 0; ti < threads; ti++) pool.emplace_back(work, ti);
+        for (auto &th : pool) th.join();
+    }
+    for (int ti = 0; ti < threads; ti++)
+        if (!ok[ti]) return CK_ERR_ARG;
+    int64_t last_end = 0;
+    // the thread that decoded symbol N-1 reports the stream end
+    for (int ti = 0; ti < threads; ti++) last_end = std::max(last_end, end_pos[ti]);
+    sub_start[n_sub] = last_end;
+    for (int64_t s = 0; s < n_sub; s++) {
+        const int64_t len = sub_start[s + 1] - sub_start[s];
+        if (sub_start[s] < 0 || len < 0 || len > 65535) return CK_ERR_ARG;
+        sub_len[s] = (uint16_t)len;
+    }
+    for (int64_t c = 0; c < n_chunks; c++) chunk_off[c] = (uint64_t)sub_start[c * (kChunk / kSub)];
+    chunk_off[n_chunks] = (uint64_t)last_end;
+    return CK_SUCCESS;
+}
+
+int cbq_huff_linear_f32(const float *x, const cbq_huff_stream *hs, float *out, int T, int M,
+                        int K, hipStream_t stream)
+{
+    if (!x || !out || T <= 0 || T > 16 || M <= 0 || K <= 0 || K % kSub != 0) return CK_ERR_ARG;
+    HuffArgs a;
+    if (!fill_args(a, hs, (int64_t)M * K)) return CK_ERR_ARG;
+    const bool value_mode = a.value_cb == nullptr;
+    const int n_cb = value_mode ? 0 : a.C;
+    if (!value_mode && (a.C <= 0 || a.C > 16384)) return CK_ERR_ARG;
+    const int64_t L = (int64_t)K / gcd64(K, kChunk) * kChunk;      // lcm(K, 4096)
+    const int64_t RW = L / K, SPL = L / kChunk;
+    if (RW > (1 << 20) || SPL > (1 << 20)) return CK_ERR_ARG;
+    const LdsPlan p = plan_lds(a.n_lut2, n_cb, stage_words_of(hs));
+    if (p.bytes > 160 * 1024) return CK_ERR_ARG;
+    if (T == 1)
+        return value_mode ? launch_gemv<1, true>(x, out, a, T, M, K, (int)RW, (int)SPL, p, stream)
+                          : launch_gemv<1, false>(x, out, a, T, M, K, (int)RW, (int)SPL, p, stream);
+    if (T <= 4)
+        return value_mode ? launch_gemv<4, true>(x, out, a, T, M, K, (int)RW, (int)SPL, p, stream)
+                          : launch_gemv<4, false>(x, out, a, T, M, K, (int)RW, (int)SPL, p, stream);
+    return value_mode ? launch_gemv<16, true>(x, out, a, T, M, K, (int)RW, (int)SPL, p, stream)
+                      : launch_gemv<16, false>(x, out, a, T, M, K, (int)RW, (int)SPL, p, stream);
+}
+
+int cbq_huff_embedding_f32(const int32_t *token_ids, const cbq_huff_stream *hs, float *out,
+                           int T, int vocab, int H, hipStream_t stream)
+{
+    if (!token_ids || !out || T <= 0 || vocab <= 0 || H <= 0 || H % kSub != 0) return CK_ERR_ARG;
+    HuffArgs a;
+    if (!fill_args(a, hs, (int64_t)vocab * H)) return CK_ERR_ARG;
+    const bool value_mode = a.value_cb == nullptr;
+    const int n_cb = value_mode ? 0 : a.C;
+    if (!value_mode && (a.C <= 0 || a.C > 16384)) return CK_ERR_ARG;
+    const LdsPlan p = plan_lds(a.n_lut2, n_cb, stage_words_of(hs));
+    if (p.bytes > 160 * 1024) return CK_ERR_ARG;
+    const int blocks = std::max(1, std::min((T + kHWaves - 1) / kHWaves, cbq_num_cus()));
+    if (value_mode)
+        hipLaunchKernelGGL((huff_embedding_kernel<true>), dim3(blocks), dim3(kHBlock), p.bytes,
+                           stream, token_ids, out, a, T, vocab, H, p.stg_words, p.lut2_lds, 0);
+    else
+        hipLaunchKernelGGL((huff_embedding_kernel<false>), dim3(blocks), dim3(kHBlock), p.bytes,
+                           stream, token_ids, out, a, T, vocab, H, p.stg_words, p.lut2_lds, n_cb);
+    return cbq_launch_status("huff_embedding_kernel");
+}
+
+int cbq_huff_decode_indices(const cbq_huff_stream *hs, int32_t *out, int64_t n_symbols,
+                            hipStream_t stream)
+{
+    if (!out) return CK_ERR_ARG;
+    HuffArgs a;
+    if (!fill_args(a, hs, n_symbols)) return CK_ERR_ARG;
+    const LdsPlan p = plan_lds(a.n_lut2, 0, stage_words_of(hs));
+    if (p.bytes > 160 * 1024) return CK_ERR_ARG;
+    const int64_t want = (a.n_chunks + kHWaves - 1) / kHWaves;
+    const int blocks = (int)std::max<int64_t>(1, std::min<int64_t>(want, (int64_t)cbq_num_cus() * 2));
+    hipLaunchKernelGGL(huff_decode_kernel, dim3(blocks), dim3(kHBlock), p.bytes, stream, out, a,
+                       p.stg_words, p.lut2_lds);
+    return cbq_launch_status("huff_decode_kernel");
+}
+
+int huff_decode_to_i32(const void *stream, const void *row_bit_start, const void *lut_sym,
+                       const void *lut_len, const void *sl_first_code,
+                       const void *sl_base_offset, const void *sl_sym, void *out, int M, int K,
+                       int max_code_len, hipStream_t stream_h)
+{
+    if (!stream || !row_bit_start || !lut_sym || !lut_len || !sl_first_code ||
+        !sl_base_offset || !sl_sym || !out)
+        return HK_ERR_ARG;
+    if (M <= 0 || K <= 0 || max_code_len > 32) return HK_ERR_ARG;
+    const int blk = 64;
+    hipLaunchKernelGGL(ref_decode_rows_kernel, dim3((M + blk - 1) / blk), dim3(blk), 0, stream_h,
+                       (const uint8_t *)stream, (const int64_t *)row_bit_start,
+                       (const int32_t *)lut_sym, (const int32_t *)lut_len,
+                       (const int32_t *)sl_first_code, (const int32_t *)sl_base_offset,
+                       (const int32_t *)sl_sym, (int32_t *)out, M, K, max_code_len);
+    return cbq_launch_status("ref_decode_rows_kernel");
+}
+
+int huff_i32_linear_f32(const void *x, const void *i32_indices, const void *codebook, void *out,
+                        int T, int M, int K, int C, hipStream_t stream_h)
+{
+    if (!x || !i32_indices || !codebook || !out) return HK_ERR_ARG;
+    if (T <= 0 || M <= 0 || K <= 0 || C <= 0) return HK_ERR_ARG;
+    const int wpb = 4;
+    hipLaunchKernelGGL(i32_linear_kernel, dim3((M + wpb - 1) / wpb), dim3(wpb * CBQ_WAVE), 0,
+                       stream_h, (const float *)x, (const int32_t *)i32_indices,
+                       (const float *)codebook, (float *)out, T, M, K, C);
+    return cbq_launch_status("i32_linear_kernel");
+}
+
+int huff_i32_embedding_f32(const void *token_ids, const void *i32_indices, const void *codebook,
+                           void *out, int T, int H, int C, hipStream_t stream_h)
+{
+    if (!token_ids || !i32_indices || !codebook || !out) return HK_ERR_ARG;
+    if (T <= 0 || H <= 0 || C <= 0 || T > 65535) return HK_ERR_ARG;
+    const int blk = 128;
+    hipLaunchKernelGGL(i32_embedding_kernel, dim3((H + blk - 1) / blk, T), dim3(blk), 0,
+                       stream_h, (const int32_t *)token_ids, (const int32_t *)i32_indices,
+                       (const float *)codebook, (float *)out, T, H, C);
+    return cbq_launch_status("i32_embedding_kernel");
+}
+
+}  // extern "C"

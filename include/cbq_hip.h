@@ -1,0 +1,183 @@
+/*
+ * cbq_hip.h -- C ABI of the MI355X (gfx950) always-compressed matmul library
+ * (libcbq_hip.so, built from codebook-quantization_amd/csrc).
+ *
+ * Weights stay as codebook indices in HBM: fixed-width b-bit indices
+ * (LSB-first bitstream, index i at bits [i*b, (i+1)*b)) or canonical-Huffman
+ * codes.  Every entry point takes plain device pointers and sizes, runs
+ * asynchronously on `stream` (NULL = default stream), never synchronises and
+ * never allocates device memory.  Return codes follow the reference
+ * (rocm/compressed_kernel.h:37-41, rocm/huffman_kernel.h:26-28):
+ *   0 success, 1 HIP runtime error (message on stderr), 2 invalid argument.
+ * Kernel faults surface asynchronously, as with any HIP launch.
+ *
+ * Layouts: W is [M = out, K = in] row-major, x is [T, K], out is [T, M];
+ * accumulation is always float32.  Outputs are written, never accumulated,
+ * so callers need not zero them.
+ */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CK_SUCCESS  0
+#define CK_ERR_HIP  1
+#define CK_ERR_ARG  2
+#define HK_SUCCESS  CK_SUCCESS
+#define HK_ERR_HIP  CK_ERR_HIP
+#define HK_ERR_ARG  CK_ERR_ARG
+
+/* Human-readable text for a return code.
+ * Replaces ck_error_string (rocm/compressed_kernel.h:41). */
+const char *ck_error_string(int err);
+
+/* ==== fixed-width codebook GEMV / skinny GEMM ============================ */
+
+/* out[t, m] = sum_k x[t, k] * codebook[min(idx[m*K + k], C-1)], float32 x/out.
+ * packed: ceil(M*K*bits/8) bytes + >= 4 pad bytes; 1 <= bits <= 16.
+ * Replaces ck_linear_f32 (rocm/compressed_kernel.h:52-59); same arguments.
+ * Any T >= 1 (T > 16 runs as successive 16-token tiles). */
+int ck_linear_f32(const float *x, const uint8_t *packed, const float *codebook,
+                  float *out, int T, int M, int K, int C, int bits,
+                  hipStream_t stream);
+
+/* Same with bfloat16 x and out (raw uint16 bf16 bit patterns; out rounded to
+ * nearest even).  Replaces ck_linear_bf16 (rocm/compressed_kernel.h:66-73). */
+int ck_linear_bf16(const void *x_bf16, const uint8_t *packed, const float *codebook,
+                   void *out_bf16, int T, int M, int K, int C, int bits,
+                   hipStream_t stream);
+
+/* ==== compressed embedding gather ======================================== */
+
+/* out[t, h] = codebook[min(idx[ids[t]*H + h], C-1)], float32 out.  ids are
+ * trusted, as in the reference.
+ * Replaces ck_embedding_f32 (rocm/compressed_kernel.h:83-90). */
+int ck_embedding_f32(const int32_t *token_ids, const uint8_t *packed,
+                     const float *codebook, float *out, int T, int H, int C,
+                     int bits, hipStream_t stream);
+
+/* As ck_embedding_f32 with the table's row count: ids outside [0, vocab)
+ * are clamped into range instead of read out of bounds.
+ * Backs GPUAcceleratedEmbedding.__call__
+ * (src/gpu_accelerated_functions.py:1005-1029). */
+int cbq_embedding_f32(const int32_t *token_ids, const uint8_t *packed,
+                      const float *codebook, float *out, int T, int vocab, int H,
+                      int C, int bits, hipStream_t stream);
+
+/* ==== canonical Huffman: reference-format entry points ==================== */
+
+/* Decode a row-indexed MSB-first Huffman stream into int32 indices [M*K] with
+ * the reference's tables (12-bit int32 LUT, -1 = no short code; int32
+ * slow-path tables; corrupt prefix -> symbol 0, +1 bit).
+ * Replaces huff_decode_to_i32 (rocm/huffman_kernel.h:57-67). */
+int huff_decode_to_i32(const void *stream, const void *row_bit_start,
+                       const void *lut_sym, const void *lut_len,
+                       const void *sl_first_code, const void *sl_base_offset,
+                       const void *sl_sym, void *out, int M, int K,
+                       int max_code_len, hipStream_t stream_h);
+
+/* GEMV over int32 indices (clamped to [0, C-1]).
+ * Replaces huff_i32_linear_f32 (rocm/huffman_kernel.h:81-87). */
+int huff_i32_linear_f32(const void *x, const void *i32_indices, const void *codebook,
+                        void *out, int T, int M, int K, int C, hipStream_t stream_h);
+
+/* Gather over int32 indices.
+ * Replaces huff_i32_embedding_f32 (rocm/huffman_kernel.h:101-107). */
+int huff_i32_embedding_f32(const void *token_ids, const void *i32_indices,
+                           const void *codebook, void *out, int T, int H, int C,
+                           hipStream_t stream_h);
+
+/* ==== canonical Huffman: fused chunk-parallel path ========================= *
+ *
+ * Device stream format ("chunked Huffman"):
+ *   words     uint32, the reference's MSB-first byte stream with the bits of
+ *             every byte reversed, read as little-endian words, so stream bit
+ *             j is bit j%32 of word j/32; >= 2 zero words of padding.
+ *   chunk_off uint64[n_chunks + 1]: bit offset of flat symbol c*4096.
+ *   sub_len   uint16[ceil(N/64)]: bits taken by symbols [64s, 64s+64).
+ *   lut1      uint32[4096] and lut2 uint32[n_lut2]: decode tables built by
+ *             cbq_huff_build_luts from the code lengths and the codebook.
+ *   canon     int32[3*33] + canon_sym: per-length first code / count / base
+ *             and symbols in canonical order, for codes beyond 24 bits.
+ * Decoding is bit-exact with the reference decoder (compressed_matmul.c:
+ * 146-186) for every bit pattern, including corrupt ones.
+ */
+
+/* Device-resident chunked-Huffman stream: plain device pointers + sizes. */
+typedef struct cbq_huff_stream {
+    const uint32_t *words;      /* LSB-first stream words (+ >= 2 zero words)   */
+    int64_t n_words;            /* length of `words`                             */
+    const uint64_t *chunk_off;  /* [ceil(N/4096) + 1] bit offsets                */
+    const uint16_t *sub_len;    /* [ceil(N/64)] sub-block bit lengths            */
+    const uint32_t *lut1;       /* [4096]                                        */
+    const uint32_t *lut2;       /* [n_lut2]                                      */
+    int32_t n_lut2;
+    const int32_t *canon;       /* [100]: first[33] count[33] base[33] invalid   */
+    const int32_t *canon_pay;   /* payloads in canonical symbol order            */
+    const float *value_cb;      /* NULL: payloads are bf16 values; else float32
+                                   codebook[C] indexed by the (clamped) symbol   */
+    int32_t C;
+    int32_t stage_words;        /* LDS words staged per wave (0 = default 1536);
+                                   larger chunks decode from global memory       */
+} cbq_huff_stream;
+
+/* Table builder (host only, no GPU needed).  payload_is_value != 0 stores
+ * the bf16 bits of codebook[min(sym, C-1)] (valid only when every codebook
+ * value is exactly a bf16); 0 stores the symbol (clamped to C-1 when
+ * clamp_to != 0, else raw).  With lut1 or lut2 NULL only *n_lut2 (and canon
+ * / canon_pay when non-NULL) are written.  canon_pay needs one slot per used
+ * symbol.  Returns CK_ERR_ARG on invalid lengths (Kraft sum > 1, > 32 bits).
+ * Tables follow the reference's build_gpu_lut / _build_slow_path_tables
+ * (src/huffman_codebook.py:353-423) in meaning, not layout. */
+int cbq_huff_build_luts(const uint8_t *lengths, int n_alpha, const float *codebook,
+                        int C, int payload_is_value, int clamp_to,
+                        uint32_t *lut1, uint32_t *lut2, int *n_lut2,
+                        int32_t *canon, int32_t *canon_pay);
+
+/* Host indexer: decode the reference-format MSB-first stream once (up to
+ * `threads` threads, split at row starts) and write chunk_off[ceil(N/4096)+1]
+ * and sub_len[ceil(N/64)] for N = M*K.  row_bit_starts[M] may be NULL (one
+ * thread).  Returns CK_ERR_ARG when the row starts disagree with the stream.
+ * Derived from huff_row_bit_starts (src/huffman_codebook.py:210-215). */
+int cbq_huff_index_stream(const uint8_t *stream_msb, int64_t stream_bytes,
+                          const uint8_t *lengths, int n_alpha,
+                          const int64_t *row_bit_starts, int M, int K,
+                          uint64_t *chunk_off, uint16_t *sub_len, int threads);
+
+/* Fused Huffman GEMV: out[t, m] = sum_k x[t, k] * codebook[decode(m*K + k)],
+ * decoded chunk-parallel straight into the dot product; no index or weight
+ * buffer.  Requires K % 64 == 0 and 1 <= T <= 16.
+ * Replaces the decode + GEMV pair of HuffmanCodebookLinear.__call__
+ * (src/gpu_huffman_functions.py:834-855) and huffman_matmul_f32_chunk
+ * (src/compressed_matmul.c:208-239). */
+int cbq_huff_linear_f32(const float *x, const cbq_huff_stream *hs, float *out,
+                        int T, int M, int K, hipStream_t stream);
+
+/* Fused Huffman embedding: out[t, h] = codebook[decode(ids[t]*H + h)]; only
+ * the requested rows are decoded (ids clamped to [0, vocab)).  H % 64 == 0.
+ * Replaces HuffmanCodebookEmbedding.__call__
+ * (src/gpu_huffman_functions.py:961-979) and huffman_embedding_f32_rows
+ * (src/compressed_matmul.c:253-281). */
+int cbq_huff_embedding_f32(const int32_t *token_ids, const cbq_huff_stream *hs,
+                           float *out, int T, int vocab, int H, hipStream_t stream);
+
+/* Decode flat symbols [0, n_symbols) to int32 with the chunked kernel (lut
+ * payloads must be raw symbols).  The bit-exact check of the fused decoder;
+ * the equivalent of huffman_decode_to_weights_f32 with an identity codebook
+ * (src/compressed_matmul.c:296-322). */
+int cbq_huff_decode_indices(const cbq_huff_stream *hs, int32_t *out,
+                            int64_t n_symbols, hipStream_t stream);
+
+/* ==== library introspection ============================================== */
+
+/* Version string of the library build. */
+const char *cbq_version(void);
+
+#ifdef __cplusplus
+}
+#endif
