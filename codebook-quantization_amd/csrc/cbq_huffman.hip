@@ -421,8 +421,14 @@ __global__ __launch_bounds__(kHBlock) void huff_embedding_kernel(
             const bool active = (r0 + lane) < KS && s < a.n_sub;
             const int src = (int)(s & (kSub - 1));
             const bool inA = (s / kSub) == cA;
-            const uint64_t my_start = inA ? __shfl(startA, src, CBQ_WAVE) : __shfl(startB, src, CBQ_WAVE);
-            const uint32_t my_len = inA ? __shfl(lenA, src, CBQ_WAVE) : __shfl(lenB, src, CBQ_WAVE);
+            // every lane takes part in every shuffle (a shuffle reading a lane
+            // that skipped it returns nothing useful); select afterwards
+            const uint64_t stA = __shfl(startA, src, CBQ_WAVE);
+            const uint64_t stB = __shfl(startB, src, CBQ_WAVE);
+            const uint32_t lnA = __shfl(lenA, src, CBQ_WAVE);
+            const uint32_t lnB = __shfl(lenB, src, CBQ_WAVE);
+            const uint64_t my_start = inA ? stA : stB;
+            const uint32_t my_len = inA ? lnA : lnB;
             const int n_act = std::min(CBQ_WAVE, KS - r0);
             const uint64_t lo = __shfl(my_start, 0, CBQ_WAVE);
             const uint64_t hi = __shfl(my_start + my_len, n_act - 1, CBQ_WAVE);

@@ -1,0 +1,122 @@
+"""Fixed-width compressed linear / embedding on gfx950 (drop-in backends).
+
+Same classes, constructor and call signatures as the reference
+(src/gpu_accelerated_functions.py:871-1029):
+
+    GPUAcceleratedLinear(name, indices_np, codebook, shape, bits)(x)
+    GPUAcceleratedEmbedding(name, indices_np, codebook, shape, bits)(ids)
+
+The packed indices (+ zero padding) and the float32 codebook are copied to
+the device once, at construction.  Each call launches one kernel of
+libcbq_hip.so on torch's current stream, with no synchronisation:
+  * linear: out = x @ W^T with W[m, k] = codebook[min(idx, C-1)], fp32
+    accumulate, output in x's dtype (bf16 x runs the bf16-I/O kernel
+    directly; other dtypes go through fp32);
+  * embedding: out[..., h] = codebook[idx[id * H + h]] as float32 (the module
+    casts to the codebook dtype, src/compressed_modules.py:322-330).
+There is no CPU fallback: construction fails without a GPU and the built
+library.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import bitpack
+import cbq_native as nat
+
+
+def _device_for(codebook: torch.Tensor) -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError("the compressed GPU path needs a ROCm GPU (none visible)")
+    return codebook.device if codebook.is_cuda else torch.device("cuda")
+
+
+def _upload_packed(indices_np, device) -> torch.Tensor:
+    arr = (np.ascontiguousarray(indices_np, dtype=np.uint8) if isinstance(indices_np, np.ndarray)
+           else indices_np.detach().cpu().numpy().astype(np.uint8))
+    return torch.from_numpy(bitpack.device_padded(arr.reshape(-1))).to(device)
+
+
+class GPUAcceleratedLinear:
+    """Packed indices + codebook in HBM; fused unpack / gather / dot on call."""
+
+    def __init__(self, name: str, indices_np, codebook: torch.Tensor, shape: tuple, bits: int):
+        self.name = name
+        self.shape = tuple(int(s) for s in shape)          # (out_features, in_features)
+        self.M, self.K = self.shape
+        self.bits = int(bits)
+        if not 1 <= self.bits <= 16:
+            raise ValueError(f"{name}: bits must be in [1, 16], got {bits}")
+        self._lib = nat.load()
+        device = _device_for(codebook)
+        self.codebook = codebook.detach().to(device=device, dtype=torch.float32).contiguous()
+        self.C = int(self.codebook.numel())
+        need = bitpack.calculate_packed_size(self.M * self.K, self.bits)
+        src_len = (indices_np.size if isinstance(indices_np, np.ndarray)
+                   else int(indices_np.numel()))
+        if src_len < need:
+            raise ValueError(f"{name}: {src_len} packed bytes < {need} needed for "
+                             f"{self.M}x{self.K} at {self.bits} bits")
+        self.packed = _upload_packed(indices_np, device)
+
+    @property
+    def compressed_bytes(self) -> int:
+        return bitpack.calculate_packed_size(self.M * self.K, self.bits)
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        in_dtype = x.dtype
+        dev = self.codebook.device
+        x = x.to(dev)
+        lead = x.shape[:-1]
+        if x.shape[-1] != self.K:
+            raise ValueError(f"{self.name}: expected last dim {self.K}, got {x.shape[-1]}")
+        T = int(x.numel() // self.K)
+        if T == 0:
+            return torch.empty(*lead, self.M, dtype=in_dtype, device=dev)
+        if in_dtype == torch.bfloat16:
+            xc = x.reshape(T, self.K).contiguous()
+            out = torch.empty(T, self.M, dtype=torch.bfloat16, device=dev)
+            rc = self._lib.ck_linear_bf16(xc.data_ptr(), self.packed.data_ptr(),
+                                          self.codebook.data_ptr(), out.data_ptr(), T, self.M,
+                                          self.K, self.C, self.bits, nat.stream_ptr(dev))
+            nat.check(rc, "ck_linear_bf16")
+            return out.reshape(*lead, self.M)
+        xc = x.reshape(T, self.K).to(torch.float32).contiguous()
+        out = torch.empty(T, self.M, dtype=torch.float32, device=dev)
+        rc = self._lib.ck_linear_f32(xc.data_ptr(), self.packed.data_ptr(),
+                                     self.codebook.data_ptr(), out.data_ptr(), T, self.M, self.K,
+                                     self.C, self.bits, nat.stream_ptr(dev))
+        nat.check(rc, "ck_linear_f32")
+        out = out.reshape(*lead, self.M)
+        return out if in_dtype == torch.float32 else out.to(in_dtype)
+
+
+class GPUAcceleratedEmbedding:
+    """Rows gathered straight from the packed table; float32 output."""
+
+    def __init__(self, name: str, indices_np, codebook: torch.Tensor, shape: tuple, bits: int):
+        self.name = name
+        self.shape = tuple(int(s) for s in shape)          # (vocab, hidden)
+        self.vocab, self.hidden = self.shape
+        self.bits = int(bits)
+        if not 1 <= self.bits <= 16:
+            raise ValueError(f"{name}: bits must be in [1, 16], got {bits}")
+        self._lib = nat.load()
+        device = _device_for(codebook)
+        self.codebook = codebook.detach().to(device=device, dtype=torch.float32).contiguous()
+        self.C = int(self.codebook.numel())
+        self.packed = _upload_packed(indices_np, device)
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        dev = self.codebook.device
+        ids = x.to(dev).reshape(-1).to(torch.int32).contiguous()
+        T = int(ids.numel())
+        out = torch.empty(T, self.hidden, dtype=torch.float32, device=dev)
+        if T:
+            rc = self._lib.cbq_embedding_f32(ids.data_ptr(), self.packed.data_ptr(),
+                                             self.codebook.data_ptr(), out.data_ptr(), T,
+                                             self.vocab, self.hidden, self.C, self.bits,
+                                             nat.stream_ptr(dev))
+            nat.check(rc, "cbq_embedding_f32")
+        return out.reshape(*x.shape, self.hidden)

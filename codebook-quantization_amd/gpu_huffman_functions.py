@@ -1,0 +1,209 @@
+"""Canonical-Huffman compressed linear / embedding on gfx950 (drop-in backends).
+
+Same classes and constructor signatures as the reference
+(src/gpu_huffman_functions.py:715-1002):
+
+    HuffmanCodebookLinear(name, huff_stream, huff_lengths, huff_n, codebook,
+                          shape, bits, huff_row_bit_starts=..., huff_lut_sym=...,
+                          huff_lut_len=..., huff_sl_first_code=...,
+                          huff_sl_base_offset=..., huff_sl_sym=...)
+
+plus two optional keys written by this package's encoder,
+`huff_chunk_offsets` and `huff_sub_lens`.  Where the reference decodes every
+row into a transient int32 [M*K] buffer and then runs a GEMV (and decodes the
+whole vocabulary for each embedding call), this backend keeps only the
+stream in HBM and decodes it chunk-parallel straight into the dot product or
+into the requested embedding rows.
+
+At construction the reference stream is turned into the device format: bytes
+bit-reversed into LSB-first words, decode tables rebuilt from `huff_lengths`
+(the reference's huff_lut_* / huff_sl_* arrays are derived from the same
+lengths and are not needed), and - when the chunk index is absent - one host
+pass over the stream (split at `huff_row_bit_starts`) computes it.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Tuple
+
+import numpy as np
+import torch
+
+import cbq_native as nat
+import huffman_codebook as hc
+
+_BF16_PAYLOAD_MAX_C = 1 << 16
+_SYMBOL_PAYLOAD_MAX_C = 16384     # fp32 codebook staged in LDS
+
+
+def _is_bf16_exact(cb: np.ndarray) -> bool:
+    return bool(np.all((cb.view(np.uint32) & 0xFFFF) == 0))
+
+
+class _DeviceStream:
+    """Device-resident chunked stream + decode tables for one tensor."""
+
+    def __init__(self, name, huff_stream, huff_lengths, huff_n, codebook_f32: np.ndarray,
+                 shape: Tuple[int, int], row_bit_starts=None, chunk_offsets=None,
+                 sub_lens=None, device=None, raw_symbols=False):
+        self.name = name
+        M, K = shape
+        n = int(huff_n)
+        if n != M * K:
+            raise ValueError(f"{name}: huff_n={n} != {M}x{K}")
+        lengths = np.ascontiguousarray(huff_lengths, np.uint8)
+        stream = np.ascontiguousarray(huff_stream, np.uint8)
+        if chunk_offsets is None or sub_lens is None:
+            chunk_offsets, sub_lens = hc.index_stream(stream, lengths, M, K, row_bit_starts)
+        chunk_offsets = np.ascontiguousarray(chunk_offsets, np.uint64)
+        sub_lens = np.ascontiguousarray(sub_lens, np.uint16)
+        if chunk_offsets.size != (n + hc.CHUNK_SYMBOLS - 1) // hc.CHUNK_SYMBOLS + 1 or \
+                sub_lens.size != (n + hc.SUB_SYMBOLS - 1) // hc.SUB_SYMBOLS:
+            raise ValueError(f"{name}: chunk index does not match {n} symbols")
+        if int(chunk_offsets[-1]) > 8 * stream.size:
+            raise ValueError(f"{name}: chunk index points past the stream")
+        self.C = int(codebook_f32.size)
+        self.value_payload = (not raw_symbols) and _is_bf16_exact(codebook_f32) and self.C > 0
+        if not self.value_payload and not raw_symbols and self.C > _SYMBOL_PAYLOAD_MAX_C:
+            raise ValueError(f"{name}: non-bf16 codebook with {self.C} > "
+                             f"{_SYMBOL_PAYLOAD_MAX_C} entries is not supported")
+        lut1, lut2, canon, pay = hc.device_luts(lengths, codebook_f32 if self.C else None,
+                                                self.C, self.value_payload,
+                                                clamp=not raw_symbols)
+        words = hc.device_words_from_stream(stream)
+        dev = device or torch.device("cuda")
+        self.words = torch.from_numpy(words.view(np.int32)).to(dev)
+        self.chunk_off = torch.from_numpy(chunk_offsets.view(np.int64)).to(dev)
+        self.sub_len = torch.from_numpy(sub_lens.view(np.int16)).to(dev)
+        self.lut1 = torch.from_numpy(lut1.view(np.int32)).to(dev)
+        self.lut2 = torch.from_numpy(lut2.view(np.int32)).to(dev)
+        self.canon = torch.from_numpy(canon).to(dev)
+        self.canon_pay = torch.from_numpy(pay).to(dev)
+        self.value_cb = (None if (self.value_payload or raw_symbols)
+                         else torch.from_numpy(np.ascontiguousarray(codebook_f32)).to(dev))
+        self.stream_bytes = int(stream.size)
+        self.table_bytes = int(chunk_offsets.nbytes + sub_lens.nbytes)
+        self.desc = nat.HuffStream(
+            words=self.words.data_ptr(), n_words=int(self.words.numel()),
+            chunk_off=self.chunk_off.data_ptr(), sub_len=self.sub_len.data_ptr(),
+            lut1=self.lut1.data_ptr(), lut2=self.lut2.data_ptr(), n_lut2=int(lut2.size),
+            canon=self.canon.data_ptr(), canon_pay=self.canon_pay.data_ptr(),
+            value_cb=None if self.value_cb is None else self.value_cb.data_ptr(),
+            C=self.C, stage_words=hc.stage_words_for(chunk_offsets))
+
+
+def _cb_numpy(codebook) -> np.ndarray:
+    if isinstance(codebook, torch.Tensor):
+        return codebook.detach().to(torch.float32).cpu().numpy().reshape(-1)
+    return np.ascontiguousarray(codebook, np.float32).reshape(-1)
+
+
+class HuffmanCodebookLinear:
+    """y = x @ W^T with W Huffman-coded in HBM; decode fused into the GEMV."""
+
+    def __init__(self, name: str, huff_stream, huff_lengths, huff_n: int,
+                 codebook, shape, bits: int,
+                 huff_row_bit_starts: Optional[np.ndarray] = None,
+                 huff_lut_sym: Optional[np.ndarray] = None,
+                 huff_lut_len: Optional[np.ndarray] = None,
+                 huff_sl_first_code: Optional[np.ndarray] = None,
+                 huff_sl_base_offset: Optional[np.ndarray] = None,
+                 huff_sl_sym: Optional[np.ndarray] = None,
+                 huff_chunk_offsets: Optional[np.ndarray] = None,
+                 huff_sub_lens: Optional[np.ndarray] = None):
+        if not torch.cuda.is_available():
+            raise RuntimeError("the compressed GPU path needs a ROCm GPU (none visible)")
+        self.name = name
+        self.shape = tuple(int(s) for s in shape)
+        self.M, self.K = self.shape
+        self.bits = int(bits)
+        if self.K % hc.SUB_SYMBOLS:
+            raise ValueError(f"{name}: in_features {self.K} must be a multiple of "
+                             f"{hc.SUB_SYMBOLS}")
+        self._lib = nat.load()
+        device = codebook.device if isinstance(codebook, torch.Tensor) and codebook.is_cuda \
+            else torch.device("cuda")
+        self._cb_np = _cb_numpy(codebook)
+        self._src = (huff_stream, huff_lengths, int(huff_n), huff_row_bit_starts)
+        self.dev = _DeviceStream(name, huff_stream, huff_lengths, huff_n, self._cb_np,
+                                 self.shape, huff_row_bit_starts, huff_chunk_offsets,
+                                 huff_sub_lens, device)
+        self.device = device
+        self._idx_dev = None
+
+    @property
+    def compressed_bytes(self) -> int:
+        return self.dev.stream_bytes + self.dev.table_bytes
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        in_dtype = x.dtype
+        x = x.to(self.device)
+        lead = x.shape[:-1]
+        if x.shape[-1] != self.K:
+            raise ValueError(f"{self.name}: expected last dim {self.K}, got {x.shape[-1]}")
+        T = int(x.numel() // self.K)
+        xc = x.reshape(T, self.K).to(torch.float32).contiguous()
+        out = torch.empty(T, self.M, dtype=torch.float32, device=self.device)
+        st = nat.stream_ptr(self.device)
+        for t0 in range(0, T, 16):
+            tt = min(16, T - t0)
+            rc = self._lib.cbq_huff_linear_f32(
+                xc.data_ptr() + t0 * self.K * 4, ctypes.byref(self.dev.desc),
+                out.data_ptr() + t0 * self.M * 4, tt, self.M, self.K, st)
+            nat.check(rc, "cbq_huff_linear_f32")
+        out = out.reshape(*lead, self.M)
+        return out if in_dtype == torch.float32 else out.to(in_dtype)
+
+    def decode_indices(self) -> torch.Tensor:
+        """All M*K decoded symbols (int32, unclamped) with the chunked kernel."""
+        if self._idx_dev is None:
+            s, l, n, rbs = self._src
+            self._idx_dev = _DeviceStream(self.name, s, l, n, self._cb_np, self.shape, rbs,
+                                          None, None, self.device, raw_symbols=True)
+        out = torch.empty(self.M * self.K, dtype=torch.int32, device=self.device)
+        rc = self._lib.cbq_huff_decode_indices(ctypes.byref(self._idx_dev.desc), out.data_ptr(),
+                                               self.M * self.K, nat.stream_ptr(self.device))
+        nat.check(rc, "cbq_huff_decode_indices")
+        return out.reshape(self.M, self.K)
+
+
+class HuffmanCodebookEmbedding:
+    """Embedding rows decoded on demand from the Huffman stream (float32)."""
+
+    def __init__(self, name: str, huff_stream, huff_lengths, huff_n: int,
+                 codebook, shape, bits: int,
+                 huff_row_bit_starts: Optional[np.ndarray] = None,
+                 huff_lut_sym: Optional[np.ndarray] = None,
+                 huff_lut_len: Optional[np.ndarray] = None,
+                 huff_sl_first_code: Optional[np.ndarray] = None,
+                 huff_sl_base_offset: Optional[np.ndarray] = None,
+                 huff_sl_sym: Optional[np.ndarray] = None,
+                 huff_chunk_offsets: Optional[np.ndarray] = None,
+                 huff_sub_lens: Optional[np.ndarray] = None):
+        if not torch.cuda.is_available():
+            raise RuntimeError("the compressed GPU path needs a ROCm GPU (none visible)")
+        self.name = name
+        self.shape = tuple(int(s) for s in shape)
+        self.vocab, self.hidden = self.shape
+        self.bits = int(bits)
+        if self.hidden % hc.SUB_SYMBOLS:
+            raise ValueError(f"{name}: hidden {self.hidden} must be a multiple of "
+                             f"{hc.SUB_SYMBOLS}")
+        self._lib = nat.load()
+        device = codebook.device if isinstance(codebook, torch.Tensor) and codebook.is_cuda \
+            else torch.device("cuda")
+        self.dev = _DeviceStream(name, huff_stream, huff_lengths, huff_n, _cb_numpy(codebook),
+                                 self.shape, huff_row_bit_starts, huff_chunk_offsets,
+                                 huff_sub_lens, device)
+        self.device = device
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        ids = x.to(self.device).reshape(-1).to(torch.int32).contiguous()
+        T = int(ids.numel())
+        out = torch.empty(T, self.hidden, dtype=torch.float32, device=self.device)
+        if T:
+            rc = self._lib.cbq_huff_embedding_f32(ids.data_ptr(), ctypes.byref(self.dev.desc),
+                                                  out.data_ptr(), T, self.vocab, self.hidden,
+                                                  nat.stream_ptr(self.device))
+            nat.check(rc, "cbq_huff_embedding_f32")
+        return out.reshape(*x.shape, self.hidden)

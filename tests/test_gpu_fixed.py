@@ -1,0 +1,171 @@
+"""Fixed-width GEMV / embedding on the GPU through the C ABI vs the oracle.
+
+Bar: rel-L2 <= 1e-5 for fp32 outputs (fp32 accumulation, different order
+from the oracle's sequential k loop); embedding gathers are bit-exact; bf16
+I/O within bf16 output rounding (rel-L2 <= 4e-3, >= 99% of outputs equal to
+the oracle's fp32 result rounded to bf16).
+"""
+import numpy as np
+import pytest
+import torch
+
+import codebook_builder as cbb
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def _nat():
+    import cbq_native
+    return cbq_native, cbq_native.load()
+
+
+def _dev_packed(pk, dev):
+    import bitpack
+    return torch.from_numpy(bitpack.device_padded(pk)).to(dev)
+
+
+def _run_linear(dev, x, pk, cb, M, K, C, bits):
+    nat, lib = _nat()
+    # the C ABI trusts its sizes: never hand it a stream shorter than M*K*bits
+    assert np.asarray(pk).size >= (M * K * bits + 7) // 8, "packed stream too short"
+    xd = torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev)
+    pd = _dev_packed(pk, dev)
+    cd = torch.from_numpy(np.ascontiguousarray(cb, np.float32)).to(dev)
+    out = torch.full((x.shape[0], M), float("nan"), device=dev)
+    rc = lib.ck_linear_f32(xd.data_ptr(), pd.data_ptr(), cd.data_ptr(), out.data_ptr(),
+                           x.shape[0], M, K, C, bits, nat.stream_ptr(dev))
+    nat.check(rc, "ck_linear_f32")
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def test_golden_cases(cuda, golden):
+    for name, c in golden["fixed"].items():
+        M, K, bits, C = int(c["M"]), int(c["K"]), int(c["bits"]), int(c["C"])
+        y = _run_linear(cuda, c["x"], c["packed"], c["cb"], M, K, C, bits)
+        ref = c["y_T16"] if name == "bf16slice" else c["y"]
+        print(name, M, K, bits, rel_l2(y, ref), flush=True)
+        assert rel_l2(y, ref) <= TOL, name
+
+
+@pytest.mark.parametrize("T", [1, 2, 4, 7, 16, 20])
+def test_config1_shape(cuda, oracle, T):
+    """Config 1: W[M=6144, K=2048] bf16 N(0, 0.02), 13-bit frequency-sorted."""
+    M, K = 6144, 2048
+    w = cbb.bf16_round(np.random.default_rng(0).standard_normal((M, K)) * 0.02)
+    d = cbb.compress_fixed(w)
+    assert d["bits"] == 13
+    x = np.random.default_rng(1).standard_normal((T, K)).astype(np.float32)
+    y = _run_linear(cuda, x, d["indices"], d["codebook"], M, K, len(d["codebook"]), 13)
+    ref = oracle.fixed_gemv(x, d["indices"], d["codebook"], M, K, 13, chunk_rows=None)
+    assert rel_l2(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("M,K,bits,C", [(100, 96, 7, 100), (77, 33, 13, 5000),
+                                        (64, 128, 16, 40000), (33, 64, 10, 1024),
+                                        (130, 4096, 14, 9686), (50, 12288, 13, 5091),
+                                        (64, 1024, 12, 4000), (40, 160, 8, 200)])
+def test_widths_shapes_and_generic_path(cuda, oracle, M, K, bits, C):
+    rng = np.random.default_rng(M + K + bits)
+    raw = rng.integers(0, 1 << bits, size=M * K)       # includes indices >= C: clamp
+    cb = (rng.standard_normal(C) * 0.02).astype(np.float32)
+    pk = oracle.pack_lsb(raw, bits)
+    for T in (1, 3):
+        x = rng.standard_normal((T, K)).astype(np.float32)
+        y = _run_linear(cuda, x, pk, cb, M, K, C, bits)
+        ref = oracle.fixed_gemv(x, pk, cb, M, K, bits, C=C, chunk_rows=None)
+        assert rel_l2(y, ref) <= TOL, (M, K, bits, C, T)
+
+
+def test_bf16_io(cuda, oracle):
+    nat, lib = _nat()
+    M, K = 512, 2048
+    w = cbb.bf16_round(np.random.default_rng(2).standard_normal((M, K)) * 0.02)
+    d = cbb.compress_fixed(w)
+    bits = d["bits"]                      # 3581 unique values -> 12-bit indices
+    assert d["indices"].size >= (M * K * bits + 7) // 8
+    for T in (1, 5):
+        xb = torch.randn(T, K).bfloat16()
+        x32 = xb.float().numpy()
+        ref = oracle.fixed_gemv(x32, d["indices"], d["codebook"], M, K, bits, chunk_rows=None)
+        xd = xb.to(cuda)
+        pd = _dev_packed(d["indices"], cuda)
+        cd = torch.from_numpy(d["codebook"]).to(cuda)
+        out = torch.empty(T, M, dtype=torch.bfloat16, device=cuda)
+        rc = lib.ck_linear_bf16(xd.data_ptr(), pd.data_ptr(), cd.data_ptr(), out.data_ptr(), T, M,
+                                K, len(d["codebook"]), bits, nat.stream_ptr(cuda))
+        nat.check(rc, "ck_linear_bf16")
+        y = out.float().cpu().numpy()
+        assert rel_l2(y, ref) <= 4e-3
+        ref_b = torch.from_numpy(ref).bfloat16().float().numpy()
+        assert (y == ref_b).mean() >= 0.99
+
+
+def test_int64_offsets_large(cuda, oracle):
+    """M*K*bits > 2^31 bits (tests/test_c_kernel.py:109-138 of the reference)."""
+    M, K, bits = 41472, 4096, 13            # 170M indices, 2.2G bits
+    rng = np.random.default_rng(7)
+    raw = rng.integers(0, 1 << bits, size=M * K, dtype=np.uint16)
+    cb = (rng.standard_normal(1 << bits) * 0.02).astype(np.float32)
+    pk = cbb.pack_torch(torch.from_numpy(raw).to(cuda), bits).cpu().numpy()
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    y = _run_linear(cuda, x, pk, cb, M, K, 1 << bits, bits)
+    rows = np.array([0, 1, M // 2, M - 2, M - 1])
+    ref = (x.astype(np.float64) @ cb[raw.reshape(M, K)[rows]].astype(np.float64).T)
+    assert rel_l2(y[:, rows], ref) <= TOL
+
+
+def test_determinism_and_back_to_back(cuda):
+    from gpu_accelerated_functions import GPUAcceleratedLinear
+    M, K = 2048, 4096
+    w = cbb.bf16_round(np.random.default_rng(4).standard_normal((M, K)) * 0.02)
+    d = cbb.compress_fixed(w)
+    lin = GPUAcceleratedLinear("det", d["indices"], torch.from_numpy(d["codebook"]), (M, K),
+                               d["bits"])
+    x = torch.randn(3, K, device=cuda)
+    outs = [lin(x) for _ in range(5)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+
+
+@pytest.mark.parametrize("H,bits,C", [(4096, 13, 5000), (2048, 14, 9000), (96, 7, 100),
+                                      (100, 12, 3000)])
+def test_embedding_exact(cuda, oracle, H, bits, C):
+    nat, lib = _nat()
+    vocab = 300
+    rng = np.random.default_rng(H + bits)
+    raw = rng.integers(0, 1 << bits, size=vocab * H)
+    cb = (rng.standard_normal(C) * 0.02).astype(np.float32)
+    pk = oracle.pack_lsb(raw, bits)
+    ids = np.array([0, vocab - 1, 17, 17, 250, 3], np.int32)
+    ref = oracle.fixed_embedding(ids, pk, cb, H, bits, C=C)
+    pd = _dev_packed(pk, cuda)
+    cd = torch.from_numpy(cb).to(cuda)
+    idd = torch.from_numpy(ids).to(cuda)
+    for fn in ("ck_embedding_f32", "cbq_embedding_f32"):
+        out = torch.full((len(ids), H), float("nan"), device=cuda)
+        if fn == "ck_embedding_f32":
+            rc = lib.ck_embedding_f32(idd.data_ptr(), pd.data_ptr(), cd.data_ptr(), out.data_ptr(),
+                                      len(ids), H, C, bits, nat.stream_ptr(cuda))
+        else:
+            rc = lib.cbq_embedding_f32(idd.data_ptr(), pd.data_ptr(), cd.data_ptr(),
+                                       out.data_ptr(), len(ids), vocab, H, C, bits,
+                                       nat.stream_ptr(cuda))
+        nat.check(rc, fn)
+        assert np.array_equal(out.cpu().numpy(), ref), fn
+
+
+def test_embedding_clamps_ids(cuda, oracle):
+    from gpu_accelerated_functions import GPUAcceleratedEmbedding
+    vocab, H, bits = 10, 64, 8
+    raw = np.random.default_rng(0).integers(0, 256, size=vocab * H)
+    cb = np.arange(256, dtype=np.float32)
+    emb = GPUAcceleratedEmbedding("e", oracle.pack_lsb(raw, bits), torch.from_numpy(cb),
+                                  (vocab, H), bits)
+    out = emb(torch.tensor([[-5, 3, 99]], device=cuda)).cpu().numpy()
+    assert out.shape == (1, 3, H)
+    assert np.array_equal(out[0, 0], cb[raw[:H]])
+    assert np.array_equal(out[0, 2], cb[raw[(vocab - 1) * H:]])

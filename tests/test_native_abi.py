@@ -1,0 +1,79 @@
+"""libcbq_hip.so loads and exports every function include/cbq_hip.h declares;
+host-only entry points work and argument validation rejects bad calls before
+any GPU work (no kernel is launched here)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                      "include", "cbq_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import cbq_native
+    try:
+        return cbq_native.load()
+    except RuntimeError as e:
+        pytest.fail(str(e))
+
+
+def test_header_symbols_exported(lib):
+    names = _declared()
+    assert "ck_linear_f32" in names and "cbq_huff_linear_f32" in names
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in cbq_hip.h but not exported"
+    import cbq_native
+    assert set(names) == set(cbq_native.SIGNATURES), "ctypes table out of sync with header"
+
+
+def test_error_strings(lib):
+    assert lib.ck_error_string(0) == b"success"
+    assert lib.ck_error_string(2) == b"invalid argument"
+    assert b"gfx950" in lib.cbq_version()
+
+
+def test_argument_validation_before_launch(lib):
+    # null pointers / bad sizes return CK_ERR_ARG without touching the GPU
+    assert lib.ck_linear_f32(None, None, None, None, 1, 1, 32, 1, 13, None) == 2
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.addressof(buf)
+    assert lib.ck_linear_f32(p, p, p, p, 0, 1, 32, 1, 13, None) == 2
+    assert lib.ck_linear_f32(p, p, p, p, 1, 1, 32, 1, 17, None) == 2
+    assert lib.ck_linear_bf16(p, p, p, p, 1, 1, 32, 0, 13, None) == 2
+    assert lib.ck_embedding_f32(p, p, p, p, 1, 0, 4, 13, None) == 2
+    assert lib.cbq_embedding_f32(p, p, p, p, 1, 0, 64, 4, 13, None) == 2
+    assert lib.huff_decode_to_i32(None, p, p, p, p, p, p, p, 1, 1, 20, None) == 2
+    assert lib.huff_i32_linear_f32(p, p, p, p, 1, 0, 1, 1, None) == 2
+    assert lib.huff_i32_embedding_f32(p, p, p, p, 1, 1, 0, None) == 2
+    import cbq_native
+    hs = cbq_native.HuffStream()
+    assert lib.cbq_huff_linear_f32(p, ctypes.byref(hs), p, 1, 4, 64, None) == 2   # empty desc
+    assert lib.cbq_huff_linear_f32(p, ctypes.byref(hs), p, 17, 4, 64, None) == 2  # T > 16
+    assert lib.cbq_huff_embedding_f32(p, ctypes.byref(hs), p, 1, 4, 60, None) == 2
+    assert lib.cbq_huff_decode_indices(ctypes.byref(hs), p, 64, None) == 2
+
+
+def test_build_luts_rejects_overfull(lib):
+    lengths = np.array([1, 1, 1], np.uint8)             # Kraft sum 1.5
+    n2 = ctypes.c_int(0)
+    rc = lib.cbq_huff_build_luts(lengths.ctypes.data, 3, None, 0, 0, 0, None, None,
+                                 ctypes.byref(n2), None, None)
+    assert rc == 2
+
+
+def test_build_luts_sizes(lib):
+    import huffman_codebook as hc
+    lengths = np.array([2, 2, 2, 3, 4, 14, 14] + [0] * 3, np.uint8)
+    lut1, lut2, canon, pay = hc.device_luts(lengths, None, 0, value_payload=False, clamp=False)
+    assert lut1.size == 4096 and lut2.size == 4     # one 14-bit prefix -> 2^2 subtable
+    assert canon[33 + 14] == 2 and list(pay[:5]) == [0, 1, 2, 3, 4]
