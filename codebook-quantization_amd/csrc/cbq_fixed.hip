@@ -18,10 +18,13 @@
 
 namespace {
 
-constexpr int kBlock = 512;                 // 8 waves share one LDS codebook
+constexpr int kBlock = 1024;                // 16 waves share one LDS codebook
 constexpr int kWavesPerBlock = kBlock / CBQ_WAVE;
 constexpr int kMaxLdsBytes = 64 * 1024;     // per-workgroup budget we allow
 constexpr int kMaxLdsCodebook = 16384;      // entries of fp32 codebook in LDS
+// The x-in-registers path runs one block per CU, so it may use most of the
+// CU's 160 KB of LDS (codebook + padded x + row partials).
+constexpr int kMaxLdsBytesXReg = 152 * 1024;
 
 template <typename XT>
 __device__ __forceinline__ void load_x32(const XT *__restrict__ p, float xv[32]);
@@ -68,78 +71,182 @@ __device__ __forceinline__ void gather_weights(const uint32_t w[BITS],
     }
 }
 
-// One wave per row (grid-stride over rows); codebook (and x when it fits) in
-// LDS.  Each lane walks its (row, group) items with a one-deep software
-// pipeline: the words of the next item are in flight while the current one
-// is unpacked, and the very first load is issued before the LDS staging
-// barrier so HBM latency overlaps the codebook copy.  T <= TMAX tokens.
-template <int BITS, int TMAX, bool XLDS, typename XT, typename OT>
+// x row layout in LDS: each 32-element group padded to 36 floats, so the
+// eight 16-byte reads a lane makes for its group hit distinct banks across
+// lanes (a 128-byte stride would put all lanes on the same banks).
+constexpr int kXGroupStride = 36;
+
+// Block = RB * WPR waves (<= 16).  The block walks row groups of RB rows;
+// each row is split over WPR waves (split-K), a wave's lanes take the row's
+// 32-index groups g = kw*64 + lane + it*64*WPR.  Each lane streams its
+// (row, group) items through a ring of D register buffers, so D groups of
+// words are in flight while one is unpacked; the first D loads are issued
+// before the LDS staging barrier.  When every lane owns a single group of
+// each row (NGW == 1) and T == 1, XREG keeps that group's 32 x values in
+// registers for the whole kernel.  Row results: wave butterfly, then
+// (WPR > 1) a sum of the WPR wave partials through LDS.  T <= TMAX tokens.
+template <int BITS, int TMAX, int D, int XMODE, typename XT, typename OT>
 __global__ __launch_bounds__(kBlock) void fixed_gemv_kernel(
     const XT *__restrict__ x, const uint32_t *__restrict__ words,
-    const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C)
+    const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C, int WPR,
+    int RB)
 {
+    constexpr bool XREG = XMODE == 2;
+    // x is staged in LDS for both XLDS and XREG (coalesced global loads; a
+    // lane-private 128-byte global read per lane would cost 64 cache-line
+    // lookups per instruction); XREG then copies a lane's 32 values to VGPRs.
+    constexpr bool XLDS = XMODE == 1 || XREG;
     extern __shared__ float lds[];
+    const int G = K >> 5;                          // 32-index groups per row
     float *s_cb = lds;
-    float *s_x = lds + ((C + 3) & ~3);
+    float *s_red = lds + ((C + 3) & ~3);           // [kWavesPerBlock][TMAX]
+    float *s_x = s_red + kWavesPerBlock * TMAX;    // [T][G * kXGroupStride]
     const int tid = threadIdx.x;
+    const int wave_count = RB * WPR;
     const int lane = tid & (CBQ_WAVE - 1);
     const int wave = tid / CBQ_WAVE;
-    const int G = K >> 5;                       // 32-index groups per row
-    const int NG = (G + CBQ_WAVE - 1) / CBQ_WAVE;  // items per lane per row (wave-uniform)
-    const int stride = gridDim.x * kWavesPerBlock;
+    const int rsub = wave / WPR, kw = wave % WPR;
+    const int NGW = (G + CBQ_WAVE * WPR - 1) / (CBQ_WAVE * WPR);   // items per row per lane
+    const int first = blockIdx.x * RB;
+    const int rstride = gridDim.x * RB;
+    const int n_iter = first < M ? (M - first + rstride - 1) / rstride : 0;
+    const int n_items = n_iter * NGW;              // block-uniform
     const uint32_t cmax = (uint32_t)(C - 1);
 
-    int row = blockIdx.x * kWavesPerBlock + wave;
-    uint32_t cur[BITS];
-    if (row < M && lane < G)
-        __builtin_memcpy(cur, words + ((size_t)row * G + lane) * BITS, sizeof(cur));
+    auto item_row = [&](int item) { return first + (item / NGW) * rstride + rsub; };
+    auto item_grp = [&](int item) { return kw * CBQ_WAVE + lane + (item % NGW) * CBQ_WAVE * WPR; };
 
-    for (int i = tid; i < C; i += kBlock) s_cb[i] = cb[i];
-    if (XLDS)
-        for (int i = tid; i < T * K; i += kBlock) s_x[i] = to_f32<XT>(x[i]);
-    __syncthreads();
-
-    while (row < M) {
-        float acc[TMAX];
+    // Prologue.  Only the first kStageWaves waves stage the codebook (and x
+    // for XLDS), each with batches of unconditional loads issued before any
+    // of their own weight loads; every other wave starts its weight prefetch
+    // at once.  The LDS barrier then waits on those few staging loads only.
+    // Every global load is unconditional (clamped addresses): loads under
+    // divergent branches make the compiler wait for all outstanding loads,
+    // which would defeat the prefetch ring.
+    constexpr int kStageWaves = 4;
+    constexpr int kStageBatch = 32;
+    const int nsw = wave_count < kStageWaves ? wave_count : kStageWaves;
+    const int st_threads = nsw * CBQ_WAVE;
+    if (wave < nsw) {
+        for (int base = 0; base < C; base += kStageBatch * st_threads) {
+            float st[kStageBatch];
 #pragma unroll
-        for (int t = 0; t < TMAX; t++) acc[t] = 0.f;
-        for (int it = 0; it < NG; it++) {
-            const int g = lane + it * CBQ_WAVE;
-            // next item of this lane: next group of the row, else first of next row
-            int g2 = g + CBQ_WAVE, row2 = row;
-            if (it + 1 == NG) { g2 = lane; row2 = row + stride; }
-            uint32_t nxt[BITS];
-            if (row2 < M && g2 < G)
-                __builtin_memcpy(nxt, words + ((size_t)row2 * G + g2) * BITS, sizeof(nxt));
-            if (g < G) {
-                float wv[32];
-                gather_weights<BITS>(cur, s_cb, cmax, wv);
+            for (int r = 0; r < kStageBatch; r++) {
+                const int i = base + tid + r * st_threads;
+                st[r] = cb[i < C ? i : C - 1];
+            }
 #pragma unroll
-                for (int t = 0; t < TMAX; t++) {
-                    if (t < T) {
-                        float xv[32];
-                        if (XLDS)
-                            __builtin_memcpy(xv, s_x + t * K + g * 32, sizeof(xv));
-                        else
-                            load_x32<XT>(x + (size_t)t * K + g * 32, xv);
-                        float a = acc[t];
+            for (int r = 0; r < kStageBatch; r++) {
+                const int i = base + tid + r * st_threads;
+                if (i < C) s_cb[i] = st[r];
+            }
+        }
+        if (XLDS) {
+            const int n = T * K;
+            for (int base = 0; base < n; base += kStageBatch * st_threads) {
+                float st[kStageBatch];
 #pragma unroll
-                        for (int j = 0; j < 32; j++) a = fmaf(xv[j], wv[j], a);
-                        acc[t] = a;
+                for (int r = 0; r < kStageBatch; r++) {
+                    const int i = base + tid + r * st_threads;
+                    st[r] = to_f32<XT>(x[i < n ? i : n - 1]);
+                }
+#pragma unroll
+                for (int r = 0; r < kStageBatch; r++) {
+                    const int i = base + tid + r * st_threads;
+                    if (i < n) {
+                        const int t = i / K, k = i - t * K;
+                        s_x[t * G * kXGroupStride + (k >> 5) * kXGroupStride + (k & 31)] = st[r];
                     }
                 }
             }
-#pragma unroll
-            for (int b = 0; b < BITS; b++) cur[b] = nxt[b];
         }
+    }
+    auto load_item = [&](uint32_t (&dst)[BITS], int item) {
+        const int r = item_row(item), g = item_grp(item);
+        const bool ok = item < n_items && r < M && g < G;
+        __builtin_memcpy(dst, words + ((size_t)(ok ? r : 0) * G + (ok ? g : 0)) * BITS,
+                         sizeof(dst));
+    };
+    uint32_t buf[D][BITS];
 #pragma unroll
-        for (int t = 0; t < TMAX; t++) {
-            if (t < T) {
-                const float s = wave_sum(acc[t]);
-                if (lane == 0) out[(size_t)t * M + row] = from_f32<OT>(s);
+    for (int d = 0; d < D; d++) load_item(buf[d], d);
+    lds_barrier();
+    float xr[XREG ? 32 : 1];
+    if (XREG) {
+        const int g = item_grp(0);
+        __builtin_memcpy(xr, s_x + (g < G ? g : 0) * kXGroupStride, sizeof(xr));
+    }
+
+    float acc[TMAX];
+#pragma unroll
+    for (int t = 0; t < TMAX; t++) acc[t] = 0.f;
+
+    for (int base = 0; base < n_items; base += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int item = base + d;
+            if (item < n_items) {
+                const int row = item_row(item), g = item_grp(item);
+                if (row < M && g < G) {
+                    float wv[32];
+                    gather_weights<BITS>(buf[d], s_cb, cmax, wv);
+                    if (XREG) {
+                        // four independent partial sums shorten the FMA chain
+                        float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+                        for (int j = 0; j < 32; j += 4) {
+                            p0 = fmaf(xr[j], wv[j], p0);
+                            p1 = fmaf(xr[j + 1], wv[j + 1], p1);
+                            p2 = fmaf(xr[j + 2], wv[j + 2], p2);
+                            p3 = fmaf(xr[j + 3], wv[j + 3], p3);
+                        }
+                        acc[0] += (p0 + p1) + (p2 + p3);
+                    } else {
+#pragma unroll
+                        for (int t = 0; t < TMAX; t++) {
+                            if (t < T) {
+                                float xv[32];
+                                if (XLDS)
+                                    __builtin_memcpy(xv, s_x + (t * G + g) * kXGroupStride, sizeof(xv));
+                                else
+                                    load_x32<XT>(x + (size_t)t * K + g * 32, xv);
+                                float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+                                for (int j = 0; j < 32; j += 2) {
+                                    p0 = fmaf(xv[j], wv[j], p0);
+                                    p1 = fmaf(xv[j + 1], wv[j + 1], p1);
+                                }
+                                acc[t] += p0 + p1;
+                            }
+                        }
+                    }
+                }
+                load_item(buf[d], item + D);
+                if (item % NGW == NGW - 1) {             // row done (block-uniform)
+#pragma unroll
+                    for (int t = 0; t < TMAX; t++) {
+                        if (t < T) {
+                            const float v = wave_sum(acc[t]);
+                            if (WPR == 1) {
+                                if (lane == 0 && row < M) out[(size_t)t * M + row] = from_f32<OT>(v);
+                            } else if (lane == 0) {
+                                s_red[wave * TMAX + t] = v;
+                            }
+                            acc[t] = 0.f;
+                        }
+                    }
+                    if (WPR > 1) {
+                        lds_barrier();
+                        if (kw == 0 && lane < T && row < M) {
+                            float v = 0.f;
+                            for (int w = 0; w < WPR; w++) v += s_red[(wave + w) * TMAX + lane];
+                            out[(size_t)lane * M + row] = from_f32<OT>(v);
+                        }
+                        lds_barrier();
+                    }
+                }
             }
         }
-        row += stride;
     }
 }
 
@@ -232,19 +339,35 @@ __global__ __launch_bounds__(kBlock) void fixed_embedding_generic_kernel(
 
 // ---- launch plumbing -------------------------------------------------------
 
-template <int BITS, int TMAX, bool XLDS, typename XT, typename OT>
+// Waves per row.  Prefer one 32-index group per lane per row (WPR = G/64
+// when that is <= 8), which lets T = 1 keep x in registers; otherwise split
+// rows only as far as needed to give every CU ~16 waves.
+int pick_wpr(int M, int G)
+{
+    const int full = (G + CBQ_WAVE - 1) / CBQ_WAVE;
+    if (full <= kWavesPerBlock) return full;
+    const int want_waves = cbq_num_cus() * 16;
+    int wpr = 1;
+    while (wpr < kWavesPerBlock && M * wpr < want_waves && G > CBQ_WAVE * wpr) wpr <<= 1;
+    return wpr;
+}
+
+template <int BITS, int TMAX, int XMODE, typename XT, typename OT>
 int launch_fast(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T,
                 int M, int K, int C, hipStream_t st)
 {
-    const size_t lds = (size_t)((C + 3) & ~3) * 4 + (XLDS ? (size_t)T * K * 4 : 0);
-    // Two 8-wave blocks per CU: each block stages its own codebook copy, so
-    // more blocks would only add L2->LDS traffic.
-    const int per_cu = std::max(1, std::min(2, (int)(160 * 1024 / std::max<size_t>(lds, 1))));
-    const int blocks = std::max(1, std::min((M + kWavesPerBlock - 1) / kWavesPerBlock,
-                                            cbq_num_cus() * per_cu));
-    hipLaunchKernelGGL((fixed_gemv_kernel<BITS, TMAX, XLDS, XT, OT>), dim3(blocks),
-                       dim3(kBlock), lds, st, x, (const uint32_t *)packed, cb, out, T, M,
-                       K, C);
+    const int G = K / 32;
+    const int wpr = pick_wpr(M, G);
+    const int rb = std::max(1, kWavesPerBlock / wpr);
+    const size_t lds = (size_t)((C + 3) & ~3) * 4 + (size_t)kWavesPerBlock * TMAX * 4 +
+                       (XMODE != 0 ? (size_t)T * G * kXGroupStride * 4 : 0);
+    // One 16-wave block per CU: each block stages its own codebook copy.
+    const int per_cu = 1;
+    const int blocks = std::max(1, std::min((M + rb - 1) / rb, cbq_num_cus() * per_cu));
+    constexpr int D = TMAX <= 4 ? 3 : 2;
+    hipLaunchKernelGGL((fixed_gemv_kernel<BITS, TMAX, D, XMODE, XT, OT>), dim3(blocks),
+                       dim3(rb * wpr * CBQ_WAVE), lds, st, x, (const uint32_t *)packed, cb, out,
+                       T, M, K, C, wpr, rb);
     return cbq_launch_status("fixed_gemv_kernel");
 }
 
@@ -252,10 +375,16 @@ template <int BITS, int TMAX, typename XT, typename OT>
 int dispatch_x(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T,
                int M, int K, int C, hipStream_t st)
 {
+    const int G = K / 32;
     const size_t cb_bytes = (size_t)((C + 3) & ~3) * 4;
-    if (cb_bytes + (size_t)T * K * 4 <= (size_t)kMaxLdsBytes)
-        return launch_fast<BITS, TMAX, true>(x, packed, cb, out, T, M, K, C, st);
-    return launch_fast<BITS, TMAX, false>(x, packed, cb, out, T, M, K, C, st);
+    if constexpr (TMAX == 1) {
+        if ((G + CBQ_WAVE - 1) / CBQ_WAVE <= kWavesPerBlock &&
+            cb_bytes + (size_t)G * kXGroupStride * 4 <= (size_t)kMaxLdsBytesXReg)
+            return launch_fast<BITS, TMAX, 2>(x, packed, cb, out, T, M, K, C, st);   // x in VGPRs
+    }
+    if (cb_bytes + (size_t)T * G * kXGroupStride * 4 <= (size_t)kMaxLdsBytes)
+        return launch_fast<BITS, TMAX, 1>(x, packed, cb, out, T, M, K, C, st);   // x in LDS
+    return launch_fast<BITS, TMAX, 0>(x, packed, cb, out, T, M, K, C, st);       // x via cache
 }
 
 template <int BITS, typename XT, typename OT>

@@ -299,7 +299,7 @@ __global__ __launch_bounds__(kHBlock) void huff_gemv_kernel(
     float *s_cb = (float *)(s_lut2 + lut2_slots);
     uint32_t *s_stg = (uint32_t *)(s_cb + ((n_cb + 3) & ~3));
     load_tables(s_lut1, s_lut2, a.lut1, a.lut2, a.n_lut2, lut2_lds, s_cb, a.value_cb, n_cb);
-    __syncthreads();
+    lds_barrier();
 
     const Tabs tb{s_lut1, lut2_lds ? s_lut2 : a.lut2, (uint32_t)a.n_lut2, a.canon, a.canon_pay};
     const int lane = threadIdx.x & (CBQ_WAVE - 1);
@@ -398,7 +398,7 @@ __global__ __launch_bounds__(kHBlock) void huff_embedding_kernel(
     float *s_cb = (float *)(s_lut2 + lut2_slots);
     uint32_t *s_stg = (uint32_t *)(s_cb + ((n_cb + 3) & ~3));
     load_tables(s_lut1, s_lut2, a.lut1, a.lut2, a.n_lut2, lut2_lds, s_cb, a.value_cb, n_cb);
-    __syncthreads();
+    lds_barrier();
 
     const Tabs tb{s_lut1, lut2_lds ? s_lut2 : a.lut2, (uint32_t)a.n_lut2, a.canon, a.canon_pay};
     const int lane = threadIdx.x & (CBQ_WAVE - 1);
@@ -470,7 +470,7 @@ __global__ __launch_bounds__(kHBlock) void huff_decode_kernel(int32_t *__restric
     const int lut2_slots = lut2_lds ? ((a.n_lut2 + 3) & ~3) : 0;
     uint32_t *s_stg = s_lut2 + lut2_slots;
     load_tables(s_lut1, s_lut2, a.lut1, a.lut2, a.n_lut2, lut2_lds, nullptr, nullptr, 0);
-    __syncthreads();
+    lds_barrier();
 
     const Tabs tb{s_lut1, lut2_lds ? s_lut2 : a.lut2, (uint32_t)a.n_lut2, a.canon, a.canon_pay};
     const int lane = threadIdx.x & (CBQ_WAVE - 1);

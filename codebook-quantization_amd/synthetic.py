@@ -1,0 +1,184 @@
+"""Synthetic compressed decoders built on the GPU (bench and e2e workloads).
+
+Weights are N(0, std) rounded to bf16 (torch's nearest-even cast), drawn per
+tensor from a seeded CUDA generator, so every tensor can be regenerated
+bit-identically.  Lossless codebooks are shared per category (attention /
+mlp_ffn / embedding) and frequency-sorted; fixed-width tensors are packed
+LSB-first; Huffman tensors get their own 24-bit-limited canonical code
+(lengths from that tensor's symbol counts, as the reference codes each
+tensor, src/adaptive_compressor.py:111-127) and the chunk index.
+"""
+from __future__ import annotations
+
+import zlib
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Tuple
+
+import numpy as np
+import torch
+
+import codebook_builder as cbb
+import huffman_codebook as hc
+
+# (name, out_features, in_features) per decoder layer
+def layer_shapes(hidden: int, inter: int, n_q: int, n_kv: int, head_dim: int):
+    return [("self_attn.q_proj", n_q * head_dim, hidden),
+            ("self_attn.k_proj", n_kv * head_dim, hidden),
+            ("self_attn.v_proj", n_kv * head_dim, hidden),
+            ("self_attn.o_proj", hidden, n_q * head_dim),
+            ("mlp.gate_proj", inter, hidden),
+            ("mlp.up_proj", inter, hidden),
+            ("mlp.down_proj", hidden, inter)]
+
+
+CONFIGS = {
+    # Qwen3-8B-style, 36 layers
+    "qwen3-8b": dict(layers=36, hidden=4096, inter=12288, n_q=32, n_kv=8, head_dim=128,
+                     vocab=151936),
+    # Qwen3-1.7B-style, 28 layers
+    "qwen3-1.7b": dict(layers=28, hidden=2048, inter=6144, n_q=16, n_kv=8, head_dim=128,
+                       vocab=151936),
+}
+
+
+def tensor_seed(name: str, base: int = 0) -> int:
+    return (zlib.crc32(name.encode()) ^ (base * 0x9E3779B1)) & 0x7FFFFFFF
+
+
+def make_bf16(shape, name: str, std: float = 0.02, base_seed: int = 0,
+              device="cuda") -> torch.Tensor:
+    g = torch.Generator(device=device)
+    g.manual_seed(tensor_seed(name, base_seed))
+    return (torch.randn(*shape, generator=g, device=device, dtype=torch.float32) * std).bfloat16()
+
+
+@dataclass
+class FixedTensor:
+    name: str
+    shape: Tuple[int, int]
+    bits: int
+    category: str
+    packed: torch.Tensor            # uint8, device, padded
+    codebook: torch.Tensor          # float32, device
+
+    @property
+    def nbytes(self) -> int:
+        return (self.shape[0] * self.shape[1] * self.bits + 7) // 8
+
+
+@dataclass
+class HuffTensor:
+    name: str
+    shape: Tuple[int, int]
+    category: str
+    lengths: np.ndarray
+    words: torch.Tensor             # int32 view of LSB-first words
+    chunk_off: torch.Tensor         # int64 (uint64 values)
+    sub_len: torch.Tensor           # int16 (uint16 values)
+    total_bits: int
+    tables: dict = field(default_factory=dict)
+
+    @property
+    def nbytes(self) -> int:
+        """Stream bytes + chunk table + sub-block table."""
+        return (self.total_bits + 7) // 8 + self.chunk_off.numel() * 8 + self.sub_len.numel() * 2
+
+
+def huffman_encode_torch(idx: torch.Tensor, lengths: np.ndarray):
+    """GPU canonical-Huffman encoder -> (int32 words, chunk_off, sub_len, bits).
+
+    Codes are bit-reversed and scattered LSB-first into 64-bit words; code
+    fields never overlap, so integer adds of the shifted fields equal their OR.
+    """
+    dev = idx.device
+    codes = hc.canonical_codes(lengths)
+    rev = hc._bitrev(codes, lengths.astype(np.int64)).astype(np.int64)
+    L_tab = torch.from_numpy(lengths.astype(np.int64)).to(dev)
+    R_tab = torch.from_numpy(rev).to(dev)
+    flat = idx.reshape(-1).to(torch.int64)
+    L = L_tab[flat]
+    starts = torch.cumsum(L, 0) - L
+    total = int(starts[-1] + L[-1])
+    words = torch.zeros(total // 64 + 3, dtype=torch.int64, device=dev)
+    w = starts >> 6
+    sh = starts & 63
+    r = R_tab[flat]
+    words.index_add_(0, w, r << sh)
+    spill = (sh + L) > 64
+    if bool(spill.any()):
+        words.index_add_(0, w[spill] + 1, r[spill] >> (64 - sh[spill]))
+    tot = torch.tensor([total], dtype=torch.int64, device=dev)
+    chunk_off = torch.cat([starts[::hc.CHUNK_SYMBOLS], tot])
+    sub_len = torch.diff(torch.cat([starts[::hc.SUB_SYMBOLS], tot])).to(torch.int16)
+    return words.view(torch.int32), chunk_off, sub_len, total
+
+
+class SyntheticDecoder:
+    """All linear weights of a decoder (+ lm_head and embedding), compressed."""
+
+    def __init__(self, config: str = "qwen3-8b", layers: Optional[int] = None,
+                 base_seed: int = 0, device="cuda", log=print):
+        c = dict(CONFIGS[config])
+        if layers is not None:
+            c["layers"] = layers
+        self.cfg = c
+        self.device = torch.device(device)
+        self.base_seed = base_seed
+        self.log = log
+        shapes = layer_shapes(c["hidden"], c["inter"], c["n_q"], c["n_kv"], c["head_dim"])
+        self.linears: List[Tuple[str, int, int]] = [
+            (f"model.layers.{i}.{n}", M, K) for i in range(c["layers"]) for n, M, K in shapes]
+        self.lm_head = ("lm_head", c["vocab"], c["hidden"])
+        self.embed = ("model.embed_tokens", c["vocab"], c["hidden"])
+
+    def all_linears(self, with_head=True):
+        return self.linears + ([self.lm_head] if with_head else [])
+
+    def _gen(self, name, M, K):
+        return make_bf16((M, K), name, base_seed=self.base_seed, device=self.device)
+
+    def category_codebooks(self, tensors) -> Dict[str, Tuple[torch.Tensor, torch.Tensor]]:
+        counts: Dict[str, torch.Tensor] = {}
+        for name, M, K in tensors:
+            cat = cbb.classify_tensor(name)
+            cnt = cbb.counts_torch(self._gen(name, M, K))
+            counts[cat] = counts[cat] + cnt if cat in counts else cnt
+        return {cat: cbb.codebook_from_counts_torch(cnt) for cat, cnt in counts.items()}
+
+    def build_fixed(self, tensors) -> Dict[str, FixedTensor]:
+        books = self.category_codebooks(tensors)
+        out = {}
+        for name, M, K in tensors:
+            cat = cbb.classify_tensor(name)
+            cb, lut = books[cat]
+            bits = cbb.bits_for(cb.numel())
+            idx = lut[cbb.patterns_torch(self._gen(name, M, K)).reshape(-1).to(torch.int64)]
+            pk = cbb.pack_torch(idx, bits)
+            padded = torch.zeros(((pk.numel() + 15) // 16) * 16 + 16, dtype=torch.uint8,
+                                 device=self.device)
+            padded[:pk.numel()] = pk
+            out[name] = FixedTensor(name, (M, K), bits, cat, padded, cb.contiguous())
+        return out
+
+    def build_huffman(self, tensors, max_len: int = hc.DEFAULT_MAX_LEN) -> Dict[str, HuffTensor]:
+        books = self.category_codebooks(tensors)
+        out = {}
+        for name, M, K in tensors:
+            cat = cbb.classify_tensor(name)
+            cb, lut = books[cat]
+            idx = lut[cbb.patterns_torch(self._gen(name, M, K)).reshape(-1).to(torch.int64)]
+            C = cb.numel()
+            counts = torch.bincount(idx, minlength=C).cpu().numpy()
+            lengths = hc.length_limited_code_lengths(counts, max_len)
+            words, chunk_off, sub_len, total = huffman_encode_torch(idx, lengths)
+            cb_np = cb.cpu().numpy()
+            lut1, lut2, canon, pay = hc.device_luts(lengths, cb_np, C, value_payload=True)
+            t = HuffTensor(name, (M, K), cat, lengths, words, chunk_off, sub_len, total)
+            t.tables = dict(lut1=torch.from_numpy(lut1.view(np.int32)).to(self.device),
+                            lut2=torch.from_numpy(lut2.view(np.int32)).to(self.device),
+                            canon=torch.from_numpy(canon).to(self.device),
+                            pay=torch.from_numpy(pay).to(self.device),
+                            stage_words=hc.stage_words_for(chunk_off.cpu().numpy()),
+                            codebook=cb)
+            out[name] = t
+        return out
