@@ -250,6 +250,216 @@ __global__ __launch_bounds__(kBlock) void fixed_gemv_kernel(
     }
 }
 
+// ---- streaming row-owner kernel --------------------------------------------
+//
+// One 8-wave block per CU.  Wave `wid` owns rows wid, wid + W, ... (W = all
+// waves of the grid) and walks them in items of 64 groups: lane l takes group
+// chunk*64 + l of the row, i.e. BITS consecutive index words, loaded with
+// dwordx4 loads into a two-deep register ring.  The loop body has no barrier,
+// no store and no divergent branch, so the only wait is on the oldest ring
+// slot.  Row sums stay in lane (row & 63) of `res` and are written 64 rows at
+// a time.  Codebook and x are staged into LDS by direct global->LDS loads
+// issued before the first weight loads; the wave waits for those alone.
+
+constexpr int kStreamWaves = 8;
+constexpr int kStreamBlock = kStreamWaves * CBQ_WAVE;
+constexpr int kStreamD = 2;
+constexpr int kStreamLds = 152 * 1024;      // codebook + staged x, per block
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+// Byte offsets into the LDS codebook of the 32 indices of one group: each
+// field is extracted already shifted left by 2 (alignbit/shift + and).  A
+// PADDED codebook has 2^BITS entries (entries >= C repeat cb[C-1]), so the
+// index clamp of the reference (idx >= C -> C-1) costs nothing; otherwise the
+// offset is clamped to 4*(C-1).
+template <int BITS, bool PADDED>
+__device__ __forceinline__ void group_offsets(const uint32_t (&w)[BITS], uint32_t cmax4,
+                                              uint32_t off[32])
+{
+    constexpr uint32_t m4 = ((1u << BITS) - 1u) << 2;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        const int o = j * BITS, q = o >> 5, s = o & 31;
+        uint32_t a;
+        if (s >= 2)
+            a = (s + BITS <= 32) ? ((w[q] >> (s - 2)) & m4)
+                                 : (funnel(w[q + 1], w[q], (uint32_t)(s - 2)) & m4);
+        else
+            a = (w[q] << (2 - s)) & m4;
+        if (!PADDED) a = a < cmax4 ? a : cmax4;
+        off[j] = a;
+    }
+}
+
+// x staged in LDS as raw XT bits, one row of K per token.  A 32-element group
+// (128 B fp32 / 64 B bf16) is stored as 16-byte chunks in swizzled order, so
+// the ds_read_b128 of 8 neighbouring lanes hit distinct bank groups.
+template <typename XT> struct XStage;
+template <> struct XStage<float> {
+    static constexpr int kGroupDw = 32;
+    __device__ static int chunk(int c, int g) { return c ^ (g & 7); }
+    __device__ static void read(const uint32_t *s, int g, float xv[32])
+    {
+        typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const u4 v = *(const u4 *)(s + g * 32 + (chunk(c, g) << 2));
+            xv[4 * c] = __uint_as_float(v.x);
+            xv[4 * c + 1] = __uint_as_float(v.y);
+            xv[4 * c + 2] = __uint_as_float(v.z);
+            xv[4 * c + 3] = __uint_as_float(v.w);
+        }
+    }
+};
+template <> struct XStage<uint16_t> {
+    static constexpr int kGroupDw = 16;
+    __device__ static int chunk(int c, int g) { return c ^ ((g >> 1) & 3); }
+    __device__ static void read(const uint32_t *s, int g, float xv[32])
+    {
+        typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const u4 v = *(const u4 *)(s + g * 16 + (chunk(c, g) << 2));
+            const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                xv[8 * c + 2 * i] = __uint_as_float(u[i] << 16);
+                xv[8 * c + 2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+            }
+        }
+    }
+};
+
+template <int BITS, int TMAX, typename XT, typename OT>
+__global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
+    const XT *__restrict__ x, const uint32_t *__restrict__ words,
+    const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C)
+{
+    constexpr bool PADDED = BITS <= 14;
+    constexpr int D = kStreamD;
+    __shared__ float s_cbp[PADDED ? (1 << BITS) : 1];
+    extern __shared__ float s_dyn[];
+    const int C_eff = C < (1 << BITS) ? C : (1 << BITS);
+    const int cb_slots = PADDED ? (1 << BITS) : ((C_eff + 63) & ~63);
+    float *s_cb = PADDED ? s_cbp : s_dyn;
+    uint32_t *s_x = (uint32_t *)(PADDED ? s_dyn : s_dyn + cb_slots);
+
+    const int G = K >> 5;
+    const int NGW = (G + CBQ_WAVE - 1) / CBQ_WAVE;
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CBQ_WAVE);
+    const int W = gridDim.x * kStreamWaves;
+    const int wid = blockIdx.x * kStreamWaves + wave;
+    const int rows = wid < M ? (M - wid + W - 1) / W : 0;
+    const int n_items = rows * NGW;
+    const uint32_t cmax4 = (uint32_t)(C_eff - 1) << 2;
+
+    // Staging: direct global->LDS dword loads, every wave a share.
+    for (int i = wave; i < (cb_slots >> 6); i += kStreamWaves) {
+        const int e = (i << 6) + lane;
+        __builtin_amdgcn_global_load_lds((const void *)(cb + (e < C ? e : C - 1)),
+                                         (lds_ptr_t)(s_cb + (i << 6)), 4, 0, 0);
+    }
+    constexpr int GD = XStage<XT>::kGroupDw;
+    const int xdw = G * GD;                        // dwords of one token's x
+    const int n_xdw = T * xdw;
+    const uint32_t *xw = (const uint32_t *)x;
+    for (int i = wave; i < ((n_xdw + 63) >> 6); i += kStreamWaves) {
+        int sl = (i << 6) + lane;                  // LDS dword slot (this lane's)
+        sl = sl < n_xdw ? sl : n_xdw - 1;          // tail lanes re-copy the last dword
+        const int t = sl / xdw, d = sl - t * xdw;
+        const int g = d / GD, p = (d % GD) >> 2;
+        const int src = t * xdw + g * GD + (XStage<XT>::chunk(p, g) << 2) + (d & 3);
+        __builtin_amdgcn_global_load_lds((const void *)(xw + src), (lds_ptr_t)(s_x + (i << 6)),
+                                         4, 0, 0);
+    }
+    // The weight addresses depend on `zero`, produced by a volatile asm with a
+    // memory clobber, so no weight load is issued before the staging loads.
+    uint32_t zero;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(zero) : : "memory");
+
+    auto item_ptr = [&](int item) {
+        const int it = item < n_items ? item : 0;
+        const int ri = it / NGW, ch = it - ri * NGW;
+        int g = ch * CBQ_WAVE + lane;
+        g = g < G ? g : G - 1;
+        const int row = rows > 0 ? wid + ri * W : 0;
+        return words + ((size_t)row * G + g) * BITS + zero;
+    };
+    uint32_t buf[D][BITS];
+#pragma unroll
+    for (int d = 0; d < D; d++) __builtin_memcpy(buf[d], item_ptr(d), sizeof(buf[d]));
+    __builtin_amdgcn_sched_barrier(0);
+    // vmcnt(N): at most N loads outstanding.  N = the fewest instructions the
+    // D ring loads can take (dwordx4), so every older staging load has landed.
+    constexpr int kAfter = D * ((BITS + 3) / 4);
+    __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | (15 << 8) | ((kAfter >> 4) << 14));
+    lds_barrier();
+
+    float acc[TMAX], res[TMAX];
+#pragma unroll
+    for (int t = 0; t < TMAX; t++) acc[t] = res[t] = 0.f;
+    int ri = 0, ch = 0, base = 0;
+    do {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int item = base + d;
+            const int g = ch * CBQ_WAVE + lane;
+            const int gg = g < G ? g : G - 1;
+            const bool valid = item < n_items && g < G;
+            uint32_t off[32];
+            group_offsets<BITS, PADDED>(buf[d], cmax4, off);
+            float wv[32];
+#pragma unroll
+            for (int j = 0; j < 32; j++) wv[j] = *(const float *)((const char *)s_cb + off[j]);
+#pragma unroll
+            for (int t = 0; t < TMAX; t++) {
+                if (t < T) {
+                    float xv[32];
+                    XStage<XT>::read(s_x + t * xdw, gg, xv);
+                    float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 32; j += 4) {
+                        p0 = fmaf(xv[j], wv[j], p0);
+                        p1 = fmaf(xv[j + 1], wv[j + 1], p1);
+                        p2 = fmaf(xv[j + 2], wv[j + 2], p2);
+                        p3 = fmaf(xv[j + 3], wv[j + 3], p3);
+                    }
+                    acc[t] += valid ? (p0 + p1) + (p2 + p3) : 0.f;
+                }
+            }
+            __builtin_memcpy(buf[d], item_ptr(item + D), sizeof(buf[d]));
+            if (++ch == NGW) {                       // row done (wave-uniform)
+                ch = 0;
+#pragma unroll
+                for (int t = 0; t < TMAX; t++) {
+                    if (t < T) {
+                        const float s = wave_sum(acc[t]);
+                        acc[t] = 0.f;
+                        res[t] = (lane == (ri & 63) && ri < rows) ? s : res[t];
+                    }
+                }
+                ri++;
+                if ((ri & 63) == 0 && ri <= rows) {
+                    const int row = wid + (ri - 64 + lane) * W;
+#pragma unroll
+                    for (int t = 0; t < TMAX; t++)
+                        if (t < T) out[(size_t)t * M + row] = from_f32<OT>(res[t]);
+                }
+            }
+        }
+        base += D;
+    } while (base < n_items);
+    const int rb = rows & ~63;
+    if (lane < rows - rb) {
+        const int row = wid + (rb + lane) * W;
+#pragma unroll
+        for (int t = 0; t < TMAX; t++)
+            if (t < T) out[(size_t)t * M + row] = from_f32<OT>(res[t]);
+    }
+}
+
 // Any width, any K, codebook read through the cache: per-element 4-byte
 // window like the reference (reads at most 3 bytes past the last index).
 template <int TMAX, typename XT, typename OT>
@@ -387,10 +597,44 @@ int dispatch_x(const XT *x, const uint8_t *packed, const float *cb, OT *out, int
     return launch_fast<BITS, TMAX, 0>(x, packed, cb, out, T, M, K, C, st);       // x via cache
 }
 
+template <int BITS, int TMAX, typename XT, typename OT>
+int launch_stream(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T, int M,
+                  int K, int C, size_t dyn_lds, hipStream_t st)
+{
+    const int blocks =
+        std::max(1, std::min(cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
+    hipLaunchKernelGGL((fixed_stream_kernel<BITS, TMAX, XT, OT>), dim3(blocks),
+                       dim3(kStreamBlock), dyn_lds, st, x, (const uint32_t *)packed, cb, out, T,
+                       M, K, C);
+    return cbq_launch_status("fixed_stream_kernel");
+}
+
+// Dynamic LDS the streaming kernel needs (0 if it does not fit): unpadded
+// codebook (BITS > 14) + all T rows of x, rounded to 64-dword staging steps.
+template <int BITS, typename XT>
+size_t stream_dyn_lds(int T, int K, int C)
+{
+    const size_t c_eff = (size_t)std::min(C, 1 << BITS);
+    const size_t cb_static = BITS <= 14 ? ((size_t)4 << BITS) : 0;
+    const size_t cb_dyn = BITS <= 14 ? 0 : ((c_eff + 63) & ~(size_t)63) * 4;
+    const size_t n_xdw = (size_t)T * (K / 32) * XStage<XT>::kGroupDw;
+    const size_t x_bytes = ((n_xdw + 63) & ~(size_t)63) * 4;
+    if (cb_static + cb_dyn + x_bytes > (size_t)kStreamLds) return 0;
+    return cb_dyn + x_bytes;
+}
+
 template <int BITS, typename XT, typename OT>
 int dispatch_t(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T,
                int M, int K, int C, hipStream_t st)
 {
+    // Streaming kernel when x of all T tokens fits in LDS beside the codebook
+    // (the x staging copies dwords, so x must be 4-byte aligned).
+    const size_t dyn = ((uintptr_t)x & 3) == 0 ? stream_dyn_lds<BITS, XT>(T, K, C) : 0;
+    if (dyn) {
+        if (T == 1) return launch_stream<BITS, 1>(x, packed, cb, out, T, M, K, C, dyn, st);
+        if (T <= 4) return launch_stream<BITS, 4>(x, packed, cb, out, T, M, K, C, dyn, st);
+        return launch_stream<BITS, 16>(x, packed, cb, out, T, M, K, C, dyn, st);
+    }
     if (T == 1) return dispatch_x<BITS, 1>(x, packed, cb, out, T, M, K, C, st);
     if (T <= 4) return dispatch_x<BITS, 4>(x, packed, cb, out, T, M, K, C, st);
     return dispatch_x<BITS, 16>(x, packed, cb, out, T, M, K, C, st);
