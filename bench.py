@@ -193,8 +193,8 @@ def main():
     achieved = b_gu / (us_gu * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                "traffic": read_traffic("fixed_gemv_gate_up_qwen3-8b_pmc.md"),
-                "kernel": f"fixed_gemv_kernel<13,1> gate/up {t.shape[1]}->{t.shape[0]}",
+                "traffic": read_traffic("fixed_stream_kernel_gate_up_qwen3-8b_pmc.md"),
+                "kernel": f"fixed_stream_kernel<13,1,f32> gate/up {t.shape[1]}->{t.shape[0]}",
                 "bytes_per_launch": b_gu, "us_per_launch": round(us_gu, 2)}
 
     result = {

@@ -21,7 +21,9 @@
  * Accumulation is fp32, k ascending, token loop innermost, exactly as the
  * reference; it is compiled with the reference wrapper's flags
  * (-O3 -march=native -funroll-loops -fopenmp, compressed_matmul_cpu.py:88-91)
- * so that gcc makes the same multiply-add contraction choices.
+ * except that -march=native becomes -march=x86-64-v3 (AVX2 + FMA), so the
+ * library also runs on other x86 hosts; gcc makes the same multiply-add
+ * contraction choices either way.
  */
 #include <stdint.h>
 #include <string.h>
