@@ -383,6 +383,232 @@ __global__ __launch_bounds__(kHBlock) void huff_gemv_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Fused GEMV, K % 4096 == 0, T == 1: k-tiled, two chunks per lane
+// ---------------------------------------------------------------------------
+//
+// With K a multiple of 4096 every 4096-symbol chunk is exactly one 4096-wide
+// k-tile of one row, so the block runs K/4096 phases.  Each phase stages one
+// x tile (16 KB) in LDS, and every wave decodes chunk (row, phase) of NCH of
+// its rows at once: lane l decodes sub-block l of each of the NCH chunks.
+// That gives NCH independent decode chains per lane, all using the same x
+// values.  Row sums build up over the phases in lane (row & 63) of `res`.
+//
+// A chunk's words reach the wave's LDS slot by direct global->LDS dwordx4
+// loads.  A lane keeps q = (its bit position) - 2 into the slot.  From that,
+// `win2 = alignbit(slot[d+1], slot[d], q)` holds stream bits q+2.. at bit 2,
+// so `win2 & 0x3ffc` is the byte offset of the code's lut1 entry.  A chunk
+// whose words exceed the slot is decoded from global memory instead.
+
+constexpr int kTWaves = 8;
+constexpr int kTBlock = kTWaves * CBQ_WAVE;
+constexpr int kXRun = 68;            // LDS floats per 64-float run of x (bank spread)
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+__device__ __forceinline__ void dma_dword(const void *g, void *lds_base)
+{
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_base, 4, 0, 0);
+}
+
+__device__ __forceinline__ void dma_dwordx4(const void *g, void *lds_base)
+{
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_base, 16, 0, 0);
+}
+
+// Second table level and the >24-bit canonical search for an entry whose
+// 12-bit prefix is a pointer (len field 0).  win2: stream bits at bit 2+.
+template <bool LUT2_LDS>
+__device__ __forceinline__ uint32_t decode_long(uint32_t e, uint32_t win2, uint32_t win,
+                                                const uint32_t *__restrict__ lut2,
+                                                uint32_t n_lut2,
+                                                const int32_t *__restrict__ canon,
+                                                const int32_t *__restrict__ pay)
+{
+    const uint32_t nb = (e >> 6) & 31u;
+    uint32_t i = (e >> 11) + __builtin_amdgcn_ubfe(win2, kLutBits + 2, nb);
+    i = i < n_lut2 ? i : n_lut2 - 1u;             // tables from other builders stay in bounds
+    e = lut2[i];
+    if ((e & 63u) == 0u) e = decode_canon(win, canon, pay);
+    return e;
+}
+
+template <int NCH, bool VALUE_MODE, bool LUT2_LDS>
+__global__ __launch_bounds__(kTBlock) void huff_tile_kernel(
+    const float *__restrict__ x, float *__restrict__ out, HuffArgs a, int M, int K,
+    int slot_words, int n_cb)
+{
+    __shared__ uint32_t s_lut1[kLutSize];                      // static: fixed LDS offset
+    extern __shared__ uint32_t hlds[];
+    uint32_t *s_lut2 = hlds;
+    const int n2 = LUT2_LDS ? ((a.n_lut2 + 63) & ~63) : 0;
+    float *s_cb = (float *)(s_lut2 + n2);
+    const int ncb = VALUE_MODE ? 0 : ((n_cb + 63) & ~63);
+    float *s_x = s_cb + ncb;                                   // 64 runs of kXRun
+    uint32_t *s_slots = (uint32_t *)(s_x + 64 * kXRun);
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CBQ_WAVE);
+    const int nwv = blockDim.x / CBQ_WAVE;                     // waves per block
+    uint32_t *slot = s_slots + wave * NCH * slot_words;
+
+    // Tables into LDS (every wave a share of 64-dword steps; sources clamped).
+    for (int i = wave; i < (kLutSize >> 6); i += nwv)
+        dma_dword(a.lut1 + (i << 6) + lane, s_lut1 + (i << 6));
+    if (LUT2_LDS)
+        for (int i = wave; i < (n2 >> 6); i += nwv) {
+            const int e = (i << 6) + lane;
+            dma_dword(a.lut2 + (e < a.n_lut2 ? e : a.n_lut2 - 1), s_lut2 + (i << 6));
+        }
+    if (!VALUE_MODE)
+        for (int i = wave; i < (ncb >> 6); i += nwv) {
+            const int e = (i << 6) + lane;
+            dma_dword(a.value_cb + (e < n_cb ? e : n_cb - 1), s_cb + (i << 6));
+        }
+    const uint32_t *lut2 = LUT2_LDS ? s_lut2 : a.lut2;
+    const uint32_t n_lut2 = (uint32_t)a.n_lut2;
+
+    const int R = K / kChunk;                                  // phases (k-tiles)
+    const int W = gridDim.x * nwv;
+    const int wid = blockIdx.x * nwv + wave;
+    const int rows = wid < M ? (M - wid + W - 1) / W : 0;
+    const int b0 = blockIdx.x * nwv;                           // the block's first wave
+    const int rows_max = b0 < M ? (M - b0 + W - 1) / W : 0;    // = wave 0's count
+    const int n_seg = (rows_max + 63) >> 6;
+
+    for (int seg = 0; seg < n_seg; seg++) {
+        float res = 0.f;
+        const int seg_rows = min(64, rows - seg * 64);         // may be <= 0
+        for (int p = 0; p < R; p++) {
+            __syncthreads();                                   // x tile no longer read
+            // x tile p: 64 runs of 64 floats, run r at s_x + r * kXRun
+            for (int r = wave; r < 64; r += nwv)
+                dma_dword(x + (size_t)p * kChunk + (r << 6) + lane, s_x + r * kXRun);
+            __syncthreads();                                   // waits for all loads
+            for (int b = 0; b < seg_rows; b += NCH) {
+                uint64_t q0[NCH];
+                bool big = false;
+                uint32_t sl[NCH];
+                int64_t wbase[NCH];
+#pragma unroll
+                for (int j = 0; j < NCH; j++) {
+                    const int ri = seg * 64 + b + j;
+                    const int64_t row = ri < rows ? wid + (int64_t)ri * W : wid;
+                    const int64_t c = __builtin_amdgcn_readfirstlane((int)(row * R + p));
+                    sl[j] = a.sub_len[c * kSub + lane];
+                    const uint64_t off0 = a.chunk_off[c], off1 = a.chunk_off[c + 1];
+                    const int64_t wb = (int64_t)(off0 >> 5) & ~(int64_t)3;
+                    // words to stage, in whole 256-word DMA steps (64 lanes x 16 B)
+                    const int64_t need = ((int64_t)((off1 + 31) >> 5) + 2 - wb + 255) & ~(int64_t)255;
+                    wbase[j] = wb;
+                    q0[j] = off0 - ((uint64_t)wb << 5);
+                    big |= need > slot_words;
+                    if (need <= slot_words) {
+                        for (int i = 0; i < need; i += 4 * CBQ_WAVE) {
+                            int64_t src = wb + i + 4 * lane;
+                            src = src < a.n_words - 4 ? src : a.n_words - 4;
+                            dma_dwordx4(a.words + src, slot + j * slot_words + i);
+                        }
+                    }
+                }
+                __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));   // vmcnt(0)
+                uint32_t q[NCH];
+                float acc[NCH];
+#pragma unroll
+                for (int j = 0; j < NCH; j++) {
+                    const uint32_t incl = wave_incl_scan(sl[j]);
+                    q[j] = (uint32_t)q0[j] + (incl - sl[j]) - 2u;
+                    acc[j] = 0.f;
+                }
+                const float *xr = s_x + lane * kXRun;
+                if (!big) {
+                    for (int i = 0; i < kSub; i += 4) {
+                        typedef float f4 __attribute__((ext_vector_type(4)));
+                        const f4 xv4 = *(const f4 *)(xr + i);
+                        const float xv[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            // Stage by stage over the NCH chains so their LDS reads
+                            // overlap.  The second table level is read by every
+                            // lane (short codes read one clamped, shared entry), so
+                            // no branch is taken for the 12..24-bit codes.
+                            uint32_t lo[NCH], hi[NCH], win2[NCH], e[NCH], e2[NCH];
+#pragma unroll
+                            for (int j = 0; j < NCH; j++) {
+                                const int d = (int)q[j] >> 5;
+                                lo[j] = slot[j * slot_words + d];
+                                hi[j] = slot[j * slot_words + d + 1];
+                            }
+#pragma unroll
+                            for (int j = 0; j < NCH; j++) {
+                                win2[j] = funnel(hi[j], lo[j], q[j]);
+                                e[j] = *(const uint32_t *)((const char *)s_lut1 + (win2[j] & 0x3ffcu));
+                            }
+                            if (LUT2_LDS) {
+#pragma unroll
+                                for (int j = 0; j < NCH; j++) {
+                                    const uint32_t nb = __builtin_amdgcn_ubfe(e[j], 6, 5);
+                                    uint32_t i2 = (e[j] >> 11) + __builtin_amdgcn_ubfe(win2[j], kLutBits + 2, nb);
+                                    i2 = i2 < n_lut2 ? i2 : n_lut2 - 1u;
+                                    e2[j] = lut2[i2];
+                                }
+#pragma unroll
+                                for (int j = 0; j < NCH; j++) e[j] = (e[j] & 63u) ? e[j] : e2[j];
+                            }
+                            bool any_long = false;
+#pragma unroll
+                            for (int j = 0; j < NCH; j++) any_long |= (e[j] & 63u) == 0u;
+                            if (any_long) {
+                                // LUT2_LDS: only codes longer than 24 bits (canonical
+                                // search); otherwise the second level from global memory.
+#pragma unroll
+                                for (int j = 0; j < NCH; j++) {
+                                    if ((e[j] & 63u) == 0u) {
+                                        const uint32_t *sj = slot + j * slot_words;
+                                        const uint32_t q2 = q[j] + 2u;
+                                        const uint32_t win = funnel(sj[(q2 >> 5) + 1], sj[q2 >> 5], q2);
+                                        e[j] = LUT2_LDS ? decode_canon(win, a.canon, a.canon_pay)
+                                                        : decode_long<LUT2_LDS>(e[j], win2[j], win, lut2,
+                                                                                n_lut2, a.canon,
+                                                                                a.canon_pay);
+                                    }
+                                }
+                            }
+#pragma unroll
+                            for (int j = 0; j < NCH; j++) {
+                                q[j] += e[j] & 63u;
+                                acc[j] = fmaf(xv[u], payload_value<VALUE_MODE>(e[j], s_cb), acc[j]);
+                            }
+                        }
+                    }
+                } else {
+                    // Oversized chunk(s): windows straight from global memory.
+                    for (int i = 0; i < kSub; i++) {
+                        const float xv = xr[i];
+#pragma unroll
+                        for (int j = 0; j < NCH; j++) {
+                            const uint32_t q2 = q[j] + 2u;
+                            const uint32_t win = window_global(a.words, a.n_words, wbase[j], q2);
+                            uint32_t e = s_lut1[win & (kLutSize - 1)];
+                            if ((e & 63u) == 0u) e = decode_long<LUT2_LDS>(e, win << 2, win,
+                                                                         lut2, n_lut2, a.canon,
+                                                                         a.canon_pay);
+                            q[j] += e & 63u;
+                            acc[j] = fmaf(xv, payload_value<VALUE_MODE>(e, s_cb), acc[j]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < NCH; j++) {
+                    const float s = wave_sum(acc[j]);
+                    if (b + j < seg_rows && lane == b + j) res += s;
+                }
+                __builtin_amdgcn_wave_barrier();               // slot reuse by the next batch
+            }
+        }
+        if (lane < seg_rows) out[wid + (int64_t)(seg * 64 + lane) * W] = res;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Embedding: one wave per requested row (H % 64 == 0)
 // ---------------------------------------------------------------------------
 
@@ -638,6 +864,51 @@ int launch_gemv(const float *x, float *out, const HuffArgs &a, int T, int M, int
 
 int64_t gcd64(int64_t a, int64_t b) { while (b) { int64_t t = a % b; a = b; b = t; } return a; }
 
+// k-tiled kernel (K % 4096 == 0, T == 1).  Returns -1 when the LDS plan does
+// not leave room for useful word slots (the caller then uses huff_gemv_kernel).
+constexpr size_t kTileLds = 160 * 1024;
+
+template <int NCH>
+int launch_tile_n(const float *x, float *out, const HuffArgs &a, int M, int K, int n_cb,
+                  int slot_cap, int waves, hipStream_t st)
+{
+    const bool value_mode = a.value_cb == nullptr;
+    const size_t lut2_bytes = (size_t)((a.n_lut2 + 63) & ~63) * 4;
+    const size_t cb_bytes = value_mode ? 0 : (size_t)((n_cb + 63) & ~63) * 4;
+    const size_t fixed_nol2 = (size_t)kLutSize * 4 + cb_bytes + 64 * kXRun * 4;
+    const bool lut2_lds = fixed_nol2 + lut2_bytes + (size_t)waves * NCH * 1536 * 4 <= kTileLds;
+    const size_t fixed = fixed_nol2 + (lut2_lds ? lut2_bytes : 0);
+    if (fixed >= kTileLds) return -1;
+    int slot = (int)((kTileLds - fixed) / ((size_t)waves * NCH * 4));
+    if (slot < 1024) return -1;
+    // The descriptor's stage_words caps the slot.  This kernel stages whole
+    // 256-word DMA steps from a 16-byte aligned start, so the cap is widened
+    // by that rounding; larger chunks decode from global memory.
+    const int cap = (slot_cap + 4 + 255) & ~255;
+    slot = std::min({slot, 2048, cap}) & ~255;
+    const size_t dyn = fixed - (size_t)kLutSize * 4 + (size_t)waves * NCH * slot * 4;
+    const int blocks = std::max(1, std::min(cbq_num_cus(), (M + waves - 1) / waves));
+#define CBQ_TILE_LAUNCH(VM, L2)                                                                \
+    hipLaunchKernelGGL((huff_tile_kernel<NCH, VM, L2>), dim3(blocks), dim3(waves * CBQ_WAVE), \
+                       dyn, st, x, out, a, M, K, slot, n_cb)
+    if (value_mode) {
+        if (lut2_lds) CBQ_TILE_LAUNCH(true, true); else CBQ_TILE_LAUNCH(true, false);
+    } else {
+        if (lut2_lds) CBQ_TILE_LAUNCH(false, true); else CBQ_TILE_LAUNCH(false, false);
+    }
+#undef CBQ_TILE_LAUNCH
+    return cbq_launch_status("huff_tile_kernel");
+}
+
+int launch_tile(const float *x, float *out, const HuffArgs &a, int M, int K, int n_cb,
+                int slot_cap, hipStream_t st)
+{
+    // 8 waves x 2 chains: LDS holds lut1 + lut2 + x tile + 16 word slots.
+    // Measured on MI355X, 4096 -> 12288: 56 us; 8x1 74 us, 4x4 76 us, 6x3
+    // (lut2 pushed out of LDS) 126 us.
+    return launch_tile_n<2>(x, out, a, M, K, n_cb, slot_cap, kTWaves, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -795,6 +1066,11 @@ int cbq_huff_linear_f32(const float *x, const cbq_huff_stream *hs, float *out, i
     const int64_t L = (int64_t)K / gcd64(K, kChunk) * kChunk;      // lcm(K, 4096)
     const int64_t RW = L / K, SPL = L / kChunk;
     if (RW > (1 << 20) || SPL > (1 << 20)) return CK_ERR_ARG;
+    if (T == 1 && K % kChunk == 0) {
+        const int cap = hs->stage_words > 0 ? hs->stage_words : 2048;
+        const int rc = launch_tile(x, out, a, M, K, n_cb, cap, stream);
+        if (rc >= 0) return rc;
+    }
     const LdsPlan p = plan_lds(a.n_lut2, n_cb, stage_words_of(hs));
     if (p.bytes > 160 * 1024) return CK_ERR_ARG;
     if (T == 1)

@@ -192,3 +192,47 @@ def test_embedding_rows_config5_like(cuda, oracle):
                                     int(enc2["huff_n"][0]), torch.from_numpy(cb2), (vocab2, H2), 13)
     ids2 = np.arange(0, vocab2, 7, dtype=np.int32)
     assert np.array_equal(emb2(torch.from_numpy(ids2).to(cuda)).cpu().numpy(), w2[ids2])
+
+
+@pytest.mark.parametrize("M,K,payload", [(300, 4096, "value"), (70, 12288, "value"),
+                                         (130, 8192, "symbol")])
+def test_k_tiled_path(cuda, oracle, M, K, payload):
+    """K % 4096 == 0 and T == 1 run the k-tiled kernel: phases over 4096-wide
+    x tiles, two chunks per lane.  Also run with a tiny staging cap, which
+    sends every chunk down the global-window path of the same kernel."""
+    rng = np.random.default_rng(M + K)
+    if payload == "value":
+        w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
+        cb, idx = cbb.frequency_sorted_codebook(w)
+    else:
+        C = 2500
+        f = np.ones(C)
+        f[:50] = rng.uniform(100, 5000, 50)
+        idx = rng.choice(C, size=M * K, p=f / f.sum())
+        cb = rng.standard_normal(C).astype(np.float32)
+    enc = hc.huffman_encode_indices(idx, shape=(M, K))
+    lin = _lin(enc, cb, M, K)
+    assert lin.dev.value_payload == (payload == "value")
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    ref = oracle.huff_gemv(x, enc, cb, M, K, chunk_rows=None)
+    y = lin(torch.from_numpy(x).to(cuda)).cpu().numpy()
+    assert rel_l2(y, ref) <= TOL
+    lin.dev.desc.stage_words = 8
+    y2 = lin(torch.from_numpy(x).to(cuda)).cpu().numpy()
+    assert rel_l2(y2, ref) <= TOL
+
+
+def test_k_tiled_long_codes(cuda, oracle):
+    """Codes up to 30 bits through the k-tiled kernel's second table level and
+    canonical stage."""
+    rng = np.random.default_rng(11)
+    lengths = np.array(list(range(1, 31)) + [30], np.uint8)
+    M, K = 24, 4096
+    p = 0.5 ** np.minimum(lengths, 12).astype(np.float64)
+    idx = rng.choice(31, size=M * K, p=p / p.sum())
+    enc = oracle.huffman_encode(idx, shape=(M, K), lengths=lengths)
+    cb = (rng.standard_normal(31) * 0.02).astype(np.float32)
+    lin = _lin(enc, cb, M, K)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    y = lin(torch.from_numpy(x).to(cuda)).cpu().numpy()
+    assert rel_l2(y, oracle.huff_gemv(x, enc, cb, M, K)) <= TOL
