@@ -724,6 +724,10 @@ int embedding_impl(const int32_t *ids, const uint8_t *packed, const float *cb, f
 
 }  // namespace
 
+// bf16 MFMA prefill path (cbq_prefill.hip); -1 = shape not handled there.
+int cbq_prefill_bf16(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
+                     int T, int M, int K, int C, int bits, hipStream_t st);
+
 int cbq_num_cus()
 {
     static int cache[64] = {0};
@@ -762,6 +766,13 @@ int ck_linear_f32(const float *x, const uint8_t *packed, const float *codebook, 
 int ck_linear_bf16(const void *x_bf16, const uint8_t *packed, const float *codebook,
                    void *out_bf16, int T, int M, int K, int C, int bits, hipStream_t stream)
 {
+    // T >= 64: the GEMM regime, bf16 MFMA with fp32 accumulation (cbq_prefill.hip)
+    if (x_bf16 && packed && codebook && out_bf16 && T >= 64 && M > 0 && K > 0 && C > 0 &&
+        bits >= 1 && bits <= 16) {
+        const int rc = cbq_prefill_bf16((const uint16_t *)x_bf16, packed, codebook,
+                                        (uint16_t *)out_bf16, T, M, K, C, bits, stream);
+        if (rc >= 0) return rc;
+    }
     return linear_any_t<uint16_t, uint16_t>((const uint16_t *)x_bf16, packed, codebook,
                                             (uint16_t *)out_bf16, T, M, K, C, bits, stream);
 }

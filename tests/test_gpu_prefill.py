@@ -1,0 +1,94 @@
+"""bf16 MFMA prefill path of ck_linear_bf16 (T >= 64) vs the oracle.
+
+Bar: rel-L2 <= 2e-3 against the fp32 reference GEMV
+on the same bf16 inputs; outputs are bf16, so >= 95% of them must also equal
+the oracle's fp32 result rounded to bf16 within one bf16 ulp.
+"""
+import numpy as np
+import pytest
+import torch
+
+import codebook_builder as cbb
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _prefill(cuda, xb, pk, cb, M, K, bits):
+    import bitpack
+    import cbq_native as nat
+    lib = nat.load()
+    T = xb.shape[0]
+    pd = torch.from_numpy(bitpack.device_padded(pk)).to(cuda)
+    cd = torch.from_numpy(np.ascontiguousarray(cb, np.float32)).to(cuda)
+    xd = xb.to(cuda).contiguous()
+    out = torch.full((T, M), float("nan"), dtype=torch.bfloat16, device=cuda)
+    rc = lib.ck_linear_bf16(xd.data_ptr(), pd.data_ptr(), cd.data_ptr(), out.data_ptr(), T, M, K,
+                            len(cb), bits, nat.stream_ptr(cuda))
+    nat.check(rc, "ck_linear_bf16")
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def _check(y, ref):
+    assert np.isfinite(y).all()
+    assert rel_l2(y, ref) <= TOL, rel_l2(y, ref)
+    ref_b = torch.from_numpy(ref).bfloat16().float().numpy()
+    ulp = np.abs(ref_b) * 2.0 ** -7 + 1e-30
+    assert (np.abs(y - ref_b) <= ulp).mean() >= 0.95
+
+
+@pytest.mark.parametrize("T,M,K", [(64, 128, 256), (100, 300, 4096), (256, 384, 2048),
+                                   (300, 200, 1024), (512, 136, 12288)])
+def test_lossless_bf16(cuda, oracle, T, M, K):
+    """Config 4 style: bf16 N(0, 0.02) weights, lossless frequency-sorted
+    codebook (13 bits), bf16 activations N(0, 1)."""
+    w = cbb.bf16_round(np.random.default_rng(T + M).standard_normal((M, K)) * 0.02)
+    d = cbb.compress_fixed(w)
+    bits = d["bits"]
+    xb = torch.randn(T, K, generator=torch.Generator().manual_seed(T)).bfloat16()
+    y = _prefill(cuda, xb, d["indices"], d["codebook"], M, K, bits)
+    ref = oracle.fixed_gemv(xb.float().numpy(), d["indices"], d["codebook"], M, K, bits,
+                            chunk_rows=None)
+    _check(y, ref)
+
+
+@pytest.mark.parametrize("bits,C", [(8, 200), (12, 4000), (13, 5000), (14, 9000)])
+def test_widths_and_clamp(cuda, oracle, bits, C):
+    """Raw indices above C-1 clamp; codebook values are bf16-exact here."""
+    T, M, K = 128, 160, 512
+    rng = np.random.default_rng(bits)
+    raw = rng.integers(0, 1 << bits, size=M * K)
+    cb = cbb.bf16_round(rng.standard_normal(C) * 0.05).astype(np.float32)
+    pk = oracle.pack_lsb(raw, bits)
+    xb = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).bfloat16()
+    y = _prefill(cuda, xb, pk, cb, M, K, bits)
+    ref = oracle.fixed_gemv(xb.float().numpy(), pk, cb, M, K, bits, C=C, chunk_rows=None)
+    _check(y, ref)
+
+
+def test_fp32_codebook_rounds_to_bf16(cuda, oracle):
+    """A codebook that is not bf16-exact feeds the MFMA rounded to bf16; the
+    result stays within the prefill tolerance."""
+    T, M, K, bits, C = 192, 256, 2048, 12, 3000
+    rng = np.random.default_rng(7)
+    raw = rng.integers(0, C, size=M * K)
+    cb = (rng.standard_normal(C) * 0.05).astype(np.float32)
+    pk = oracle.pack_lsb(raw, bits)
+    xb = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).bfloat16()
+    y = _prefill(cuda, xb, pk, cb, M, K, bits)
+    ref = oracle.fixed_gemv(xb.float().numpy(), pk, cb, M, K, bits, C=C, chunk_rows=None)
+    assert rel_l2(y, ref) <= TOL
+
+
+def test_matches_token_tile_path(cuda):
+    """T = 64 runs the MFMA path, T = 16 the VALU token tiles: rows common to
+    both agree within bf16 output rounding."""
+    M, K = 512, 4096
+    w = cbb.bf16_round(np.random.default_rng(1).standard_normal((M, K)) * 0.02)
+    d = cbb.compress_fixed(w)
+    xb = torch.randn(64, K, generator=torch.Generator().manual_seed(3)).bfloat16()
+    y64 = _prefill(cuda, xb, d["indices"], d["codebook"], M, K, d["bits"])
+    y16 = _prefill(cuda, xb[:16].clone(), d["indices"], d["codebook"], M, K, d["bits"])
+    assert rel_l2(y64[:16], y16) <= TOL
