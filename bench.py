@@ -29,6 +29,7 @@ sys.path.insert(0, os.path.join(ROOT, "codebook-quantization_amd"))
 
 METRIC = "compressed GEMV HBM GB/s (% of peak) + decode tok/s, batch 1, 9B-scale shapes"
 HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16
 
 
 def log(*a):
@@ -108,6 +109,91 @@ def cpu_baseline(np, packed, cb, x, M, K, bits, seconds):
                        f"{nbytes / as_called / 1e9:.3f} GB/s")}
 
 
+def prefill_section(torch, nat, lib, dev, fixed, kinds, args):
+    """bf16 MFMA prefill over the same fixed-width weights,
+    T = 512 and 2048 tokens of bf16 N(0, 1) activations; per shape the mean
+    launch time over all layers' distinct weights (graph-replayed)."""
+    out = {"peak_tflops": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "shapes": {}}
+    for T in (512, 2048):
+        for kind in ("q_proj", "k_proj", "gate_proj", "down_proj"):
+            ns = kinds[kind][:8]
+            t0 = fixed[ns[0]]
+            M, K = t0.shape
+            x = torch.randn(T, K, device=dev).bfloat16()
+            o = torch.empty(T, M, device=dev, dtype=torch.bfloat16)
+
+            def run(ns=ns, x=x, o=o):
+                st = nat.stream_ptr(dev)
+                for n in ns:
+                    t = fixed[n]
+                    rc = lib.ck_linear_bf16(x.data_ptr(), t.packed.data_ptr(), t.codebook.data_ptr(),
+                                            o.data_ptr(), T, M, K, t.codebook.numel(), t.bits, st)
+                    if rc:
+                        raise RuntimeError(f"ck_linear_bf16 rc={rc} on {n}")
+            ms, _ = timed_graph(torch, run, max(2, args.steps // 4), 1)
+            us = ms * 1e3 / len(ns)
+            tf = 2.0 * T * M * K / (us * 1e-6) / 1e12
+            out["shapes"][f"T{T}_{kind}"] = {"shape": f"{K}->{M}", "us_per_launch": round(us, 1),
+                                             "TFLOP/s": round(tf, 1),
+                                             "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+    g = out["shapes"]["T2048_gate_proj"]
+    out["roofline"] = {"bound": "mfma", "achieved": g["TFLOP/s"], "peak": MFMA_BF16_PEAK_TFLOPS,
+                       "unit": "TFLOP/s", "frac": g["frac"],
+                       "kernel": "fixed_prefill_kernel<13> gate/up 4096->12288, T=2048"}
+    return out
+
+
+def e2e_section(torch, dec, args):
+    """always-compressed greedy decode of the random-init
+    36-layer Qwen3-8B-shape decoder at batch 1: all linears, the lm_head and
+    the embedding Huffman-coded (24-bit canonical codes, 4096-symbol chunks);
+    128-token uniform random prompt, then args.e2e_tokens greedy tokens (EOS
+    ignored).  tok/s over the decode steps, which are captured once as a HIP
+    graph and replayed.  The same model with fixed-width 13-bit indices (the
+    same weights) runs too; its tokens must agree."""
+    import numpy as np
+    import decoder as D
+    import synthetic
+    c = dec.cfg
+    cfg = D.DecoderConfig(layers=c["layers"], hidden=c["hidden"], inter=c["inter"], n_q=c["n_q"],
+                          n_kv=c["n_kv"], head_dim=c["head_dim"], vocab=c["vocab"])
+    names = dec.all_linears() + [dec.embed]
+    prompt = [int(t) for t in np.random.default_rng(2).integers(0, cfg.vocab, 128)]
+    n_new = args.e2e_tokens
+    out = {"prompt_tokens": len(prompt), "new_tokens": n_new, "batch": 1}
+    toks = {}
+    for enc in ("huffman", "fixed"):
+        t0 = time.time()
+        tensors = dec.build_huffman(names) if enc == "huffman" else dec.build_fixed(names)
+        torch.cuda.synchronize()
+        build_s = time.time() - t0
+        model = D.from_synthetic(cfg, tensors, max_len=len(prompt) + n_new)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.reset()
+        model.forward(torch.tensor(prompt))
+        torch.cuda.synchronize()
+        prefill_s = time.perf_counter() - t0
+        timing = {}
+        toks[enc] = model.generate_graph(prompt, n_new, timing)
+        step_bytes = sum((t.nbytes if enc == "huffman" else t.nbytes) for n, t in tensors.items()
+                         if n != dec.embed[0])
+        tps = timing["decode_steps"] / timing["decode_s"]
+        out[enc] = {"decode_tok_per_s": round(tps, 2),
+                    "ms_per_token": round(1e3 / tps, 3),
+                    "weight_GB_per_token": round(step_bytes / 1e9, 3),
+                    "weight_GB/s": round(step_bytes * tps / 1e9, 1),
+                    "prefill_ms_128_tokens": round(prefill_s * 1e3, 1),
+                    "build_s": round(build_s, 1), "first_tokens": toks[enc][:8]}
+        log(f"e2e {enc}: {tps:.1f} tok/s")
+        del tensors, model
+        torch.cuda.empty_cache()
+    out["tokens_equal_huffman_vs_fixed"] = toks["huffman"] == toks["fixed"]
+    out["token_agreement"] = round(sum(a == b for a, b in zip(toks["huffman"], toks["fixed"])) /
+                                   max(1, n_new), 4)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -116,6 +202,9 @@ def main():
     ap.add_argument("--config", default="qwen3-8b")
     ap.add_argument("--layers", type=int, default=None)
     ap.add_argument("--no-huffman", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--e2e-tokens", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-probe", type=int, default=0,
@@ -211,6 +300,9 @@ def main():
         "breakdown": breakdown,
     }
 
+    if not args.no_prefill:
+        result["prefill"] = prefill_section(torch, nat, lib, dev, fixed, kinds, args)
+
     if not args.no_cpu_baseline:
         n0 = gu[0]
         t = fixed[n0]
@@ -262,9 +354,12 @@ def main():
                          "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(hb_gu / (us_hgu * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
                          "traffic": read_traffic("huff_gemv_gate_up_qwen3-8b_pmc.md"),
-                         "kernel": "huff_gemv_kernel<1,value> gate/up",
+                         "kernel": "huff_tile_kernel<2,value,lut2-lds> gate/up 4096->12288",
                          "bytes_per_launch": hb_gu, "us_per_launch": round(us_hgu, 2)}}
         log(f"huffman sweep: {ms_h:.3f} ms/step, {hbytes / 1e9:.2f} GB/step")
+
+    if not args.no_e2e:
+        result["e2e"] = e2e_section(torch, dec, args)
 
     print(json.dumps(result), flush=True)
 

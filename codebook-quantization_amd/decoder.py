@@ -1,0 +1,359 @@
+"""Always-compressed Qwen3-style greedy decoder (batch 1) on the gfx950 library.
+
+This is the end-to-end caller of the compressed path: every linear of every
+layer, the lm_head and the token embedding stay compressed in HBM, as
+fixed-width indices or canonical Huffman, and run through libcbq_hip.so.
+The glue around them is written in fp32 torch ops and follows the HF Qwen3
+modelling that the reference's compressed modules plug into
+(src/model_loader.py:213-277):
+
+- RMSNorm: x * rsqrt(mean(x^2) + eps) * weight;
+- q/k head RMSNorm;
+- rotary embedding ("default" rope, rotate-half form);
+- grouped-query causal attention with an fp32 softmax;
+- SiLU-gated MLP;
+- final norm, then argmax over the logits.
+
+For a random-init model the norm weights are ones, as at HF initialisation.
+
+Activations are fp32 throughout, so the compressed GEMVs run their fp32
+kernels (rel-L2 <= 1e-5 against the reference's C kernel).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Callable, Dict, List, Optional
+
+import numpy as np
+import torch
+
+LAYER_LINEARS = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                 "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj")
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    layers: int
+    hidden: int
+    inter: int
+    n_q: int
+    n_kv: int
+    head_dim: int
+    vocab: int
+    rope_theta: float = 1.0e6          # Qwen3-8B's published config
+    eps: float = 1.0e-6
+
+    def linear_shapes(self):
+        """(name, out_features, in_features) of every compressed matrix."""
+        h, hd = self.hidden, self.head_dim
+        per = {"self_attn.q_proj": (self.n_q * hd, h), "self_attn.k_proj": (self.n_kv * hd, h),
+               "self_attn.v_proj": (self.n_kv * hd, h), "self_attn.o_proj": (h, self.n_q * hd),
+               "mlp.gate_proj": (self.inter, h), "mlp.up_proj": (self.inter, h),
+               "mlp.down_proj": (h, self.inter)}
+        out = [(f"model.layers.{i}.{n}", *per[n]) for i in range(self.layers) for n in LAYER_LINEARS]
+        return out + [("lm_head", self.vocab, h)]
+
+
+QWEN3_8B = DecoderConfig(layers=36, hidden=4096, inter=12288, n_q=32, n_kv=8, head_dim=128,
+                         vocab=151936)
+
+
+def rope_tables(cfg: DecoderConfig, max_len: int):
+    """cos, sin [max_len, head_dim] float32, computed as HF's default rotary
+    embedding does: fp32 inverse frequencies, fp32 angles, duplicated halves."""
+    d = cfg.head_dim
+    inv = (1.0 / (np.float32(cfg.rope_theta) ** (np.arange(0, d, 2, dtype=np.int64)
+                                                  .astype(np.float32) / np.float32(d))))
+    inv = inv.astype(np.float32)
+    pos = np.arange(max_len, dtype=np.float32)
+    freqs = (pos[:, None] * inv[None, :]).astype(np.float32)
+    emb = np.concatenate([freqs, freqs], axis=-1)
+    t = torch.from_numpy(emb)
+    return t.cos().numpy(), t.sin().numpy()
+
+
+Linear = Callable[[torch.Tensor], torch.Tensor]        # [T, K] fp32 -> [T, M] fp32
+
+
+class Qwen3Decoder:
+    """Greedy decoder over compressed linears / embedding (callables)."""
+
+    def __init__(self, cfg: DecoderConfig, linears: Dict[str, Linear], embed: Callable,
+                 device: torch.device, max_len: int = 512):
+        self.cfg = cfg
+        self.linears = linears
+        self.embed = embed
+        self.device = torch.device(device)
+        self.max_len = max_len
+        cos, sin = rope_tables(cfg, max_len)
+        self.cos = torch.from_numpy(cos).to(self.device)
+        self.sin = torch.from_numpy(sin).to(self.device)
+        kv = (cfg.layers, 2, cfg.n_kv, max_len, cfg.head_dim)
+        self.cache = torch.zeros(kv, dtype=torch.float32, device=self.device)
+        self.pos = 0
+
+    # ---- building blocks (HF Qwen3 semantics, fp32) -------------------------
+    def _rms(self, x: torch.Tensor) -> torch.Tensor:
+        var = x.pow(2).mean(-1, keepdim=True)
+        return x * torch.rsqrt(var + self.cfg.eps)
+
+    def _rope(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        # x [T, heads, hd]
+        cos = self.cos[pos][:, None, :]
+        sin = self.sin[pos][:, None, :]
+        h = x.shape[-1] // 2
+        rot = torch.cat([-x[..., h:], x[..., :h]], dim=-1)
+        return x * cos + rot * sin
+
+    def _attend(self, i: int, q: torch.Tensor, L: int, pos: torch.Tensor) -> torch.Tensor:
+        """Causal GQA over cache positions [0, L): q [T, n_q, hd] -> [T, n_q*hd].
+        Query head h reads kv head h // (n_q / n_kv), as HF's repeat_kv; the
+        grouping is a reshape, so no kv copy is made."""
+        c = self.cfg
+        T = q.shape[0]
+        rep = c.n_q // c.n_kv
+        kk = self.cache[i, 0, :, :L]                                    # [n_kv, L, hd]
+        vv = self.cache[i, 1, :, :L]
+        qg = q.reshape(T, c.n_kv, rep, c.head_dim).permute(1, 0, 2, 3).reshape(c.n_kv, T * rep,
+                                                                            c.head_dim)
+        scores = torch.matmul(qg, kk.transpose(1, 2).contiguous()) * (c.head_dim ** -0.5)
+        # query row r of group g is token r // rep
+        tpos = pos.repeat_interleave(rep)                               # [T * rep]
+        causal = torch.arange(L, device=self.device)[None, :] > tpos[:, None]
+        scores = scores.masked_fill(causal[None], float("-inf"))
+        probs = torch.softmax(scores, dim=-1)
+        att = torch.matmul(probs, vv)                                   # [n_kv, T*rep, hd]
+        return att.reshape(c.n_kv, T, rep, c.head_dim).permute(1, 0, 2, 3).reshape(
+            T, c.n_q * c.head_dim)
+
+    def _layer(self, i: int, h: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        c = self.cfg
+        T = h.shape[0]
+        p = f"model.layers.{i}."
+        x = self._rms(h)
+        q = self.linears[p + "self_attn.q_proj"](x).view(T, c.n_q, c.head_dim)
+        k = self.linears[p + "self_attn.k_proj"](x).view(T, c.n_kv, c.head_dim)
+        v = self.linears[p + "self_attn.v_proj"](x).view(T, c.n_kv, c.head_dim)
+        q = self._rope(self._rms(q), pos)
+        k = self._rope(self._rms(k), pos)
+        s0 = int(pos[0])
+        self.cache[i, 0, :, s0:s0 + T] = k.transpose(0, 1)
+        self.cache[i, 1, :, s0:s0 + T] = v.transpose(0, 1)
+        L = s0 + T
+        att = self._attend(i, q, L, pos)
+        h = h + self.linears[p + "self_attn.o_proj"](att)
+        x = self._rms(h)
+        g = self.linears[p + "mlp.gate_proj"](x)
+        u = self.linears[p + "mlp.up_proj"](x)
+        return h + self.linears[p + "mlp.down_proj"](torch.nn.functional.silu(g) * u)
+
+    # ---- captured decode step (static shapes) -------------------------------
+    def _graph_step(self, ids_buf: torch.Tensor, pos_buf: torch.Tensor, toks: torch.Tensor,
+                    first_pos: int):
+        """One token at device position pos_buf[0]; attention spans the whole
+        cache with positions > pos masked, so shapes never change.  Writes the
+        argmax into ids_buf (next input) and toks[pos - first_pos], and
+        advances pos_buf."""
+        c = self.cfg
+        pos = pos_buf
+        h = self.embed(ids_buf).reshape(1, c.hidden).to(torch.float32)
+        for i in range(c.layers):
+            p = f"model.layers.{i}."
+            x = self._rms(h)
+            q = self.linears[p + "self_attn.q_proj"](x).view(1, c.n_q, c.head_dim)
+            k = self.linears[p + "self_attn.k_proj"](x).view(1, c.n_kv, c.head_dim)
+            v = self.linears[p + "self_attn.v_proj"](x).view(1, c.n_kv, c.head_dim)
+            q = self._rope(self._rms(q), pos)
+            k = self._rope(self._rms(k), pos)
+            self.cache[i, 0].index_copy_(1, pos, k.transpose(0, 1))
+            self.cache[i, 1].index_copy_(1, pos, v.transpose(0, 1))
+            att = self._attend(i, q, self.max_len, pos)
+            h = h + self.linears[p + "self_attn.o_proj"](att)
+            x = self._rms(h)
+            g = self.linears[p + "mlp.gate_proj"](x)
+            u = self.linears[p + "mlp.up_proj"](x)
+            h = h + self.linears[p + "mlp.down_proj"](torch.nn.functional.silu(g) * u)
+        logits = self.linears["lm_head"](self._rms(h)).reshape(-1)
+        tok = torch.argmax(logits).reshape(1)
+        ids_buf.copy_(tok)
+        toks.index_copy_(0, pos - first_pos, tok)
+        pos_buf.add_(1)
+
+    @torch.no_grad()
+    def generate_graph(self, prompt: List[int], n_new: int, timing: Optional[dict] = None):
+        """generate() with the decode steps captured once as a HIP graph and
+        replayed (no host round trip per token).  timing, if given, receives
+        decode_s (wall time of the n_new - 1 replayed steps, synchronised)."""
+        self.reset()
+        logits = self.forward(torch.tensor(prompt, dtype=torch.int64))
+        plen = len(prompt)
+        ids_buf = torch.argmax(logits).reshape(1).to(torch.int64)
+        toks = torch.zeros(n_new, dtype=torch.int64, device=self.device)
+        toks[0] = ids_buf[0]
+        pos_buf = torch.tensor([plen], dtype=torch.int64, device=self.device)
+        first = plen - 1                      # toks[k] holds the token sampled at pos plen-1+k
+        if n_new > 1:
+            snap = (self.cache.clone(), ids_buf.clone(), pos_buf.clone())
+            s = torch.cuda.Stream(self.device)
+            s.wait_stream(torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(s):
+                self._graph_step(ids_buf, pos_buf, toks, first)   # warm-up (eager, then undone)
+            torch.cuda.current_stream(self.device).wait_stream(s)
+            self.cache.copy_(snap[0]); ids_buf.copy_(snap[1]); pos_buf.copy_(snap[2])
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._graph_step(ids_buf, pos_buf, toks, first)
+            torch.cuda.synchronize(self.device)
+            import time
+            t0 = time.perf_counter()
+            for _ in range(n_new - 1):
+                graph.replay()
+            torch.cuda.synchronize(self.device)
+            if timing is not None:
+                timing["decode_s"] = time.perf_counter() - t0
+                timing["decode_steps"] = n_new - 1
+        self.pos = plen + n_new - 1
+        return [int(t) for t in toks.cpu()]
+
+    # ---- public API ----------------------------------------------------------
+    def reset(self):
+        self.pos = 0
+
+    @torch.no_grad()
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        """Run ids [T] at the next positions; return the last position's
+        logits [vocab] (fp32)."""
+        T = int(ids.numel())
+        if self.pos + T > self.max_len:
+            raise ValueError(f"sequence of {self.pos + T} exceeds max_len {self.max_len}")
+        pos = torch.arange(self.pos, self.pos + T, device=self.device)
+        h = self.embed(ids.to(self.device)).reshape(T, self.cfg.hidden).to(torch.float32)
+        for i in range(self.cfg.layers):
+            h = self._layer(i, h, pos)
+        self.pos += T
+        x = self._rms(h[-1:])
+        return self.linears["lm_head"](x).reshape(-1)
+
+    @torch.no_grad()
+    def generate(self, prompt: List[int], n_new: int, return_logits: bool = False):
+        """Greedy: prompt prefill, then n_new tokens (EOS ignored)."""
+        self.reset()
+        logits = self.forward(torch.tensor(prompt, dtype=torch.int64))
+        out, first = [], logits.clone() if return_logits else None
+        for _ in range(n_new):
+            tok = int(torch.argmax(logits))
+            out.append(tok)
+            if len(out) == n_new:
+                break
+            logits = self.forward(torch.tensor([tok], dtype=torch.int64))
+        return (out, first) if return_logits else out
+
+
+# ---- builders ------------------------------------------------------------------
+
+def from_compressed(cfg: DecoderConfig, comp: Dict[str, dict], device="cuda",
+                    max_len: int = 512) -> Qwen3Decoder:
+    """Decoder over reference-format data dicts (as produced by the
+    compressor; see synthetic.compress_model_cpu).  Fixed-width tensors use
+    GPUAcceleratedLinear/Embedding, Huffman ones HuffmanCodebookLinear/
+    Embedding, exactly as AdaptiveCodebookLinear.from_compressed would."""
+    from gpu_accelerated_functions import GPUAcceleratedEmbedding, GPUAcceleratedLinear
+    from gpu_huffman_functions import HuffmanCodebookEmbedding, HuffmanCodebookLinear
+    dev = torch.device(device)
+
+    def make(name, d, emb=False):
+        cb = torch.from_numpy(np.asarray(d["codebook"], np.float32)).to(dev)
+        shape, bits = tuple(d["shape"]), int(d["bits"])
+        if d.get("encoding") == "huffman":
+            cls = HuffmanCodebookEmbedding if emb else HuffmanCodebookLinear
+            kw = {k: d[k] for k in ("huff_row_bit_starts", "huff_chunk_offsets", "huff_sub_lens")
+                  if k in d}
+            return cls(name, d["huff_stream"], d["huff_lengths"], int(np.asarray(d["huff_n"])[0]),
+                       cb, shape, bits, **kw)
+        cls = GPUAcceleratedEmbedding if emb else GPUAcceleratedLinear
+        return cls(name, d["indices"], cb, shape, bits)
+
+    linears = {n: make(n, comp[n]) for n, _, _ in cfg.linear_shapes()}
+    embed = make("model.embed_tokens", comp["model.embed_tokens"], emb=True)
+    return Qwen3Decoder(cfg, linears, embed, dev, max_len)
+
+
+def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda",
+                   max_len: int = 512) -> Qwen3Decoder:
+    """Decoder over device-resident synthetic tensors (synthetic.FixedTensor /
+    HuffTensor, built on the GPU for the 9B-shape bench); calls the C ABI
+    directly on torch's current stream."""
+    import ctypes
+    import cbq_native as nat
+    import synthetic
+    lib = nat.load()
+    dev = torch.device(device)
+
+    def fixed_linear(t):
+        M, K = t.shape
+
+        def f(x):
+            x = x.reshape(-1, K).contiguous()
+            T = x.shape[0]
+            out = torch.empty(T, M, device=dev)
+            nat.check(lib.ck_linear_f32(x.data_ptr(), t.packed.data_ptr(), t.codebook.data_ptr(),
+                                        out.data_ptr(), T, M, K, t.codebook.numel(), t.bits,
+                                        nat.stream_ptr(dev)), "ck_linear_f32")
+            return out
+        return f
+
+    def huff_desc(t):
+        tb = t.tables
+        return nat.HuffStream(words=t.words.data_ptr(), n_words=t.words.numel(),
+                              chunk_off=t.chunk_off.data_ptr(), sub_len=t.sub_len.data_ptr(),
+                              lut1=tb["lut1"].data_ptr(), lut2=tb["lut2"].data_ptr(),
+                              n_lut2=tb["lut2"].numel(), canon=tb["canon"].data_ptr(),
+                              canon_pay=tb["pay"].data_ptr(), value_cb=None,
+                              C=tb["codebook"].numel(), stage_words=tb["stage_words"])
+
+    def huff_linear(t):
+        M, K = t.shape
+        desc = huff_desc(t)
+
+        def f(x, desc=desc):
+            x = x.reshape(-1, K).contiguous()
+            T = x.shape[0]
+            out = torch.empty(T, M, device=dev)
+            for t0 in range(0, T, 16):
+                tt = min(16, T - t0)
+                nat.check(lib.cbq_huff_linear_f32(x.data_ptr() + t0 * K * 4, ctypes.byref(desc),
+                                                  out.data_ptr() + t0 * M * 4, tt, M, K,
+                                                  nat.stream_ptr(dev)), "cbq_huff_linear_f32")
+            return out
+        f.desc = desc
+        return f
+
+    def embed_fn(t):
+        V, H = t.shape
+        if isinstance(t, synthetic.HuffTensor):
+            desc = huff_desc(t)
+
+            def e(ids, desc=desc):
+                ids = ids.reshape(-1).to(torch.int32)
+                out = torch.empty(ids.numel(), H, device=dev)
+                nat.check(lib.cbq_huff_embedding_f32(ids.data_ptr(), ctypes.byref(desc),
+                                                     out.data_ptr(), ids.numel(), V, H,
+                                                     nat.stream_ptr(dev)), "cbq_huff_embedding_f32")
+                return out
+            return e
+
+        def e2(ids):
+            ids = ids.reshape(-1).to(torch.int32)
+            out = torch.empty(ids.numel(), H, device=dev)
+            nat.check(lib.cbq_embedding_f32(ids.data_ptr(), t.packed.data_ptr(),
+                                            t.codebook.data_ptr(), out.data_ptr(), ids.numel(),
+                                            V, H, t.codebook.numel(), t.bits, nat.stream_ptr(dev)),
+                      "cbq_embedding_f32")
+            return out
+        return e2
+
+    linears = {}
+    for n, _, _ in cfg.linear_shapes():
+        t = tensors[n]
+        linears[n] = huff_linear(t) if isinstance(t, synthetic.HuffTensor) else fixed_linear(t)
+    return Qwen3Decoder(cfg, linears, embed_fn(tensors["model.embed_tokens"]), dev, max_len)

@@ -182,3 +182,41 @@ class SyntheticDecoder:
                             codebook=cb)
             out[name] = t
         return out
+
+
+# ---- CPU (numpy) builder for small models: tests and golden fixtures --------
+
+def make_bf16_cpu(shape, name: str, std: float = 0.02, base_seed: int = 0) -> np.ndarray:
+    """N(0, std) rounded to bf16 (nearest even), from PCG64 seeded per tensor."""
+    rng = np.random.default_rng(tensor_seed(name, base_seed))
+    return cbb.bf16_round(rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
+
+
+def compress_model_cpu(cfg, base_seed: int = 0, encoding: str = "fixed",
+                       huffman_max_len: int = hc.DEFAULT_MAX_LEN) -> Dict[str, dict]:
+    """Every linear, the lm_head and the embedding of a decoder.DecoderConfig,
+    compressed on the CPU as reference-format data dicts (shared
+    per-category frequency-sorted codebooks, src/adaptive_compressor.py:870-969).
+    Dense weights come back under "_dense" (bf16 values as float32) for the
+    golden-fixture generator."""
+    names = [(n, M, K) for n, M, K in cfg.linear_shapes()]
+    names.append(("model.embed_tokens", cfg.vocab, cfg.hidden))
+    dense = {n: make_bf16_cpu((M, K), n, base_seed=base_seed) for n, M, K in names}
+    cats: Dict[str, list] = {}
+    for n, _, _ in names:
+        cats.setdefault(cbb.classify_tensor(n), []).append(n)
+    books = {c: cbb.shared_codebook(dense[n] for n in ns) for c, ns in cats.items()}
+    out: Dict[str, dict] = {}
+    for n, M, K in names:
+        cb, lut = books[cbb.classify_tensor(n)]
+        if encoding == "huffman":
+            idx = lut[cbb.bf16_patterns(dense[n]).reshape(-1)]
+            enc = hc.huffman_encode_indices(idx, shape=(M, K), max_len=huffman_max_len)
+            d = {"mode": "direct_codebook", "encoding": "huffman", "shape": (M, K),
+                 "bits": cbb.bits_for(len(cb)), "codebook": cb}
+            d.update(enc)
+        else:
+            d = cbb.compress_fixed(dense[n], codebook=cb, lut=lut)
+        d["_dense"] = dense[n]
+        out[n] = d
+    return out

@@ -1,0 +1,133 @@
+"""CPU oracle of the always-compressed greedy decoder (TEST INFRASTRUCTURE ONLY).
+
+The same Qwen3-style math as codebook-quantization_amd/decoder.py, written
+in numpy float32, with every compressed GEMV and embedding row computed by
+this directory's C restatement of the reference kernels
+(src/compressed_matmul.c: compressed_matmul_f32_chunk, huffman_matmul_f32_chunk,
+huffman_embedding_f32_rows).  Only tests/ and the bench's CPU leg may use it.
+
+The glue follows HF Qwen3 modelling, which the reference's compressed modules
+plug into (src/model_loader.py:213-277): RMSNorm, q/k head norm, default
+rotary embedding, grouped-query causal attention with an fp32 softmax, and a
+SiLU-gated MLP.  Norm weights are ones (random init).
+tests/golden/gen_e2e_golden.py pins this oracle against transformers'
+Qwen3ForCausalLM itself.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import cbq_oracle as O
+
+
+def rope_tables(head_dim: int, theta: float, max_len: int):
+    """cos, sin [max_len, head_dim] float32, as HF's default rotary embedding
+    computes them (fp32 inverse frequencies and angles; torch cos/sin)."""
+    import torch
+    inv = 1.0 / (torch.tensor(theta, dtype=torch.float32) **
+                 (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
+    pos = torch.arange(max_len, dtype=torch.float32)
+    freqs = pos[:, None] * inv[None, :]
+    emb = torch.cat([freqs, freqs], dim=-1)
+    return emb.cos().numpy(), emb.sin().numpy()
+
+
+class CpuQwen3:
+    def __init__(self, cfg, comp: dict, max_len: int = 256, threads=None):
+        self.cfg = cfg
+        self.comp = comp
+        self.threads = threads
+        self.cos, self.sin = rope_tables(cfg.head_dim, cfg.rope_theta, max_len)
+        self.max_len = max_len
+        self.reset()
+
+    def reset(self):
+        c = self.cfg
+        self.cache = np.zeros((c.layers, 2, c.n_kv, self.max_len, c.head_dim), np.float32)
+        self.pos = 0
+
+    def linear(self, name: str, x: np.ndarray) -> np.ndarray:
+        d = self.comp[name]
+        M, K = d["shape"]
+        cb = np.asarray(d["codebook"], np.float32)
+        x = np.ascontiguousarray(x, np.float32)
+        if d.get("encoding") == "huffman":
+            return O.huff_gemv(x, d, cb, M, K, chunk_rows=None, threads=self.threads)
+        return O.fixed_gemv(x, d["indices"], cb, M, K, int(d["bits"]), chunk_rows=None,
+                            threads=self.threads)
+
+    def embed(self, ids: np.ndarray) -> np.ndarray:
+        d = self.comp["model.embed_tokens"]
+        V, H = d["shape"]
+        cb = np.asarray(d["codebook"], np.float32)
+        ids = np.clip(np.asarray(ids, np.int32), 0, V - 1)
+        if d.get("encoding") == "huffman":
+            return O.huff_embedding(ids, d, cb, H)
+        return O.fixed_embedding(ids, d["indices"], cb, H, int(d["bits"]))
+
+    def _rms(self, x):
+        var = np.mean(x * x, axis=-1, keepdims=True, dtype=np.float32)
+        return (x / np.sqrt(var + np.float32(self.cfg.eps))).astype(np.float32)
+
+    def _rope(self, x, pos):
+        cos = self.cos[pos][:, None, :]
+        sin = self.sin[pos][:, None, :]
+        h = x.shape[-1] // 2
+        rot = np.concatenate([-x[..., h:], x[..., :h]], axis=-1)
+        return (x * cos + rot * sin).astype(np.float32)
+
+    def _layer(self, i, h, pos):
+        c = self.cfg
+        T = h.shape[0]
+        p = f"model.layers.{i}."
+        x = self._rms(h)
+        q = self.linear(p + "self_attn.q_proj", x).reshape(T, c.n_q, c.head_dim)
+        k = self.linear(p + "self_attn.k_proj", x).reshape(T, c.n_kv, c.head_dim)
+        v = self.linear(p + "self_attn.v_proj", x).reshape(T, c.n_kv, c.head_dim)
+        q = self._rope(self._rms(q), pos)
+        k = self._rope(self._rms(k), pos)
+        s0 = int(pos[0])
+        self.cache[i, 0, :, s0:s0 + T] = k.transpose(1, 0, 2)
+        self.cache[i, 1, :, s0:s0 + T] = v.transpose(1, 0, 2)
+        L = s0 + T
+        rep = c.n_q // c.n_kv
+        kk = np.repeat(self.cache[i, 0, :, :L], rep, axis=0)             # [n_q, L, hd]
+        vv = np.repeat(self.cache[i, 1, :, :L], rep, axis=0)
+        qq = q.transpose(1, 0, 2)                                        # [n_q, T, hd]
+        scores = (qq @ kk.transpose(0, 2, 1)) * np.float32(c.head_dim ** -0.5)
+        if T > 1:
+            causal = np.arange(L)[None, :] > pos[:, None]
+            scores = np.where(causal[None], np.float32(-np.inf), scores)
+        scores = scores - scores.max(-1, keepdims=True)
+        e = np.exp(scores).astype(np.float32)
+        probs = e / e.sum(-1, keepdims=True)
+        att = (probs @ vv).transpose(1, 0, 2).reshape(T, c.n_q * c.head_dim).astype(np.float32)
+        h = h + self.linear(p + "self_attn.o_proj", att)
+        x = self._rms(h)
+        g = self.linear(p + "mlp.gate_proj", x)
+        u = self.linear(p + "mlp.up_proj", x)
+        silu = (g / (np.float32(1) + np.exp(-g))).astype(np.float32)
+        return (h + self.linear(p + "mlp.down_proj", silu * u)).astype(np.float32)
+
+    def forward(self, ids) -> np.ndarray:
+        ids = np.asarray(ids, np.int64).reshape(-1)
+        T = ids.size
+        pos = np.arange(self.pos, self.pos + T)
+        h = self.embed(ids).reshape(T, self.cfg.hidden).astype(np.float32)
+        for i in range(self.cfg.layers):
+            h = self._layer(i, h, pos)
+        self.pos += T
+        return self.linear("lm_head", self._rms(h[-1:])).reshape(-1)
+
+    def generate(self, prompt, n_new: int, return_logits: bool = False):
+        self.reset()
+        logits = self.forward(prompt)
+        first = logits.copy()
+        out = []
+        for _ in range(n_new):
+            tok = int(np.argmax(logits))
+            out.append(tok)
+            if len(out) == n_new:
+                break
+            logits = self.forward([tok])
+        return (out, first) if return_logits else out
