@@ -354,7 +354,7 @@ def main():
                          "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(hb_gu / (us_hgu * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
                          "traffic": read_traffic("huff_gemv_gate_up_qwen3-8b_pmc.md"),
-                         "kernel": "huff_tile_kernel<2,value,lut2-lds> gate/up 4096->12288",
+                         "kernel": "huff_tile_fast_kernel<16,1> gate/up 4096->12288",
                          "bytes_per_launch": hb_gu, "us_per_launch": round(us_hgu, 2)}}
         log(f"huffman sweep: {ms_h:.3f} ms/step, {hbytes / 1e9:.2f} GB/step")
 

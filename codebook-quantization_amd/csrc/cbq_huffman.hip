@@ -608,6 +608,188 @@ __global__ __launch_bounds__(kTBlock) void huff_tile_kernel(
     }
 }
 
+// Fast variant for bf16-value payloads with lut2 <= 8192 entries.  One static
+// LDS array at fixed offsets (lut1 at 0, so a code's lut1 byte offset is the
+// LDS address; lut2 and the x tile within the 16-bit DS offset range), an
+// XOR-swizzled x tile (no padding), and a 13-bit lut2 base field, so that the
+// per-symbol step needs no clamp and no base adds.  A block whose lut2 holds
+// unresolved (> 24-bit) entries decodes every chunk on the general path.
+constexpr int kFastSlot = 1536;                               // words per chain slot
+constexpr int kFastLut2 = 8192;                               // lut2 entries in LDS
+constexpr int kFastChains = 16;                               // chains per block
+constexpr int kFOffLut1 = kFastLut2;                          // word offsets into s_lds
+constexpr int kFOffX = kFOffLut1 + kLutSize;
+constexpr int kFOffSlots = kFOffX + kChunk;
+constexpr int kFastLdsWords = kFOffSlots + kFastChains * kFastSlot;
+static_assert(kFastLdsWords * 4 == 160 * 1024, "fast Huffman kernel fills the 160 KB LDS");
+
+template <int NW, int NCH>
+__global__ __launch_bounds__(NW * CBQ_WAVE) void huff_tile_fast_kernel(
+    const float *__restrict__ x, float *__restrict__ out, HuffArgs a, int M, int K,
+    int slot_cap)
+{
+    static_assert(NW * NCH == kFastChains, "one slot per chain");
+    __shared__ __attribute__((aligned(16))) uint32_t s_lds[kFastLdsWords];
+    uint32_t *const s_lut2 = s_lds;
+    uint32_t *const s_lut1 = s_lds + kFOffLut1;
+    float *const s_x = (float *)(s_lds + kFOffX);
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CBQ_WAVE);
+    uint32_t *const s_slot = s_lds + kFOffSlots + wave * (NCH * kFastSlot);
+    int slot_addr[NCH];                                           // LDS byte addresses, in SGPRs
+#pragma unroll
+    for (int j = 0; j < NCH; j++)
+        slot_addr[j] = __builtin_amdgcn_readfirstlane(4 * (kFOffSlots + (wave * NCH + j) * kFastSlot));
+
+    for (int i = wave; i < (kLutSize >> 6); i += NW)
+        dma_dword(a.lut1 + (i << 6) + lane, s_lut1 + (i << 6));
+    const int n2 = (a.n_lut2 + 63) & ~63;
+    for (int i = wave; i < (n2 >> 6); i += NW) {
+        const int e = (i << 6) + lane;
+        dma_dword(a.lut2 + (e < a.n_lut2 ? e : a.n_lut2 - 1), s_lut2 + (i << 6));
+    }
+    __syncthreads();
+    // 0 entries mark codes beyond 24 bits (resolved from the canon tables).
+    int unresolved = 0;
+    for (int i = threadIdx.x; i < a.n_lut2; i += NW * CBQ_WAVE) unresolved |= s_lut2[i] == 0u;
+    {   // block-wide OR through the (not yet used) x tile
+        const bool wany = __ballot(unresolved) != 0;
+        if (lane == 0) ((uint32_t *)s_x)[wave] = wany ? 1u : 0u;
+    }
+    __syncthreads();
+    uint32_t any_unresolved = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) any_unresolved |= ((const uint32_t *)s_x)[w];
+    const bool general = any_unresolved != 0;
+
+    const int R = K / kChunk;
+    const int W = gridDim.x * NW;
+    const int wid = blockIdx.x * NW + wave;
+    const int rows = wid < M ? (M - wid + W - 1) / W : 0;
+    const int b0 = blockIdx.x * NW;
+    const int rows_max = b0 < M ? (M - b0 + W - 1) / W : 0;
+    const int n_seg = (rows_max + 63) >> 6;
+    // lane's x run: element i at column i ^ xsw (16 lanes cover all banks)
+    const float *const xr = s_x + lane * 64;
+    const int xsw = (lane & 15) << 2;
+
+    for (int seg = 0; seg < n_seg; seg++) {
+        float res = 0.f;
+        const int seg_rows = min(64, rows - seg * 64);
+        for (int p = 0; p < R; p++) {
+            __syncthreads();
+            for (int r = wave; r < 64; r += NW)
+                dma_dword(x + (size_t)p * kChunk + (r << 6) + (lane ^ ((r & 15) << 2)),
+                          s_x + (r << 6));
+            __syncthreads();
+            for (int b = 0; b < seg_rows; b += NCH) {
+                uint64_t q0[NCH];
+                bool big = general;
+                uint32_t sl[NCH];
+                int64_t wbase[NCH];
+#pragma unroll
+                for (int j = 0; j < NCH; j++) {
+                    const int ri = seg * 64 + b + j;
+                    const int64_t row = ri < rows ? wid + (int64_t)ri * W : wid;
+                    const int64_t c = __builtin_amdgcn_readfirstlane((int)(row * R + p));
+                    sl[j] = a.sub_len[c * kSub + lane];
+                    const uint64_t off0 = a.chunk_off[c], off1 = a.chunk_off[c + 1];
+                    const int64_t wb = (int64_t)(off0 >> 5) & ~(int64_t)3;
+                    const int64_t need =
+                        ((int64_t)((off1 + 31) >> 5) + 2 - wb + 255) & ~(int64_t)255;
+                    wbase[j] = wb;
+                    q0[j] = off0 - ((uint64_t)wb << 5);
+                    big |= need > slot_cap;
+                    if (need <= slot_cap && !general) {
+                        for (int i = 0; i < need; i += 4 * CBQ_WAVE) {
+                            int64_t src = wb + i + 4 * lane;
+                            src = src < a.n_words - 4 ? src : a.n_words - 4;
+                            dma_dwordx4(a.words + src, s_slot + j * kFastSlot + i);
+                        }
+                    }
+                }
+                __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));   // vmcnt(0)
+                uint32_t q[NCH];
+                float acc[NCH];
+#pragma unroll
+                for (int j = 0; j < NCH; j++) {
+                    const uint32_t incl = wave_incl_scan(sl[j]);
+                    q[j] = (uint32_t)q0[j] + (incl - sl[j]) - 2u;
+                    acc[j] = 0.f;
+                }
+                if (!big) {
+                    for (int i = 0; i < kSub; i += 4) {
+                        typedef float f4 __attribute__((ext_vector_type(4)));
+                        const f4 xv4 = *(const f4 *)(xr + (i ^ xsw));
+                        const float xv[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            uint32_t lo[NCH], hi[NCH], win2[NCH], e[NCH];
+#pragma unroll
+                            for (int j = 0; j < NCH; j++) {
+                                const int d = (int)q[j] >> 5;
+                                const uint32_t *w = (const uint32_t *)((const char *)s_lds + slot_addr[j]) + d;
+                                lo[j] = w[0];
+                                hi[j] = w[1];
+                            }
+#pragma unroll
+                            for (int j = 0; j < NCH; j++) {
+                                win2[j] = funnel(hi[j], lo[j], q[j]);
+                                // the masked window is the byte offset of the lut1 entry
+                                e[j] = *(const uint32_t *)((const char *)s_lut1 + (win2[j] & 0x3ffcu));
+                            }
+                            uint32_t nb[NCH], e2[NCH];
+#pragma unroll
+                            for (int j = 0; j < NCH; j++) {
+                                // Pointer: lut2 entry base + ext.  lut2 sits at LDS address 0 and
+                                // a 13-bit base plus a 15-bit ext stays below 160 KB whatever
+                                // the entry holds.  Leaves (nb = 0) all read entry 0 (one
+                                // broadcast), which the select drops.
+                                nb[j] = __builtin_amdgcn_ubfe(e[j], 6, 4);
+                                const uint32_t base = nb[j] ? __builtin_amdgcn_ubfe(e[j], 11, 13) : 0u;
+                                const uint32_t i2 = base + __builtin_amdgcn_ubfe(win2[j], kLutBits + 2, nb[j]);
+                                e2[j] = s_lut2[i2];
+                            }
+#pragma unroll
+                            for (int j = 0; j < NCH; j++) {
+                                asm volatile("" : "+v"(e2[j]));   // read unconditionally: no branch
+                                e[j] = nb[j] ? e2[j] : e[j];
+                            }
+#pragma unroll
+                            for (int j = 0; j < NCH; j++) {
+                                q[j] += e[j] & 0xffu;            // bits 6-7 of a leaf are 0
+                                acc[j] = fmaf(xv[u], __uint_as_float(e[j] & 0xffff0000u), acc[j]);
+                            }
+                        }
+                    }
+                } else {
+                    for (int i = 0; i < kSub; i++) {
+                        const float xv = xr[i ^ xsw];
+#pragma unroll
+                        for (int j = 0; j < NCH; j++) {
+                            const uint32_t q2 = q[j] + 2u;
+                            const uint32_t win = window_global(a.words, a.n_words, wbase[j], q2);
+                            uint32_t e = s_lut1[win & (kLutSize - 1)];
+                            if ((e & 63u) == 0u)
+                                e = decode_long<true>(e, win << 2, win, s_lut2, (uint32_t)a.n_lut2,
+                                                      a.canon, a.canon_pay);
+                            q[j] += e & 63u;
+                            acc[j] = fmaf(xv, __uint_as_float(e & 0xffff0000u), acc[j]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < NCH; j++) {
+                    const float s = wave_sum(acc[j]);
+                    if (b + j < seg_rows && lane == b + j) res += s;
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
+        if (lane < seg_rows) out[wid + (int64_t)(seg * 64 + lane) * W] = res;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Embedding: one wave per requested row (H % 64 == 0)
 // ---------------------------------------------------------------------------
@@ -903,6 +1085,15 @@ int launch_tile_n(const float *x, float *out, const HuffArgs &a, int M, int K, i
 int launch_tile(const float *x, float *out, const HuffArgs &a, int M, int K, int n_cb,
                 int slot_cap, hipStream_t st)
 {
+    if (a.value_cb == nullptr && a.n_lut2 <= kFastLut2 && a.n_words >= 4) {
+        const int cap = std::min(kFastSlot, (slot_cap + 4 + 255) & ~255) & ~255;
+        // 16 waves x 1 chain measured 45 us for 4096 -> 12288 on MI355X (8 x 2: 52 us);
+        // the step is bound by LDS bank conflicts of the window and lut1 reads.
+        const int blocks = std::max(1, std::min(cbq_num_cus(), (M + 15) / 16));
+        hipLaunchKernelGGL((huff_tile_fast_kernel<16, 1>), dim3(blocks), dim3(16 * CBQ_WAVE), 0, st,
+                           x, out, a, M, K, cap);
+        return cbq_launch_status("huff_tile_fast_kernel");
+    }
     // 8 waves x 2 chains: LDS holds lut1 + lut2 + x tile + 16 word slots.
     // Measured on MI355X, 4096 -> 12288: 56 us; 8x1 74 us, 4x4 76 us, 6x3
     // (lut2 pushed out of LDS) 126 us.
