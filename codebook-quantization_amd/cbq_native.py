@@ -1,4 +1,5 @@
-"""ctypes binding of libcbq_hip.so, the gfx950 C ABI (include/cbq_hip.h).
+"""ctypes binding of libcbq_hip.so, the gfx950 C ABI (include/cbq_hip.h,
+include/cbq_decode.h).
 
 The library is loaded after torch so that it binds to the HIP runtime torch
 already loaded (same SONAME), which makes torch's device pointers and
@@ -35,7 +36,7 @@ class HuffStream(ctypes.Structure):
     ]
 
 
-# name -> (restype, argtypes); every symbol declared in include/cbq_hip.h
+# name -> (restype, argtypes); every symbol declared in include/*.h
 SIGNATURES = {
     "ck_error_string": (ctypes.c_char_p, [_i]),
     "cbq_version": (ctypes.c_char_p, []),
@@ -51,6 +52,11 @@ SIGNATURES = {
     "cbq_huff_linear_f32": (_i, [_vp, ctypes.POINTER(HuffStream), _vp, _i, _i, _i, _vp]),
     "cbq_huff_embedding_f32": (_i, [_vp, ctypes.POINTER(HuffStream), _vp, _i, _i, _i, _vp]),
     "cbq_huff_decode_indices": (_i, [ctypes.POINTER(HuffStream), _vp, _i64, _vp]),
+    # include/cbq_decode.h
+    "cbq_add_rmsnorm_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, ctypes.c_float, _vp]),
+    "cbq_head_norm_rope_f32": (_i, [_vp] * 11 + [_i] * 5 + [ctypes.c_float, _vp]),
+    "cbq_attn_decode_f32": (_i, [_vp] * 5 + [_i] * 4 + [ctypes.c_float, _vp]),
+    "cbq_silu_mul_f32": (_i, [_vp, _vp, _vp, _i64, _vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

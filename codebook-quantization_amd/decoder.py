@@ -3,9 +3,11 @@
 This is the end-to-end caller of the compressed path: every linear of every
 layer, the lm_head and the token embedding stay compressed in HBM, as
 fixed-width indices or canonical Huffman, and run through libcbq_hip.so.
-The glue around them is written in fp32 torch ops and follows the HF Qwen3
-modelling that the reference's compressed modules plug into
-(src/model_loader.py:213-277):
+The glue around them runs as fused fp32 HIP kernels of the same library
+(include/cbq_decode.h: residual add + RMSNorm, head norm + rope + KV-cache
+write, single-token attention, SiLU product); multi-token attention uses
+torch matmuls.  It follows the HF Qwen3 modelling that the reference's
+compressed modules plug into (src/model_loader.py:213-277):
 
 - RMSNorm: x * rsqrt(mean(x^2) + eps) * weight;
 - q/k head RMSNorm;
@@ -75,6 +77,54 @@ def rope_tables(cfg: DecoderConfig, max_len: int):
 Linear = Callable[[torch.Tensor], torch.Tensor]        # [T, K] fp32 -> [T, M] fp32
 
 
+class _Glue:
+    """The fused decoder kernels of libcbq_hip.so (include/cbq_decode.h) on
+    torch's current stream; outputs are fresh tensors (graph-pool memory
+    under capture)."""
+
+    def __init__(self, cfg: DecoderConfig):
+        import cbq_native as nat
+        self.nat = nat
+        self.lib = nat.load()
+        self.cfg = cfg
+
+    def add_rms(self, h: torch.Tensor, delta: Optional[torch.Tensor]) -> torch.Tensor:
+        """h += delta (in place, when given); returns rmsnorm(h)."""
+        T, H = h.shape
+        out = torch.empty_like(h)
+        self.nat.check(self.lib.cbq_add_rmsnorm_f32(
+            h.data_ptr(), None if delta is None else delta.data_ptr(), None, out.data_ptr(),
+            T, H, self.cfg.eps, self.nat.stream_ptr(h.device)), "cbq_add_rmsnorm_f32")
+        return out
+
+    def head_norm_rope(self, q, k, v, cos, sin, pos_dev, k_cache, v_cache) -> torch.Tensor:
+        c = self.cfg
+        T = q.shape[0]
+        q_out = torch.empty(T, c.n_q * c.head_dim, dtype=torch.float32, device=q.device)
+        self.nat.check(self.lib.cbq_head_norm_rope_f32(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None, cos.data_ptr(), sin.data_ptr(),
+            pos_dev.data_ptr(), q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+            T, c.n_q, c.n_kv, c.head_dim, k_cache.shape[1], c.eps,
+            self.nat.stream_ptr(q.device)), "cbq_head_norm_rope_f32")
+        return q_out
+
+    def attend1(self, q, k_cache, v_cache, pos_dev) -> torch.Tensor:
+        c = self.cfg
+        out = torch.empty(1, c.n_q * c.head_dim, dtype=torch.float32, device=q.device)
+        self.nat.check(self.lib.cbq_attn_decode_f32(
+            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), pos_dev.data_ptr(),
+            out.data_ptr(), c.n_q, c.n_kv, c.head_dim, k_cache.shape[1],
+            float(c.head_dim ** -0.5), self.nat.stream_ptr(q.device)), "cbq_attn_decode_f32")
+        return out
+
+    def silu_mul(self, g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
+        out = torch.empty_like(g)
+        self.nat.check(self.lib.cbq_silu_mul_f32(g.data_ptr(), u.data_ptr(), out.data_ptr(),
+                                                 g.numel(), self.nat.stream_ptr(g.device)),
+                       "cbq_silu_mul_f32")
+        return out
+
+
 class Qwen3Decoder:
     """Greedy decoder over compressed linears / embedding (callables)."""
 
@@ -91,20 +141,9 @@ class Qwen3Decoder:
         kv = (cfg.layers, 2, cfg.n_kv, max_len, cfg.head_dim)
         self.cache = torch.zeros(kv, dtype=torch.float32, device=self.device)
         self.pos = 0
+        self.glue = _Glue(cfg)
 
     # ---- building blocks (HF Qwen3 semantics, fp32) -------------------------
-    def _rms(self, x: torch.Tensor) -> torch.Tensor:
-        var = x.pow(2).mean(-1, keepdim=True)
-        return x * torch.rsqrt(var + self.cfg.eps)
-
-    def _rope(self, x: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-        # x [T, heads, hd]
-        cos = self.cos[pos][:, None, :]
-        sin = self.sin[pos][:, None, :]
-        h = x.shape[-1] // 2
-        rot = torch.cat([-x[..., h:], x[..., :h]], dim=-1)
-        return x * cos + rot * sin
-
     def _attend(self, i: int, q: torch.Tensor, L: int, pos: torch.Tensor) -> torch.Tensor:
         """Causal GQA over cache positions [0, L): q [T, n_q, hd] -> [T, n_q*hd].
         Query head h reads kv head h // (n_q / n_kv), as HF's repeat_kv; the
@@ -126,26 +165,28 @@ class Qwen3Decoder:
         return att.reshape(c.n_kv, T, rep, c.head_dim).permute(1, 0, 2, 3).reshape(
             T, c.n_q * c.head_dim)
 
-    def _layer(self, i: int, h: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+    def _layer(self, i: int, h: torch.Tensor, x: torch.Tensor, pos: torch.Tensor,
+               pos_dev: torch.Tensor, L: int) -> torch.Tensor:
+        """One layer over T tokens at positions pos (pos_dev: device int64
+        holding pos[0]; L = pos[-1] + 1, or max_len for the captured step).
+        x = rmsnorm(h) on entry; h is updated in place; returns the next
+        rmsnorm(h)."""
         c = self.cfg
         T = h.shape[0]
         p = f"model.layers.{i}."
-        x = self._rms(h)
-        q = self.linears[p + "self_attn.q_proj"](x).view(T, c.n_q, c.head_dim)
-        k = self.linears[p + "self_attn.k_proj"](x).view(T, c.n_kv, c.head_dim)
-        v = self.linears[p + "self_attn.v_proj"](x).view(T, c.n_kv, c.head_dim)
-        q = self._rope(self._rms(q), pos)
-        k = self._rope(self._rms(k), pos)
-        s0 = int(pos[0])
-        self.cache[i, 0, :, s0:s0 + T] = k.transpose(0, 1)
-        self.cache[i, 1, :, s0:s0 + T] = v.transpose(0, 1)
-        L = s0 + T
-        att = self._attend(i, q, L, pos)
-        h = h + self.linears[p + "self_attn.o_proj"](att)
-        x = self._rms(h)
-        g = self.linears[p + "mlp.gate_proj"](x)
-        u = self.linears[p + "mlp.up_proj"](x)
-        return h + self.linears[p + "mlp.down_proj"](torch.nn.functional.silu(g) * u)
+        g = self.glue
+        q = self.linears[p + "self_attn.q_proj"](x)
+        k = self.linears[p + "self_attn.k_proj"](x)
+        v = self.linears[p + "self_attn.v_proj"](x)
+        q = g.head_norm_rope(q, k, v, self.cos, self.sin, pos_dev, self.cache[i, 0],
+                             self.cache[i, 1])
+        if T == 1:
+            att = g.attend1(q, self.cache[i, 0], self.cache[i, 1], pos_dev)
+        else:
+            att = self._attend(i, q.view(T, c.n_q, c.head_dim), L, pos)
+        x = g.add_rms(h, self.linears[p + "self_attn.o_proj"](att))
+        a = g.silu_mul(self.linears[p + "mlp.gate_proj"](x), self.linears[p + "mlp.up_proj"](x))
+        return g.add_rms(h, self.linears[p + "mlp.down_proj"](a))
 
     # ---- captured decode step (static shapes) -------------------------------
     def _graph_step(self, ids_buf: torch.Tensor, pos_buf: torch.Tensor, toks: torch.Tensor,
@@ -155,28 +196,14 @@ class Qwen3Decoder:
         argmax into ids_buf (next input) and toks[pos - first_pos], and
         advances pos_buf."""
         c = self.cfg
-        pos = pos_buf
         h = self.embed(ids_buf).reshape(1, c.hidden).to(torch.float32)
+        x = self.glue.add_rms(h, None)
         for i in range(c.layers):
-            p = f"model.layers.{i}."
-            x = self._rms(h)
-            q = self.linears[p + "self_attn.q_proj"](x).view(1, c.n_q, c.head_dim)
-            k = self.linears[p + "self_attn.k_proj"](x).view(1, c.n_kv, c.head_dim)
-            v = self.linears[p + "self_attn.v_proj"](x).view(1, c.n_kv, c.head_dim)
-            q = self._rope(self._rms(q), pos)
-            k = self._rope(self._rms(k), pos)
-            self.cache[i, 0].index_copy_(1, pos, k.transpose(0, 1))
-            self.cache[i, 1].index_copy_(1, pos, v.transpose(0, 1))
-            att = self._attend(i, q, self.max_len, pos)
-            h = h + self.linears[p + "self_attn.o_proj"](att)
-            x = self._rms(h)
-            g = self.linears[p + "mlp.gate_proj"](x)
-            u = self.linears[p + "mlp.up_proj"](x)
-            h = h + self.linears[p + "mlp.down_proj"](torch.nn.functional.silu(g) * u)
-        logits = self.linears["lm_head"](self._rms(h)).reshape(-1)
+            x = self._layer(i, h, x, pos_buf, pos_buf, self.max_len)
+        logits = self.linears["lm_head"](x).reshape(-1)
         tok = torch.argmax(logits).reshape(1)
         ids_buf.copy_(tok)
-        toks.index_copy_(0, pos - first_pos, tok)
+        toks.index_copy_(0, pos_buf - first_pos, tok)
         pos_buf.add_(1)
 
     @torch.no_grad()
@@ -227,12 +254,13 @@ class Qwen3Decoder:
         if self.pos + T > self.max_len:
             raise ValueError(f"sequence of {self.pos + T} exceeds max_len {self.max_len}")
         pos = torch.arange(self.pos, self.pos + T, device=self.device)
+        pos_dev = pos[:1].contiguous()
         h = self.embed(ids.to(self.device)).reshape(T, self.cfg.hidden).to(torch.float32)
+        x = self.glue.add_rms(h, None)
         for i in range(self.cfg.layers):
-            h = self._layer(i, h, pos)
+            x = self._layer(i, h, x, pos, pos_dev, self.pos + T)
         self.pos += T
-        x = self._rms(h[-1:])
-        return self.linears["lm_head"](x).reshape(-1)
+        return self.linears["lm_head"](x[-1:]).reshape(-1)
 
     @torch.no_grad()
     def generate(self, prompt: List[int], n_new: int, return_logits: bool = False):

@@ -1,0 +1,62 @@
+/*
+ * cbq_decode.h -- fused fp32 decoder glue of the always-compressed greedy
+ * decode (libcbq_hip.so, csrc/cbq_decode.hip).
+ *
+ * These entry points have no counterpart in the reference's C/HIP libraries:
+ * there the glue between compressed linears is HF Qwen3 modelling in PyTorch
+ * (src/model_loader.py:213-277 swaps the compressed modules into
+ * Qwen3ForCausalLM).  They exist so that one decode step is a short sequence
+ * of launches (a HIP graph of ~12 kernels per layer) instead of several
+ * dozen small PyTorch kernels per layer.  Semantics are HF Qwen3's, in fp32:
+ * RMSNorm x * rsqrt(mean(x^2) + eps) (* weight), per-head q/k RMSNorm, the
+ * default rotary embedding x * cos + rotate_half(x) * sin, grouped-query
+ * attention with an fp32 softmax, and silu(g) * u.
+ *
+ * Conventions as cbq_hip.h: device pointers, asynchronous on `stream`,
+ * no allocation, return 0 / 1 (HIP error) / 2 (invalid argument).
+ */
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* For each of the T rows of h [T, H]: h += delta (when delta is not NULL),
+ * then out = h * rsqrt(mean(h^2) + eps) (* weight[H] when not NULL).
+ * out may not alias h.  H % 4 == 0. */
+int cbq_add_rmsnorm_f32(float *h, const float *delta, const float *weight, float *out,
+                        int T, int H, float eps, hipStream_t stream);
+
+/* Per token t < T at position pos[0] + t (pos: one device int64):
+ *   q_out[t, i]  = rope(rmsnorm(q[t, i]) * q_weight)          i < n_q
+ *   k_cache[j, pos + t] = rope(rmsnorm(k[t, j]) * k_weight)    j < n_kv
+ *   v_cache[j, pos + t] = v[t, j]
+ * q [T, n_q, hd], k and v [T, n_kv, hd]; caches [n_kv, max_len, hd];
+ * cos/sin tables [max_len, hd].  Weights may be NULL (ones).  Tokens whose
+ * position falls outside [0, max_len) are not written to the caches and
+ * use table row 0.  hd even, 2 <= hd <= 256. */
+int cbq_head_norm_rope_f32(const float *q, const float *k, const float *v,
+                           const float *q_weight, const float *k_weight,
+                           const float *cos_table, const float *sin_table,
+                           const int64_t *pos, float *q_out, float *k_cache,
+                           float *v_cache, int T, int n_q, int n_kv, int hd,
+                           int max_len, float eps, hipStream_t stream);
+
+/* Single-token causal attention over cache positions [0, pos[0]] (clamped
+ * to [1, max_len] positions): query head i reads kv head i / (n_q / n_kv).
+ * out[i] = softmax(q[i] . k[j] * scale) . v[j]; q and out [n_q, hd].
+ * hd in {64, 128, 256}; n_q % n_kv == 0; max_len <= 32768. */
+int cbq_attn_decode_f32(const float *q, const float *k_cache, const float *v_cache,
+                        const int64_t *pos, float *out, int n_q, int n_kv, int hd,
+                        int max_len, float scale, hipStream_t stream);
+
+/* out[i] = silu(g[i]) * u[i] = g / (1 + exp(-g)) * u, i < n. */
+int cbq_silu_mul_f32(const float *g, const float *u, float *out, int64_t n,
+                     hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif

@@ -2,7 +2,8 @@
 
 decoder.from_compressed builds the model from reference-format data dicts,
 as AdaptiveCodebookLinear.from_compressed would.  Every linear, the lm_head
-and the embedding run through libcbq_hip.so; the glue is fp32 torch.  Greedy
+and the embedding run through libcbq_hip.so, and so does the fp32 glue
+(include/cbq_decode.h; multi-token attention is torch matmuls).  Greedy
 tokens must equal the golden ones (tests/golden/e2e_golden.npz, from
 transformers' Qwen3ForCausalLM on the same dense weights), for fixed-width
 and Huffman weights alike.

@@ -1,4 +1,4 @@
-"""libcbq_hip.so loads and exports every function include/cbq_hip.h declares;
+"""libcbq_hip.so loads and exports every function include/*.h declares;
 host-only entry points work and argument validation rejects bad calls before
 any GPU work (no kernel is launched here)."""
 import ctypes
@@ -8,14 +8,18 @@ import re
 import numpy as np
 import pytest
 
-HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
-                      "include", "cbq_hip.h")
+INCLUDE = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
 
 
 def _declared():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(\w+)\s*\(", text, flags=re.M)))
+    names = set()
+    for f in sorted(os.listdir(INCLUDE)):
+        if not f.endswith(".h"):
+            continue
+        text = open(os.path.join(INCLUDE, f)).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names |= set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(\w+)\s*\(", text, flags=re.M))
+    return sorted(names)
 
 
 @pytest.fixture(scope="module")
@@ -30,8 +34,9 @@ def lib():
 def test_header_symbols_exported(lib):
     names = _declared()
     assert "ck_linear_f32" in names and "cbq_huff_linear_f32" in names
+    assert "cbq_attn_decode_f32" in names
     for n in names:
-        assert hasattr(lib, n), f"{n} declared in cbq_hip.h but not exported"
+        assert hasattr(lib, n), f"{n} declared in include/ but not exported"
     import cbq_native
     assert set(names) == set(cbq_native.SIGNATURES), "ctypes table out of sync with header"
 
@@ -61,6 +66,15 @@ def test_argument_validation_before_launch(lib):
     assert lib.cbq_huff_linear_f32(p, ctypes.byref(hs), p, 17, 4, 64, None) == 2  # T > 16
     assert lib.cbq_huff_embedding_f32(p, ctypes.byref(hs), p, 1, 4, 60, None) == 2
     assert lib.cbq_huff_decode_indices(ctypes.byref(hs), p, 64, None) == 2
+    # decoder glue (include/cbq_decode.h)
+    assert lib.cbq_add_rmsnorm_f32(p, None, None, p, 1, 64, 1e-6, None) == 2     # out aliases h
+    assert lib.cbq_add_rmsnorm_f32(p, None, None, None, 1, 64, 1e-6, None) == 2
+    assert lib.cbq_head_norm_rope_f32(*([p] * 11), 1, 4, 2, 300, 16, 1e-6, None) == 2   # hd > 256
+    assert lib.cbq_head_norm_rope_f32(*([p] * 11), 1, 4, 2, 7, 16, 1e-6, None) == 2     # odd hd
+    assert lib.cbq_attn_decode_f32(p, p, p, p, p, 6, 4, 128, 16, 1.0, None) == 2        # 6 % 4
+    assert lib.cbq_attn_decode_f32(p, p, p, p, p, 4, 2, 96, 16, 1.0, None) == 2         # hd 96
+    assert lib.cbq_attn_decode_f32(p, p, p, p, p, 4, 2, 128, 40000, 1.0, None) == 2     # > 32768
+    assert lib.cbq_silu_mul_f32(p, p, p, 0, None) == 2
 
 
 def test_build_luts_rejects_overfull(lib):
