@@ -1,6 +1,7 @@
 // Fused fp32 decoder glue for gfx950: residual add + RMSNorm, per-head
 // RMSNorm + rotary embedding + KV-cache write, single-token grouped-query
-// attention, and the SiLU-gated product.  HF Qwen3 semantics (the modelling
+// attention (alone or with the head norm, rope and cache write folded in),
+// the SiLU-gated product and the greedy pick.  HF Qwen3 semantics (the modelling
 // code the reference's compressed modules plug into,
 // src/model_loader.py:213-277); products and sums that PyTorch rounds one at
 // a time are rounded one at a time here too (no contraction into FMAs),
@@ -46,33 +47,44 @@ __device__ __forceinline__ float block_max(float v, float *s_red)
     return t;
 }
 
-// One block per row.
-__global__ __launch_bounds__(kGlueBlock) void add_rmsnorm_kernel(
+// One block per row, the row held in registers (H <= kNormThreads * kNormPer):
+// every load is issued before the reduction, so a row costs one memory
+// round trip rather than one per loop iteration.
+constexpr int kNormThreads = 1024;
+constexpr int kNormPer = 16;
+
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
     float *__restrict__ h, const float *__restrict__ delta, const float *__restrict__ weight,
     float *__restrict__ out, int H, float eps)
 {
-    __shared__ float s_red[kGlueBlock / CBQ_WAVE];
+    __shared__ float s_red[kNormThreads / CBQ_WAVE];
     float *hr = h + (size_t)blockIdx.x * H;
     float *orow = out + (size_t)blockIdx.x * H;
-    float ss = 0.f;
-    if (delta) {
-        const float *dr = delta + (size_t)blockIdx.x * H;
-        for (int i = threadIdx.x; i < H; i += kGlueBlock) {
-            const float v = __fadd_rn(hr[i], dr[i]);
-            hr[i] = v;
-            ss = __fadd_rn(ss, __fmul_rn(v, v));
-        }
-    } else {
-        for (int i = threadIdx.x; i < H; i += kGlueBlock) {
-            const float v = hr[i];
-            ss = __fadd_rn(ss, __fmul_rn(v, v));
+    const float *dr = delta ? delta + (size_t)blockIdx.x * H : nullptr;
+    float v[kNormPer];
+#pragma unroll
+    for (int j = 0; j < kNormPer; j++) {
+        const int i = threadIdx.x + j * kNormThreads;
+        v[j] = i < H ? hr[i] : 0.f;
+    }
+    if (dr) {
+#pragma unroll
+        for (int j = 0; j < kNormPer; j++) {
+            const int i = threadIdx.x + j * kNormThreads;
+            if (i < H) {
+                v[j] = __fadd_rn(v[j], dr[i]);
+                hr[i] = v[j];
+            }
         }
     }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kNormPer; j++) ss = __fadd_rn(ss, __fmul_rn(v[j], v[j]));
     const float r = rsqrtf(block_sum(ss, s_red) / (float)H + eps);
-    for (int i = threadIdx.x; i < H; i += kGlueBlock) {
-        float o = __fmul_rn(hr[i], r);
-        if (weight) o = __fmul_rn(weight[i], o);
-        orow[i] = o;
+#pragma unroll
+    for (int j = 0; j < kNormPer; j++) {
+        const int i = threadIdx.x + j * kNormThreads;
+        if (i < H) orow[i] = weight ? __fmul_rn(weight[i], __fmul_rn(v[j], r)) : __fmul_rn(v[j], r);
     }
 }
 
@@ -187,6 +199,192 @@ __global__ __launch_bounds__(kGlueBlock) void attn_decode_kernel(
     }
 }
 
+// Single-token attention with the q/k head norm + rope and the KV-cache write
+// folded in.  One block per query head: waves 0 and 1 normalise and rotate
+// the query head and its group's new key, wave 2 stages the new value; the
+// group's first block stores key and value at row pos.  Cached rows [0, pos)
+// come from memory, the new row from LDS, so no block waits on another.
+constexpr int kAttnThreads = 512;
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_rope_decode_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ qw, const float *__restrict__ kw, const float *__restrict__ cos_t,
+    const float *__restrict__ sin_t, const int64_t *__restrict__ pos, float *__restrict__ kc,
+    float *__restrict__ vc, float *__restrict__ out, int group, int max_len, float scale,
+    float eps)
+{
+    extern __shared__ float s_att[];                              // [max_len + 1]
+    __shared__ float s_raw[2][HD];
+    __shared__ float s_q[HD], s_k[HD], s_v[HD];
+    __shared__ __attribute__((aligned(16))) float s_part[4 * kAttnThreads];
+    __shared__ float s_red[kAttnThreads / CBQ_WAVE];
+    const int h = blockIdx.x, g = h / group, tid = threadIdx.x;
+    const int wave = tid / CBQ_WAVE, lane = tid & (CBQ_WAVE - 1);
+    const int64_t p = pos[0];
+    const bool store = p >= 0 && p < max_len;
+    const int64_t trow = store ? p : 0;                           // cos/sin row
+    const int n_old = (int)(p < 0 ? 0 : (p > max_len ? max_len : p));
+
+    float r = 0.f;
+    if (wave < 2) {
+        const float *src = wave == 0 ? q + (size_t)h * HD : k + (size_t)g * HD;
+        float ss = 0.f;
+        for (int d = lane; d < HD; d += CBQ_WAVE) {
+            const float x = src[d];
+            s_raw[wave][d] = x;
+            ss = __fadd_rn(ss, __fmul_rn(x, x));
+        }
+        r = rsqrtf(wave_sum(ss) / (float)HD + eps);
+    } else if (wave == 2) {
+        for (int d = lane; d < HD; d += CBQ_WAVE) s_v[d] = v[(size_t)g * HD + d];
+    }
+    __syncthreads();
+    if (wave < 2) {
+        const float *w = wave == 0 ? qw : kw;
+        float *dst = wave == 0 ? s_q : s_k;
+        constexpr int half = HD / 2;
+        for (int d = lane; d < HD; d += CBQ_WAVE) {
+            const int dp = d < half ? d + half : d - half;
+            float xn = __fmul_rn(s_raw[wave][d], r), xp = __fmul_rn(s_raw[wave][dp], r);
+            if (w) { xn = __fmul_rn(w[d], xn); xp = __fmul_rn(w[dp], xp); }
+            const float rot = d < half ? -xp : xp;
+            dst[d] = __fadd_rn(__fmul_rn(xn, cos_t[trow * HD + d]), __fmul_rn(rot, sin_t[trow * HD + d]));
+        }
+    }
+    __syncthreads();
+    if (store && h % group == 0)
+        for (int d = tid; d < HD; d += kAttnThreads) {
+            kc[((size_t)g * max_len + p) * HD + d] = s_k[d];
+            vc[((size_t)g * max_len + p) * HD + d] = s_v[d];
+        }
+
+    const float *K = kc + (size_t)g * max_len * HD;
+    const float *V = vc + (size_t)g * max_len * HD;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    float mx = -INFINITY;
+    for (int j = tid; j <= n_old; j += kAttnThreads) {
+        float acc = 0.f;
+        if (j < n_old) {
+            const f4 *kr = (const f4 *)(K + (size_t)j * HD);
+#pragma unroll 8
+            for (int d4 = 0; d4 < HD / 4; d4++) {
+                const f4 kv = kr[d4];
+                acc = fmaf(s_q[4 * d4 + 0], kv.x, acc);
+                acc = fmaf(s_q[4 * d4 + 1], kv.y, acc);
+                acc = fmaf(s_q[4 * d4 + 2], kv.z, acc);
+                acc = fmaf(s_q[4 * d4 + 3], kv.w, acc);
+            }
+        } else {
+            for (int d = 0; d < HD; d++) acc = fmaf(s_q[d], s_k[d], acc);
+        }
+        const float sc = __fmul_rn(acc, scale);
+        s_att[j] = sc;
+        mx = fmaxf(mx, sc);
+    }
+    mx = block_max(mx, s_red);
+    float sum = 0.f;
+    for (int j = tid; j <= n_old; j += kAttnThreads) {
+        const float e = expf(__fsub_rn(s_att[j], mx));
+        s_att[j] = e;
+        sum = __fadd_rn(sum, e);
+    }
+    sum = block_sum(sum, s_red);                                  // ends with a barrier
+    for (int j = tid; j <= n_old; j += kAttnThreads) s_att[j] = __fdiv_rn(s_att[j], sum);
+    __syncthreads();
+
+    // out = sum_j p_j v_j: thread (gg, d4) owns dims [4 d4, 4 d4 + 4) of rows gg, gg + G, ...
+    constexpr int Q = HD / 4, G = kAttnThreads / Q;
+    const int gg = tid / Q, d4 = tid % Q;
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    int j = gg;
+    for (; j + 3 * G < n_old; j += 4 * G) {
+        const f4 v0 = ((const f4 *)(V + (size_t)j * HD))[d4];
+        const f4 v1 = ((const f4 *)(V + (size_t)(j + G) * HD))[d4];
+        const f4 v2 = ((const f4 *)(V + (size_t)(j + 2 * G) * HD))[d4];
+        const f4 v3 = ((const f4 *)(V + (size_t)(j + 3 * G) * HD))[d4];
+        acc = __builtin_elementwise_fma((f4)s_att[j], v0, acc);
+        acc = __builtin_elementwise_fma((f4)s_att[j + G], v1, acc);
+        acc = __builtin_elementwise_fma((f4)s_att[j + 2 * G], v2, acc);
+        acc = __builtin_elementwise_fma((f4)s_att[j + 3 * G], v3, acc);
+    }
+    for (; j < n_old; j += G)
+        acc = __builtin_elementwise_fma((f4)s_att[j], ((const f4 *)(V + (size_t)j * HD))[d4], acc);
+    ((f4 *)s_part)[tid] = acc;
+    __syncthreads();
+    if (tid < HD) {
+        float t = 0.f;
+        for (int i = 0; i < G; i++) t += s_part[i * HD + tid];
+        out[(size_t)h * HD + tid] = fmaf(s_att[n_old], s_v[tid], t);
+    }
+}
+
+// Greedy pick of a decode step in two launches: kArgBlocks blocks reduce
+// slices of the logits to (value, index) partials in the caller's workspace,
+// one block reduces those and does the step bookkeeping.  Order: first
+// maximum; NaN ranks highest (first NaN wins), as torch.argmax.
+constexpr int kArgThreads = 512;
+constexpr int kArgBlocks = 128;
+
+__device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib)
+{
+    const bool na = a != a, nb = b != b;
+    if (na || nb) return na && (!nb || ia < ib);
+    return a > b || (a == b && ia < ib);
+}
+
+__device__ __forceinline__ void arg_block_reduce(float &best, int &bi, float *s_v, int *s_i)
+{
+    for (int o = CBQ_WAVE >> 1; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, CBQ_WAVE);
+        const int oi = __shfl_xor(bi, o, CBQ_WAVE);
+        if (arg_better(ov, oi, best, bi)) { best = ov; bi = oi; }
+    }
+    if ((threadIdx.x & (CBQ_WAVE - 1)) == 0) {
+        s_v[threadIdx.x / CBQ_WAVE] = best;
+        s_i[threadIdx.x / CBQ_WAVE] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int w = 1; w < (int)(blockDim.x / CBQ_WAVE); w++)
+            if (arg_better(s_v[w], s_i[w], best, bi)) { best = s_v[w]; bi = s_i[w]; }
+}
+
+__global__ __launch_bounds__(kArgThreads) void argmax_partial_kernel(
+    const float *__restrict__ x, int n, float *__restrict__ part_v, int *__restrict__ part_i)
+{
+    __shared__ float s_v[kArgThreads / CBQ_WAVE];
+    __shared__ int s_i[kArgThreads / CBQ_WAVE];
+    float best = -INFINITY;
+    int bi = n;                                    // "none": loses to any real index
+    for (int i = blockIdx.x * kArgThreads + threadIdx.x; i < n; i += kArgBlocks * kArgThreads) {
+        const float xv = x[i];
+        if (arg_better(xv, i, best, bi)) { best = xv; bi = i; }
+    }
+    arg_block_reduce(best, bi, s_v, s_i);
+    if (threadIdx.x == 0) { part_v[blockIdx.x] = best; part_i[blockIdx.x] = bi; }
+}
+
+__global__ __launch_bounds__(kArgBlocks) void argmax_final_kernel(
+    const float *__restrict__ part_v, const int *__restrict__ part_i, int n,
+    int32_t *__restrict__ ids32, int64_t *__restrict__ toks, int64_t *__restrict__ pos,
+    int64_t first, int64_t n_toks)
+{
+    __shared__ float s_v[kArgBlocks / CBQ_WAVE];
+    __shared__ int s_i[kArgBlocks / CBQ_WAVE];
+    float best = part_v[threadIdx.x];
+    int bi = part_i[threadIdx.x];
+    arg_block_reduce(best, bi, s_v, s_i);
+    if (threadIdx.x == 0) {
+        const int tok = bi < n ? bi : 0;
+        ids32[0] = tok;
+        const int64_t p = pos[0];
+        const int64_t kk = p - first;
+        if (kk >= 0 && kk < n_toks) toks[kk] = tok;
+        pos[0] = p + 1;
+    }
+}
+
 __global__ __launch_bounds__(kGlueBlock) void silu_mul_kernel(const float *__restrict__ g,
                                                              const float *__restrict__ u,
                                                              float *__restrict__ out, int64_t n)
@@ -205,9 +403,10 @@ extern "C" {
 int cbq_add_rmsnorm_f32(float *h, const float *delta, const float *weight, float *out, int T,
                         int H, float eps, hipStream_t stream)
 {
-    if (!h || !out || out == h || T <= 0 || H <= 0 || T > 65535) return CK_ERR_ARG;
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(T), dim3(kGlueBlock), 0, stream, h, delta, weight,
-                       out, H, eps);
+    if (!h || !out || out == h || T <= 0 || H <= 0 || T > 65535 || H > kNormThreads * kNormPer)
+        return CK_ERR_ARG;
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(T), dim3(kNormThreads), 0, stream, h, delta,
+                       weight, out, H, eps);
     return cbq_launch_status("add_rmsnorm_kernel");
 }
 
@@ -254,6 +453,47 @@ int cbq_attn_decode_f32(const float *q, const float *k_cache, const float *v_cac
         return CK_ERR_ARG;
     }
     return cbq_launch_status("attn_decode_kernel");
+}
+
+int cbq_attn_rope_decode_f32(const float *q, const float *k, const float *v,
+                             const float *q_weight, const float *k_weight,
+                             const float *cos_table, const float *sin_table, const int64_t *pos,
+                             float *k_cache, float *v_cache, float *out, int n_q, int n_kv,
+                             int hd, int max_len, float scale, float eps, hipStream_t stream)
+{
+    if (!q || !k || !v || !cos_table || !sin_table || !pos || !k_cache || !v_cache || !out)
+        return CK_ERR_ARG;
+    if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || max_len <= 0 || max_len > kAttnMaxLen)
+        return CK_ERR_ARG;
+    if (((uintptr_t)k_cache & 15) != 0) return CK_ERR_ARG;       // 16-byte key rows
+    const size_t lds = (size_t)(max_len + 1) * sizeof(float);
+    const int group = n_q / n_kv;
+#define CBQ_ATTN_ROPE(HD)                                                                     \
+    hipLaunchKernelGGL(attn_rope_decode_kernel<HD>, dim3(n_q), dim3(kAttnThreads), lds, stream, \
+                       q, k, v, q_weight, k_weight, cos_table, sin_table, pos, k_cache, v_cache, \
+                       out, group, max_len, scale, eps)
+    switch (hd) {
+    case 64: CBQ_ATTN_ROPE(64); break;
+    case 128: CBQ_ATTN_ROPE(128); break;
+    case 256: CBQ_ATTN_ROPE(256); break;
+    default: return CK_ERR_ARG;
+    }
+#undef CBQ_ATTN_ROPE
+    return cbq_launch_status("attn_rope_decode_kernel");
+}
+
+int cbq_argmax_step(const float *logits, int n, void *workspace, int32_t *ids32, int64_t *toks,
+                    int64_t *pos, int64_t first, int64_t n_toks, hipStream_t stream)
+{
+    if (!logits || n <= 0 || !workspace || !ids32 || !toks || !pos || n_toks <= 0)
+        return CK_ERR_ARG;
+    float *part_v = (float *)workspace;
+    int *part_i = (int *)(part_v + kArgBlocks);
+    hipLaunchKernelGGL(argmax_partial_kernel, dim3(kArgBlocks), dim3(kArgThreads), 0, stream,
+                       logits, n, part_v, part_i);
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(kArgBlocks), 0, stream, part_v, part_i,
+                       n, ids32, toks, pos, first, n_toks);
+    return cbq_launch_status("argmax_final_kernel");
 }
 
 int cbq_silu_mul_f32(const float *g, const float *u, float *out, int64_t n, hipStream_t stream)

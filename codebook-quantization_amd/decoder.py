@@ -108,14 +108,25 @@ class _Glue:
             self.nat.stream_ptr(q.device)), "cbq_head_norm_rope_f32")
         return q_out
 
-    def attend1(self, q, k_cache, v_cache, pos_dev) -> torch.Tensor:
+    def attend_rope1(self, q, k, v, cos, sin, pos_dev, k_cache, v_cache) -> torch.Tensor:
+        """One token: head norm + rope of q and k, cache write, attention."""
         c = self.cfg
         out = torch.empty(1, c.n_q * c.head_dim, dtype=torch.float32, device=q.device)
-        self.nat.check(self.lib.cbq_attn_decode_f32(
-            q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), pos_dev.data_ptr(),
-            out.data_ptr(), c.n_q, c.n_kv, c.head_dim, k_cache.shape[1],
-            float(c.head_dim ** -0.5), self.nat.stream_ptr(q.device)), "cbq_attn_decode_f32")
+        self.nat.check(self.lib.cbq_attn_rope_decode_f32(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None, cos.data_ptr(), sin.data_ptr(),
+            pos_dev.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
+            c.n_q, c.n_kv, c.head_dim, k_cache.shape[1], float(c.head_dim ** -0.5), c.eps,
+            self.nat.stream_ptr(q.device)), "cbq_attn_rope_decode_f32")
         return out
+
+    def argmax_step(self, logits, ids32, toks, pos_dev, first: int) -> None:
+        """ids32[0] = argmax(logits); toks[pos - first] = it; pos += 1."""
+        if getattr(self, "_ws", None) is None or self._ws.device != logits.device:
+            self._ws = torch.empty(256, dtype=torch.int32, device=logits.device)
+        self.nat.check(self.lib.cbq_argmax_step(
+            logits.data_ptr(), logits.numel(), self._ws.data_ptr(), ids32.data_ptr(), toks.data_ptr(),
+            pos_dev.data_ptr(), first, toks.numel(), self.nat.stream_ptr(logits.device)),
+            "cbq_argmax_step")
 
     def silu_mul(self, g: torch.Tensor, u: torch.Tensor) -> torch.Tensor:
         out = torch.empty_like(g)
@@ -175,25 +186,38 @@ class Qwen3Decoder:
         T = h.shape[0]
         p = f"model.layers.{i}."
         g = self.glue
-        q = self.linears[p + "self_attn.q_proj"](x)
-        k = self.linears[p + "self_attn.k_proj"](x)
-        v = self.linears[p + "self_attn.v_proj"](x)
-        q = g.head_norm_rope(q, k, v, self.cos, self.sin, pos_dev, self.cache[i, 0],
-                             self.cache[i, 1])
-        if T == 1:
-            att = g.attend1(q, self.cache[i, 0], self.cache[i, 1], pos_dev)
+        qkv = self.linears.get(p + "self_attn.qkv_proj")
+        if qkv is not None:                          # row-stacked q/k/v: one launch
+            y = qkv(x)
+            nq, nk = c.n_q * c.head_dim, c.n_kv * c.head_dim
+            q, k, v = (y[:, :nq].contiguous(), y[:, nq:nq + nk].contiguous(),
+                       y[:, nq + nk:].contiguous())
         else:
+            q = self.linears[p + "self_attn.q_proj"](x)
+            k = self.linears[p + "self_attn.k_proj"](x)
+            v = self.linears[p + "self_attn.v_proj"](x)
+        if T == 1:
+            att = g.attend_rope1(q, k, v, self.cos, self.sin, pos_dev, self.cache[i, 0],
+                                 self.cache[i, 1])
+        else:
+            q = g.head_norm_rope(q, k, v, self.cos, self.sin, pos_dev, self.cache[i, 0],
+                                 self.cache[i, 1])
             att = self._attend(i, q.view(T, c.n_q, c.head_dim), L, pos)
         x = g.add_rms(h, self.linears[p + "self_attn.o_proj"](att))
-        a = g.silu_mul(self.linears[p + "mlp.gate_proj"](x), self.linears[p + "mlp.up_proj"](x))
+        gu = self.linears.get(p + "mlp.gate_up_proj")
+        if gu is not None:                           # row-stacked gate/up: one launch
+            y = gu(x)
+            a = g.silu_mul(y[:, :c.inter].contiguous(), y[:, c.inter:].contiguous())
+        else:
+            a = g.silu_mul(self.linears[p + "mlp.gate_proj"](x), self.linears[p + "mlp.up_proj"](x))
         return g.add_rms(h, self.linears[p + "mlp.down_proj"](a))
 
     # ---- captured decode step (static shapes) -------------------------------
     def _graph_step(self, ids_buf: torch.Tensor, pos_buf: torch.Tensor, toks: torch.Tensor,
                     first_pos: int):
-        """One token at device position pos_buf[0]; attention spans the whole
-        cache with positions > pos masked, so shapes never change.  Writes the
-        argmax into ids_buf (next input) and toks[pos - first_pos], and
+        """One token at device position pos_buf[0] (kernels read the position
+        from device memory, so launch shapes never change).  Writes the argmax
+        into ids_buf (int32, next input) and toks[pos - first_pos], and
         advances pos_buf."""
         c = self.cfg
         h = self.embed(ids_buf).reshape(1, c.hidden).to(torch.float32)
@@ -201,10 +225,7 @@ class Qwen3Decoder:
         for i in range(c.layers):
             x = self._layer(i, h, x, pos_buf, pos_buf, self.max_len)
         logits = self.linears["lm_head"](x).reshape(-1)
-        tok = torch.argmax(logits).reshape(1)
-        ids_buf.copy_(tok)
-        toks.index_copy_(0, pos_buf - first_pos, tok)
-        pos_buf.add_(1)
+        self.glue.argmax_step(logits, ids_buf, toks, pos_buf, first_pos)
 
     @torch.no_grad()
     def generate_graph(self, prompt: List[int], n_new: int, timing: Optional[dict] = None):
@@ -214,7 +235,7 @@ class Qwen3Decoder:
         self.reset()
         logits = self.forward(torch.tensor(prompt, dtype=torch.int64))
         plen = len(prompt)
-        ids_buf = torch.argmax(logits).reshape(1).to(torch.int64)
+        ids_buf = torch.argmax(logits).reshape(1).to(torch.int32)
         toks = torch.zeros(n_new, dtype=torch.int64, device=self.device)
         toks[0] = ids_buf[0]
         pos_buf = torch.tensor([plen], dtype=torch.int64, device=self.device)
@@ -307,10 +328,12 @@ def from_compressed(cfg: DecoderConfig, comp: Dict[str, dict], device="cuda",
 
 
 def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda",
-                   max_len: int = 512) -> Qwen3Decoder:
+                   max_len: int = 512, stack: bool = True) -> Qwen3Decoder:
     """Decoder over device-resident synthetic tensors (synthetic.FixedTensor /
     HuffTensor, built on the GPU for the 9B-shape bench); calls the C ABI
-    directly on torch's current stream."""
+    directly on torch's current stream.  With stack, each layer's fixed-width
+    q/k/v and gate/up are row-stacked into one matrix each (one GEMV launch
+    instead of three / two)."""
     import ctypes
     import cbq_native as nat
     import synthetic
@@ -381,7 +404,23 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         return e2
 
     linears = {}
+    for i in range(cfg.layers):
+        p = f"model.layers.{i}."
+        for fused, parts in (("self_attn.qkv_proj", ("self_attn.q_proj", "self_attn.k_proj",
+                                                     "self_attn.v_proj")),
+                             ("mlp.gate_up_proj", ("mlp.gate_proj", "mlp.up_proj"))):
+            ts = [tensors[p + n] for n in parts]
+            st = None
+            if stack and all(isinstance(t, synthetic.FixedTensor) for t in ts):
+                st = synthetic.stack_fixed(ts, p + fused)
+            if st is not None:
+                linears[p + fused] = fixed_linear(st)
     for n, _, _ in cfg.linear_shapes():
         t = tensors[n]
+        stem, _, leaf = n.rpartition(".")
+        fused = {"q_proj": "qkv_proj", "k_proj": "qkv_proj", "v_proj": "qkv_proj",
+                 "gate_proj": "gate_up_proj", "up_proj": "gate_up_proj"}.get(leaf)
+        if fused is not None and f"{stem}.{fused}" in linears:
+            continue
         linears[n] = huff_linear(t) if isinstance(t, synthetic.HuffTensor) else fixed_linear(t)
     return Qwen3Decoder(cfg, linears, embed_fn(tensors["model.embed_tokens"]), dev, max_len)

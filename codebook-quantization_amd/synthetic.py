@@ -66,6 +66,27 @@ class FixedTensor:
         return (self.shape[0] * self.shape[1] * self.bits + 7) // 8
 
 
+def stack_fixed(parts, name: str) -> Optional[FixedTensor]:
+    """Row-stack fixed-width tensors that share K, the index width and the
+    codebook (q/k/v, gate/up): when every part's index stream ends on a byte
+    boundary, the concatenated bytes are exactly the packed stream of the
+    stacked [sum M, K] matrix, so one GEMV launch computes all parts.
+    None when the parts do not qualify."""
+    K, bits, cb = parts[0].shape[1], parts[0].bits, parts[0].codebook
+    for t in parts:
+        if (t.shape[1] != K or t.bits != bits or t.codebook.data_ptr() != cb.data_ptr()
+                or t.codebook.numel() != cb.numel() or (t.shape[0] * K * bits) % 8):
+            return None
+    M = sum(t.shape[0] for t in parts)
+    nb = (M * K * bits) // 8
+    packed = torch.zeros(((nb + 15) // 16) * 16 + 16, dtype=torch.uint8, device=cb.device)
+    o = 0
+    for t in parts:
+        packed[o:o + t.nbytes] = t.packed[:t.nbytes]
+        o += t.nbytes
+    return FixedTensor(name, (M, K), bits, parts[0].category, packed, cb)
+
+
 @dataclass
 class HuffTensor:
     name: str

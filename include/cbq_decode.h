@@ -26,7 +26,7 @@ extern "C" {
 
 /* For each of the T rows of h [T, H]: h += delta (when delta is not NULL),
  * then out = h * rsqrt(mean(h^2) + eps) (* weight[H] when not NULL).
- * out may not alias h.  H % 4 == 0. */
+ * out may not alias h.  H <= 16384. */
 int cbq_add_rmsnorm_f32(float *h, const float *delta, const float *weight, float *out,
                         int T, int H, float eps, hipStream_t stream);
 
@@ -52,6 +52,27 @@ int cbq_head_norm_rope_f32(const float *q, const float *k, const float *v,
 int cbq_attn_decode_f32(const float *q, const float *k_cache, const float *v_cache,
                         const int64_t *pos, float *out, int n_q, int n_kv, int hd,
                         int max_len, float scale, hipStream_t stream);
+
+/* One decode token (T = 1) at position p = pos[0]: the q/k head norm and
+ * rope of cbq_head_norm_rope_f32 and the attention of cbq_attn_decode_f32 in
+ * one launch.  The new key/value row is stored at cache row p (when
+ * p < max_len) and attended from on-chip memory; cached rows [0, p) come
+ * from k_cache/v_cache.  q [n_q, hd], k and v [n_kv, hd], out [n_q, hd]. */
+int cbq_attn_rope_decode_f32(const float *q, const float *k, const float *v,
+                             const float *q_weight, const float *k_weight,
+                             const float *cos_table, const float *sin_table,
+                             const int64_t *pos, float *k_cache, float *v_cache,
+                             float *out, int n_q, int n_kv, int hd, int max_len,
+                             float scale, float eps, hipStream_t stream);
+
+/* Greedy pick of a captured decode step: tok = argmax(logits[0, n)) (first
+ * maximum; NaN ranks highest, as torch.argmax); ids32[0] = tok;
+ * toks[pos[0] - first] = tok when that index lies in [0, n_toks);
+ * pos[0] += 1.  Two launches, no host round trip; workspace is device
+ * scratch of >= 1024 bytes (partial maxima), overwritten by every call. */
+int cbq_argmax_step(const float *logits, int n, void *workspace, int32_t *ids32,
+                    int64_t *toks, int64_t *pos, int64_t first, int64_t n_toks,
+                    hipStream_t stream);
 
 /* out[i] = silu(g[i]) * u[i] = g / (1 + exp(-g)) * u, i < n. */
 int cbq_silu_mul_f32(const float *g, const float *u, float *out, int64_t n,

@@ -135,3 +135,58 @@ def test_silu_mul(cuda, lib):
                                    nat.stream_ptr(cuda)), "silu")
     ref = torch.nn.functional.silu(g) * u
     assert _rel(out, ref) <= 1e-6
+
+
+@pytest.mark.parametrize("hd,n_q,n_kv,pos0,max_len", [(128, 32, 8, 0, 512), (128, 32, 8, 200, 512),
+                                                      (64, 4, 2, 63, 64), (256, 8, 2, 17, 64)])
+def test_attn_rope_decode_matches_two_step(cuda, lib, hd, n_q, n_kv, pos0, max_len):
+    """The fused one-token kernel equals head_norm_rope followed by
+    attn_decode, and writes the same cache row."""
+    g = torch.Generator().manual_seed(pos0 * 3 + hd)
+    q = torch.randn(n_q * hd, generator=g).to(cuda)
+    k = torch.randn(n_kv * hd, generator=g).to(cuda)
+    v = torch.randn(n_kv * hd, generator=g).to(cuda)
+    cfg = decoder.DecoderConfig(layers=1, hidden=n_q * hd, inter=64, n_q=n_q, n_kv=n_kv,
+                                head_dim=hd, vocab=16)
+    cos, sin = (torch.from_numpy(a).to(cuda) for a in decoder.rope_tables(cfg, max_len))
+    kc = torch.randn(n_kv, max_len, hd, generator=g).to(cuda)
+    vc = torch.randn(n_kv, max_len, hd, generator=g).to(cuda)
+    kc2, vc2 = kc.clone(), vc.clone()
+    pos = torch.tensor([pos0], dtype=torch.int64, device=cuda)
+    st = nat.stream_ptr(cuda)
+    out = torch.empty(n_q * hd, device=cuda)
+    nat.check(lib.cbq_attn_rope_decode_f32(q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None,
+                                           cos.data_ptr(), sin.data_ptr(), pos.data_ptr(),
+                                           kc.data_ptr(), vc.data_ptr(), out.data_ptr(), n_q, n_kv,
+                                           hd, max_len, hd ** -0.5, 1e-6, st), "fused")
+    qr = torch.empty_like(q)
+    nat.check(lib.cbq_head_norm_rope_f32(q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None,
+                                         cos.data_ptr(), sin.data_ptr(), pos.data_ptr(),
+                                         qr.data_ptr(), kc2.data_ptr(), vc2.data_ptr(), 1, n_q,
+                                         n_kv, hd, max_len, 1e-6, st), "rope")
+    ref = torch.empty_like(out)
+    nat.check(lib.cbq_attn_decode_f32(qr.data_ptr(), kc2.data_ptr(), vc2.data_ptr(),
+                                      pos.data_ptr(), ref.data_ptr(), n_q, n_kv, hd, max_len,
+                                      hd ** -0.5, st), "attn")
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    assert _rel(out, ref) <= 1e-6
+
+
+@pytest.mark.parametrize("n", [1, 7, 151936])
+def test_argmax_step(cuda, lib, n):
+    x = torch.randn(n, device=cuda)
+    if n > 7:
+        x[90000] = x[100000] = x.max() + 1        # tie across slices: the first index wins
+    ids = torch.full((1,), -5, dtype=torch.int32, device=cuda)
+    toks = torch.zeros(8, dtype=torch.int64, device=cuda)
+    pos = torch.tensor([20], dtype=torch.int64, device=cuda)
+    ws = torch.empty(256, dtype=torch.int32, device=cuda)
+    nat.check(lib.cbq_argmax_step(x.data_ptr(), n, ws.data_ptr(), ids.data_ptr(), toks.data_ptr(),
+                                  pos.data_ptr(), 17, 8, nat.stream_ptr(cuda)), "argmax")
+    want = int(torch.argmax(x))
+    assert int(ids[0]) == want and int(toks[3]) == want and int(pos[0]) == 21
+    assert int(toks.sum()) == want                  # nothing else written
+    pos.fill_(40)                                   # index outside toks: only ids and pos change
+    nat.check(lib.cbq_argmax_step(x.data_ptr(), n, ws.data_ptr(), ids.data_ptr(), toks.data_ptr(),
+                                  pos.data_ptr(), 17, 8, nat.stream_ptr(cuda)), "argmax")
+    assert int(pos[0]) == 41 and int(toks.sum()) == want
