@@ -328,15 +328,27 @@ def main():
                 canon=tb["canon"].data_ptr(), canon_pay=tb["pay"].data_ptr(), value_cb=None,
                 C=tb["codebook"].numel(), stage_words=tb["stage_words"])
         import ctypes
+        from gpu_huffman_functions import build_columns, columns_eligible
+        cols = {}                               # column layout + unified tables (T = 1 GEMV)
+        for n, t in huff.items():
+            if columns_eligible(descs[n], t.shape[1]):
+                cols[n] = build_columns(descs[n], t.shape[0] * t.shape[1], dev, t.lengths,
+                                        t.tables["codebook"].cpu().numpy())
+        torch.cuda.synchronize()
 
         def launch_huff(ns):
             st = nat.stream_ptr(dev)
             for n in ns:
                 M, K = huff[n].shape
-                rc = lib.cbq_huff_linear_f32(xs[K].data_ptr(), ctypes.byref(descs[n]),
-                                             outs[n].data_ptr(), 1, M, K, st)
+                if n in cols:
+                    rc = lib.cbq_huff_linear_col_f32(xs[K].data_ptr(), ctypes.byref(descs[n]),
+                                                     ctypes.byref(cols[n][1]), outs[n].data_ptr(),
+                                                     M, K, st)
+                else:
+                    rc = lib.cbq_huff_linear_f32(xs[K].data_ptr(), ctypes.byref(descs[n]),
+                                                 outs[n].data_ptr(), 1, M, K, st)
                 if rc:
-                    raise RuntimeError(f"cbq_huff_linear_f32 rc={rc} on {n}")
+                    raise RuntimeError(f"Huffman GEMV rc={rc} on {n}")
 
         hbytes = sum(huff_bytes(t) for t in huff.values())
         ms_h, _ = timed_graph(torch, lambda: launch_huff(names), args.steps, args.warmup)
@@ -345,6 +357,7 @@ def main():
         us_hgu = ms_hgu * 1e3 / len(gu)
         bits_per_sym = 8.0 * sum(h.nbytes for h in huff.values()) / sum(
             h.shape[0] * h.shape[1] for h in huff.values())
+        col_gu = cols[gu[0]][0][0].numel() * 4 if gu[0] in cols else None
         result["huffman"] = {
             "value": round(hbytes / (ms_h * 1e-3) / 1e9, 1), "unit": "GB/s",
             "ms_per_step": round(ms_h, 4), "bytes_per_step": hbytes,
@@ -353,9 +366,10 @@ def main():
             "roofline": {"bound": "hbm", "achieved": round(hb_gu / (us_hgu * 1e-6) / 1e9, 1),
                          "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": round(hb_gu / (us_hgu * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
-                         "traffic": read_traffic("huff_gemv_gate_up_qwen3-8b_pmc.md"),
-                         "kernel": "huff_tile_fast_kernel<16,1> gate/up 4096->12288",
-                         "bytes_per_launch": hb_gu, "us_per_launch": round(us_hgu, 2)}}
+                         "traffic": read_traffic("huff_col_kernel_gate_up_qwen3-8b_pmc.md"),
+                         "kernel": "huff_col_kernel<16,unified> gate/up 4096->12288",
+                         "bytes_per_launch": hb_gu, "column_layout_bytes": col_gu,
+                         "us_per_launch": round(us_hgu, 2)}}
         log(f"huffman sweep: {ms_h:.3f} ms/step, {hbytes / 1e9:.2f} GB/step")
 
     if not args.no_e2e:

@@ -36,6 +36,12 @@ class HuffStream(ctypes.Structure):
     ]
 
 
+class HuffColumns(ctypes.Structure):
+    """struct cbq_huff_columns (include/cbq_hip.h)."""
+    _fields_ = [("cwords", _vp), ("row_off", _vp), ("n_chunks", _i64),
+                ("ulut1", _vp), ("ulut2", _vp), ("n_ulut2", ctypes.c_int32)]
+
+
 # name -> (restype, argtypes); every symbol declared in include/*.h
 SIGNATURES = {
     "ck_error_string": (ctypes.c_char_p, [_i]),
@@ -52,6 +58,11 @@ SIGNATURES = {
     "cbq_huff_linear_f32": (_i, [_vp, ctypes.POINTER(HuffStream), _vp, _i, _i, _i, _vp]),
     "cbq_huff_embedding_f32": (_i, [_vp, ctypes.POINTER(HuffStream), _vp, _i, _i, _i, _vp]),
     "cbq_huff_decode_indices": (_i, [ctypes.POINTER(HuffStream), _vp, _i64, _vp]),
+    "cbq_huff_column_rows": (_i, [ctypes.POINTER(HuffStream), _i64, _vp, _vp]),
+    "cbq_huff_build_ulut": (_i, [_vp, _i, _vp, _i, _vp, _vp, _vp]),
+    "cbq_huff_columnize": (_i, [ctypes.POINTER(HuffStream), _i64, _vp, _vp, _vp]),
+    "cbq_huff_linear_col_f32": (_i, [_vp, ctypes.POINTER(HuffStream), ctypes.POINTER(HuffColumns),
+                                     _vp, _i, _i, _vp]),
     # include/cbq_decode.h
     "cbq_add_rmsnorm_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, ctypes.c_float, _vp]),
     "cbq_head_norm_rope_f32": (_i, [_vp] * 11 + [_i] * 5 + [ctypes.c_float, _vp]),

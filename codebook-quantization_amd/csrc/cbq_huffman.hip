@@ -27,6 +27,7 @@
 #include "cbq_device.h"
 
 #include <algorithm>
+#include <climits>
 #include <thread>
 #include <vector>
 
@@ -791,6 +792,205 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void huff_tile_fast_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Column layout.  Chunk c's 64 sub-blocks are stored side by side: sub-block
+// l's bits, LSB-first from bit 0, in words cwords[(row_off[c] + r) * 64 + l]
+// for r < rows(c) = max_l ceil(sub_len / 32) (bits past a sub-block's end
+// are 0), followed by kColPadRows zero rows.  Every lane of a wave then reads
+// its own LDS bank whatever its bit position, the window reads carry no bank
+// conflicts, and a lane starts at bit 0 (no scan of sub-block lengths).
+// ---------------------------------------------------------------------------
+constexpr int kColPadRows = 4;
+constexpr int kColSlotRows = kFastSlot / kSub;                // 24 rows per wave slot
+
+// rows[c] = max(1, max_l ceil(sub_len[c*64 + l] / 32)); one wave per chunk.
+__global__ __launch_bounds__(256) void col_rows_kernel(const uint16_t *__restrict__ sub_len,
+                                                       int64_t n_sub, int64_t n_chunks,
+                                                       uint32_t *__restrict__ rows)
+{
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int64_t c = (int64_t)blockIdx.x * 4 + threadIdx.x / CBQ_WAVE;
+    if (c >= n_chunks) return;                                 // whole waves
+    const int64_t sb = c * kSub + lane;
+    uint32_t r = ((sb < n_sub ? (uint32_t)sub_len[sb] : 0u) + 31u) >> 5;
+    for (int o = CBQ_WAVE >> 1; o > 0; o >>= 1) r = max(r, (uint32_t)__shfl_xor((int)r, o, CBQ_WAVE));
+    if (lane == 0) rows[c] = r > 0 ? r : 1u;
+}
+
+// One wave per chunk: lane l copies its sub-block's bits into column l.
+__global__ __launch_bounds__(256) void columnize_kernel(HuffArgs a,
+                                                        const uint32_t *__restrict__ row_off,
+                                                        uint32_t *__restrict__ cwords)
+{
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int64_t c = (int64_t)blockIdx.x * 4 + threadIdx.x / CBQ_WAVE;
+    if (c >= a.n_chunks) return;
+    const int64_t sb = c * kSub + lane;
+    const uint32_t len = sb < a.n_sub ? a.sub_len[sb] : 0u;
+    const uint32_t incl = wave_incl_scan(len);
+    const uint64_t start = a.chunk_off[c] + (uint64_t)(incl - len);
+    const uint32_t r0 = row_off[c], H = row_off[c + 1] - r0;
+    for (uint32_t r = 0; r < H; r++) {
+        const uint32_t have = len > 32u * r ? len - 32u * r : 0u;
+        uint32_t w = 0u;
+        if (have > 0u) {
+            const uint64_t b = start + 32ull * r;
+            w = window_global(a.words, a.n_words, (int64_t)(b >> 5), (uint32_t)(b & 31u));
+            if (have < 32u) w &= (1u << have) - 1u;
+        }
+        cwords[((size_t)r0 + r) * kSub + lane] = w;
+    }
+}
+
+// 32 column bits of `lane` from bit pos of its sub-block, from global memory.
+__device__ __forceinline__ uint32_t col_window_global(const uint32_t *__restrict__ cwords,
+                                                      uint32_t r0, int lane, uint32_t pos)
+{
+    const size_t w = ((size_t)r0 + (pos >> 5)) * kSub + lane;
+    return funnel(cwords[w + kSub], cwords[w], pos);
+}
+
+// Fused GEMV over the column layout, T = 1, bf16-value payloads, K % 4096 == 0.
+// LDS as huff_tile_fast_kernel (lut2 at 0, lut1, swizzled x tile, 16 slots of
+// 24 rows); one chunk per wave step.
+template <int NW, bool UNIFIED>
+__global__ __launch_bounds__(NW * CBQ_WAVE) void huff_col_kernel(
+    const float *__restrict__ x, float *__restrict__ out, HuffArgs a,
+    const uint32_t *__restrict__ cwords, const uint32_t *__restrict__ row_off, int M, int K)
+{
+    static_assert(NW <= kFastChains, "one slot per wave");
+    __shared__ __attribute__((aligned(16))) uint32_t s_lds[kFastLdsWords];
+    uint32_t *const s_lut2 = s_lds;
+    uint32_t *const s_lut1 = s_lds + kFOffLut1;
+    float *const s_x = (float *)(s_lds + kFOffX);
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CBQ_WAVE);
+    uint32_t *const s_slot = s_lds + kFOffSlots + wave * kFastSlot;
+    // byte address of this lane's column in the slot
+    const int lane_addr = __builtin_amdgcn_readfirstlane(4 * (kFOffSlots + wave * kFastSlot)) + 4 * lane;
+
+    for (int i = wave; i < (kLutSize >> 6); i += NW)
+        dma_dword(a.lut1 + (i << 6) + lane, s_lut1 + (i << 6));
+    const int n2 = (a.n_lut2 + 63) & ~63;
+    for (int i = wave; i < (n2 >> 6); i += NW) {
+        const int e = (i << 6) + lane;
+        dma_dword(a.lut2 + (e < a.n_lut2 ? e : a.n_lut2 - 1), s_lut2 + (i << 6));
+    }
+    __syncthreads();
+    int unresolved = 0;
+    for (int i = threadIdx.x; i < a.n_lut2; i += NW * CBQ_WAVE) unresolved |= s_lut2[i] == 0u;
+    {
+        const bool wany = __ballot(unresolved) != 0;
+        if (lane == 0) ((uint32_t *)s_x)[wave] = wany ? 1u : 0u;
+    }
+    __syncthreads();
+    uint32_t any_unresolved = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) any_unresolved |= ((const uint32_t *)s_x)[w];
+    // unified tables hold no unresolved entries (the builder refuses codes
+    // beyond 24 bits), and their short-code entries are not leaves
+    const bool general = !UNIFIED && any_unresolved != 0;
+
+    const int R = K / kChunk;
+    const int W = gridDim.x * NW;
+    const int wid = blockIdx.x * NW + wave;
+    const int rows = wid < M ? (M - wid + W - 1) / W : 0;
+    const int b0 = blockIdx.x * NW;
+    const int rows_max = b0 < M ? (M - b0 + W - 1) / W : 0;
+    const int n_seg = (rows_max + 63) >> 6;
+    const float *const xr = s_x + lane * 64;
+    const int xsw = (lane & 15) << 2;
+
+    for (int seg = 0; seg < n_seg; seg++) {
+        float res = 0.f;
+        const int seg_rows = min(64, rows - seg * 64);
+        for (int p = 0; p < R; p++) {
+            __syncthreads();
+            for (int r = wave; r < 64; r += NW)
+                dma_dword(x + (size_t)p * kChunk + (r << 6) + (lane ^ ((r & 15) << 2)),
+                          s_x + (r << 6));
+            __syncthreads();
+            for (int b = 0; b < seg_rows; b++) {
+                const int64_t row = wid + (int64_t)(seg * 64 + b) * W;
+                const int64_t c = __builtin_amdgcn_readfirstlane((int)(row * R + p));
+                const uint32_t r0 = row_off[c], H = row_off[c + 1] - r0;
+                const bool big = general || H > (uint32_t)(kColSlotRows - 1);
+                if (!big)
+                    for (uint32_t i = 0; i < H; i += 4)
+                        dma_dwordx4(cwords + ((size_t)r0 + i) * kSub + 4 * lane, s_slot + i * kSub);
+                __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));   // vmcnt(0)
+                uint32_t q = 0xfffffffeu;                  // bit -2: win2 & 0x3ffc = 4 * lut1 index
+                float acc = 0.f;
+                if (!big && UNIFIED) {
+                    // Unified tables: every lut1 entry points into lut2 (a short code at
+                    // its own leaf, nb = 0), so the step has no select.
+                    for (int i = 0; i < kSub; i += 4) {
+                        typedef float f4 __attribute__((ext_vector_type(4)));
+                        const f4 xv4 = *(const f4 *)(xr + (i ^ xsw));
+                        const float xv[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            const int d = __builtin_amdgcn_sbfe((int)q, 5, 27);
+                            const char *wp = (const char *)s_lds + lane_addr + d * (4 * kSub);
+                            const uint32_t lo = *(const uint32_t *)wp;
+                            const uint32_t hi = *(const uint32_t *)(wp + 4 * kSub);
+                            const uint32_t win2 = funnel(hi, lo, q);
+                            const uint32_t e1 = *(const uint32_t *)((const char *)s_lut1 + (win2 & 0x3ffcu));
+                            const uint32_t ext = __builtin_amdgcn_ubfe(win2, kLutBits + 2, e1 & 15u);
+                            // byte offset (base + ext) * 4, kept inside lut2 whatever e1 holds
+                            const uint32_t off = ((e1 >> 16) + (ext << 2)) & (uint32_t)(4 * kFastLut2 - 4);
+                            const uint32_t e = *(const uint32_t *)((const char *)s_lut2 + off);
+                            q += e & 0xffu;                    // bits 6-7 of a leaf are 0
+                            acc = fmaf(xv[u], __uint_as_float(e & 0xffff0000u), acc);
+                        }
+                    }
+                } else if (!big) {
+                    for (int i = 0; i < kSub; i += 4) {
+                        typedef float f4 __attribute__((ext_vector_type(4)));
+                        const f4 xv4 = *(const f4 *)(xr + (i ^ xsw));
+                        const float xv[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            const int d = (int)q >> 5;
+                            const char *wp = (const char *)s_lds + lane_addr + d * (4 * kSub);
+                            const uint32_t lo = *(const uint32_t *)wp;
+                            const uint32_t hi = *(const uint32_t *)(wp + 4 * kSub);
+                            const uint32_t win2 = funnel(hi, lo, q);
+                            uint32_t e = *(const uint32_t *)((const char *)s_lut1 + (win2 & 0x3ffcu));
+                            const uint32_t nb = __builtin_amdgcn_ubfe(e, 6, 4);
+                            const uint32_t base = nb ? __builtin_amdgcn_ubfe(e, 11, 13) : 0u;
+                            uint32_t e2 = s_lut2[base + __builtin_amdgcn_ubfe(win2, kLutBits + 2, nb)];
+                            asm volatile("" : "+v"(e2));       // read unconditionally: no branch
+                            e = nb ? e2 : e;
+                            q += e & 0xffu;                    // bits 6-7 of a leaf are 0
+                            acc = fmaf(xv[u], __uint_as_float(e & 0xffff0000u), acc);
+                        }
+                    }
+                } else {
+                    for (int i = 0; i < kSub; i++) {
+                        const float xv = xr[i ^ xsw];
+                        const uint32_t win = col_window_global(cwords, r0, lane, q + 2u);
+                        uint32_t e = s_lut1[win & (kLutSize - 1)];
+                        if (UNIFIED) {
+                            const uint32_t ext = __builtin_amdgcn_ubfe(win, kLutBits, e & 15u);
+                            e = s_lut2[((e >> 18) + ext) & (kFastLut2 - 1)];
+                        } else if ((e & 63u) == 0u) {
+                            e = decode_long<true>(e, win << 2, win, s_lut2, (uint32_t)a.n_lut2,
+                                                  a.canon, a.canon_pay);
+                        }
+                        q += e & 63u;
+                        acc = fmaf(xv, __uint_as_float(e & 0xffff0000u), acc);
+                    }
+                }
+                const float s = wave_sum(acc);
+                if (lane == b) res += s;
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
+        if (lane < seg_rows) out[wid + (int64_t)(seg * 64 + lane) * W] = res;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Embedding: one wave per requested row (H % 64 == 0)
 // ---------------------------------------------------------------------------
 
@@ -1184,6 +1384,65 @@ int cbq_huff_build_luts(const uint8_t *lengths, int n_alpha, const float *codebo
     return CK_SUCCESS;
 }
 
+int cbq_huff_build_ulut(const uint8_t *lengths, int n_alpha, const float *codebook, int C,
+                        uint32_t *ulut1, uint32_t *ulut2, int *n_ulut2)
+{
+    if (!lengths || n_alpha <= 0 || n_alpha > 65536 || !codebook || C <= 0 || !n_ulut2)
+        return CK_ERR_ARG;
+    Canon cn;
+    if (!make_canon(lengths, n_alpha, cn) || cn.max_len > 2 * kLutBits) return CK_ERR_ARG;
+    auto payload = [&](int sym) -> uint32_t {
+        uint32_t u;
+        __builtin_memcpy(&u, &codebook[std::min(sym, C - 1)], 4);
+        return u >> 16;
+    };
+    // entry 0: the "no code" leaf (symbol 0, one bit); then one leaf per short
+    // code; then the per-prefix subtables of the long codes
+    std::vector<int> maxlen(kLutSize, 0);
+    int n_short = 0;
+    for (int sy = 0; sy < n_alpha; sy++) {
+        const int L = lengths[sy];
+        if (!L) continue;
+        if (L <= kLutBits) { n_short++; continue; }
+        const uint32_t key = bitrev(cn.code[sy] >> (L - kLutBits), kLutBits);
+        maxlen[key] = std::max(maxlen[key], L);
+    }
+    std::vector<uint32_t> base(kLutSize, 0), nbits(kLutSize, 0);
+    int64_t total = 1 + n_short;
+    for (int k = 0; k < kLutSize; k++) {
+        if (!maxlen[k]) continue;
+        nbits[k] = (uint32_t)(maxlen[k] - kLutBits);
+        base[k] = (uint32_t)total;
+        total += 1ll << nbits[k];
+    }
+    if (total >= (1 << 14)) return CK_ERR_ARG;           // base * 4 must fit 16 bits
+    *n_ulut2 = (int)total;
+    if (!ulut1 || !ulut2) return CK_SUCCESS;
+    const uint32_t invalid = leaf(1, payload(0));
+    for (int64_t i = 0; i < total; i++) ulut2[i] = invalid;
+    for (int k = 0; k < kLutSize; k++) ulut1[k] = maxlen[k] ? (base[k] << 18) | nbits[k] : 0u;
+    int next = 1;
+    for (int sy = 0; sy < n_alpha; sy++) {
+        const int L = lengths[sy];
+        if (!L) continue;
+        const uint32_t e = leaf(L, payload(sy));
+        if (L <= kLutBits) {
+            ulut2[next] = e;
+            const uint32_t r = bitrev(cn.code[sy], L);
+            for (uint32_t hi = 0; hi < (1u << (kLutBits - L)); hi++)
+                ulut1[r | (hi << L)] = (uint32_t)next << 18;
+            next++;
+        } else {
+            const uint32_t key = bitrev(cn.code[sy] >> (L - kLutBits), kLutBits);
+            const int rest = L - kLutBits;
+            const uint32_t suf = bitrev(cn.code[sy] & ((1u << rest) - 1u), rest);
+            for (uint32_t hi = 0; hi < (1u << (nbits[key] - rest)); hi++)
+                ulut2[base[key] + (suf | (hi << rest))] = e;
+        }
+    }
+    return CK_SUCCESS;
+}
+
 int cbq_huff_index_stream(const uint8_t *stream_msb, int64_t stream_bytes,
                           const uint8_t *lengths, int n_alpha, const int64_t *row_bit_starts,
                           int M, int K, uint64_t *chunk_off, uint16_t *sub_len, int threads)
@@ -1272,6 +1531,73 @@ int cbq_huff_linear_f32(const float *x, const cbq_huff_stream *hs, float *out, i
                           : launch_gemv<4, false>(x, out, a, T, M, K, (int)RW, (int)SPL, p, stream);
     return value_mode ? launch_gemv<16, true>(x, out, a, T, M, K, (int)RW, (int)SPL, p, stream)
                       : launch_gemv<16, false>(x, out, a, T, M, K, (int)RW, (int)SPL, p, stream);
+}
+
+int cbq_huff_column_rows(const cbq_huff_stream *hs, int64_t n_symbols, uint32_t *rows,
+                         hipStream_t stream)
+{
+    if (!hs || !hs->sub_len || !rows || n_symbols <= 0) return CK_ERR_ARG;
+    const int64_t n_chunks = (n_symbols + kChunk - 1) / kChunk;
+    const int64_t n_sub = (n_symbols + kSub - 1) / kSub;
+    const int64_t blocks = (n_chunks + 3) / 4;
+    if (blocks > INT32_MAX) return CK_ERR_ARG;
+    hipLaunchKernelGGL(col_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, hs->sub_len,
+                       n_sub, n_chunks, rows);
+    return cbq_launch_status("col_rows_kernel");
+}
+
+int cbq_huff_columnize(const cbq_huff_stream *hs, int64_t n_symbols, const uint32_t *row_off,
+                       uint32_t *cwords, hipStream_t stream)
+{
+    HuffArgs a;
+    if (!fill_args(a, hs, n_symbols) || !row_off || !cwords) return CK_ERR_ARG;
+    const int64_t blocks = (a.n_chunks + 3) / 4;
+    if (blocks > INT32_MAX) return CK_ERR_ARG;
+    hipLaunchKernelGGL(columnize_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a, row_off,
+                       cwords);
+    return cbq_launch_status("columnize_kernel");
+}
+
+int cbq_huff_linear_col_f32(const float *x, const cbq_huff_stream *hs,
+                            const cbq_huff_columns *cols, float *out, int M, int K,
+                            hipStream_t stream)
+{
+    if (!x || !out || !hs || !cols || M <= 0 || K <= 0 || K % kChunk != 0) return CK_ERR_ARG;
+    if (!hs->lut1 || !hs->lut2 || hs->n_lut2 < 1 || hs->n_lut2 > kFastLut2 || !hs->canon ||
+        !hs->canon_pay || hs->value_cb != nullptr)
+        return CK_ERR_ARG;
+    if (!cols->cwords || !cols->row_off || cols->n_chunks != (int64_t)M * K / kChunk)
+        return CK_ERR_ARG;
+    HuffArgs a = {};
+    a.lut1 = hs->lut1; a.lut2 = hs->lut2; a.n_lut2 = hs->n_lut2;
+    a.canon = hs->canon; a.canon_pay = hs->canon_pay; a.C = hs->C;
+    a.n_sym = (int64_t)M * K; a.n_chunks = cols->n_chunks; a.n_sub = a.n_sym / kSub;
+    const bool unified = cols->ulut1 && cols->ulut2 && cols->n_ulut2 >= 1 &&
+                         cols->n_ulut2 <= kFastLut2;
+    if (unified) { a.lut1 = cols->ulut1; a.lut2 = cols->ulut2; a.n_lut2 = cols->n_ulut2; }
+    // Waves per block (one block per CU: the LDS is static): 16 when every CU
+    // gets >= 16 rows, else fewer so that small matrices still reach all CUs.
+    // MI355X, 1024 x 4096: 16 waves 14.7 us, 4 waves 13.7 us; 4096 x 4096: 16
+    // waves 17.9 us, 8 waves 23.4 us.  A step is a chain of three dependent
+    // LDS reads (~440 cycles), so throughput scales with resident waves.
+    const int per = M / cbq_num_cus();
+    const int nw = per >= 16 ? 16 : per >= 8 ? 8 : 4;
+    const int blocks = std::max(1, std::min(cbq_num_cus(), (M + nw - 1) / nw));
+#define CBQ_COL_LAUNCH(NWV)                                                                    \
+    do {                                                                                       \
+        if (unified)                                                                           \
+            hipLaunchKernelGGL((huff_col_kernel<NWV, true>), dim3(blocks), dim3(NWV * CBQ_WAVE), \
+                               0, stream, x, out, a, cols->cwords, cols->row_off, M, K);       \
+        else                                                                                   \
+            hipLaunchKernelGGL((huff_col_kernel<NWV, false>), dim3(blocks),                    \
+                               dim3(NWV * CBQ_WAVE), 0, stream, x, out, a, cols->cwords,       \
+                               cols->row_off, M, K);                                           \
+    } while (0)
+    if (nw == 4) CBQ_COL_LAUNCH(4);
+    else if (nw == 8) CBQ_COL_LAUNCH(8);
+    else CBQ_COL_LAUNCH(16);
+#undef CBQ_COL_LAUNCH
+    return cbq_launch_status("huff_col_kernel");
 }
 
 int cbq_huff_embedding_f32(const int32_t *token_ids, const cbq_huff_stream *hs, float *out,

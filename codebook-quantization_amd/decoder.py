@@ -337,6 +337,7 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
     import ctypes
     import cbq_native as nat
     import synthetic
+    from gpu_huffman_functions import build_columns, columns_eligible
     lib = nat.load()
     dev = torch.device(device)
 
@@ -365,11 +366,20 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
     def huff_linear(t):
         M, K = t.shape
         desc = huff_desc(t)
+        cols = None
+        if columns_eligible(desc, K):            # single-token GEMV on the column layout
+            cols = build_columns(desc, M * K, dev, t.lengths, t.tables["codebook"].cpu().numpy())
 
-        def f(x, desc=desc):
+        def f(x, desc=desc, cols=cols):
             x = x.reshape(-1, K).contiguous()
             T = x.shape[0]
             out = torch.empty(T, M, device=dev)
+            if T == 1 and cols is not None:
+                nat.check(lib.cbq_huff_linear_col_f32(x.data_ptr(), ctypes.byref(desc),
+                                                      ctypes.byref(cols[1]), out.data_ptr(), M, K,
+                                                      nat.stream_ptr(dev)),
+                          "cbq_huff_linear_col_f32")
+                return out
             for t0 in range(0, T, 16):
                 tt = min(16, T - t0)
                 nat.check(lib.cbq_huff_linear_f32(x.data_ptr() + t0 * K * 4, ctypes.byref(desc),

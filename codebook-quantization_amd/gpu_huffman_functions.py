@@ -92,6 +92,46 @@ class _DeviceStream:
             C=self.C, stage_words=hc.stage_words_for(chunk_offsets))
 
 
+def build_columns(desc: "nat.HuffStream", n_sym: int, device, lengths=None,
+                  codebook: Optional[np.ndarray] = None):
+    """Column layout of a device stream (struct cbq_huff_columns): chunk c's
+    64 sub-blocks side by side, built on the device; with the code lengths
+    and the (bf16-exact) codebook also the unified decode tables when the
+    code qualifies.  Returns the device tensors to keep alive and the
+    descriptor."""
+    lib = nat.load()
+    n_chunks = (n_sym + hc.CHUNK_SYMBOLS - 1) // hc.CHUNK_SYMBOLS
+    st = nat.stream_ptr(device)
+    rows = torch.empty(n_chunks, dtype=torch.int32, device=device)
+    nat.check(lib.cbq_huff_column_rows(ctypes.byref(desc), n_sym, rows.data_ptr(), st),
+              "cbq_huff_column_rows")
+    cum = torch.cumsum(rows.to(torch.int64), 0)
+    total = int(cum[-1])
+    if total + 4 >= 2 ** 31:
+        raise ValueError(f"column layout of {total} rows exceeds the 32-bit row index")
+    row_off = torch.zeros(n_chunks + 1, dtype=torch.int32, device=device)
+    row_off[1:] = cum.to(torch.int32)
+    cwords = torch.zeros((total + 4) * hc.SUB_SYMBOLS, dtype=torch.int32, device=device)
+    nat.check(lib.cbq_huff_columnize(ctypes.byref(desc), n_sym, row_off.data_ptr(),
+                                     cwords.data_ptr(), st), "cbq_huff_columnize")
+    keep = [cwords, row_off]
+    cols = nat.HuffColumns(cwords=cwords.data_ptr(), row_off=row_off.data_ptr(), n_chunks=n_chunks)
+    if lengths is not None and codebook is not None:
+        u = hc.unified_luts(lengths, codebook)
+        if u is not None and u[1].size <= 8192:
+            u1 = torch.from_numpy(u[0].view(np.int32)).to(device)
+            u2 = torch.from_numpy(u[1].view(np.int32)).to(device)
+            keep += [u1, u2]
+            cols.ulut1, cols.ulut2, cols.n_ulut2 = u1.data_ptr(), u2.data_ptr(), int(u[1].size)
+    return keep, cols
+
+
+def columns_eligible(desc: "nat.HuffStream", K: int) -> bool:
+    """The column GEMV serves T = 1 rows of whole 4096-symbol chunks with
+    bf16-value payloads and a second table level that fits its LDS."""
+    return K % hc.CHUNK_SYMBOLS == 0 and not desc.value_cb and 1 <= desc.n_lut2 <= 8192
+
+
 def _cb_numpy(codebook) -> np.ndarray:
     if isinstance(codebook, torch.Tensor):
         return codebook.detach().to(torch.float32).cpu().numpy().reshape(-1)
@@ -130,6 +170,13 @@ class HuffmanCodebookLinear:
                                  huff_sub_lens, device)
         self.device = device
         self._idx_dev = None
+        # single-token GEMVs read the column layout when the shape allows
+        self.cols = None
+        if columns_eligible(self.dev.desc, self.K):
+            self._col_keep, self.cols = build_columns(
+                self.dev.desc, self.M * self.K, device, np.asarray(huff_lengths, np.uint8),
+                self._cb_np)
+            self._cwords, self._row_off = self._col_keep[0], self._col_keep[1]
 
     @property
     def compressed_bytes(self) -> int:
@@ -145,6 +192,11 @@ class HuffmanCodebookLinear:
         xc = x.reshape(T, self.K).to(torch.float32).contiguous()
         out = torch.empty(T, self.M, dtype=torch.float32, device=self.device)
         st = nat.stream_ptr(self.device)
+        if T == 1 and self.cols is not None:
+            nat.check(self._lib.cbq_huff_linear_col_f32(
+                xc.data_ptr(), ctypes.byref(self.dev.desc), ctypes.byref(self.cols),
+                out.data_ptr(), self.M, self.K, st), "cbq_huff_linear_col_f32")
+            T = 0
         for t0 in range(0, T, 16):
             tt = min(16, T - t0)
             rc = self._lib.cbq_huff_linear_f32(

@@ -270,6 +270,25 @@ def device_luts(lengths, codebook: Optional[np.ndarray], C: int, value_payload: 
     return lut1, lut2, canon, pay
 
 
+def unified_luts(lengths, codebook: np.ndarray):
+    """ulut1[4096], ulut2 for the column GEMV (bf16-value payloads, codes of
+    at most 24 bits), or None when the code does not qualify."""
+    lib = _native()
+    lengths = np.ascontiguousarray(lengths, np.uint8)
+    cb = np.ascontiguousarray(codebook, np.float32)
+    n2 = ctypes.c_int(0)
+    if lib.cbq_huff_build_ulut(lengths.ctypes.data, len(lengths), cb.ctypes.data, int(cb.size),
+                               None, None, ctypes.byref(n2)):
+        return None
+    u1 = np.zeros(LUT_SIZE, np.uint32)
+    u2 = np.zeros(n2.value, np.uint32)
+    rc = lib.cbq_huff_build_ulut(lengths.ctypes.data, len(lengths), cb.ctypes.data, int(cb.size),
+                                 u1.ctypes.data, u2.ctypes.data, ctypes.byref(n2))
+    if rc:
+        raise ValueError(f"cbq_huff_build_ulut rc={rc}")
+    return u1, u2
+
+
 def index_stream(stream, lengths, M: int, K: int, row_bit_starts=None,
                  threads: int = 0) -> Tuple[np.ndarray, np.ndarray]:
     """chunk offsets and sub-block lengths of a reference-format stream."""

@@ -166,6 +166,49 @@ int cbq_huff_linear_f32(const float *x, const cbq_huff_stream *hs, float *out,
 int cbq_huff_embedding_f32(const int32_t *token_ids, const cbq_huff_stream *hs,
                            float *out, int T, int vocab, int H, hipStream_t stream);
 
+/* Column layout of a chunked stream, built on the device by
+ * cbq_huff_column_rows + cbq_huff_columnize: chunk c's 64 sub-blocks side by
+ * side, sub-block l's bits LSB-first in cwords[(row_off[c] + r) * 64 + l],
+ * r < rows(c) = max_l ceil(sub_len / 32); bits past a sub-block are 0 and
+ * 4 zero rows follow the last chunk.  No counterpart in the reference: a
+ * load-time re-layout of its stream (same codes, ~6% more bytes) so that the
+ * GEMV's window reads are free of LDS bank conflicts. */
+typedef struct cbq_huff_columns {
+    const uint32_t *cwords;     /* [(row_off[n_chunks] + 4) * 64]                */
+    const uint32_t *row_off;    /* [n_chunks + 1], row_off[0] = 0               */
+    int64_t n_chunks;           /* ceil(n_symbols / 4096)                        */
+    const uint32_t *ulut1;      /* optional unified tables (cbq_huff_build_ulut) */
+    const uint32_t *ulut2;      /*   replacing hs->lut1 / lut2 in the GEMV; NULL */
+    int32_t n_ulut2;            /*   = use hs's tables                           */
+} cbq_huff_columns;
+
+/* Unified decode tables for bf16-value payloads of codes <= 24 bits (host
+ * only): every ulut1[4096] entry is (base << 18) | nb and the code's leaf is
+ * ulut2[base + next nb stream bits] (short codes: nb = 0, one leaf per
+ * symbol), so the GEMV step needs no leaf/pointer select.  Leaves as lut2's.
+ * With ulut1 or ulut2 NULL only *n_ulut2 is written.  CK_ERR_ARG for
+ * invalid lengths, codes beyond 24 bits or more than 16383 entries. */
+int cbq_huff_build_ulut(const uint8_t *lengths, int n_alpha, const float *codebook, int C,
+                        uint32_t *ulut1, uint32_t *ulut2, int *n_ulut2);
+
+/* rows[c] = max(1, max_l ceil(sub_len[64 c + l] / 32)) for every chunk; the
+ * caller's exclusive prefix sum of rows is row_off.  Needs hs->sub_len. */
+int cbq_huff_column_rows(const cbq_huff_stream *hs, int64_t n_symbols, uint32_t *rows,
+                         hipStream_t stream);
+
+/* Fill cwords (zeroed by the caller, (row_off[n_chunks] + 4) * 64 words)
+ * from the stream's words / chunk_off / sub_len. */
+int cbq_huff_columnize(const cbq_huff_stream *hs, int64_t n_symbols, const uint32_t *row_off,
+                       uint32_t *cwords, hipStream_t stream);
+
+/* cbq_huff_linear_f32 for T = 1 over the column layout: out[m] =
+ * sum_k x[k] * value(decode(m*K + k)).  Uses hs's tables only (bf16-value
+ * payloads, value_cb NULL, n_lut2 <= 8192); K % 4096 == 0.  Same result as
+ * cbq_huff_linear_f32 (same per-lane accumulation order). */
+int cbq_huff_linear_col_f32(const float *x, const cbq_huff_stream *hs,
+                            const cbq_huff_columns *cols, float *out, int M, int K,
+                            hipStream_t stream);
+
 /* Decode flat symbols [0, n_symbols) to int32 with the chunked kernel (lut
  * payloads must be raw symbols).  The bit-exact check of the fused decoder;
  * the equivalent of huffman_decode_to_weights_f32 with an identity codebook
