@@ -48,6 +48,8 @@ SIGNATURES = {
     "cbq_version": (ctypes.c_char_p, []),
     "ck_linear_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "ck_linear_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "cbq_linear_affine_f32": (_i, [_vp, _vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _i, _i, _i, _i,
+                                   _vp]),
     "ck_embedding_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "cbq_embedding_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "huff_decode_to_i32": (_i, [_vp] * 8 + [_i, _i, _i, _vp]),

@@ -14,6 +14,8 @@
 // output written.
 #include "cbq_device.h"
 
+#include <cstdlib>
+
 #include <algorithm>
 
 namespace {
@@ -292,6 +294,18 @@ __device__ __forceinline__ void group_offsets(const uint32_t (&w)[BITS], uint32_
     }
 }
 
+// The 32 raw BITS-wide indices of a lane's group.
+template <int BITS>
+__device__ __forceinline__ void group_indices(const uint32_t (&w)[BITS], uint32_t idx[32])
+{
+    constexpr uint32_t m = (1u << BITS) - 1u;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        const int o = j * BITS, q = o >> 5, s = o & 31;
+        idx[j] = (s + BITS <= 32) ? ((w[q] >> s) & m) : (funnel(w[q + 1], w[q], (uint32_t)s) & m);
+    }
+}
+
 // x staged in LDS as raw XT bits, one row of K per token.  A 32-element group
 // (128 B fp32 / 64 B bf16) is stored as 16-byte chunks in swizzled order, so
 // the ds_read_b128 of 8 neighbouring lanes hit distinct bank groups.
@@ -331,17 +345,22 @@ template <> struct XStage<uint16_t> {
     }
 };
 
-template <int BITS, int TMAX, typename XT, typename OT>
+// AFFINE: no codebook table; index i stands for the bf16 value with bits
+// aff_lo + i (i < aff_w), 0x8000 + aff_lo + i - aff_w (i < 2 aff_w), else 0:
+// the re-indexed form of a codebook whose nonzero values all have bf16
+// magnitudes in [aff_lo, aff_lo + aff_w) (cbq_linear_affine_f32).
+template <int BITS, int TMAX, typename XT, typename OT, bool AFFINE = false>
 __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     const XT *__restrict__ x, const uint32_t *__restrict__ words,
-    const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C)
+    const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C,
+    uint32_t aff_lo, uint32_t aff_w)
 {
-    constexpr bool PADDED = BITS <= 14;
+    constexpr bool PADDED = BITS <= 14 && !AFFINE;
     constexpr int D = kStreamD;
     __shared__ float s_cbp[PADDED ? (1 << BITS) : 1];
     extern __shared__ float s_dyn[];
     const int C_eff = C < (1 << BITS) ? C : (1 << BITS);
-    const int cb_slots = PADDED ? (1 << BITS) : ((C_eff + 63) & ~63);
+    const int cb_slots = AFFINE ? 0 : PADDED ? (1 << BITS) : ((C_eff + 63) & ~63);
     float *s_cb = PADDED ? s_cbp : s_dyn;
     uint32_t *s_x = (uint32_t *)(PADDED ? s_dyn : s_dyn + cb_slots);
 
@@ -380,7 +399,8 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     asm volatile("v_mov_b32 %0, 0" : "=v"(zero) : : "memory");
 
     auto item_ptr = [&](int item) {
-        const int it = item < n_items ? item : 0;
+        // past the wave's last item: re-read the last one (an L2 hit, no HBM traffic)
+        const int it = item < n_items ? item : (n_items > 0 ? n_items - 1 : 0);
         const int ri = it / NGW, ch = it - ri * NGW;
         int g = ch * CBQ_WAVE + lane;
         g = g < G ? g : G - 1;
@@ -408,11 +428,22 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
             const int g = ch * CBQ_WAVE + lane;
             const int gg = g < G ? g : G - 1;
             const bool valid = item < n_items && g < G;
-            uint32_t off[32];
-            group_offsets<BITS, PADDED>(buf[d], cmax4, off);
             float wv[32];
+            if constexpr (AFFINE) {
+                uint32_t idx[32];
+                group_indices<BITS>(buf[d], idx);
+                const uint32_t neg = aff_lo + 0x8000u - aff_w, w2 = 2u * aff_w;
 #pragma unroll
-            for (int j = 0; j < 32; j++) wv[j] = *(const float *)((const char *)s_cb + off[j]);
+                for (int j = 0; j < 32; j++) {
+                    const uint32_t b = (idx[j] + (idx[j] < aff_w ? aff_lo : neg)) << 16;
+                    wv[j] = __uint_as_float(idx[j] < w2 ? b : 0u);      // index 2w: zero
+                }
+            } else {
+                uint32_t off[32];
+                group_offsets<BITS, PADDED>(buf[d], cmax4, off);
+#pragma unroll
+                for (int j = 0; j < 32; j++) wv[j] = *(const float *)((const char *)s_cb + off[j]);
+            }
 #pragma unroll
             for (int t = 0; t < TMAX; t++) {
                 if (t < T) {
@@ -597,16 +628,46 @@ int dispatch_x(const XT *x, const uint8_t *packed, const float *cb, OT *out, int
     return launch_fast<BITS, TMAX, 0>(x, packed, cb, out, T, M, K, C, st);       // x via cache
 }
 
+int stream_bpc()
+{
+    const char *e = getenv("CBQ_STREAM_BPC");
+    return e ? atoi(e) : 1;
+}
+
 template <int BITS, int TMAX, typename XT, typename OT>
 int launch_stream(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T, int M,
                   int K, int C, size_t dyn_lds, hipStream_t st)
 {
     const int blocks =
-        std::max(1, std::min(cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
+        std::max(1, std::min(stream_bpc() * cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
     hipLaunchKernelGGL((fixed_stream_kernel<BITS, TMAX, XT, OT>), dim3(blocks),
                        dim3(kStreamBlock), dyn_lds, st, x, (const uint32_t *)packed, cb, out, T,
-                       M, K, C);
+                       M, K, C, 0u, 0u);
     return cbq_launch_status("fixed_stream_kernel");
+}
+
+template <int BITS, int TMAX>
+int launch_affine(const float *x, const uint8_t *packed, uint32_t lo, uint32_t w, float *out,
+                  int T, int M, int K, size_t dyn_lds, hipStream_t st)
+{
+    const int blocks =
+        std::max(1, std::min(stream_bpc() * cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
+    hipLaunchKernelGGL((fixed_stream_kernel<BITS, TMAX, float, float, true>), dim3(blocks),
+                       dim3(kStreamBlock), dyn_lds, st, x, (const uint32_t *)packed,
+                       (const float *)nullptr, out, T, M, K, 1, lo, w);
+    return cbq_launch_status("fixed_stream_kernel<affine>");
+}
+
+template <int BITS>
+int dispatch_affine(const float *x, const uint8_t *packed, uint32_t lo, uint32_t w, float *out,
+                    int T, int M, int K, hipStream_t st)
+{
+    const size_t n_xdw = (size_t)T * (K / 32) * XStage<float>::kGroupDw;
+    const size_t dyn = ((n_xdw + 63) & ~(size_t)63) * 4;
+    if (dyn > (size_t)kStreamLds) return CK_ERR_ARG;
+    if (T == 1) return launch_affine<BITS, 1>(x, packed, lo, w, out, T, M, K, dyn, st);
+    if (T <= 4) return launch_affine<BITS, 4>(x, packed, lo, w, out, T, M, K, dyn, st);
+    return launch_affine<BITS, 16>(x, packed, lo, w, out, T, M, K, dyn, st);
 }
 
 // Dynamic LDS the streaming kernel needs (0 if it does not fit): unpadded
@@ -761,6 +822,31 @@ int ck_linear_f32(const float *x, const uint8_t *packed, const float *codebook, 
                   int T, int M, int K, int C, int bits, hipStream_t stream)
 {
     return linear_any_t<float, float>(x, packed, codebook, out, T, M, K, C, bits, stream);
+}
+
+int cbq_linear_affine_f32(const float *x, const uint8_t *packed, uint32_t lo, uint32_t w,
+                          float *out, int T, int M, int K, int bits, hipStream_t stream)
+{
+    if (!x || !packed || !out || T <= 0 || M <= 0 || K <= 0 || K % 32 != 0) return CK_ERR_ARG;
+    if (((uintptr_t)x & 3) || ((uintptr_t)packed & 3)) return CK_ERR_ARG;
+    if (w == 0 || lo == 0 || lo + w > 0x8000u || 2ull * w > (1ull << bits)) return CK_ERR_ARG;
+    for (int t0 = 0; t0 < T; t0 += 16) {
+        const int tt = std::min(16, T - t0);
+        const float *xt = x + (size_t)t0 * K;
+        float *ot = out + (size_t)t0 * M;
+        int rc;
+        switch (bits) {
+        case 8: rc = dispatch_affine<8>(xt, packed, lo, w, ot, tt, M, K, stream); break;
+        case 10: rc = dispatch_affine<10>(xt, packed, lo, w, ot, tt, M, K, stream); break;
+        case 11: rc = dispatch_affine<11>(xt, packed, lo, w, ot, tt, M, K, stream); break;
+        case 12: rc = dispatch_affine<12>(xt, packed, lo, w, ot, tt, M, K, stream); break;
+        case 13: rc = dispatch_affine<13>(xt, packed, lo, w, ot, tt, M, K, stream); break;
+        case 14: rc = dispatch_affine<14>(xt, packed, lo, w, ot, tt, M, K, stream); break;
+        default: return CK_ERR_ARG;
+        }
+        if (rc) return rc;
+    }
+    return CK_SUCCESS;
 }
 
 int ck_linear_bf16(const void *x_bf16, const uint8_t *packed, const float *codebook,

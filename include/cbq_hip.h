@@ -46,6 +46,19 @@ int ck_linear_f32(const float *x, const uint8_t *packed, const float *codebook,
                   float *out, int T, int M, int K, int C, int bits,
                   hipStream_t stream);
 
+/* Fixed-width GEMV with an implicit (affine) codebook: index i stands for
+ * the bf16 value with bit pattern lo + i (i < w), 0x8000 + lo + i - w
+ * (w <= i < 2w), and 0.0 for i >= 2w.  This is the load-time re-indexed
+ * form of a lossless bf16 codebook whose nonzero magnitudes all lie in
+ * [lo, lo + w) (every frequency-sorted codebook of normally distributed
+ * weights qualifies); the decoded weights are the codebook's values
+ * bit-for-bit, without an LDS table gather.  float32 x/out, any T (tiles of
+ * 16); K % 32 == 0; x and packed 4-byte aligned; 1 <= lo, lo + w <= 0x8000,
+ * 2w <= 2^bits, bits in {8, 10..14}.  No counterpart in the reference: an
+ * alternative resident form behind ck_linear_f32's interface. */
+int cbq_linear_affine_f32(const float *x, const uint8_t *packed, uint32_t lo, uint32_t w,
+                          float *out, int T, int M, int K, int bits, hipStream_t stream);
+
 /* Same with bfloat16 x and out (raw uint16 bf16 bit patterns; out rounded to
  * nearest even).  Replaces ck_linear_bf16 (rocm/compressed_kernel.h:66-73). */
 int ck_linear_bf16(const void *x_bf16, const uint8_t *packed, const float *codebook,
