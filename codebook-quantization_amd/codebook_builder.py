@@ -139,3 +139,27 @@ def pack_torch(idx: torch.Tensor, bits: int) -> torch.Tensor:
         out.index_add_(0, w[spill] + 1, i64[spill] >> (64 - sh[spill]))
     nbytes = (n * bits + 7) // 8
     return out.view(torch.uint8)[:nbytes]
+
+
+def affine_form(codebook, bits: int):
+    """(lo, w, remap) when the codebook's values are bf16 numbers whose
+    nonzero magnitudes (bf16 bit patterns without sign) all lie in
+    [lo, lo + w) with 2w + 1 <= 2^bits, else None.  remap[i] is the
+    implicit-codebook index of entry i for cbq_linear_affine_f32: the
+    magnitude offset for positive values, w + offset for negative ones, 2w
+    for +-0."""
+    cb = np.ascontiguousarray(codebook, np.float32).reshape(-1)
+    u = cb.view(np.uint32)
+    if cb.size == 0 or (u & 0xFFFF).any():
+        return None
+    v16 = (u >> 16).astype(np.int64)
+    mag, sign = v16 & 0x7FFF, v16 >> 15
+    nz = mag > 0
+    if not nz.any():
+        return None
+    lo = int(mag[nz].min())
+    w = int(mag[nz].max()) - lo + 1
+    if 2 * w + 1 > (1 << bits) or lo + w > 0x8000:
+        return None
+    remap = np.where(nz, (mag - lo) + sign * w, 2 * w).astype(np.int64)
+    return lo, w, remap

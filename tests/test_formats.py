@@ -246,3 +246,10 @@ def test_stage_words():
     co = np.array([0, 40000, 80100, 90000], np.uint64)
     sw = hc.stage_words_for(co)
     assert sw % 64 == 0 and sw >= (80100 + 31) // 32 - 40000 // 32 + 2
+
+
+def test_affine_form_rejects_wide_or_non_bf16():
+    assert cbb.affine_form(np.array([1.0, 1e-30, -3e3], np.float32), 8) is None   # too wide
+    assert cbb.affine_form(np.array([0.1, 0.2], np.float32), 13) is None          # not bf16
+    lo, w, remap = cbb.affine_form(np.array([0.5, -0.5, 0.0, 0.75], np.float32), 8)
+    assert list(remap) == [0, w, 2 * w, remap[3]] and remap[3] < w

@@ -169,3 +169,40 @@ def test_embedding_clamps_ids(cuda, oracle):
     assert out.shape == (1, 3, H)
     assert np.array_equal(out[0, 0], cb[raw[:H]])
     assert np.array_equal(out[0, 2], cb[raw[(vocab - 1) * H:]])
+
+
+@pytest.mark.parametrize("T", [1, 3, 20])
+def test_affine_implicit_codebook_bit_exact(cuda, oracle, T):
+    """cbq_linear_affine_f32 over re-indexed weights equals ck_linear_f32 over
+    the frequency-sorted codebook bit for bit (same values, same order of
+    accumulation), zeros of either sign included; and matches the oracle."""
+    import bitpack
+    import cbq_native as nat
+    rng = np.random.default_rng(40 + T)
+    M, K = 200, 1024
+    w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
+    w[3, 7], w[150, 1000] = 0.0, -0.0
+    cb, idx = cbb.frequency_sorted_codebook(w)
+    bits = 13                  # the 9B-shape width; a small sample's codebook is narrower
+    assert len(cb) <= 1 << bits
+    aff = cbb.affine_form(cb, bits)
+    assert aff is not None
+    lo, wid, remap = aff
+    packed = bitpack.device_padded(bitpack.pack_any_bits(idx.reshape(-1), bits))
+    packed_aff = bitpack.device_padded(bitpack.pack_any_bits(remap[idx.reshape(-1)], bits))
+    lib = nat.load()
+    x = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).to(cuda)
+    cbt = torch.from_numpy(cb).to(cuda)
+    pk = torch.from_numpy(packed).to(cuda)
+    pka = torch.from_numpy(packed_aff).to(cuda)
+    y = torch.empty(T, M, device=cuda)
+    ya = torch.empty(T, M, device=cuda)
+    st = nat.stream_ptr(cuda)
+    nat.check(lib.ck_linear_f32(x.data_ptr(), pk.data_ptr(), cbt.data_ptr(), y.data_ptr(), T, M, K,
+                                len(cb), bits, st), "table")
+    nat.check(lib.cbq_linear_affine_f32(x.data_ptr(), pka.data_ptr(), lo, wid, ya.data_ptr(), T, M,
+                                        K, bits, st), "affine")
+    assert torch.equal(y, ya)
+    ref = oracle.fixed_gemv(x.cpu().numpy(), packed, cb, M, K, bits)
+    assert rel_l2(ya.cpu().numpy(), ref) <= 1e-5
+
