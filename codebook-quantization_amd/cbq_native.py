@@ -65,6 +65,7 @@ SIGNATURES = {
     "cbq_huff_columnize": (_i, [ctypes.POINTER(HuffStream), _i64, _vp, _vp, _vp]),
     "cbq_huff_linear_col_f32": (_i, [_vp, ctypes.POINTER(HuffStream), ctypes.POINTER(HuffColumns),
                                      _vp, _i, _i, _vp]),
+    "cbq_huff_linear_col_multi_f32": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _vp]),
     # include/cbq_decode.h
     "cbq_add_rmsnorm_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, ctypes.c_float, _vp]),
     "cbq_head_norm_rope_f32": (_i, [_vp] * 11 + [_i] * 5 + [ctypes.c_float, _vp]),

@@ -849,15 +849,44 @@ __device__ __forceinline__ uint32_t col_window_global(const uint32_t *__restrict
     return funnel(cwords[w + kSub], cwords[w], pos);
 }
 
+// One matrix of a (possibly grouped) column GEMV launch: blocks
+// [block0, block0 + nblocks) of the grid compute out = W x for it.
+struct ColSeg {
+    HuffArgs a;
+    const uint32_t *cwords;
+    const uint32_t *row_off;
+    float *out;
+    int M;
+    int block0;
+    int nblocks;
+};
+constexpr int kColMaxSeg = 4;
+struct ColSegs {
+    ColSeg s[kColMaxSeg];
+    int n;
+};
+
 // Fused GEMV over the column layout, T = 1, bf16-value payloads, K % 4096 == 0.
 // LDS as huff_tile_fast_kernel (lut2 at 0, lut1, swizzled x tile, 16 slots of
-// 24 rows); one chunk per wave step.
+// 24 rows); one chunk per wave step.  A grouped launch runs up to four
+// matrices that share x (one layer's q/k/v): each block serves one of them
+// and stages that matrix's tables.
 template <int NW, bool UNIFIED>
-__global__ __launch_bounds__(NW * CBQ_WAVE) void huff_col_kernel(
-    const float *__restrict__ x, float *__restrict__ out, HuffArgs a,
-    const uint32_t *__restrict__ cwords, const uint32_t *__restrict__ row_off, int M, int K)
+__global__ __launch_bounds__(NW * CBQ_WAVE) void huff_col_kernel(const float *__restrict__ x,
+                                                                ColSegs segs, int K)
 {
     static_assert(NW <= kFastChains, "one slot per wave");
+    int sidx = 0;
+#pragma unroll
+    for (int i = 1; i < kColMaxSeg; i++)
+        if (i < segs.n && (int)blockIdx.x >= segs.s[i].block0) sidx = i;
+    const ColSeg &S = segs.s[sidx];
+    const HuffArgs a = S.a;
+    const uint32_t *__restrict__ cwords = S.cwords;
+    const uint32_t *__restrict__ row_off = S.row_off;
+    float *__restrict__ out = S.out;
+    const int M = S.M;
+    const int bid = (int)blockIdx.x - S.block0;             // block within its matrix
     __shared__ __attribute__((aligned(16))) uint32_t s_lds[kFastLdsWords];
     uint32_t *const s_lut2 = s_lds;
     uint32_t *const s_lut1 = s_lds + kFOffLut1;
@@ -891,10 +920,10 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void huff_col_kernel(
     const bool general = !UNIFIED && any_unresolved != 0;
 
     const int R = K / kChunk;
-    const int W = gridDim.x * NW;
-    const int wid = blockIdx.x * NW + wave;
+    const int W = S.nblocks * NW;
+    const int wid = bid * NW + wave;
     const int rows = wid < M ? (M - wid + W - 1) / W : 0;
-    const int b0 = blockIdx.x * NW;
+    const int b0 = bid * NW;
     const int rows_max = b0 < M ? (M - b0 + W - 1) / W : 0;
     const int n_seg = (rows_max + 63) >> 6;
     const float *const xr = s_x + lane * 64;
@@ -1558,46 +1587,76 @@ int cbq_huff_columnize(const cbq_huff_stream *hs, int64_t n_symbols, const uint3
     return cbq_launch_status("columnize_kernel");
 }
 
-int cbq_huff_linear_col_f32(const float *x, const cbq_huff_stream *hs,
-                            const cbq_huff_columns *cols, float *out, int M, int K,
-                            hipStream_t stream)
+int cbq_huff_linear_col_multi_f32(const float *x, int n, const cbq_huff_stream *const *hs,
+                                  const cbq_huff_columns *const *cols, float *const *outs,
+                                  const int *Ms, int K, hipStream_t stream)
 {
-    if (!x || !out || !hs || !cols || M <= 0 || K <= 0 || K % kChunk != 0) return CK_ERR_ARG;
-    if (!hs->lut1 || !hs->lut2 || hs->n_lut2 < 1 || hs->n_lut2 > kFastLut2 || !hs->canon ||
-        !hs->canon_pay || hs->value_cb != nullptr)
+    if (!x || n < 1 || n > kColMaxSeg || !hs || !cols || !outs || !Ms || K <= 0 ||
+        K % kChunk != 0)
         return CK_ERR_ARG;
-    if (!cols->cwords || !cols->row_off || cols->n_chunks != (int64_t)M * K / kChunk)
-        return CK_ERR_ARG;
-    HuffArgs a = {};
-    a.lut1 = hs->lut1; a.lut2 = hs->lut2; a.n_lut2 = hs->n_lut2;
-    a.canon = hs->canon; a.canon_pay = hs->canon_pay; a.C = hs->C;
-    a.n_sym = (int64_t)M * K; a.n_chunks = cols->n_chunks; a.n_sub = a.n_sym / kSub;
-    const bool unified = cols->ulut1 && cols->ulut2 && cols->n_ulut2 >= 1 &&
-                         cols->n_ulut2 <= kFastLut2;
-    if (unified) { a.lut1 = cols->ulut1; a.lut2 = cols->ulut2; a.n_lut2 = cols->n_ulut2; }
+    ColSegs segs = {};
+    segs.n = n;
+    bool unified = true;
+    int m_max = 0;
+    for (int i = 0; i < n; i++) {
+        const cbq_huff_stream *h = hs[i];
+        const cbq_huff_columns *c = cols[i];
+        const int M = Ms[i];
+        if (!h || !c || !outs[i] || M <= 0) return CK_ERR_ARG;
+        if (!h->lut1 || !h->lut2 || h->n_lut2 < 1 || h->n_lut2 > kFastLut2 || !h->canon ||
+            !h->canon_pay || h->value_cb != nullptr)
+            return CK_ERR_ARG;
+        if (!c->cwords || !c->row_off || c->n_chunks != (int64_t)M * K / kChunk) return CK_ERR_ARG;
+        unified = unified && c->ulut1 && c->ulut2 && c->n_ulut2 >= 1 && c->n_ulut2 <= kFastLut2;
+        m_max = std::max(m_max, M);
+    }
     // Waves per block (one block per CU: the LDS is static): 16 when every CU
-    // gets >= 16 rows, else fewer so that small matrices still reach all CUs.
-    // MI355X, 1024 x 4096: 16 waves 14.7 us, 4 waves 13.7 us; 4096 x 4096: 16
-    // waves 17.9 us, 8 waves 23.4 us.  A step is a chain of three dependent
-    // LDS reads (~440 cycles), so throughput scales with resident waves.
-    const int per = M / cbq_num_cus();
+    // gets >= 16 rows of the largest matrix, else fewer so that small matrices
+    // still reach all CUs.  MI355X, 1024 x 4096: 16 waves 14.7 us, 4 waves
+    // 13.7 us; 4096 x 4096: 16 waves 17.9 us, 8 waves 23.4 us.  A step is a
+    // chain of three dependent LDS reads (~440 cycles), so throughput scales
+    // with resident waves.
+    const int per = m_max / cbq_num_cus();
     const int nw = per >= 16 ? 16 : per >= 8 ? 8 : 4;
-    const int blocks = std::max(1, std::min(cbq_num_cus(), (M + nw - 1) / nw));
+    int blocks = 0;
+    for (int i = 0; i < n; i++) {
+        ColSeg &g = segs.s[i];
+        const int M = Ms[i];
+        HuffArgs &a = g.a;
+        a = HuffArgs{};
+        if (unified) {
+            a.lut1 = cols[i]->ulut1; a.lut2 = cols[i]->ulut2; a.n_lut2 = cols[i]->n_ulut2;
+        } else {
+            a.lut1 = hs[i]->lut1; a.lut2 = hs[i]->lut2; a.n_lut2 = hs[i]->n_lut2;
+        }
+        a.canon = hs[i]->canon; a.canon_pay = hs[i]->canon_pay; a.C = hs[i]->C;
+        a.n_sym = (int64_t)M * K; a.n_chunks = cols[i]->n_chunks; a.n_sub = a.n_sym / kSub;
+        g.cwords = cols[i]->cwords; g.row_off = cols[i]->row_off; g.out = outs[i]; g.M = M;
+        g.block0 = blocks;
+        g.nblocks = std::max(1, std::min(cbq_num_cus(), (M + nw - 1) / nw));
+        blocks += g.nblocks;
+    }
 #define CBQ_COL_LAUNCH(NWV)                                                                    \
     do {                                                                                       \
         if (unified)                                                                           \
             hipLaunchKernelGGL((huff_col_kernel<NWV, true>), dim3(blocks), dim3(NWV * CBQ_WAVE), \
-                               0, stream, x, out, a, cols->cwords, cols->row_off, M, K);       \
+                               0, stream, x, segs, K);                                          \
         else                                                                                   \
             hipLaunchKernelGGL((huff_col_kernel<NWV, false>), dim3(blocks),                    \
-                               dim3(NWV * CBQ_WAVE), 0, stream, x, out, a, cols->cwords,       \
-                               cols->row_off, M, K);                                           \
+                               dim3(NWV * CBQ_WAVE), 0, stream, x, segs, K);                    \
     } while (0)
     if (nw == 4) CBQ_COL_LAUNCH(4);
     else if (nw == 8) CBQ_COL_LAUNCH(8);
     else CBQ_COL_LAUNCH(16);
 #undef CBQ_COL_LAUNCH
     return cbq_launch_status("huff_col_kernel");
+}
+
+int cbq_huff_linear_col_f32(const float *x, const cbq_huff_stream *hs,
+                            const cbq_huff_columns *cols, float *out, int M, int K,
+                            hipStream_t stream)
+{
+    return cbq_huff_linear_col_multi_f32(x, 1, &hs, &cols, &out, &M, K, stream);
 }
 
 int cbq_huff_embedding_f32(const int32_t *token_ids, const cbq_huff_stream *hs, float *out,

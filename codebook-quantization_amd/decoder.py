@@ -331,9 +331,10 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                    max_len: int = 512, stack: bool = True) -> Qwen3Decoder:
     """Decoder over device-resident synthetic tensors (synthetic.FixedTensor /
     HuffTensor, built on the GPU for the 9B-shape bench); calls the C ABI
-    directly on torch's current stream.  With stack, each layer's fixed-width
-    q/k/v and gate/up are row-stacked into one matrix each (one GEMV launch
-    instead of three / two)."""
+    directly on torch's current stream.  With stack, each layer's q/k/v and
+    gate/up run as one GEMV launch each instead of three / two: fixed-width
+    rows are stacked into one matrix, Huffman matrices (one code each) share
+    a grouped launch."""
     import ctypes
     import cbq_native as nat
     import synthetic
@@ -363,11 +364,11 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                               canon_pay=tb["pay"].data_ptr(), value_cb=None,
                               C=tb["codebook"].numel(), stage_words=tb["stage_words"])
 
-    def huff_linear(t):
+    def huff_linear(t, with_cols=True):
         M, K = t.shape
         desc = huff_desc(t)
         cols = None
-        if columns_eligible(desc, K):            # single-token GEMV on the column layout
+        if with_cols and columns_eligible(desc, K):   # single-token GEMV on the column layout
             cols = build_columns(desc, M * K, dev, t.lengths, t.tables["codebook"].cpu().numpy())
 
         def f(x, desc=desc, cols=cols):
@@ -387,6 +388,41 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                                                   nat.stream_ptr(dev)), "cbq_huff_linear_f32")
             return out
         f.desc = desc
+        return f
+
+    def huff_group(ts, name):
+        """One grouped column-GEMV launch for matrices sharing x (q/k/v,
+        gate/up), each with its own code; None when a part does not
+        qualify for the column layout."""
+        K = ts[0].shape[1]
+        descs = [huff_desc(t) for t in ts]
+        if any(t.shape[1] != K for t in ts) or not all(columns_eligible(d, K) for d in descs):
+            return None
+        cols = [build_columns(d, t.shape[0] * K, dev, t.lengths, t.tables["codebook"].cpu().numpy())
+                for d, t in zip(descs, ts)]
+        Ms = [t.shape[0] for t in ts]
+        n = len(ts)
+        hs_arr = (ctypes.POINTER(nat.HuffStream) * n)(*[ctypes.pointer(d) for d in descs])
+        col_arr = (ctypes.POINTER(nat.HuffColumns) * n)(*[ctypes.pointer(c[1]) for c in cols])
+        m_arr = (ctypes.c_int * n)(*Ms)
+        singles = [huff_linear(t, with_cols=False) for t in ts]   # multi-token calls, per part
+
+        def f(x, keep=(descs, cols, hs_arr, col_arr, m_arr)):
+            x = x.reshape(-1, K).contiguous()
+            T = x.shape[0]
+            if T > 1:
+                return torch.cat([g(x) for g in singles], dim=1)
+            out = torch.empty(1, sum(Ms), device=dev)
+            offs, o = [], 0
+            for M in Ms:
+                offs.append(out.data_ptr() + 4 * o)
+                o += M
+            out_arr = (ctypes.c_void_p * n)(*offs)
+            nat.check(lib.cbq_huff_linear_col_multi_f32(
+                x.data_ptr(), n, hs_arr, col_arr, out_arr, m_arr, K, nat.stream_ptr(dev)),
+                "cbq_huff_linear_col_multi_f32")
+            return out
+        f.name = name
         return f
 
     def embed_fn(t):
@@ -420,11 +456,16 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                                                      "self_attn.v_proj")),
                              ("mlp.gate_up_proj", ("mlp.gate_proj", "mlp.up_proj"))):
             ts = [tensors[p + n] for n in parts]
-            st = None
-            if stack and all(isinstance(t, synthetic.FixedTensor) for t in ts):
+            if not stack:
+                continue
+            if all(isinstance(t, synthetic.FixedTensor) for t in ts):
                 st = synthetic.stack_fixed(ts, p + fused)
-            if st is not None:
-                linears[p + fused] = fixed_linear(st)
+                if st is not None:
+                    linears[p + fused] = fixed_linear(st)
+            elif all(isinstance(t, synthetic.HuffTensor) for t in ts):
+                g = huff_group(ts, p + fused)
+                if g is not None:
+                    linears[p + fused] = g
     for n, _, _ in cfg.linear_shapes():
         t = tensors[n]
         stem, _, leaf = n.rpartition(".")

@@ -222,6 +222,16 @@ int cbq_huff_linear_col_f32(const float *x, const cbq_huff_stream *hs,
                             const cbq_huff_columns *cols, float *out, int M, int K,
                             hipStream_t stream);
 
+/* One launch of cbq_huff_linear_col_f32 for n <= 4 matrices that share x
+ * and K (a layer's q/k/v, each with its own Huffman code): outs[i] =
+ * W_i x, W_i [Ms[i], K] described by hs[i] / cols[i] (host arrays of
+ * pointers).  Each block of the grid serves one matrix, so small matrices
+ * run side by side instead of one after another.  No counterpart in the
+ * reference.  Results equal n single calls bit for bit. */
+int cbq_huff_linear_col_multi_f32(const float *x, int n, const cbq_huff_stream *const *hs,
+                                  const cbq_huff_columns *const *cols, float *const *outs,
+                                  const int *Ms, int K, hipStream_t stream);
+
 /* Decode flat symbols [0, n_symbols) to int32 with the chunked kernel (lut
  * payloads must be raw symbols).  The bit-exact check of the fused decoder;
  * the equivalent of huffman_decode_to_weights_f32 with an identity codebook

@@ -67,3 +67,64 @@ def test_stacked_decoder_tokens(cuda, built):
     tb = b.generate_graph(prompt, 12)
     assert ta == tb
     assert b.generate(prompt, 12) == tb                     # eager loop agrees too
+
+
+@pytest.fixture(scope="module")
+def built_huff(cuda):
+    dec = synthetic.SyntheticDecoder("qwen3-8b", layers=2, log=lambda *a: None)
+    names = dec.all_linears() + [dec.embed]
+    return dec, dec.build_huffman(names)
+
+
+def test_grouped_huffman_launch_equals_single(cuda, built_huff):
+    """cbq_huff_linear_col_multi_f32 over a layer's q/k/v (three codes)
+    equals three single column GEMVs bit for bit."""
+    from gpu_huffman_functions import build_columns
+    dec, tensors = built_huff
+    lib = nat.load()
+    p = "model.layers.1."
+    ts = [tensors[p + n] for n in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj")]
+    K = 4096
+    descs, cols = [], []
+    for t in ts:
+        tb = t.tables
+        d = nat.HuffStream(words=t.words.data_ptr(), n_words=t.words.numel(),
+                           chunk_off=t.chunk_off.data_ptr(), sub_len=t.sub_len.data_ptr(),
+                           lut1=tb["lut1"].data_ptr(), lut2=tb["lut2"].data_ptr(),
+                           n_lut2=tb["lut2"].numel(), canon=tb["canon"].data_ptr(),
+                           canon_pay=tb["pay"].data_ptr(), value_cb=None,
+                           C=tb["codebook"].numel(), stage_words=tb["stage_words"])
+        descs.append(d)
+        cols.append(build_columns(d, t.shape[0] * K, cuda, t.lengths,
+                                  tb["codebook"].cpu().numpy()))
+    x = torch.randn(1, K, device=cuda)
+    Ms = [t.shape[0] for t in ts]
+    y = torch.empty(1, sum(Ms), device=cuda)
+    st = nat.stream_ptr(cuda)
+    offs = [y.data_ptr() + 4 * sum(Ms[:i]) for i in range(3)]
+    nat.check(lib.cbq_huff_linear_col_multi_f32(
+        x.data_ptr(), 3, (ctypes.POINTER(nat.HuffStream) * 3)(*[ctypes.pointer(d) for d in descs]),
+        (ctypes.POINTER(nat.HuffColumns) * 3)(*[ctypes.pointer(c[1]) for c in cols]),
+        (ctypes.c_void_p * 3)(*offs), (ctypes.c_int * 3)(*Ms), K, st), "multi")
+    o = 0
+    for d, c, M in zip(descs, cols, Ms):
+        ys = torch.empty(1, M, device=cuda)
+        nat.check(lib.cbq_huff_linear_col_f32(x.data_ptr(), ctypes.byref(d), ctypes.byref(c[1]),
+                                              ys.data_ptr(), M, K, st), "single")
+        assert torch.equal(y[:, o:o + M], ys)
+        o += M
+
+
+def test_grouped_huffman_decoder_tokens(cuda, built_huff):
+    dec, tensors = built_huff
+    c = dec.cfg
+    cfg = decoder.DecoderConfig(layers=c["layers"], hidden=c["hidden"], inter=c["inter"],
+                                n_q=c["n_q"], n_kv=c["n_kv"], head_dim=c["head_dim"],
+                                vocab=c["vocab"])
+    prompt = list(range(300, 316))
+    a = decoder.from_synthetic(cfg, tensors, max_len=40, stack=True)
+    assert "model.layers.0.self_attn.qkv_proj" in a.linears
+    ta = a.generate_graph(prompt, 10)
+    del a
+    b = decoder.from_synthetic(cfg, tensors, max_len=40, stack=False)
+    assert ta == b.generate_graph(prompt, 10)
