@@ -18,6 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 SO_PATH = os.path.join(HERE, "libcbq_hip.so")
 
 CK_SUCCESS, CK_ERR_HIP, CK_ERR_ARG = 0, 1, 2
+XF_SILU, XF_ADD_RMS, XF_RMS = 1, 2, 3            # CBQ_XF_* of include/cbq_hip.h
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -66,6 +67,10 @@ SIGNATURES = {
     "cbq_huff_linear_col_f32": (_i, [_vp, ctypes.POINTER(HuffStream), ctypes.POINTER(HuffColumns),
                                      _vp, _i, _i, _vp]),
     "cbq_huff_linear_col_multi_f32": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _vp]),
+    "cbq_huff_linear_col_xform_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _i, _vp, _vp, _vp,
+                                           _vp, _i, _vp]),
+    "cbq_linear_xform_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _i, _i, _i,
+                                  _i, _vp]),
     # include/cbq_decode.h
     "cbq_add_rmsnorm_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, ctypes.c_float, _vp]),
     "cbq_head_norm_rope_f32": (_i, [_vp] * 11 + [_i] * 5 + [ctypes.c_float, _vp]),

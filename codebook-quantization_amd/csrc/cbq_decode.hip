@@ -11,6 +11,10 @@
 
 #include <math.h>
 
+// hipcc contracts a * b + c into an fma by default; the glue rounds each
+// product and sum on its own (explicit fmaf calls stay fused).
+#pragma clang fp contract(off)
+
 namespace {
 
 constexpr int kGlueBlock = 256;                     // 4 waves
@@ -79,7 +83,7 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
     }
     float ss = 0.f;
 #pragma unroll
-    for (int j = 0; j < kNormPer; j++) ss = __fadd_rn(ss, __fmul_rn(v[j], v[j]));
+    for (int j = 0; j < kNormPer; j++) ss = add_square(ss, v[j]);
     const float r = rsqrtf(block_sum(ss, s_red) / (float)H + eps);
 #pragma unroll
     for (int j = 0; j < kNormPer; j++) {
@@ -392,7 +396,7 @@ __global__ __launch_bounds__(kGlueBlock) void silu_mul_kernel(const float *__res
     const int64_t stride = (int64_t)gridDim.x * kGlueBlock;
     for (int64_t i = (int64_t)blockIdx.x * kGlueBlock + threadIdx.x; i < n; i += stride) {
         const float x = g[i];
-        out[i] = __fmul_rn(__fdiv_rn(x, __fadd_rn(1.0f, expf(-x))), u[i]);
+        out[i] = silu_mul_value(x, u[i]);
     }
 }
 

@@ -66,6 +66,47 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v)
     return v;
 }
 
+// The decoder's glue arithmetic, shared by the standalone glue kernels and
+// the GEMVs that fold the glue into their x staging, so that both paths
+// round alike.  hipcc contracts a * b + c into one fma by default, and
+// whether it does depends on the surrounding code; these helpers switch
+// contraction off, so every operation rounds on its own (as torch's
+// elementwise ops do) wherever they are inlined.
+
+// ss + v * v, two roundings.
+__device__ __forceinline__ float add_square(float ss, float v)
+{
+#pragma clang fp contract(off)
+    return ss + v * v;
+}
+
+// silu(g) * u = g / (1 + exp(-g)) * u, each step rounded.
+__device__ __forceinline__ float silu_mul_value(float g, float u)
+{
+#pragma clang fp contract(off)
+    return __fdiv_rn(g, 1.0f + expf(-g)) * u;
+}
+
+// The activation transforms a GEMV can apply while it stages x (T = 1):
+// 1: silu(x0) * x1; 2: rmsnorm(x0 + x1) (x0 + x1 also stored to h_out by
+// one block); 3: rmsnorm(x0).  Rounded as the separate decoder kernels
+// round, so fused and unfused paths give identical x.
+enum { XF_NONE = 0, XF_SILU = CBQ_XF_SILU, XF_ADD_RMS = CBQ_XF_ADD_RMS, XF_RMS = CBQ_XF_RMS };
+
+__device__ __forceinline__ float xform_value(int mode, const float *__restrict__ x0,
+                                             const float *__restrict__ x1, float *h_out,
+                                             bool store_h, int i, float r)
+{
+#pragma clang fp contract(off)
+    if (mode == XF_SILU) return silu_mul_value(x0[i], x1[i]);
+    float v = x0[i];
+    if (mode == XF_ADD_RMS) {
+        v = v + x1[i];
+        if (store_h) h_out[i] = v;
+    }
+    return v * r;
+}
+
 // Workgroup barrier for LDS hand-off only: waits for this wave's LDS
 // operations, then s_barrier.  Unlike __syncthreads() it does not wait for
 // outstanding global loads, so prefetched weight data stays in flight.
@@ -73,6 +114,88 @@ __device__ __forceinline__ void lds_barrier()
 {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
+
+// The glue-transformed x of a one-token GEMV, held in registers (K <= 16384).
+// Thread tid of an NTHR-thread block owns the elements i = vt + 1024 j
+// (i < K) of its virtual threads vt = tid + k NTHR, k < 1024 / NTHR,
+// j < 16.  load() only issues the global loads, so a kernel can start its
+// weight stream before finish() consumes them.  The RMSNorm sum runs in
+// exactly the order of a 1024-thread block whose thread vt adds the
+// squares of v[vt + 1024 j] for j = 0..15 (terms past K are +0), whose
+// waves reduce by wave_sum and whose 16 wave sums add in wave order: the
+// decoder's standalone RMSNorm kernel.
+template <int NTHR, int XMODE>
+struct GlueTile {
+    static_assert(1024 % NTHR == 0 && NTHR >= CBQ_WAVE, "block size divides 1024");
+    static constexpr int VPT = 1024 / NTHR;
+    static constexpr bool TWO = XMODE == XF_SILU || XMODE == XF_ADD_RMS;
+    float a[VPT][16];
+    float b[TWO ? VPT : 1][16];
+
+    __device__ __forceinline__ void load(const float *__restrict__ x0,
+                                         const float *__restrict__ x1, int K)
+    {
+#pragma unroll
+        for (int k = 0; k < VPT; k++)
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int i = (int)threadIdx.x + k * NTHR + j * 1024;
+                a[k][j] = i < K ? x0[i] : 0.f;
+                if constexpr (TWO) b[k][j] = i < K ? x1[i] : 0.f;
+            }
+    }
+
+    // Applies the transform in place; returns the RMSNorm scale (1 for
+    // SiLU).  Norm modes contain one block barrier (LDS only, global loads stay
+    // in flight) and use s_red16 (16
+    // floats of LDS, not written again before the next barrier).
+    __device__ __forceinline__ float finish(int K, float eps, float *s_red16)
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+        for (int k = 0; k < VPT; k++)
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                if constexpr (XMODE == XF_SILU) a[k][j] = silu_mul_value(a[k][j], b[k][j]);
+                if constexpr (XMODE == XF_ADD_RMS) a[k][j] = a[k][j] + b[k][j];
+            }
+        if constexpr (XMODE == XF_SILU) return 1.f;
+#pragma unroll
+        for (int k = 0; k < VPT; k++) {
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < 16; j++) ss = add_square(ss, a[k][j]);
+            ss = wave_sum(ss);
+            if ((threadIdx.x & (CBQ_WAVE - 1)) == 0)
+                s_red16[((int)threadIdx.x + k * NTHR) / CBQ_WAVE] = ss;
+        }
+        lds_barrier();
+        float t = 0.f;
+#pragma unroll
+        for (int w = 0; w < 16; w++) t += s_red16[w];
+        return rsqrtf(t / (float)K + eps);
+    }
+
+    // Element i of the staged x (v * r for the norms, v for SiLU).
+    __device__ __forceinline__ float value(int k, int j, float r) const
+    {
+#pragma clang fp contract(off)
+        return XMODE == XF_SILU ? a[k][j] : a[k][j] * r;
+    }
+
+    // x0 + x1 (ADD_RMS) to h_out.
+    __device__ __forceinline__ void store_sum(float *h_out, int K) const
+    {
+        if constexpr (XMODE == XF_ADD_RMS)
+#pragma unroll
+            for (int k = 0; k < VPT; k++)
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const int i = (int)threadIdx.x + k * NTHR + j * 1024;
+                    if (i < K) h_out[i] = a[k][j];
+                }
+    }
+};
 
 // b-bit field starting at bit `s` of the little-endian pair (hi:lo).
 __device__ __forceinline__ uint32_t funnel(uint32_t hi, uint32_t lo, uint32_t s)

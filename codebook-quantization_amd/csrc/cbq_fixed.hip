@@ -14,7 +14,6 @@
 // output written.
 #include "cbq_device.h"
 
-#include <cstdlib>
 
 #include <algorithm>
 
@@ -349,15 +348,20 @@ template <> struct XStage<uint16_t> {
 // aff_lo + i (i < aff_w), 0x8000 + aff_lo + i - aff_w (i < 2 aff_w), else 0:
 // the re-indexed form of a codebook whose nonzero values all have bf16
 // magnitudes in [aff_lo, aff_lo + aff_w) (cbq_linear_affine_f32).
-template <int BITS, int TMAX, typename XT, typename OT, bool AFFINE = false>
+// XMODE (T = 1, float x): x is staged as xform_value(XMODE, x, x1, ...) -
+// silu(x) * x1, or the RMSNorm of x (+ x1) with block 0 storing x + x1 to
+// h_out - so the decoder's separate glue launch disappears.
+template <int BITS, int TMAX, typename XT, typename OT, bool AFFINE = false, int XMODE = XF_NONE>
 __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     const XT *__restrict__ x, const uint32_t *__restrict__ words,
     const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C,
-    uint32_t aff_lo, uint32_t aff_w)
+    uint32_t aff_lo, uint32_t aff_w, const float *__restrict__ x1, float *__restrict__ h_out,
+    float eps)
 {
     constexpr bool PADDED = BITS <= 14 && !AFFINE;
     constexpr int D = kStreamD;
     __shared__ float s_cbp[PADDED ? (1 << BITS) : 1];
+    __shared__ float s_red16[XMODE >= XF_ADD_RMS ? 16 : 1];
     extern __shared__ float s_dyn[];
     const int C_eff = C < (1 << BITS) ? C : (1 << BITS);
     const int cb_slots = AFFINE ? 0 : PADDED ? (1 << BITS) : ((C_eff + 63) & ~63);
@@ -384,15 +388,20 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     const int xdw = G * GD;                        // dwords of one token's x
     const int n_xdw = T * xdw;
     const uint32_t *xw = (const uint32_t *)x;
-    for (int i = wave; i < ((n_xdw + 63) >> 6); i += kStreamWaves) {
-        int sl = (i << 6) + lane;                  // LDS dword slot (this lane's)
-        sl = sl < n_xdw ? sl : n_xdw - 1;          // tail lanes re-copy the last dword
-        const int t = sl / xdw, d = sl - t * xdw;
-        const int g = d / GD, p = (d % GD) >> 2;
-        const int src = t * xdw + g * GD + (XStage<XT>::chunk(p, g) << 2) + (d & 3);
-        __builtin_amdgcn_global_load_lds((const void *)(xw + src), (lds_ptr_t)(s_x + (i << 6)),
-                                         4, 0, 0);
+    if constexpr (XMODE == XF_NONE) {
+        for (int i = wave; i < ((n_xdw + 63) >> 6); i += kStreamWaves) {
+            int sl = (i << 6) + lane;              // LDS dword slot (this lane's)
+            sl = sl < n_xdw ? sl : n_xdw - 1;      // tail lanes re-copy the last dword
+            const int t = sl / xdw, d = sl - t * xdw;
+            const int g = d / GD, p = (d % GD) >> 2;
+            const int src = t * xdw + g * GD + (XStage<XT>::chunk(p, g) << 2) + (d & 3);
+            __builtin_amdgcn_global_load_lds((const void *)(xw + src),
+                                             (lds_ptr_t)(s_x + (i << 6)), 4, 0, 0);
+        }
     }
+    // Folded glue: x0 (and x1) into registers ahead of the weight stream.
+    GlueTile<kStreamBlock, XMODE> tile;
+    if constexpr (XMODE != XF_NONE) tile.load((const float *)x, x1, K);
     // The weight addresses depend on `zero`, produced by a volatile asm with a
     // memory clobber, so no weight load is issued before the staging loads.
     uint32_t zero;
@@ -411,11 +420,28 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
 #pragma unroll
     for (int d = 0; d < D; d++) __builtin_memcpy(buf[d], item_ptr(d), sizeof(buf[d]));
     __builtin_amdgcn_sched_barrier(0);
-    // vmcnt(N): at most N loads outstanding.  N = the fewest instructions the
-    // D ring loads can take (dwordx4), so every older staging load has landed.
-    constexpr int kAfter = D * ((BITS + 3) / 4);
-    __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | (15 << 8) | ((kAfter >> 4) << 14));
-    lds_barrier();
+    if constexpr (XMODE == XF_NONE) {
+        // vmcnt(N): at most N loads outstanding.  N = the fewest instructions the
+        // D ring loads can take (dwordx4), so every older staging load has landed.
+        constexpr int kAfter = D * ((BITS + 3) / 4);
+        __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | (15 << 8) | ((kAfter >> 4) << 14));
+        lds_barrier();
+    } else {
+        // the transformed x from registers, while the first weight loads fly;
+        // element i goes where the swizzled staging above would put it
+        const float r = tile.finish(K, eps, s_red16);
+        if (XMODE == XF_ADD_RMS && blockIdx.x == 0 && h_out != nullptr) tile.store_sum(h_out, K);
+#pragma unroll
+        for (int k = 0; k < tile.VPT; k++)
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const int i = (int)threadIdx.x + k * kStreamBlock + j * 1024;
+                const int g = i >> 5;
+                const int sl = (g << 5) + ((((i >> 2) & 7) ^ (g & 7)) << 2) + (i & 3);
+                if (i < K) s_x[sl] = __float_as_uint(tile.value(k, j, r));
+            }
+        lds_barrier();
+    }
 
     float acc[TMAX], res[TMAX];
 #pragma unroll
@@ -628,21 +654,15 @@ int dispatch_x(const XT *x, const uint8_t *packed, const float *cb, OT *out, int
     return launch_fast<BITS, TMAX, 0>(x, packed, cb, out, T, M, K, C, st);       // x via cache
 }
 
-int stream_bpc()
-{
-    const char *e = getenv("CBQ_STREAM_BPC");
-    return e ? atoi(e) : 1;
-}
-
 template <int BITS, int TMAX, typename XT, typename OT>
 int launch_stream(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T, int M,
                   int K, int C, size_t dyn_lds, hipStream_t st)
 {
     const int blocks =
-        std::max(1, std::min(stream_bpc() * cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
+        std::max(1, std::min(cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
     hipLaunchKernelGGL((fixed_stream_kernel<BITS, TMAX, XT, OT>), dim3(blocks),
                        dim3(kStreamBlock), dyn_lds, st, x, (const uint32_t *)packed, cb, out, T,
-                       M, K, C, 0u, 0u);
+                       M, K, C, 0u, 0u, (const float *)nullptr, (float *)nullptr, 0.f);
     return cbq_launch_status("fixed_stream_kernel");
 }
 
@@ -651,10 +671,11 @@ int launch_affine(const float *x, const uint8_t *packed, uint32_t lo, uint32_t w
                   int T, int M, int K, size_t dyn_lds, hipStream_t st)
 {
     const int blocks =
-        std::max(1, std::min(stream_bpc() * cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
+        std::max(1, std::min(cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
     hipLaunchKernelGGL((fixed_stream_kernel<BITS, TMAX, float, float, true>), dim3(blocks),
                        dim3(kStreamBlock), dyn_lds, st, x, (const uint32_t *)packed,
-                       (const float *)nullptr, out, T, M, K, 1, lo, w);
+                       (const float *)nullptr, out, T, M, K, 1, lo, w, (const float *)nullptr,
+                       (float *)nullptr, 0.f);
     return cbq_launch_status("fixed_stream_kernel<affine>");
 }
 
@@ -822,6 +843,46 @@ int ck_linear_f32(const float *x, const uint8_t *packed, const float *codebook, 
                   int T, int M, int K, int C, int bits, hipStream_t stream)
 {
     return linear_any_t<float, float>(x, packed, codebook, out, T, M, K, C, bits, stream);
+}
+
+int cbq_linear_xform_f32(const float *x0, const float *x1, float *h_out, int mode, float eps,
+                         const uint8_t *packed, const float *codebook, float *out, int M, int K,
+                         int C, int bits, hipStream_t stream)
+{
+    if (!x0 || !packed || !codebook || !out || M <= 0 || K <= 0 || K % 32 != 0 || C <= 0 ||
+        C > kMaxLdsCodebook)
+        return CK_ERR_ARG;
+    if (mode < XF_SILU || mode > XF_RMS || ((mode == XF_SILU || mode == XF_ADD_RMS) && !x1))
+        return CK_ERR_ARG;
+    if (mode != XF_SILU && K > 16384) return CK_ERR_ARG;
+    if (((uintptr_t)packed & 3) != 0) return CK_ERR_ARG;
+    const int blocks =
+        std::max(1, std::min(cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
+    size_t dyn = 0;
+#define CBQ_XF(B, MODE)                                                                        \
+    hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE>), dim3(blocks),    \
+                       dim3(kStreamBlock), dyn, stream, x0, (const uint32_t *)packed, codebook, \
+                       out, 1, M, K, C, 0u, 0u, x1, h_out, eps)
+#define CBQ_XF_MODES(B)                                                                        \
+    do {                                                                                       \
+        dyn = stream_dyn_lds<B, float>(1, K, C);                                               \
+        if (!dyn) return CK_ERR_ARG;                                                           \
+        if (mode == XF_SILU) CBQ_XF(B, XF_SILU);                                               \
+        else if (mode == XF_ADD_RMS) CBQ_XF(B, XF_ADD_RMS);                                    \
+        else CBQ_XF(B, XF_RMS);                                                                \
+    } while (0)
+    switch (bits) {
+    case 8: CBQ_XF_MODES(8); break;
+    case 10: CBQ_XF_MODES(10); break;
+    case 11: CBQ_XF_MODES(11); break;
+    case 12: CBQ_XF_MODES(12); break;
+    case 13: CBQ_XF_MODES(13); break;
+    case 14: CBQ_XF_MODES(14); break;
+    default: return CK_ERR_ARG;
+    }
+#undef CBQ_XF_MODES
+#undef CBQ_XF
+    return cbq_launch_status("fixed_stream_kernel<xform>");
 }
 
 int cbq_linear_affine_f32(const float *x, const uint8_t *packed, uint32_t lo, uint32_t w,

@@ -871,9 +871,14 @@ struct ColSegs {
 // 24 rows); one chunk per wave step.  A grouped launch runs up to four
 // matrices that share x (one layer's q/k/v): each block serves one of them
 // and stages that matrix's tables.
-template <int NW, bool UNIFIED>
+// XMODE: x is staged as xform_value(XMODE, x, x1, ...) - silu(x) * x1, or
+// the RMSNorm of x (+ x1) with the grid's first block storing x + x1 to h_out.
+template <int NW, bool UNIFIED, int XMODE = XF_NONE>
 __global__ __launch_bounds__(NW * CBQ_WAVE) void huff_col_kernel(const float *__restrict__ x,
-                                                                ColSegs segs, int K)
+                                                                ColSegs segs, int K,
+                                                                const float *__restrict__ x1,
+                                                                float *__restrict__ h_out,
+                                                                float eps)
 {
     static_assert(NW <= kFastChains, "one slot per wave");
     int sidx = 0;
@@ -897,6 +902,9 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void huff_col_kernel(const float *__
     // byte address of this lane's column in the slot
     const int lane_addr = __builtin_amdgcn_readfirstlane(4 * (kFOffSlots + wave * kFastSlot)) + 4 * lane;
 
+    // Folded glue: x0 (and x1) into registers while the tables stage.
+    GlueTile<NW * CBQ_WAVE, XMODE == XF_SILU ? XF_NONE : XMODE> tile;
+    if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS) tile.load(x, x1, K);
     for (int i = wave; i < (kLutSize >> 6); i += NW)
         dma_dword(a.lut1 + (i << 6) + lane, s_lut1 + (i << 6));
     const int n2 = (a.n_lut2 + 63) & ~63;
@@ -918,6 +926,10 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void huff_col_kernel(const float *__
     // unified tables hold no unresolved entries (the builder refuses codes
     // beyond 24 bits), and their short-code entries are not leaves
     const bool general = !UNIFIED && any_unresolved != 0;
+    float xr_scale = 1.f;
+    if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS)
+        xr_scale = tile.finish(K, eps, s_x + kFastChains);   // past the flags
+    const bool store_h = XMODE == XF_ADD_RMS && blockIdx.x == 0 && h_out != nullptr;
 
     const int R = K / kChunk;
     const int W = S.nblocks * NW;
@@ -934,9 +946,16 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void huff_col_kernel(const float *__
         const int seg_rows = min(64, rows - seg * 64);
         for (int p = 0; p < R; p++) {
             __syncthreads();
-            for (int r = wave; r < 64; r += NW)
-                dma_dword(x + (size_t)p * kChunk + (r << 6) + (lane ^ ((r & 15) << 2)),
-                          s_x + (r << 6));
+            if constexpr (XMODE == XF_NONE) {
+                for (int r = wave; r < 64; r += NW)
+                    dma_dword(x + (size_t)p * kChunk + (r << 6) + (lane ^ ((r & 15) << 2)),
+                              s_x + (r << 6));
+            } else {
+                for (int r = wave; r < 64; r += NW)
+                    s_x[(r << 6) + lane] =
+                        xform_value(XMODE, x, x1, h_out, store_h,
+                                    p * kChunk + (r << 6) + (lane ^ ((r & 15) << 2)), xr_scale);
+            }
             __syncthreads();
             for (int b = 0; b < seg_rows; b++) {
                 const int64_t row = wid + (int64_t)(seg * 64 + b) * W;
@@ -1587,12 +1606,16 @@ int cbq_huff_columnize(const cbq_huff_stream *hs, int64_t n_symbols, const uint3
     return cbq_launch_status("columnize_kernel");
 }
 
-int cbq_huff_linear_col_multi_f32(const float *x, int n, const cbq_huff_stream *const *hs,
+int cbq_huff_linear_col_xform_f32(const float *x, const float *x1, float *h_out, int mode,
+                                  float eps, int n, const cbq_huff_stream *const *hs,
                                   const cbq_huff_columns *const *cols, float *const *outs,
                                   const int *Ms, int K, hipStream_t stream)
 {
     if (!x || n < 1 || n > kColMaxSeg || !hs || !cols || !outs || !Ms || K <= 0 ||
         K % kChunk != 0)
+        return CK_ERR_ARG;
+    if (mode < XF_NONE || mode > XF_RMS || ((mode == XF_SILU || mode == XF_ADD_RMS) && !x1) ||
+        (mode >= XF_ADD_RMS && K > 16384))
         return CK_ERR_ARG;
     ColSegs segs = {};
     segs.n = n;
@@ -1636,20 +1659,35 @@ int cbq_huff_linear_col_multi_f32(const float *x, int n, const cbq_huff_stream *
         g.nblocks = std::max(1, std::min(cbq_num_cus(), (M + nw - 1) / nw));
         blocks += g.nblocks;
     }
+    if (mode != XF_NONE && !unified) return CK_ERR_ARG;   // transforms need unified tables
+#define CBQ_COL_XF(NWV, MODE)                                                                  \
+    hipLaunchKernelGGL((huff_col_kernel<NWV, true, MODE>), dim3(blocks), dim3(NWV * CBQ_WAVE),  \
+                       0, stream, x, segs, K, x1, h_out, eps)
 #define CBQ_COL_LAUNCH(NWV)                                                                    \
     do {                                                                                       \
-        if (unified)                                                                           \
-            hipLaunchKernelGGL((huff_col_kernel<NWV, true>), dim3(blocks), dim3(NWV * CBQ_WAVE), \
-                               0, stream, x, segs, K);                                          \
+        if (mode == XF_SILU) CBQ_COL_XF(NWV, XF_SILU);                                         \
+        else if (mode == XF_ADD_RMS) CBQ_COL_XF(NWV, XF_ADD_RMS);                              \
+        else if (mode == XF_RMS) CBQ_COL_XF(NWV, XF_RMS);                                      \
+        else if (unified) CBQ_COL_XF(NWV, XF_NONE);                                            \
         else                                                                                   \
             hipLaunchKernelGGL((huff_col_kernel<NWV, false>), dim3(blocks),                    \
-                               dim3(NWV * CBQ_WAVE), 0, stream, x, segs, K);                    \
+                               dim3(NWV * CBQ_WAVE), 0, stream, x, segs, K,                    \
+                               (const float *)nullptr, (float *)nullptr, 0.f);                  \
     } while (0)
     if (nw == 4) CBQ_COL_LAUNCH(4);
     else if (nw == 8) CBQ_COL_LAUNCH(8);
     else CBQ_COL_LAUNCH(16);
 #undef CBQ_COL_LAUNCH
+#undef CBQ_COL_XF
     return cbq_launch_status("huff_col_kernel");
+}
+
+int cbq_huff_linear_col_multi_f32(const float *x, int n, const cbq_huff_stream *const *hs,
+                                  const cbq_huff_columns *const *cols, float *const *outs,
+                                  const int *Ms, int K, hipStream_t stream)
+{
+    return cbq_huff_linear_col_xform_f32(x, nullptr, nullptr, XF_NONE, 0.f, n, hs, cols, outs, Ms,
+                                         K, stream);
 }
 
 int cbq_huff_linear_col_f32(const float *x, const cbq_huff_stream *hs,

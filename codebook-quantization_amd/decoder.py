@@ -140,7 +140,7 @@ class Qwen3Decoder:
     """Greedy decoder over compressed linears / embedding (callables)."""
 
     def __init__(self, cfg: DecoderConfig, linears: Dict[str, Linear], embed: Callable,
-                 device: torch.device, max_len: int = 512):
+                 device: torch.device, max_len: int = 512, fuse_glue: bool = True):
         self.cfg = cfg
         self.linears = linears
         self.embed = embed
@@ -153,6 +153,14 @@ class Qwen3Decoder:
         self.cache = torch.zeros(kv, dtype=torch.float32, device=self.device)
         self.pos = 0
         self.glue = _Glue(cfg)
+        # One-token steps fold RMSNorm / SiLU into the GEMVs' x staging when
+        # every linear that consumes them offers `xform` (stacked q/k/v and
+        # gate/up, down, lm_head): 5 launches per layer instead of 8, with
+        # values identical to the separate glue kernels.
+        need = ["lm_head"] + [f"model.layers.{i}.{n}" for i in range(cfg.layers)
+                              for n in ("self_attn.qkv_proj", "mlp.gate_up_proj", "mlp.down_proj")]
+        self.fused = fuse_glue and all(callable(getattr(linears.get(n), "xform", None))
+                                       for n in need)
 
     # ---- building blocks (HF Qwen3 semantics, fp32) -------------------------
     def _attend(self, i: int, q: torch.Tensor, L: int, pos: torch.Tensor) -> torch.Tensor:
@@ -221,11 +229,43 @@ class Qwen3Decoder:
         advances pos_buf."""
         c = self.cfg
         h = self.embed(ids_buf).reshape(1, c.hidden).to(torch.float32)
-        x = self.glue.add_rms(h, None)
-        for i in range(c.layers):
-            x = self._layer(i, h, x, pos_buf, pos_buf, self.max_len)
-        logits = self.linears["lm_head"](x).reshape(-1)
+        if self.fused:
+            logits = self._forward1_fused(h, pos_buf)
+        else:
+            x = self.glue.add_rms(h, None)
+            for i in range(c.layers):
+                x = self._layer(i, h, x, pos_buf, pos_buf, self.max_len)
+            logits = self.linears["lm_head"](x).reshape(-1)
         self.glue.argmax_step(logits, ids_buf, toks, pos_buf, first_pos)
+
+    def _forward1_fused(self, h: torch.Tensor, pos_dev: torch.Tensor) -> torch.Tensor:
+        """One token through every layer with the norms and the SiLU product
+        applied by the GEMVs that consume them; h [1, hidden] is the
+        embedding.  Returns the logits [vocab]."""
+        import cbq_native as nat
+        c = self.cfg
+        L = self.linears
+        nq, nk = c.n_q * c.head_dim, c.n_kv * c.head_dim
+        delta = None                                # residual not yet added to h
+        for i in range(c.layers):
+            p = f"model.layers.{i}."
+            if delta is None:
+                y = L[p + "self_attn.qkv_proj"].xform(h, None, None, nat.XF_RMS)
+            else:
+                h2 = torch.empty_like(h)
+                y = L[p + "self_attn.qkv_proj"].xform(h, delta, h2, nat.XF_ADD_RMS)
+                h = h2
+            att = self.glue.attend_rope1(y[:, :nq], y[:, nq:nq + nk], y[:, nq + nk:], self.cos,
+                                         self.sin, pos_dev, self.cache[i, 0], self.cache[i, 1])
+            o = L[p + "self_attn.o_proj"](att)
+            h2 = torch.empty_like(h)
+            gu = L[p + "mlp.gate_up_proj"].xform(h, o, h2, nat.XF_ADD_RMS)
+            h = h2
+            delta = L[p + "mlp.down_proj"].xform(gu[:, :c.inter], gu[:, c.inter:], None,
+                                                 nat.XF_SILU)
+        if delta is None:
+            return L["lm_head"].xform(h, None, None, nat.XF_RMS).reshape(-1)
+        return L["lm_head"].xform(h, delta, None, nat.XF_ADD_RMS).reshape(-1)
 
     @torch.no_grad()
     def generate_graph(self, prompt: List[int], n_new: int, timing: Optional[dict] = None):
@@ -277,6 +317,10 @@ class Qwen3Decoder:
         pos = torch.arange(self.pos, self.pos + T, device=self.device)
         pos_dev = pos[:1].contiguous()
         h = self.embed(ids.to(self.device)).reshape(T, self.cfg.hidden).to(torch.float32)
+        if T == 1 and self.fused:
+            logits = self._forward1_fused(h, pos_dev)
+            self.pos += 1
+            return logits
         x = self.glue.add_rms(h, None)
         for i in range(self.cfg.layers):
             x = self._layer(i, h, x, pos, pos_dev, self.pos + T)
@@ -328,7 +372,7 @@ def from_compressed(cfg: DecoderConfig, comp: Dict[str, dict], device="cuda",
 
 
 def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda",
-                   max_len: int = 512, stack: bool = True) -> Qwen3Decoder:
+                   max_len: int = 512, stack: bool = True, fuse_glue: bool = True) -> Qwen3Decoder:
     """Decoder over device-resident synthetic tensors (synthetic.FixedTensor /
     HuffTensor, built on the GPU for the 9B-shape bench); calls the C ABI
     directly on torch's current stream.  With stack, each layer's q/k/v and
@@ -353,6 +397,17 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                                         out.data_ptr(), T, M, K, t.codebook.numel(), t.bits,
                                         nat.stream_ptr(dev)), "ck_linear_f32")
             return out
+
+        def xform(x0, x1, h_out, mode):
+            """One token, x = transform(x0, x1) staged by the GEMV."""
+            out = torch.empty(1, M, device=dev)
+            nat.check(lib.cbq_linear_xform_f32(
+                x0.data_ptr(), None if x1 is None else x1.data_ptr(),
+                None if h_out is None else h_out.data_ptr(), mode, cfg.eps, t.packed.data_ptr(),
+                t.codebook.data_ptr(), out.data_ptr(), M, K, t.codebook.numel(), t.bits,
+                nat.stream_ptr(dev)), "cbq_linear_xform_f32")
+            return out
+        f.xform = xform
         return f
 
     def huff_desc(t):
@@ -388,6 +443,21 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                                                   nat.stream_ptr(dev)), "cbq_huff_linear_f32")
             return out
         f.desc = desc
+        if cols is not None and cols[1].ulut1:
+            hs1 = (ctypes.POINTER(nat.HuffStream) * 1)(ctypes.pointer(desc))
+            col1 = (ctypes.POINTER(nat.HuffColumns) * 1)(ctypes.pointer(cols[1]))
+            m1 = (ctypes.c_int * 1)(M)
+
+            def xform(x0, x1, h_out, mode, keep=(hs1, col1, m1)):
+                """One token, x = transform(x0, x1) staged by the GEMV."""
+                out = torch.empty(1, M, device=dev)
+                nat.check(lib.cbq_huff_linear_col_xform_f32(
+                    x0.data_ptr(), None if x1 is None else x1.data_ptr(),
+                    None if h_out is None else h_out.data_ptr(), mode, cfg.eps, 1, hs1, col1,
+                    (ctypes.c_void_p * 1)(out.data_ptr()), m1, K, nat.stream_ptr(dev)),
+                    "cbq_huff_linear_col_xform_f32")
+                return out
+            f.xform = xform
         return f
 
     def huff_group(ts, name):
@@ -422,7 +492,23 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                 x.data_ptr(), n, hs_arr, col_arr, out_arr, m_arr, K, nat.stream_ptr(dev)),
                 "cbq_huff_linear_col_multi_f32")
             return out
+
+        def xform(x0, x1, h_out, mode, keep=(descs, cols, hs_arr, col_arr, m_arr)):
+            """One token, x = transform(x0, x1) staged by the grouped GEMV."""
+            out = torch.empty(1, sum(Ms), device=dev)
+            offs, o = [], 0
+            for M in Ms:
+                offs.append(out.data_ptr() + 4 * o)
+                o += M
+            nat.check(lib.cbq_huff_linear_col_xform_f32(
+                x0.data_ptr(), None if x1 is None else x1.data_ptr(),
+                None if h_out is None else h_out.data_ptr(), mode, cfg.eps, n, hs_arr, col_arr,
+                (ctypes.c_void_p * n)(*offs), m_arr, K, nat.stream_ptr(dev)),
+                "cbq_huff_linear_col_xform_f32")
+            return out
         f.name = name
+        if all(c[1].ulut1 for c in cols):
+            f.xform = xform
         return f
 
     def embed_fn(t):
@@ -474,4 +560,5 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         if fused is not None and f"{stem}.{fused}" in linears:
             continue
         linears[n] = huff_linear(t) if isinstance(t, synthetic.HuffTensor) else fixed_linear(t)
-    return Qwen3Decoder(cfg, linears, embed_fn(tensors["model.embed_tokens"]), dev, max_len)
+    return Qwen3Decoder(cfg, linears, embed_fn(tensors["model.embed_tokens"]), dev, max_len,
+                        fuse_glue=fuse_glue)

@@ -232,6 +232,34 @@ int cbq_huff_linear_col_multi_f32(const float *x, int n, const cbq_huff_stream *
                                   const cbq_huff_columns *const *cols, float *const *outs,
                                   const int *Ms, int K, hipStream_t stream);
 
+/* Activation transforms a single-token GEMV applies while staging x, which
+ * replace the decoder's separate glue launches (include/cbq_decode.h):
+ *   CBQ_XF_SILU     x = silu(x0) * x1                 (the down projection)
+ *   CBQ_XF_ADD_RMS  h = x0 + x1, x = rmsnorm(h); one block stores h to
+ *                   h_out (NULL: not stored)          (a layer's first GEMVs)
+ *   CBQ_XF_RMS      x = rmsnorm(x0)
+ * RMSNorm has unit weight and the reduction order of cbq_add_rmsnorm_f32,
+ * and every step rounds as the separate kernels do, so fused and unfused
+ * decoders produce identical values.  K <= 16384 for the norms.  No
+ * counterpart in the reference (its glue is HF PyTorch code). */
+#define CBQ_XF_SILU    1
+#define CBQ_XF_ADD_RMS 2
+#define CBQ_XF_RMS     3
+
+/* ck_linear_f32 for T = 1 with x = transform(x0, x1) (mode above); fixed
+ * width widths {8, 10..14}, K % 32 == 0, C <= 16384, packed 4-byte aligned;
+ * CK_ERR_ARG otherwise (use the plain entry point and the glue kernels). */
+int cbq_linear_xform_f32(const float *x0, const float *x1, float *h_out, int mode, float eps,
+                         const uint8_t *packed, const float *codebook, float *out, int M, int K,
+                         int C, int bits, hipStream_t stream);
+
+/* cbq_huff_linear_col_multi_f32 with x = transform(x0, x1) (mode above, or
+ * 0 for none); modes other than 0 need every matrix's unified tables. */
+int cbq_huff_linear_col_xform_f32(const float *x0, const float *x1, float *h_out, int mode,
+                                  float eps, int n, const cbq_huff_stream *const *hs,
+                                  const cbq_huff_columns *const *cols, float *const *outs,
+                                  const int *Ms, int K, hipStream_t stream);
+
 /* Decode flat symbols [0, n_symbols) to int32 with the chunked kernel (lut
  * payloads must be raw symbols).  The bit-exact check of the fused decoder;
  * the equivalent of huffman_decode_to_weights_f32 with an identity codebook

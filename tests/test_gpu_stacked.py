@@ -128,3 +128,4 @@ def test_grouped_huffman_decoder_tokens(cuda, built_huff):
     del a
     b = decoder.from_synthetic(cfg, tensors, max_len=40, stack=False)
     assert ta == b.generate_graph(prompt, 10)
+

@@ -75,6 +75,20 @@ def test_argument_validation_before_launch(lib):
     assert lib.cbq_attn_decode_f32(p, p, p, p, p, 4, 2, 96, 16, 1.0, None) == 2         # hd 96
     assert lib.cbq_attn_decode_f32(p, p, p, p, p, 4, 2, 128, 40000, 1.0, None) == 2     # > 32768
     assert lib.cbq_silu_mul_f32(p, p, p, 0, None) == 2
+    # GEMVs that stage x through the glue (XF_SILU 1, XF_ADD_RMS 2, XF_RMS 3)
+    xf = lib.cbq_linear_xform_f32
+    assert xf(p, p, None, 0, 1e-6, p, p, p, 64, 4096, 16, 13, None) == 2        # no transform
+    assert xf(p, p, None, 4, 1e-6, p, p, p, 64, 4096, 16, 13, None) == 2        # unknown mode
+    assert xf(p, None, None, 1, 1e-6, p, p, p, 64, 4096, 16, 13, None) == 2     # silu needs x1
+    assert xf(p, None, None, 2, 1e-6, p, p, p, 64, 4096, 16, 13, None) == 2     # add needs x1
+    assert xf(p, None, None, 3, 1e-6, p, p, p, 64, 32768, 16, 13, None) == 2    # norm K > 16384
+    one = (ctypes.c_void_p * 1)(p)
+    m1 = (ctypes.c_int * 1)(64)
+    hxf = lib.cbq_huff_linear_col_xform_f32
+    assert hxf(p, None, None, 1, 1e-6, 1, one, one, one, m1, 4096, None) == 2   # silu needs x1
+    assert hxf(p, p, None, 5, 1e-6, 1, one, one, one, m1, 4096, None) == 2      # unknown mode
+    assert hxf(p, None, None, 3, 1e-6, 1, one, one, one, m1, 20480, None) == 2  # norm K > 16384
+    assert hxf(p, None, None, 3, 1e-6, 5, one, one, one, m1, 4096, None) == 2   # > 4 matrices
 
 
 def test_build_luts_rejects_overfull(lib):
