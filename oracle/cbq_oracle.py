@@ -27,10 +27,11 @@ How each part is pinned (tests/test_oracle.py):
     diagnostics/test_huffman_gpu.py:30-35 (stream D3 93 1B 1B), Kraft
     equality, prefix-freeness, brute-force decode, and decoding by the
     compiled reference C back to the input indices.
-  - heap code lengths: optimal cost against an independent brute-force /
-    package-merge optimum on small alphabets and hand-derived tie-break KATs.
-    The exact tie-break for large alphabets is parity unpinned (it affects
-    stream bytes only, never decoded indices).
+  - heap code lengths and the stream encoder: equal to the reference's own
+    Python encoder on the fixtures of tests/golden/heap_golden.npz (tied
+    large alphabets, the 32-bit cap, one-symbol and empty alphabets, stream
+    bytes and tables; tests/test_heap_golden.py), plus optimal cost against
+    an independent brute-force / package-merge optimum on small alphabets.
 """
 from __future__ import annotations
 
