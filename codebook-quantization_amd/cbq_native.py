@@ -43,6 +43,12 @@ class HuffColumns(ctypes.Structure):
                 ("ulut1", _vp), ("ulut2", _vp), ("n_ulut2", ctypes.c_int32)]
 
 
+class SplitMatrix(ctypes.Structure):
+    """struct cbq_split_matrix (include/cbq_hip.h)."""
+    _fields_ = [("cwords", _vp), ("row_off", _vp), ("raw", _vp), ("lut", _vp),
+                ("n_chunks", _i64)]
+
+
 # name -> (restype, argtypes); every symbol declared in include/*.h
 SIGNATURES = {
     "ck_error_string": (ctypes.c_char_p, [_i]),
@@ -71,6 +77,10 @@ SIGNATURES = {
                                            _vp, _i, _vp]),
     "cbq_linear_xform_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _i, _i, _i,
                                   _i, _vp]),
+    "cbq_split_bits": (_i, [_vp, _i64, _vp, _i, _vp, _vp]),
+    "cbq_split_pack": (_i, [_vp, _i64, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
+    "cbq_split_linear_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _i, _vp, _vp, _vp, _i,
+                                  _vp]),
     # include/cbq_decode.h
     "cbq_add_rmsnorm_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, ctypes.c_float, _vp]),
     "cbq_head_norm_rope_f32": (_i, [_vp] * 11 + [_i] * 5 + [ctypes.c_float, _vp]),

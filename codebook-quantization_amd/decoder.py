@@ -372,19 +372,52 @@ def from_compressed(cfg: DecoderConfig, comp: Dict[str, dict], device="cuda",
 
 
 def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda",
-                   max_len: int = 512, stack: bool = True, fuse_glue: bool = True) -> Qwen3Decoder:
+                   max_len: int = 512, stack: bool = True, fuse_glue: bool = True,
+                   split: bool = True) -> Qwen3Decoder:
     """Decoder over device-resident synthetic tensors (synthetic.FixedTensor /
     HuffTensor, built on the GPU for the 9B-shape bench); calls the C ABI
     directly on torch's current stream.  With stack, each layer's q/k/v and
     gate/up run as one GEMV launch each instead of three / two: fixed-width
     rows are stacked into one matrix, Huffman matrices (one code each) share
-    a grouped launch."""
+    a grouped launch.  With split, Huffman single-token GEMVs run on the
+    split-exponent format (built from each matrix's decoded stream) where it
+    applies, else on the column layout."""
     import ctypes
     import cbq_native as nat
     import synthetic
-    from gpu_huffman_functions import build_columns, columns_eligible
+    from gpu_huffman_functions import (build_columns, build_split, columns_eligible,
+                                       decode_symbols)
     lib = nat.load()
     dev = torch.device(device)
+
+    def huff_split(t):
+        M, K = t.shape
+        if not split or K % 4096:
+            return None
+        idx = decode_symbols(t.words, t.chunk_off, t.sub_len, t.lengths, M * K, dev)
+        sp = build_split(idx, t.tables["codebook"].cpu().numpy(), dev)
+        del idx
+        return sp
+
+    def split_fns(sps, Ms, K):
+        """(one-token GEMV, xform) over split-format matrices sharing x."""
+        n = len(sps)
+        mats = (ctypes.POINTER(nat.SplitMatrix) * n)(*[ctypes.pointer(sp[1]) for sp in sps])
+        m_arr = (ctypes.c_int * n)(*Ms)
+
+        def xform(x0, x1, h_out, mode, keep=(sps, mats, m_arr)):
+            out = torch.empty(1, sum(Ms), device=dev)
+            offs = [out.data_ptr() + 4 * sum(Ms[:i]) for i in range(n)]
+            nat.check(lib.cbq_split_linear_f32(
+                x0.data_ptr(), None if x1 is None else x1.data_ptr(),
+                None if h_out is None else h_out.data_ptr(), mode, cfg.eps, n, mats,
+                (ctypes.c_void_p * n)(*offs), m_arr, K, nat.stream_ptr(dev)),
+                "cbq_split_linear_f32")
+            return out
+
+        def one(x):
+            return xform(x.reshape(1, K).contiguous(), None, None, 0)
+        return one, xform
 
     def fixed_linear(t):
         M, K = t.shape
@@ -423,12 +456,17 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         M, K = t.shape
         desc = huff_desc(t)
         cols = None
-        if with_cols and columns_eligible(desc, K):   # single-token GEMV on the column layout
+        sp = huff_split(t) if with_cols else None
+        if sp is not None:
+            one, sxform = split_fns([sp], [M], K)
+        elif with_cols and columns_eligible(desc, K):   # single-token GEMV on the column layout
             cols = build_columns(desc, M * K, dev, t.lengths, t.tables["codebook"].cpu().numpy())
 
         def f(x, desc=desc, cols=cols):
             x = x.reshape(-1, K).contiguous()
             T = x.shape[0]
+            if T == 1 and sp is not None:
+                return one(x)
             out = torch.empty(T, M, device=dev)
             if T == 1 and cols is not None:
                 nat.check(lib.cbq_huff_linear_col_f32(x.data_ptr(), ctypes.byref(desc),
@@ -443,7 +481,10 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                                                   nat.stream_ptr(dev)), "cbq_huff_linear_f32")
             return out
         f.desc = desc
-        if cols is not None and cols[1].ulut1:
+        if sp is not None:
+            f.xform = sxform
+            f.split = sp
+        elif cols is not None and cols[1].ulut1:
             hs1 = (ctypes.POINTER(nat.HuffStream) * 1)(ctypes.pointer(desc))
             col1 = (ctypes.POINTER(nat.HuffColumns) * 1)(ctypes.pointer(cols[1]))
             m1 = (ctypes.c_int * 1)(M)
@@ -465,8 +506,24 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         gate/up), each with its own code; None when a part does not
         qualify for the column layout."""
         K = ts[0].shape[1]
+        if any(t.shape[1] != K for t in ts):
+            return None
+        sps = [huff_split(t) for t in ts]
+        if all(sp is not None for sp in sps):
+            Ms = [t.shape[0] for t in ts]
+            one, sxform = split_fns(sps, Ms, K)
+            singles = [huff_linear(t, with_cols=False) for t in ts]   # multi-token calls
+
+            def g(x):
+                x = x.reshape(-1, K).contiguous()
+                if x.shape[0] > 1:
+                    return torch.cat([h(x) for h in singles], dim=1)
+                return one(x)
+            g.xform = sxform
+            g.name = name
+            return g
         descs = [huff_desc(t) for t in ts]
-        if any(t.shape[1] != K for t in ts) or not all(columns_eligible(d, K) for d in descs):
+        if not all(columns_eligible(d, K) for d in descs):
             return None
         cols = [build_columns(d, t.shape[0] * K, dev, t.lengths, t.tables["codebook"].cpu().numpy())
                 for d, t in zip(descs, ts)]

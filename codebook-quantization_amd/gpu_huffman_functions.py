@@ -126,6 +126,71 @@ def build_columns(desc: "nat.HuffStream", n_sym: int, device, lengths=None,
     return keep, cols
 
 
+def build_split(indices: torch.Tensor, codebook: np.ndarray, device):
+    """Split-exponent format (struct cbq_split_matrix) of decoded symbols
+    (int32 [n], n % 4096 == 0), built on the device; None when a codebook
+    value is not bf16 or the exponents need codes longer than 7 bits.
+    Returns the device tensors to keep alive and the descriptor."""
+    n = int(indices.numel())
+    if n == 0 or n % hc.CHUNK_SYMBOLS:
+        return None
+    counts = torch.bincount(indices.reshape(-1).clamp_min(0).to(torch.int64)).cpu().numpy()
+    t = hc.split_tables(codebook, counts)
+    if t is None:
+        return None
+    sym_code, sym_raw, lut = t
+    lib = nat.load()
+    st = nat.stream_ptr(device)
+    sc = torch.from_numpy(sym_code.view(np.int32)).to(device)
+    sr = torch.from_numpy(sym_raw).to(device)
+    lt = torch.from_numpy(lut.view(np.int32)).to(device)
+    n_chunks = n // hc.CHUNK_SYMBOLS
+    sub_bits = torch.empty(n // hc.SUB_SYMBOLS, dtype=torch.int32, device=device)
+    nat.check(lib.cbq_split_bits(indices.data_ptr(), n, sc.data_ptr(), int(sym_code.size),
+                                 sub_bits.data_ptr(), st), "cbq_split_bits")
+    widest = sub_bits.view(n_chunks, hc.SUB_SYMBOLS).amax(1).to(torch.int64)
+    cum = torch.cumsum(torch.clamp_min((widest + 31) // 32, 1), 0)
+    total = int(cum[-1])
+    if total >= 2 ** 31 // hc.SUB_SYMBOLS:
+        raise ValueError(f"split layout of {total} rows exceeds the 32-bit row index")
+    row_off = torch.zeros(n_chunks + 1, dtype=torch.int32, device=device)
+    row_off[1:] = cum.to(torch.int32)
+    cwords = torch.empty(total * hc.SUB_SYMBOLS, dtype=torch.int32, device=device)
+    raw = torch.empty(n, dtype=torch.uint8, device=device)
+    nat.check(lib.cbq_split_pack(indices.data_ptr(), n, sc.data_ptr(), sr.data_ptr(),
+                                 int(sym_code.size), row_off.data_ptr(), cwords.data_ptr(),
+                                 raw.data_ptr(), st), "cbq_split_pack")
+    desc = nat.SplitMatrix(cwords=cwords.data_ptr(), row_off=row_off.data_ptr(),
+                           raw=raw.data_ptr(), lut=lt.data_ptr(), n_chunks=n_chunks)
+    return [cwords, row_off, raw, lt], desc
+
+
+def split_bytes(keep) -> int:
+    """Bytes the split GEMV streams: column words, row offsets, raw bytes, table."""
+    return sum(int(t.numel() * t.element_size()) for t in keep)
+
+
+def decode_symbols(words: torch.Tensor, chunk_off: torch.Tensor, sub_len: torch.Tensor,
+                   lengths: np.ndarray, n: int, device) -> torch.Tensor:
+    """Decoded symbols (int32 [n]) of a device-format stream, via symbol-payload
+    tables and cbq_huff_decode_indices."""
+    lengths = np.ascontiguousarray(lengths, np.uint8)
+    lut1, lut2, canon, pay = hc.device_luts(lengths, None, int(lengths.size), False, clamp=False)
+    keep = [torch.from_numpy(a.view(np.int32) if a.dtype == np.uint32 else a).to(device)
+            for a in (lut1, lut2)] + [torch.from_numpy(canon).to(device),
+                                      torch.from_numpy(pay).to(device)]
+    desc = nat.HuffStream(words=words.data_ptr(), n_words=int(words.numel()),
+                          chunk_off=chunk_off.data_ptr(), sub_len=sub_len.data_ptr(),
+                          lut1=keep[0].data_ptr(), lut2=keep[1].data_ptr(), n_lut2=int(lut2.size),
+                          canon=keep[2].data_ptr(), canon_pay=keep[3].data_ptr(), value_cb=None,
+                          C=int(lengths.size), stage_words=hc.stage_words_for(chunk_off.cpu().numpy()))
+    out = torch.empty(n, dtype=torch.int32, device=device)
+    nat.check(nat.load().cbq_huff_decode_indices(ctypes.byref(desc), out.data_ptr(), n,
+                                                 nat.stream_ptr(device)), "cbq_huff_decode_indices")
+    torch.cuda.synchronize(device)
+    return out
+
+
 def columns_eligible(desc: "nat.HuffStream", K: int) -> bool:
     """The column GEMV serves T = 1 rows of whole 4096-symbol chunks with
     bf16-value payloads and a second table level that fits its LDS."""
@@ -150,7 +215,8 @@ class HuffmanCodebookLinear:
                  huff_sl_base_offset: Optional[np.ndarray] = None,
                  huff_sl_sym: Optional[np.ndarray] = None,
                  huff_chunk_offsets: Optional[np.ndarray] = None,
-                 huff_sub_lens: Optional[np.ndarray] = None):
+                 huff_sub_lens: Optional[np.ndarray] = None,
+                 split_format: bool = True):
         if not torch.cuda.is_available():
             raise RuntimeError("the compressed GPU path needs a ROCm GPU (none visible)")
         self.name = name
@@ -170,9 +236,16 @@ class HuffmanCodebookLinear:
                                  huff_sub_lens, device)
         self.device = device
         self._idx_dev = None
-        # single-token GEMVs read the column layout when the shape allows
+        # single-token GEMVs read the split-exponent format when the codebook
+        # is bf16-exact, else the column layout when the shape allows
         self.cols = None
-        if columns_eligible(self.dev.desc, self.K):
+        self.split = None
+        if split_format and self.K % hc.CHUNK_SYMBOLS == 0:
+            idx = self.decode_indices().reshape(-1)
+            self.split = build_split(idx, self._cb_np, device)
+            del idx
+            self._idx_dev = None
+        if self.split is None and columns_eligible(self.dev.desc, self.K):
             self._col_keep, self.cols = build_columns(
                 self.dev.desc, self.M * self.K, device, np.asarray(huff_lengths, np.uint8),
                 self._cb_np)
@@ -192,7 +265,14 @@ class HuffmanCodebookLinear:
         xc = x.reshape(T, self.K).to(torch.float32).contiguous()
         out = torch.empty(T, self.M, dtype=torch.float32, device=self.device)
         st = nat.stream_ptr(self.device)
-        if T == 1 and self.cols is not None:
+        if T == 1 and self.split is not None:
+            nat.check(self._lib.cbq_split_linear_f32(
+                xc.data_ptr(), None, None, 0, 0.0, 1,
+                (ctypes.POINTER(nat.SplitMatrix) * 1)(ctypes.pointer(self.split[1])),
+                (ctypes.c_void_p * 1)(out.data_ptr()), (ctypes.c_int * 1)(self.M), self.K, st),
+                "cbq_split_linear_f32")
+            T = 0
+        elif T == 1 and self.cols is not None:
             nat.check(self._lib.cbq_huff_linear_col_f32(
                 xc.data_ptr(), ctypes.byref(self.dev.desc), ctypes.byref(self.cols),
                 out.data_ptr(), self.M, self.K, st), "cbq_huff_linear_col_f32")

@@ -225,6 +225,50 @@ def huffman_encode_indices(indices, shape: Optional[tuple] = None,
     return out
 
 
+SPLIT_MAX_LEN = 7          # exponent code limit of the split-exponent format
+
+
+def split_tables(codebook, counts) -> Optional[Tuple[np.ndarray, np.ndarray, np.ndarray]]:
+    """Symbol tables of the split-exponent device format (cbq_split_matrix,
+    include/cbq_hip.h) for a bf16-exact codebook: symbol i stands for the
+    value codebook[min(i, C-1)] (the reference's clamp); its exponent byte
+    gets a canonical code of at most SPLIT_MAX_LEN bits from the exponent
+    histogram implied by `counts` (occurrences per symbol), and its sign and
+    7 mantissa bits travel raw.  Returns (sym_code uint32: bit-reversed code
+    | len << 24, sym_raw uint8: sign << 7 | mantissa, lut uint32[128]:
+    (exp << 23) | len for the next 7 stream bits), or None when a value is
+    not bf16 or more than 128 exponents occur."""
+    cb = np.ascontiguousarray(codebook, np.float32).reshape(-1)
+    bits = cb.view(np.uint32)
+    if cb.size == 0 or np.any(bits & 0xFFFF):
+        return None
+    counts = np.asarray(counts, np.int64).reshape(-1)
+    n_sym = max(int(counts.size), int(cb.size))
+    b16 = (bits[np.minimum(np.arange(n_sym), cb.size - 1)] >> 16).astype(np.int64)
+    exp = (b16 >> 7) & 0xFF
+    raw = (((b16 >> 8) & 0x80) | (b16 & 0x7F)).astype(np.uint8)
+    cnt = np.zeros(n_sym, np.int64)
+    cnt[:counts.size] = counts
+    ecount = np.bincount(exp, weights=cnt, minlength=256).astype(np.int64)
+    if np.count_nonzero(ecount) == 0:
+        ecount[exp[0]] = 1
+    if np.count_nonzero(ecount) > (1 << SPLIT_MAX_LEN):
+        return None
+    lengths = length_limited_code_lengths(ecount, SPLIT_MAX_LEN)
+    rev = _bitrev(canonical_codes(lengths), lengths.astype(np.int64)).astype(np.uint32)
+    sym_code = (rev[exp] | (lengths[exp].astype(np.uint32) << 24)).astype(np.uint32)
+    lut = np.zeros(1 << SPLIT_MAX_LEN, np.uint32)
+    filled = np.zeros(lut.size, bool)
+    for e in np.nonzero(lengths)[0]:
+        L = int(lengths[e])
+        j = int(rev[e]) + (np.arange(1 << (SPLIT_MAX_LEN - L)) << L)
+        lut[j] = (np.uint32(e) << np.uint32(23)) | np.uint32(L)
+        filled[j] = True
+    if not filled.all():                     # incomplete code (one exponent): never read
+        lut[~filled] = lut[filled][0]
+    return sym_code, raw, lut
+
+
 def device_words_from_stream(stream) -> np.ndarray:
     """Reference MSB-first byte stream -> LSB-first uint32 words, padded with
     >= 2 zero words (the device window reads word d and d + 1)."""

@@ -217,7 +217,7 @@ def test_k_tiled_path(cuda, oracle, M, K, payload):
     ref = oracle.huff_gemv(x, enc, cb, M, K, chunk_rows=None)
     y = lin(torch.from_numpy(x).to(cuda)).cpu().numpy()
     assert rel_l2(y, ref) <= TOL
-    lin.cols = None                       # packed-stream kernel (value payloads use columns)
+    lin.cols = lin.split = None           # packed-stream kernel (value payloads use columns)
     y1 = lin(torch.from_numpy(x).to(cuda)).cpu().numpy()
     assert rel_l2(y1, ref) <= TOL
     lin.dev.desc.stage_words = 8
@@ -236,7 +236,7 @@ def test_k_tiled_long_codes(cuda, oracle):
     enc = oracle.huffman_encode(idx, shape=(M, K), lengths=lengths)
     cb = (rng.standard_normal(31) * 0.02).astype(np.float32)
     lin = _lin(enc, cb, M, K)
-    lin.cols = None                       # packed-stream kernel
+    lin.cols = lin.split = None           # packed-stream kernel
     x = rng.standard_normal((1, K)).astype(np.float32)
     y = lin(torch.from_numpy(x).to(cuda)).cpu().numpy()
     assert rel_l2(y, oracle.huff_gemv(x, enc, cb, M, K)) <= TOL

@@ -1,0 +1,168 @@
+"""Split-exponent format on the GPU: cbq_split_pack writes exactly the CPU
+packer's layout, and cbq_split_linear_f32 (single, grouped, with the folded
+glue) equals the column-layout Huffman GEMV bit for bit on the same weights."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import cbq_native as nat
+import decoder
+import synthetic
+from gpu_huffman_functions import build_columns, build_split, decode_symbols
+import huffman_codebook as hc
+from test_split_format import bf16_codebook, cpu_pack
+
+pytestmark = pytest.mark.gpu
+
+
+def test_pack_matches_cpu_packer(cuda):
+    rng = np.random.default_rng(3)
+    cb = bf16_codebook(rng, 700)
+    p = 1.0 / np.arange(1, cb.size + 1) ** 1.1
+    idx = rng.choice(cb.size, size=3 * 4096, p=p / p.sum()).astype(np.int32)
+    keep, desc = build_split(torch.from_numpy(idx).to(cuda), cb, cuda)
+    cwords, row_off, raw, lut = keep
+    sym_code, sym_raw, lut_h = hc.split_tables(cb, np.bincount(idx))
+    cw, ro, rw = cpu_pack(idx.astype(np.int64), sym_code, sym_raw)
+    assert np.array_equal(row_off.cpu().numpy(), ro)
+    assert np.array_equal(cwords.cpu().numpy().view(np.uint32).reshape(-1, 64), cw)
+    assert np.array_equal(raw.cpu().numpy(), rw)
+    assert np.array_equal(lut.cpu().numpy().view(np.uint32), lut_h)
+
+
+@pytest.fixture(scope="module")
+def huff(cuda):
+    dec = synthetic.SyntheticDecoder("qwen3-8b", layers=1, log=lambda *a: None)
+    p = "model.layers.0."
+    names = [n for n in dec.all_linears() if n[0].startswith(p)]
+    return dec, dec.build_huffman(names)
+
+
+def _desc(t):
+    tb = t.tables
+    return nat.HuffStream(words=t.words.data_ptr(), n_words=t.words.numel(),
+                          chunk_off=t.chunk_off.data_ptr(), sub_len=t.sub_len.data_ptr(),
+                          lut1=tb["lut1"].data_ptr(), lut2=tb["lut2"].data_ptr(),
+                          n_lut2=tb["lut2"].numel(), canon=tb["canon"].data_ptr(),
+                          canon_pay=tb["pay"].data_ptr(), value_cb=None,
+                          C=tb["codebook"].numel(), stage_words=tb["stage_words"])
+
+
+def _both(t, cuda):
+    M, K = t.shape
+    d = _desc(t)
+    cb = t.tables["codebook"].cpu().numpy()
+    col = build_columns(d, M * K, cuda, t.lengths, cb)
+    idx = decode_symbols(t.words, t.chunk_off, t.sub_len, t.lengths, M * K, cuda)
+    sp = build_split(idx, cb, cuda)
+    assert sp is not None
+    return d, col, sp
+
+
+def _split(lib, x, sps, Ms, K, mode=0, x1=None, h_out=None, eps=1e-6):
+    n = len(sps)
+    out = torch.empty(1, sum(Ms), device=x.device)
+    offs = [out.data_ptr() + 4 * sum(Ms[:i]) for i in range(n)]
+    nat.check(lib.cbq_split_linear_f32(
+        x.data_ptr(), None if x1 is None else x1.data_ptr(),
+        None if h_out is None else h_out.data_ptr(), mode, eps, n,
+        (ctypes.POINTER(nat.SplitMatrix) * n)(*[ctypes.pointer(s[1]) for s in sps]),
+        (ctypes.c_void_p * n)(*offs), (ctypes.c_int * n)(*Ms), K, nat.stream_ptr(x.device)),
+        "cbq_split_linear_f32")
+    return out
+
+
+@pytest.mark.parametrize("name", ["mlp.gate_proj", "self_attn.k_proj", "mlp.down_proj"])
+def test_split_equals_column_gemv(cuda, huff, name):
+    dec, tensors = huff
+    t = tensors["model.layers.0." + name]
+    M, K = t.shape
+    d, col, sp = _both(t, cuda)
+    lib = nat.load()
+    gen = torch.Generator(device=cuda).manual_seed(1)
+    for rep in range(2):
+        x = torch.randn(1, K, device=cuda, generator=gen)
+        want = torch.empty(1, M, device=cuda)
+        nat.check(lib.cbq_huff_linear_col_f32(x.data_ptr(), ctypes.byref(d), ctypes.byref(col[1]),
+                                              want.data_ptr(), M, K, nat.stream_ptr(cuda)), "col")
+        got = _split(lib, x, [sp], [M], K)
+        assert torch.equal(got, want), (name, rep, float((got - want).abs().max()))
+    # and against the dense weights (decoded values) in fp64
+    idx = decode_symbols(t.words, t.chunk_off, t.sub_len, t.lengths, M * K, cuda).to(torch.int64)
+    cbt = t.tables["codebook"].to(cuda)
+    W = cbt[idx.clamp_max(cbt.numel() - 1)].reshape(M, K).double()
+    ref = (W @ x.double().reshape(K, 1)).reshape(1, M)
+    rel = float((got.double() - ref).norm() / ref.norm())
+    assert rel < 1e-5, rel
+
+
+def test_grouped_split_and_folded_glue(cuda, huff):
+    dec, tensors = huff
+    p = "model.layers.0."
+    ts = [tensors[p + n] for n in ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj")]
+    K = ts[0].shape[1]
+    Ms = [t.shape[0] for t in ts]
+    built = [_both(t, cuda) for t in ts]
+    lib = nat.load()
+    gen = torch.Generator(device=cuda).manual_seed(2)
+    h = torch.randn(1, K, device=cuda, generator=gen) * 2
+    dl = torch.randn(1, K, device=cuda, generator=gen)
+    n = 3
+    hs = (ctypes.POINTER(nat.HuffStream) * n)(*[ctypes.pointer(b[0]) for b in built])
+    cols = (ctypes.POINTER(nat.HuffColumns) * n)(*[ctypes.pointer(b[1][1]) for b in built])
+    for mode in (0, nat.XF_RMS, nat.XF_ADD_RMS):
+        want = torch.empty(1, sum(Ms), device=cuda)
+        offs = [want.data_ptr() + 4 * sum(Ms[:i]) for i in range(n)]
+        h1 = torch.full_like(h, float("nan"))
+        nat.check(lib.cbq_huff_linear_col_xform_f32(
+            h.data_ptr(), dl.data_ptr() if mode == nat.XF_ADD_RMS else None,
+            h1.data_ptr() if mode == nat.XF_ADD_RMS else None, mode, 1e-6, n, hs, cols,
+            (ctypes.c_void_p * n)(*offs), (ctypes.c_int * n)(*Ms), K, nat.stream_ptr(cuda)), "col")
+        h2 = torch.full_like(h, float("nan"))
+        got = _split(lib, h, [b[2] for b in built], Ms, K, mode,
+                     dl if mode == nat.XF_ADD_RMS else None,
+                     h2 if mode == nat.XF_ADD_RMS else None)
+        assert torch.equal(got, want), mode
+        if mode == nat.XF_ADD_RMS:
+            assert torch.equal(h1, h2)
+    # SiLU product into down_proj
+    t = tensors[p + "mlp.down_proj"]
+    M, Kd = t.shape
+    d, col, sp = _both(t, cuda)
+    a = torch.randn(1, Kd, device=cuda, generator=gen)
+    b = torch.randn(1, Kd, device=cuda, generator=gen)
+    want = torch.empty(1, M, device=cuda)
+    nat.check(lib.cbq_huff_linear_col_xform_f32(
+        a.data_ptr(), b.data_ptr(), None, nat.XF_SILU, 1e-6, 1,
+        (ctypes.POINTER(nat.HuffStream) * 1)(ctypes.pointer(d)),
+        (ctypes.POINTER(nat.HuffColumns) * 1)(ctypes.pointer(col[1])),
+        (ctypes.c_void_p * 1)(want.data_ptr()), (ctypes.c_int * 1)(M), Kd, nat.stream_ptr(cuda)),
+        "col silu")
+    got = _split(lib, a, [sp], [M], Kd, nat.XF_SILU, b)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("M,K", [(300, 4096), (70, 12288)])
+def test_module_split_equals_columns(cuda, oracle, M, K):
+    """HuffmanCodebookLinear builds the split format from the reference-format
+    stream; its one-token output equals the column path's bit for bit and
+    the reference C kernel's within fp32 tolerance."""
+    import codebook_builder as cbb
+    from conftest import rel_l2
+    from test_gpu_huffman import _lin
+    rng = np.random.default_rng(M + K)
+    w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
+    cb, idx = cbb.frequency_sorted_codebook(w)
+    enc = hc.huffman_encode_indices(idx, shape=(M, K))
+    a = _lin(enc, cb, M, K)
+    b = _lin(enc, cb, M, K, split_format=False)
+    assert a.split is not None and b.split is None and b.cols is not None
+    x = torch.from_numpy(rng.standard_normal((1, K)).astype(np.float32)).to(cuda)
+    ya, yb = a(x), b(x)
+    assert torch.equal(ya, yb)
+    ref = oracle.huff_gemv(x.cpu().numpy(), enc, cb, M, K, chunk_rows=None)
+    assert rel_l2(ya.cpu().numpy(), ref) <= 1e-5
+    y3 = a(torch.cat([x, x, x]))                           # T > 1 stays on the stream kernel
+    assert rel_l2(y3[1:2].cpu().numpy(), ref) <= 1e-5
