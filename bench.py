@@ -360,28 +360,65 @@ def main():
                 canon=tb["canon"].data_ptr(), canon_pay=tb["pay"].data_ptr(), value_cb=None,
                 C=tb["codebook"].numel(), stage_words=tb["stage_words"])
         import ctypes
-        from gpu_huffman_functions import build_columns, columns_eligible
-        cols = {}                               # column layout + unified tables (T = 1 GEMV)
+        from gpu_huffman_functions import (build_columns, build_split, columns_eligible,
+                                           decode_symbols, split_bytes)
+        # split-exponent format (the single-token GEMV's format), decoded from
+        # each matrix's own stream; column layout for the gate/up comparison
+        splits = {}
         for n, t in huff.items():
+            M, K = t.shape
+            if K % 4096 == 0:
+                idx = decode_symbols(t.words, t.chunk_off, t.sub_len, t.lengths, M * K, dev)
+                sp = build_split(idx, t.tables["codebook"].cpu().numpy(), dev)
+                del idx
+                if sp is not None:
+                    splits[n] = sp
+        cols = {}
+        for n in gu:
+            t = huff[n]
             if columns_eligible(descs[n], t.shape[1]):
                 cols[n] = build_columns(descs[n], t.shape[0] * t.shape[1], dev, t.lengths,
                                         t.tables["codebook"].cpu().numpy())
         torch.cuda.synchronize()
+        log(f"split format for {len(splits)} of {len(huff)} Huffman tensors")
+
+        def split_args(ns):
+            k = len(ns)
+            return (k, (ctypes.POINTER(nat.SplitMatrix) * k)(*[ctypes.pointer(splits[n][1])
+                                                               for n in ns]),
+                    (ctypes.c_void_p * k)(*[outs[n].data_ptr() for n in ns]),
+                    (ctypes.c_int * k)(*[huff[n].shape[0] for n in ns]), huff[ns[0]].shape[1])
+
+        def launch_split(a):
+            k, mats, out_a, m_a, K = a
+            rc = lib.cbq_split_linear_f32(xs[K].data_ptr(), None, None, 0, 0.0, k, mats, out_a,
+                                          m_a, K, nat.stream_ptr(dev))
+            if rc:
+                raise RuntimeError(f"split GEMV rc={rc}")
 
         def launch_huff(ns):
             st = nat.stream_ptr(dev)
             for n in ns:
                 M, K = huff[n].shape
-                if n in cols:
-                    rc = lib.cbq_huff_linear_col_f32(xs[K].data_ptr(), ctypes.byref(descs[n]),
-                                                     ctypes.byref(cols[n][1]), outs[n].data_ptr(),
-                                                     M, K, st)
-                else:
-                    rc = lib.cbq_huff_linear_f32(xs[K].data_ptr(), ctypes.byref(descs[n]),
-                                                 outs[n].data_ptr(), 1, M, K, st)
+                if n in splits:
+                    launch_split(single[n])
+                    continue
+                rc = lib.cbq_huff_linear_f32(xs[K].data_ptr(), ctypes.byref(descs[n]),
+                                             outs[n].data_ptr(), 1, M, K, st)
                 if rc:
                     raise RuntimeError(f"Huffman GEMV rc={rc} on {n}")
 
+        def launch_cols(ns):
+            st = nat.stream_ptr(dev)
+            for n in ns:
+                M, K = huff[n].shape
+                rc = lib.cbq_huff_linear_col_f32(xs[K].data_ptr(), ctypes.byref(descs[n]),
+                                                 ctypes.byref(cols[n][1]), outs[n].data_ptr(),
+                                                 M, K, st)
+                if rc:
+                    raise RuntimeError(f"column GEMV rc={rc} on {n}")
+
+        single = {n: split_args([n]) for n in splits}
         # the decoder's launches: per layer q/k/v and gate/up grouped (one code
         # each, one launch), o, down; then the lm_head
         n_arr = {}
@@ -391,13 +428,8 @@ def main():
             for parts in (("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"),
                           ("mlp.gate_proj", "mlp.up_proj")):
                 ns = [p + n for n in parts]
-                if all(n in cols for n in ns):
-                    k = len(ns)
-                    n_arr[ns[0]] = (
-                        k, (ctypes.POINTER(nat.HuffStream) * k)(*[ctypes.pointer(descs[n]) for n in ns]),
-                        (ctypes.POINTER(nat.HuffColumns) * k)(*[ctypes.pointer(cols[n][1]) for n in ns]),
-                        (ctypes.c_void_p * k)(*[outs[n].data_ptr() for n in ns]),
-                        (ctypes.c_int * k)(*[huff[n].shape[0] for n in ns]), huff[ns[0]].shape[1])
+                if all(n in splits for n in ns):
+                    n_arr[ns[0]] = split_args(ns)
                     groups.append(ns[0])
                 else:
                     groups += ns
@@ -405,39 +437,46 @@ def main():
         groups += [n for n in names if "layers" not in n]
 
         def launch_huff_step():
-            st = nat.stream_ptr(dev)
             for n in groups:
                 if n in n_arr:
-                    k, hs_a, col_a, out_a, m_a, K = n_arr[n]
-                    rc = lib.cbq_huff_linear_col_multi_f32(xs[K].data_ptr(), k, hs_a, col_a, out_a,
-                                                           m_a, K, st)
-                    if rc:
-                        raise RuntimeError(f"grouped Huffman GEMV rc={rc} at {n}")
+                    launch_split(n_arr[n])
                 else:
                     launch_huff([n])
 
         hbytes = sum(huff_bytes(t) for t in huff.values())
+        sbytes = sum(split_bytes(splits[n][0]) + 4 * (huff[n].shape[0] + huff[n].shape[1])
+                     if n in splits else huff_bytes(huff[n]) for n in huff)
         ms_h, _ = timed_graph(torch, launch_huff_step, args.steps, args.warmup)
         ms_hgu, _ = timed_graph(torch, lambda: launch_huff(gu), args.steps, args.warmup)
-        hb_gu = huff_bytes(huff[gu[0]])
         us_hgu = ms_hgu * 1e3 / len(gu)
-        bits_per_sym = 8.0 * sum(h.nbytes for h in huff.values()) / sum(
-            h.shape[0] * h.shape[1] for h in huff.values())
-        col_gu = cols[gu[0]][0][0].numel() * 4 if gu[0] in cols else None
+        g0 = huff[gu[0]]
+        sb_gu = split_bytes(splits[gu[0]][0]) + 4 * (g0.shape[0] + g0.shape[1])
+        us_cgu = None
+        if all(n in cols for n in gu):
+            ms_cgu, _ = timed_graph(torch, lambda: launch_cols(gu), args.steps, args.warmup)
+            us_cgu = ms_cgu * 1e3 / len(gu)
+        n_w = sum(h.shape[0] * h.shape[1] for h in huff.values())
         result["huffman"] = {
-            "value": round(hbytes / (ms_h * 1e-3) / 1e9, 1), "unit": "GB/s",
-            "ms_per_step": round(ms_h, 4), "bytes_per_step": hbytes,
+            "value": round(sbytes / (ms_h * 1e-3) / 1e9, 1), "unit": "GB/s",
+            "ms_per_step": round(ms_h, 4), "bytes_per_step": sbytes,
+            "format": "split-exponent (raw sign+mantissa byte, <=7-bit Huffman exponent code), "
+                      "built on the GPU from each matrix's canonical-Huffman index stream",
+            "stream_bytes_per_step": hbytes,
+            "stream_equivalent_GB/s": round(hbytes / (ms_h * 1e-3) / 1e9, 1),
             "launches_per_step": len(groups),
-            "bits_per_weight_incl_index": round(bits_per_sym, 3),
+            "bits_per_weight_split": round(8.0 * sbytes / n_w, 3),
+            "bits_per_weight_stream_incl_index": round(
+                8.0 * sum(h.nbytes for h in huff.values()) / n_w, 3),
             "weight_stream_tok_per_s": round(1000.0 / ms_h, 1),
-            "roofline": {"bound": "hbm", "achieved": round(hb_gu / (us_hgu * 1e-6) / 1e9, 1),
+            "column_kernel_gate_up_us_per_launch": None if us_cgu is None else round(us_cgu, 2),
+            "roofline": {"bound": "hbm", "achieved": round(sb_gu / (us_hgu * 1e-6) / 1e9, 1),
                          "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                         "frac": round(hb_gu / (us_hgu * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
-                         "traffic": read_traffic("huff_col_kernel_gate_up_qwen3-8b_pmc.md"),
-                         "kernel": "huff_col_kernel<16,unified> gate/up 4096->12288",
-                         "bytes_per_launch": hb_gu, "column_layout_bytes": col_gu,
-                         "us_per_launch": round(us_hgu, 2)}}
-        log(f"huffman sweep: {ms_h:.3f} ms/step, {hbytes / 1e9:.2f} GB/step, {len(groups)} launches")
+                         "frac": round(sb_gu / (us_hgu * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                         "traffic": read_traffic("split_gemv_kernel_gate_up_qwen3-8b_pmc.md"),
+                         "kernel": "split_gemv_kernel<16> gate/up 4096->12288",
+                         "bytes_per_launch": sb_gu, "us_per_launch": round(us_hgu, 2)}}
+        log(f"huffman sweep (split format): {ms_h:.3f} ms/step, {sbytes / 1e9:.2f} GB/step, "
+            f"{len(groups)} launches; gate/up {us_hgu:.2f} us (column kernel {us_cgu} us)")
 
     if not args.no_e2e:
         result["e2e"] = e2e_section(torch, dec, args)
