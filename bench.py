@@ -362,7 +362,7 @@ def main():
         import ctypes
         from gpu_huffman_functions import (build_columns, build_split, columns_eligible,
                                            decode_symbols, split_bytes)
-        # split-exponent format (the single-token GEMV's format), decoded from
+        # split format (the single-token GEMV's format), decoded from
         # each matrix's own stream; column layout for the gate/up comparison
         splits = {}
         for n, t in huff.items():
@@ -459,7 +459,7 @@ def main():
         result["huffman"] = {
             "value": round(sbytes / (ms_h * 1e-3) / 1e9, 1), "unit": "GB/s",
             "ms_per_step": round(ms_h, 4), "bytes_per_step": sbytes,
-            "format": "split-exponent (raw sign+mantissa byte, <=7-bit Huffman exponent code), "
+            "format": "split (raw low byte of bf16, <=7-bit Huffman code of the high byte), "
                       "built on the GPU from each matrix's canonical-Huffman index stream",
             "stream_bytes_per_step": hbytes,
             "stream_equivalent_GB/s": round(hbytes / (ms_h * 1e-3) / 1e9, 1),

@@ -1,4 +1,4 @@
-// Split-exponent device format and its one-token GEMV, for gfx950.
+// Split device format and its one-token GEMV, for gfx950.
 //
 // The canonical-Huffman index stream of the reference
 // (src/huffman_codebook.py:126-226) spends ~10.5 bits per weight, and its
@@ -6,18 +6,21 @@
 // codebook value is a bf16 number (the lossless direct-codebook mode), the
 // same weights can be held instead as
 //
-//   raw   one byte per weight: sign (bit 7) | the 7 mantissa bits;
-//   exp   the 8-bit exponent, Huffman-coded with codes of at most 7 bits
-//         (~2.6 bits per weight on N(0, sigma) weights),
+//   raw   one byte per weight: the low byte of its bf16 bits (exponent bit 0
+//         and the 7 mantissa bits);
+//   code  the high byte (sign and exponent bits 7..1), Huffman-coded with
+//         codes of at most 7 bits (~2.9 bits per weight on N(0, sigma)
+//         weights),
 //
-// ~10.6 bits per weight, built once at load from the decoded indices.  The
-// exponent codes of each 64-weight sub-block form an LSB-first bit stream
-// stored in the column layout: chunk c (4096 weights, 64 sub-blocks) owns
-// rows row_off[c] .. row_off[c+1]-1 of 64 words, word l of a row belonging
-// to sub-block l, so a wave reads a row with one conflict-free LDS access.
-// A 128-entry table maps the next 7 stream bits to (exp << 23) | len, and
-// the weight is ((sign|mantissa byte, placed by v_perm) & 0x807fffff) |
-// (entry & 0x7f800000): one table read and ~7 VALU operations per weight.
+// built once at load from the decoded indices.  The codes of each 64-weight
+// sub-block form an LSB-first bit stream stored in the column layout: chunk
+// c (4096 weights, 64 sub-blocks) owns rows row_off[c] .. row_off[c+1]-1 of
+// 64 words, word l of a row belonging to sub-block l, so a wave reads a row
+// with one conflict-free LDS access.  Codes have at most 7 bits, so any 14
+// stream bits hold the next two codes whole: a 16384-entry table (64 KiB of
+// LDS) maps them to hi1 << 24 | hi2 << 16 | (len1 + len2), and one v_perm
+// assembles a weight's fp32 bits from its table byte and its raw byte: one
+// table read per two weights and ~4.5 VALU operations per weight.
 //
 // The GEMV walks a chunk exactly as the column-layout Huffman GEMV does (lane
 // l takes sub-block l, symbols in order, fmaf into one accumulator, wave sum
@@ -31,12 +34,13 @@ namespace {
 
 constexpr int kSChunk = 4096;
 constexpr int kSSub = 64;
-constexpr int kSMaxLen = 7;                       // exponent code length limit
-constexpr int kSLut = 1 << kSMaxLen;              // 128 table entries
-// A chunk has at most ceil(64 * 7 / 32) = 14 rows; the slot holds one more,
-// since the window of a sub-block's last codes reads the row after them.
-constexpr int kSRows = 15;
-constexpr int kSSlotWords = kSRows * kSSub;       // one wave's chunk slot
+constexpr int kSMaxLen = 7;                       // code length limit
+constexpr int kSLut = 1 << (2 * kSMaxLen);        // two-code table entries
+// A chunk has at most ceil(64 * 7 / 32) = 14 rows; the slot holds two more,
+// since the decoder reads up to two rows past a sub-block's last code.
+constexpr int kSRows = 14;
+constexpr int kSSlotRows = 16;
+constexpr int kSSlotWords = kSSlotRows * kSSub;   // one wave's chunk slot
 constexpr int kSMaxSeg = 4;
 
 constexpr int split_lds_words(int nw) { return kSLut + kSChunk + nw * kSSlotWords; }
@@ -60,7 +64,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 // One item's global data in registers: the 64 raw bytes of this lane's
-// sub-block and its exponent-code words (rows 0 .. H-1 of the chunk).
+// sub-block and its code words (rows 0 .. H-1 of the chunk).
 struct SplitItem {
     uint32_t raw[16];
     uint32_t ew[kSRows];
@@ -84,35 +88,43 @@ __device__ __forceinline__ void split_load(SplitItem &it, const SplitSeg &S, int
 }
 
 // Decodes the 64 weights of this lane's sub-block against the staged x and
-// returns the dot product.  slot: this wave's LDS rows (already written);
-// lane_addr: byte address of the lane's column in row 0 of the slot.
+// returns the dot product.  s_lds: the two-code table at LDS address 0 and
+// this wave's slot (already written); lane_addr: byte address of the lane's
+// column in row 0 of the slot.  A group of 4 codes spans at most 28 bits, so
+// the next group's window starts in the current word or the one after it:
+// the words (d, d+1) of the current window and word d+2, read one group
+// ahead, stay in registers and the table reads are the only LDS accesses on
+// the dependent chain.
 __device__ __forceinline__ float split_decode(const uint32_t (&raw)[16], const uint32_t *s_lds,
                                               int lane_addr, const float *xr, int xsw)
 {
     float acc = 0.f;
-    uint32_t q = 0;
+    int qm = -2;                                      // stream bit position - 2
+    int d = -1;                                       // word of bit qm
+    const char *base = (const char *)s_lds + lane_addr;
+    uint32_t w0 = *(const uint32_t *)(base - 4 * kSSub);
+    uint32_t w1 = *(const uint32_t *)base;
 #pragma unroll
     for (int g = 0; g < 16; g++) {
+        const uint32_t w2 = *(const uint32_t *)(base + (d + 2) * (4 * kSSub));
         const f4 xv4 = *(const f4 *)(xr + ((4 * g) ^ xsw));
         const float xv[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
-        // 30 stream bits from bit q on, in bits 2..31 (bits 0-1: the two before)
-        const int qm = (int)q - 2;
-        const int d = qm >> 5;
-        const char *wp = (const char *)s_lds + lane_addr + d * (4 * kSSub);
-        const uint32_t lo = *(const uint32_t *)wp;
-        const uint32_t hi = *(const uint32_t *)(wp + 4 * kSSub);
-        uint32_t w = __builtin_amdgcn_alignbit(hi, lo, (uint32_t)qm);
+        uint32_t w = __builtin_amdgcn_alignbit(w1, w0, (uint32_t)qm);   // 30 bits in 2..31
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < 4; u += 2) {
             const uint32_t e = *(const uint32_t *)((const char *)s_lds + (w & (4u * kSLut - 4u)));
-            // raw byte u in bytes 3 and 2: sign lands in bit 31, mantissa in 16..22
-            const uint32_t sel = (uint32_t)(u << 24) | (uint32_t)(u << 16) | 0x0c0cu;
-            const uint32_t R = __builtin_amdgcn_perm(raw[g], raw[g], sel);
-            const uint32_t v = (R & 0x807fffffu) | (e & 0x7f800000u);
-            acc = fmaf(xv[u], __uint_as_float(v), acc);
+            // weight = high byte from the table entry | raw low byte, << 16
+            const uint32_t v0 = __builtin_amdgcn_perm(e, raw[g], 0x07000c0cu | (u << 16));
+            const uint32_t v1 = __builtin_amdgcn_perm(e, raw[g], 0x06000c0cu | ((u + 1) << 16));
+            acc = fmaf(xv[u], __uint_as_float(v0), acc);
+            acc = fmaf(xv[u + 1], __uint_as_float(v1), acc);
             w >>= (e & 31u);
-            q += e & 0xffu;
+            qm += (int)(e & 0xffu);
         }
+        const bool step = (qm >> 5) != d;
+        d += step ? 1 : 0;
+        w0 = step ? w1 : w0;
+        w1 = step ? w2 : w1;
     }
     return acc;
 }
@@ -139,14 +151,6 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
     const int lane_addr =
         __builtin_amdgcn_readfirstlane(4 * (kSLut + kSChunk + wave * kSSlotWords)) + 4 * lane;
 
-    GlueTile<NW * CBQ_WAVE, XMODE == XF_SILU ? XF_NONE : XMODE> tile;
-    if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS) tile.load(x, x1, K);
-    if (threadIdx.x < kSLut) s_lds[threadIdx.x] = S.lut[threadIdx.x];
-    float xr_scale = 1.f;
-    if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS)
-        xr_scale = tile.finish(K, eps, s_x);      // s_x is staged after the next barrier
-    const bool store_h = XMODE == XF_ADD_RMS && blockIdx.x == 0 && h_out != nullptr;
-
     const int R = K / kSChunk;
     const int W = S.nblocks * NW;
     const int wid = bid * NW + wave;
@@ -156,6 +160,33 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
     const int n_seg = (rows_max + 63) >> 6;
     const float *const xr = s_x + lane * 64;
     const int xsw = (lane & 15) << 2;
+    auto chunk_of = [&](int seg, int p, int b, uint32_t &r0, uint32_t &H) {
+        const int64_t row = wid + (int64_t)(seg * 64 + b) * W;
+        const int64_t c = __builtin_amdgcn_readfirstlane((int)(row * R + p));
+        r0 = S.row_off[c];
+        H = S.row_off[c + 1] - r0;
+        H = H < (uint32_t)kSRows ? H : (uint32_t)kSRows;
+        return c;
+    };
+
+    GlueTile<NW * CBQ_WAVE, XMODE == XF_SILU ? XF_NONE : XMODE> tile;
+    if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS) tile.load(x, x1, K);
+    // Two items in flight: the next one's loads go out before this one is
+    // decoded.  The wave's first item is requested before the table staging.
+    SplitItem A, B;
+    uint32_t rA = 0, hA = 0, rB = 0, hB = 0;
+    if (rows > 0) {
+        const int64_t c = chunk_of(0, 0, 0, rA, hA);
+        split_load(A, S, c, rA, hA, lane);
+    }
+    for (int i = wave; i < kSLut / (4 * CBQ_WAVE); i += NW)
+        __builtin_amdgcn_global_load_lds(S.lut + i * 4 * CBQ_WAVE + 4 * lane,
+                                         (__attribute__((address_space(3))) void *)(s_lds + i * 4 * CBQ_WAVE),
+                                         16, 0, 0);
+    float xr_scale = 1.f;
+    if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS)
+        xr_scale = tile.finish(K, eps, s_x);      // s_x is staged after the next barrier
+    const bool store_h = XMODE == XF_ADD_RMS && blockIdx.x == 0 && h_out != nullptr;
 
     for (int seg = 0; seg < n_seg; seg++) {
         float res = 0.f;
@@ -174,26 +205,15 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
                                     p * kSChunk + (r << 6) + (lane ^ ((r & 15) << 2)), xr_scale);
             }
             __syncthreads();
-            auto chunk_of = [&](int b, uint32_t &r0, uint32_t &H) {
-                const int64_t row = wid + (int64_t)(seg * 64 + b) * W;
-                const int64_t c = __builtin_amdgcn_readfirstlane((int)(row * R + p));
-                r0 = S.row_off[c];
-                H = S.row_off[c + 1] - r0;
-                H = H < (uint32_t)kSRows ? H : (uint32_t)kSRows;
-                return c;
-            };
-            // Two items in flight: the next one's loads go out before this
-            // one is decoded.  The slot is rewritten only after the previous
-            // item's reads (LDS operations of a wave complete in order).
-            SplitItem A, B;
-            uint32_t rA = 0, hA = 0, rB = 0, hB = 0;
-            if (seg_rows > 0) {
-                const int64_t c = chunk_of(0, rA, hA);
+            // The slot is rewritten only after the previous item's reads (LDS
+            // operations of a wave complete in order).
+            if (seg_rows > 0 && (seg > 0 || p > 0)) {
+                const int64_t c = chunk_of(seg, p, 0, rA, hA);
                 split_load(A, S, c, rA, hA, lane);
             }
             for (int b = 0; b < seg_rows; b += 2) {
                 if (b + 1 < seg_rows) {
-                    const int64_t c = chunk_of(b + 1, rB, hB);
+                    const int64_t c = chunk_of(seg, p, b + 1, rB, hB);
                     split_load(B, S, c, rB, hB, lane);
                 }
 #pragma unroll
@@ -205,7 +225,7 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
                 }
                 if (b + 1 >= seg_rows) break;
                 if (b + 2 < seg_rows) {
-                    const int64_t c = chunk_of(b + 2, rA, hA);
+                    const int64_t c = chunk_of(seg, p, b + 2, rA, hA);
                     split_load(A, S, c, rA, hA, lane);
                 }
 #pragma unroll
@@ -223,7 +243,7 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
 
 // ---- build ------------------------------------------------------------------
 
-// sym_code[i]: bit-reversed exponent code | len << 24 of symbol i.
+// sym_code[i]: bit-reversed high-byte code | len << 24 of symbol i.
 __global__ void split_bits_kernel(const int32_t *__restrict__ idx, int64_t n_sub,
                                   const uint32_t *__restrict__ sym_code, int n_sym,
                                   uint32_t *__restrict__ sub_bits)
@@ -327,7 +347,7 @@ int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode
         if (!m || !m->cwords || !m->row_off || !m->raw || !m->lut || !outs[i] || Ms[i] <= 0)
             return CK_ERR_ARG;
         if (m->n_chunks != (int64_t)Ms[i] * (K / kSChunk)) return CK_ERR_ARG;
-        if (((uintptr_t)m->raw & 15) != 0) return CK_ERR_ARG;
+        if (((uintptr_t)m->raw & 15) != 0 || ((uintptr_t)m->lut & 15) != 0) return CK_ERR_ARG;
         SplitSeg &g = segs.s[i];
         g.cwords = m->cwords;
         g.row_off = m->row_off;

@@ -380,7 +380,7 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
     gate/up run as one GEMV launch each instead of three / two: fixed-width
     rows are stacked into one matrix, Huffman matrices (one code each) share
     a grouped launch.  With split, Huffman single-token GEMVs run on the
-    split-exponent format (built from each matrix's decoded stream) where it
+    split format (built from each matrix's decoded stream) where it
     applies, else on the column layout."""
     import ctypes
     import cbq_native as nat

@@ -127,7 +127,7 @@ def build_columns(desc: "nat.HuffStream", n_sym: int, device, lengths=None,
 
 
 def build_split(indices: torch.Tensor, codebook: np.ndarray, device):
-    """Split-exponent format (struct cbq_split_matrix) of decoded symbols
+    """Split format (struct cbq_split_matrix) of decoded symbols
     (int32 [n], n % 4096 == 0), built on the device; None when a codebook
     value is not bf16 or the exponents need codes longer than 7 bits.
     Returns the device tensors to keep alive and the descriptor."""
@@ -236,7 +236,7 @@ class HuffmanCodebookLinear:
                                  huff_sub_lens, device)
         self.device = device
         self._idx_dev = None
-        # single-token GEMVs read the split-exponent format when the codebook
+        # single-token GEMVs read the split format when the codebook
         # is bf16-exact, else the column layout when the shape allows
         self.cols = None
         self.split = None

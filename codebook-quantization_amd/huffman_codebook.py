@@ -225,19 +225,21 @@ def huffman_encode_indices(indices, shape: Optional[tuple] = None,
     return out
 
 
-SPLIT_MAX_LEN = 7          # exponent code limit of the split-exponent format
+SPLIT_MAX_LEN = 7          # high-byte code limit of the split format
 
 
 def split_tables(codebook, counts) -> Optional[Tuple[np.ndarray, np.ndarray, np.ndarray]]:
-    """Symbol tables of the split-exponent device format (cbq_split_matrix,
+    """Symbol tables of the split device format (cbq_split_matrix,
     include/cbq_hip.h) for a bf16-exact codebook: symbol i stands for the
-    value codebook[min(i, C-1)] (the reference's clamp); its exponent byte
-    gets a canonical code of at most SPLIT_MAX_LEN bits from the exponent
-    histogram implied by `counts` (occurrences per symbol), and its sign and
-    7 mantissa bits travel raw.  Returns (sym_code uint32: bit-reversed code
-    | len << 24, sym_raw uint8: sign << 7 | mantissa, lut uint32[128]:
-    (exp << 23) | len for the next 7 stream bits), or None when a value is
-    not bf16 or more than 128 exponents occur."""
+    value codebook[min(i, C-1)] (the reference's clamp); the high byte of
+    its bf16 bits (sign and exponent bits 7..1) gets a canonical code of at
+    most SPLIT_MAX_LEN bits from the high-byte histogram implied by `counts`
+    (occurrences per symbol), and the low byte (exponent bit 0 and the 7
+    mantissa bits) travels raw.  Returns (sym_code uint32: bit-reversed code
+    | len << 24, sym_raw uint8: low byte, lut uint32[16384]: the next two
+    codes for every 14 stream bits j, as hi1 << 24 | hi2 << 16 | (len1 +
+    len2)), or None when a value is not bf16 or more than 128 high bytes
+    occur.  Two codes of at most 7 bits always fit in 14 bits."""
     cb = np.ascontiguousarray(codebook, np.float32).reshape(-1)
     bits = cb.view(np.uint32)
     if cb.size == 0 or np.any(bits & 0xFFFF):
@@ -245,28 +247,32 @@ def split_tables(codebook, counts) -> Optional[Tuple[np.ndarray, np.ndarray, np.
     counts = np.asarray(counts, np.int64).reshape(-1)
     n_sym = max(int(counts.size), int(cb.size))
     b16 = (bits[np.minimum(np.arange(n_sym), cb.size - 1)] >> 16).astype(np.int64)
-    exp = (b16 >> 7) & 0xFF
-    raw = (((b16 >> 8) & 0x80) | (b16 & 0x7F)).astype(np.uint8)
+    hi = b16 >> 8
+    raw = (b16 & 0xFF).astype(np.uint8)
     cnt = np.zeros(n_sym, np.int64)
     cnt[:counts.size] = counts
-    ecount = np.bincount(exp, weights=cnt, minlength=256).astype(np.int64)
-    if np.count_nonzero(ecount) == 0:
-        ecount[exp[0]] = 1
-    if np.count_nonzero(ecount) > (1 << SPLIT_MAX_LEN):
+    hcount = np.bincount(hi, weights=cnt, minlength=256).astype(np.int64)
+    if np.count_nonzero(hcount) == 0:
+        hcount[hi[0]] = 1
+    if np.count_nonzero(hcount) > (1 << SPLIT_MAX_LEN):
         return None
-    lengths = length_limited_code_lengths(ecount, SPLIT_MAX_LEN)
+    lengths = length_limited_code_lengths(hcount, SPLIT_MAX_LEN)
     rev = _bitrev(canonical_codes(lengths), lengths.astype(np.int64)).astype(np.uint32)
-    sym_code = (rev[exp] | (lengths[exp].astype(np.uint32) << 24)).astype(np.uint32)
-    lut = np.zeros(1 << SPLIT_MAX_LEN, np.uint32)
-    filled = np.zeros(lut.size, bool)
-    for e in np.nonzero(lengths)[0]:
-        L = int(lengths[e])
-        j = int(rev[e]) + (np.arange(1 << (SPLIT_MAX_LEN - L)) << L)
-        lut[j] = (np.uint32(e) << np.uint32(23)) | np.uint32(L)
+    sym_code = (rev[hi] | (lengths[hi].astype(np.uint32) << 24)).astype(np.uint32)
+    one = np.zeros(1 << SPLIT_MAX_LEN, np.int64)          # next 7 bits -> hi << 24 | len
+    filled = np.zeros(one.size, bool)
+    for h in np.nonzero(lengths)[0]:
+        L = int(lengths[h])
+        j = int(rev[h]) + (np.arange(1 << (SPLIT_MAX_LEN - L)) << L)
+        one[j] = (int(h) << 24) | L
         filled[j] = True
-    if not filled.all():                     # incomplete code (one exponent): never read
-        lut[~filled] = lut[filled][0]
-    return sym_code, raw, lut
+    if not filled.all():                     # incomplete code (one symbol): never read
+        one[~filled] = one[filled][0]
+    j = np.arange(1 << (2 * SPLIT_MAX_LEN), dtype=np.int64)
+    e1 = one[j & 127]
+    e2 = one[(j >> (e1 & 0xFF)) & 127]
+    pair = (e1 & 0xFF000000) | ((e2 >> 8) & 0x00FF0000) | ((e1 & 0xFF) + (e2 & 0xFF))
+    return sym_code, raw, pair.astype(np.uint32)
 
 
 def device_words_from_stream(stream) -> np.ndarray:

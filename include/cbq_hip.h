@@ -260,32 +260,33 @@ int cbq_huff_linear_col_xform_f32(const float *x0, const float *x1, float *h_out
                                   const cbq_huff_columns *const *cols, float *const *outs,
                                   const int *Ms, int K, hipStream_t stream);
 
-/* ---- Split-exponent device format (no counterpart in the reference) -------
+/* ---- Split device format (no counterpart in the reference) ----------------
  * A load-time re-encoding of a Huffman-coded matrix whose codebook values are
  * all bf16 numbers, for the single-token GEMV that HuffmanCodebookLinear
  * runs for T = 1 (src/gpu_huffman_functions.py:834-855): one raw byte per
- * weight (sign << 7 | 7 mantissa bits, natural order) and the 8-bit exponent
- * Huffman-coded with codes of at most 7 bits, LSB-first per 64-weight
- * sub-block, stored in the column layout (chunk c = 4096 weights owns rows
- * row_off[c] .. row_off[c+1]-1 of 64 words, at most 14).  lut[j] for the
- * next 7 stream bits j is (exp << 23) | len.  n_symbols % 4096 == 0. */
+ * weight (the low byte of its bf16 bits, natural order) and the high byte
+ * (sign, exponent bits 7..1) Huffman-coded with codes of at most 7 bits,
+ * LSB-first per 64-weight sub-block, stored in the column layout (chunk c =
+ * 4096 weights owns rows row_off[c] .. row_off[c+1]-1 of 64 words, at most
+ * 14).  lut[j] for the next 14 stream bits j (always two whole codes) is
+ * hi1 << 24 | hi2 << 16 | (len1 + len2).  n_symbols % 4096 == 0. */
 typedef struct cbq_split_matrix {
     const uint32_t *cwords;   /* total rows x 64 words (+ nothing past the last row) */
     const uint32_t *row_off;  /* [n_chunks + 1] */
-    const uint8_t *raw;       /* [n_chunks * 4096], 16-byte aligned */
-    const uint32_t *lut;      /* [128] */
+    const uint8_t *raw;       /* [n_chunks * 4096] low bytes, 16-byte aligned */
+    const uint32_t *lut;      /* [16384], 16-byte aligned */
     int64_t n_chunks;
 } cbq_split_matrix;
 
 /* Build, step 1: sub_bits[s] = code bits of sub-block s (64 symbols) of the
- * decoded indices; sym_code[i] = bit-reversed exponent code of symbol i |
+ * decoded indices; sym_code[i] = bit-reversed high-byte code of symbol i |
  * len << 24 (indices clamp to [0, n_sym)).  The caller derives row_off:
  * rows(c) = max(1, ceil(max over the chunk's 64 sub_bits / 32)). */
 int cbq_split_bits(const int32_t *indices, int64_t n_symbols, const uint32_t *sym_code, int n_sym,
                    uint32_t *sub_bits, hipStream_t stream);
 
 /* Build, step 2: writes the column words (every row of every chunk) and the
- * raw bytes (sym_raw[i]: sign << 7 | mantissa of symbol i's bf16 value). */
+ * raw bytes (sym_raw[i]: the low byte of symbol i's bf16 value). */
 int cbq_split_pack(const int32_t *indices, int64_t n_symbols, const uint32_t *sym_code,
                    const uint8_t *sym_raw, int n_sym, const uint32_t *row_off, uint32_t *cwords,
                    uint8_t *raw, hipStream_t stream);

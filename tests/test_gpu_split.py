@@ -1,4 +1,4 @@
-"""Split-exponent format on the GPU: cbq_split_pack writes exactly the CPU
+"""Split format on the GPU: cbq_split_pack writes exactly the CPU
 packer's layout, and cbq_split_linear_f32 (single, grouped, with the folded
 glue) equals the column-layout Huffman GEMV bit for bit on the same weights."""
 import ctypes

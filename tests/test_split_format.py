@@ -1,8 +1,8 @@
-"""Host-side tables of the split-exponent device format (huffman_codebook.
+"""Host-side tables of the split device format (huffman_codebook.
 split_tables): a CPU packer and a CPU restatement of the GPU decode step
-(window of 30 bits at q - 2, 7-bit table index, shift by the code length)
-recover every weight bit for bit, codes stay within 7 bits, and the code is
-a complete prefix code over the exponents that occur."""
+(window of 30 bits at q - 2, 14-bit two-code table index, shift by the two
+code lengths) recover every weight bit for bit, codes stay within 7 bits,
+and the code is a complete prefix code over the high bytes that occur."""
 import numpy as np
 import pytest
 
@@ -37,7 +37,9 @@ def cpu_pack(idx, sym_code, sym_raw):
 
 
 def cpu_decode(cw, row_off, raw, lut, n):
-    """The kernel's decode walk, restated on the CPU: float32 bits per weight."""
+    """The kernel's decode walk, restated on the CPU: float32 bits per weight.
+    Per group of 4 weights one 30-bit window (alignbit at q - 2), then two
+    table reads, each giving two high bytes and their total code length."""
     out = np.zeros(n, np.uint32)
     for s in range(n // 64):
         c, l = divmod(s, 64)
@@ -49,11 +51,11 @@ def cpu_decode(cw, row_off, raw, lut, n):
         q = 0
         for g in range(16):
             w = (stream >> q) & 0xFFFFFFFF             # alignbit(hi, lo, q - 2)
-            for u in range(4):
-                e = int(lut[(w & 0x1FC) >> 2])
-                i = s * 64 + 4 * g + u
-                rb = int(raw[i])
-                out[i] = ((rb & 0x80) << 24) | (rb & 0x7F) << 16 | (e & 0x7F800000)
+            for u in range(0, 4, 2):
+                e = int(lut[(w & 0xFFFC) >> 2])
+                for k, hb in ((0, e >> 24), (1, (e >> 16) & 0xFF)):
+                    i = s * 64 + 4 * g + u + k
+                    out[i] = (hb << 24) | (int(raw[i]) << 16)
                 w >>= (e & 31)
                 q += e & 0xFF
     return out
@@ -82,20 +84,21 @@ def test_split_code_is_complete_prefix_code():
     cb = bf16_codebook(rng, 2000)
     counts = rng.integers(0, 50, cb.size)
     sym_code, _, lut = hc.split_tables(cb, counts)
-    exps = (cb.view(np.uint32) >> 23) & 0xFF
-    used = np.unique(exps[counts > 0])
-    lens = {int(e): int(sym_code[np.nonzero(exps == e)[0][0]] >> 24) for e in used}
+    his = cb.view(np.uint32) >> 24
+    used = np.unique(his[counts > 0])
+    lens = {int(h): int(sym_code[np.nonzero(his == h)[0][0]] >> 24) for h in used}
     assert sum(2.0 ** -L for L in lens.values()) == pytest.approx(1.0)
-    # every table entry names a used exponent and its own code length
-    assert set(int(v) >> 23 for v in lut) == set(int(e) for e in used)
-    for v in lut:
-        assert lens[int(v) >> 23] == int(v) & 0xFF
+    # every table entry names two used high bytes and their total code length
+    assert set(int(v) >> 24 for v in lut) == set(int(h) for h in used)
+    for v in lut[::97]:
+        h1, h2 = int(v) >> 24, (int(v) >> 16) & 0xFF
+        assert lens[h1] + lens[h2] == int(v) & 0xFF
 
 
-def test_split_rejects_non_bf16_and_too_many_exponents():
+def test_split_rejects_non_bf16_and_too_many_high_bytes():
     cb = np.array([0.5, 0.1], np.float32)              # 0.1 is not a bf16 number
     assert hc.split_tables(cb, [3, 4]) is None
-    e = np.arange(1, 140, dtype=np.uint32) << 23        # 139 distinct exponents
+    e = np.arange(1, 140, dtype=np.uint32) << 24        # 139 distinct high bytes
     assert hc.split_tables(e.view(np.float32), np.ones(139)) is None
 
 
