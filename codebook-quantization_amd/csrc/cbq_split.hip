@@ -64,10 +64,11 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 // One item's global data in registers: the 64 raw bytes of this lane's
-// sub-block and its code words (rows 0 .. H-1 of the chunk).
+// sub-block, and the chunk's code rows 0 .. H-1 (rounded up to 4) as 16-byte
+// pieces: piece k of lane l is row 4k + l/16, words 4(l%16) .. 4(l%16)+3.
 struct SplitItem {
     uint32_t raw[16];
-    uint32_t ew[kSRows];
+    u4 ew[(kSRows + 3) / 4];
 };
 
 __device__ __forceinline__ void split_load(SplitItem &it, const SplitSeg &S, int64_t c, uint32_t r0,
@@ -82,9 +83,19 @@ __device__ __forceinline__ void split_load(SplitItem &it, const SplitSeg &S, int
         it.raw[4 * k + 2] = v.z;
         it.raw[4 * k + 3] = v.w;
     }
-    const uint32_t *wp = S.cwords + (size_t)r0 * kSSub + lane;
+    const u4 *wp = (const u4 *)(S.cwords + (size_t)r0 * kSSub) + lane;
 #pragma unroll
-    for (int r = 0; r < kSRows; r++) it.ew[r] = r < (int)H ? wp[(size_t)r * kSSub] : 0u;
+    for (int k = 0; k < (kSRows + 3) / 4; k++)
+        if (4 * k < (int)H) it.ew[k] = wp[k * kSSub];
+}
+
+// Writes an item's code rows into the wave's slot (same row-major layout).
+__device__ __forceinline__ void split_stage(const SplitItem &it, uint32_t H, uint32_t *s_slot,
+                                            int lane)
+{
+#pragma unroll
+    for (int k = 0; k < (kSRows + 3) / 4; k++)
+        if (4 * k < (int)H) *(u4 *)(s_slot + k * 4 * kSSub + 4 * lane) = it.ew[k];
 }
 
 // Decodes the 64 weights of this lane's sub-block against the staged x and
@@ -216,9 +227,7 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
                     const int64_t c = chunk_of(seg, p, b + 1, rB, hB);
                     split_load(B, S, c, rB, hB, lane);
                 }
-#pragma unroll
-                for (int r = 0; r < kSRows; r++)
-                    if (r < (int)hA) s_slot[r * kSSub + lane] = A.ew[r];
+                split_stage(A, hA, s_slot, lane);
                 {
                     const float s = wave_sum(split_decode(A.raw, s_lds, lane_addr, xr, xsw));
                     if (lane == b) res += s;
@@ -228,9 +237,7 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
                     const int64_t c = chunk_of(seg, p, b + 2, rA, hA);
                     split_load(A, S, c, rA, hA, lane);
                 }
-#pragma unroll
-                for (int r = 0; r < kSRows; r++)
-                    if (r < (int)hB) s_slot[r * kSSub + lane] = B.ew[r];
+                split_stage(B, hB, s_slot, lane);
                 {
                     const float s = wave_sum(split_decode(B.raw, s_lds, lane_addr, xr, xsw));
                     if (lane == b + 1) res += s;
@@ -347,7 +354,9 @@ int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode
         if (!m || !m->cwords || !m->row_off || !m->raw || !m->lut || !outs[i] || Ms[i] <= 0)
             return CK_ERR_ARG;
         if (m->n_chunks != (int64_t)Ms[i] * (K / kSChunk)) return CK_ERR_ARG;
-        if (((uintptr_t)m->raw & 15) != 0 || ((uintptr_t)m->lut & 15) != 0) return CK_ERR_ARG;
+        if (((uintptr_t)m->raw & 15) != 0 || ((uintptr_t)m->lut & 15) != 0 ||
+            ((uintptr_t)m->cwords & 15) != 0)
+            return CK_ERR_ARG;
         SplitSeg &g = segs.s[i];
         g.cwords = m->cwords;
         g.row_off = m->row_off;

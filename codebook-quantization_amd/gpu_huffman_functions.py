@@ -155,7 +155,7 @@ def build_split(indices: torch.Tensor, codebook: np.ndarray, device):
         raise ValueError(f"split layout of {total} rows exceeds the 32-bit row index")
     row_off = torch.zeros(n_chunks + 1, dtype=torch.int32, device=device)
     row_off[1:] = cum.to(torch.int32)
-    cwords = torch.empty(total * hc.SUB_SYMBOLS, dtype=torch.int32, device=device)
+    cwords = torch.zeros((total + 3) * hc.SUB_SYMBOLS, dtype=torch.int32, device=device)
     raw = torch.empty(n, dtype=torch.uint8, device=device)
     nat.check(lib.cbq_split_pack(indices.data_ptr(), n, sc.data_ptr(), sr.data_ptr(),
                                  int(sym_code.size), row_off.data_ptr(), cwords.data_ptr(),

@@ -271,7 +271,7 @@ int cbq_huff_linear_col_xform_f32(const float *x0, const float *x1, float *h_out
  * 14).  lut[j] for the next 14 stream bits j (always two whole codes) is
  * hi1 << 24 | hi2 << 16 | (len1 + len2).  n_symbols % 4096 == 0. */
 typedef struct cbq_split_matrix {
-    const uint32_t *cwords;   /* total rows x 64 words (+ nothing past the last row) */
+    const uint32_t *cwords;   /* total rows x 64 words, then 3 readable rows, 16-byte aligned */
     const uint32_t *row_off;  /* [n_chunks + 1] */
     const uint8_t *raw;       /* [n_chunks * 4096] low bytes, 16-byte aligned */
     const uint32_t *lut;      /* [16384], 16-byte aligned */

@@ -27,7 +27,9 @@ def test_pack_matches_cpu_packer(cuda):
     sym_code, sym_raw, lut_h = hc.split_tables(cb, np.bincount(idx))
     cw, ro, rw = cpu_pack(idx.astype(np.int64), sym_code, sym_raw)
     assert np.array_equal(row_off.cpu().numpy(), ro)
-    assert np.array_equal(cwords.cpu().numpy().view(np.uint32).reshape(-1, 64), cw)
+    got = cwords.cpu().numpy().view(np.uint32).reshape(-1, 64)
+    assert np.array_equal(got[:cw.shape[0]], cw) and got.shape[0] == cw.shape[0] + 3
+    assert not got[cw.shape[0]:].any()                     # readable zero rows past the end
     assert np.array_equal(raw.cpu().numpy(), rw)
     assert np.array_equal(lut.cpu().numpy().view(np.uint32), lut_h)
 
