@@ -132,10 +132,10 @@ __device__ __forceinline__ float split_decode(const uint32_t (&raw)[16], const u
             w >>= (e & 31u);
             qm += (int)(e & 0xffu);
         }
-        const bool step = (qm >> 5) != d;
-        d += step ? 1 : 0;
-        w0 = step ? w1 : w0;
-        w1 = step ? w2 : w1;
+        const int dn = qm >> 5;                       // d or d + 1
+        w0 = dn != d ? w1 : w0;
+        w1 = dn != d ? w2 : w1;
+        d = dn;
     }
     return acc;
 }
