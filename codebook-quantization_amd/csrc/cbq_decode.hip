@@ -220,7 +220,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rope_decode_kernel(
 {
     extern __shared__ float s_att[];                              // [max_len + 1]
     __shared__ float s_raw[2][HD];
-    __shared__ float s_q[HD], s_k[HD], s_v[HD];
+    __shared__ float s_q[HD], s_k[HD], s_v[HD], s_cs[2][HD];
     __shared__ __attribute__((aligned(16))) float s_part[4 * kAttnThreads];
     __shared__ float s_red[kAttnThreads / CBQ_WAVE];
     const int h = blockIdx.x, g = h / group, tid = threadIdx.x;
@@ -242,6 +242,26 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rope_decode_kernel(
         r = rsqrtf(wave_sum(ss) / (float)HD + eps);
     } else if (wave == 2) {
         for (int d = lane; d < HD; d += CBQ_WAVE) s_v[d] = v[(size_t)g * HD + d];
+    } else if (wave < 5) {
+        const float *src = (wave == 3 ? cos_t : sin_t) + trow * HD;
+        for (int d = lane; d < HD; d += CBQ_WAVE) s_cs[wave - 3][d] = src[d];
+    }
+    // Warm L2 with the cached K and V rows [0, min(n_old, 512)) (one dword
+    // per 128-byte line) while the head vectors are normalised; the values
+    // are only kept until the end of the kernel.
+    constexpr int kLines = 8 * HD / 256;                          // lines of one K + one V row, / 4
+    uint32_t warm[2 * kLines];
+    {
+        const int rows = n_old < kAttnThreads ? n_old : kAttnThreads;
+        const uint32_t *kb = (const uint32_t *)(kc + (size_t)g * max_len * HD);
+        const uint32_t *vb = (const uint32_t *)(vc + (size_t)g * max_len * HD);
+#pragma unroll
+        for (int i = 0; i < kLines; i++) {
+            const int line = i * kAttnThreads + tid;             // line of the [rows, HD] block
+            const bool in = line < rows * (HD / 32);
+            warm[2 * i] = in ? kb[line * 32] : 0u;
+            warm[2 * i + 1] = in ? vb[line * 32] : 0u;
+        }
     }
     __syncthreads();
     if (wave < 2) {
@@ -253,7 +273,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rope_decode_kernel(
             float xn = __fmul_rn(s_raw[wave][d], r), xp = __fmul_rn(s_raw[wave][dp], r);
             if (w) { xn = __fmul_rn(w[d], xn); xp = __fmul_rn(w[dp], xp); }
             const float rot = d < half ? -xp : xp;
-            dst[d] = __fadd_rn(__fmul_rn(xn, cos_t[trow * HD + d]), __fmul_rn(rot, sin_t[trow * HD + d]));
+            dst[d] = __fadd_rn(__fmul_rn(xn, s_cs[0][d]), __fmul_rn(rot, s_cs[1][d]));
         }
     }
     __syncthreads();
@@ -321,6 +341,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rope_decode_kernel(
         for (int i = 0; i < G; i++) t += s_part[i * HD + tid];
         out[(size_t)h * HD + tid] = fmaf(s_att[n_old], s_v[tid], t);
     }
+    uint32_t sink = 0;
+#pragma unroll
+    for (int i = 0; i < 2 * kLines; i++) sink ^= warm[i];
+    asm volatile("" ::"v"(sink));                                 // keeps the warming loads
 }
 
 // Greedy pick of a decode step in two launches: kArgBlocks blocks reduce
