@@ -126,19 +126,23 @@ def prefill_section(torch, nat, lib, dev, fixed, kinds, args):
             M, K = t0.shape
             x = torch.randn(T, K, device=dev).bfloat16()
             o = torch.empty(T, M, device=dev, dtype=torch.bfloat16)
+            nws = int(lib.cbq_linear_bf16_workspace(T, M, K))
+            ws = torch.empty(max(1, nws // 4), dtype=torch.float32, device=dev)
 
-            def run(ns=ns, x=x, o=o):
+            def run(ns=ns, x=x, o=o, ws=ws, nws=nws):
                 st = nat.stream_ptr(dev)
                 for n in ns:
                     t = fixed[n]
-                    rc = lib.ck_linear_bf16(x.data_ptr(), t.packed.data_ptr(), t.codebook.data_ptr(),
-                                            o.data_ptr(), T, M, K, t.codebook.numel(), t.bits, st)
+                    rc = lib.cbq_linear_bf16_ws(x.data_ptr(), t.packed.data_ptr(),
+                                                t.codebook.data_ptr(), o.data_ptr(), T, M, K,
+                                                t.codebook.numel(), t.bits, ws.data_ptr(), nws, st)
                     if rc:
-                        raise RuntimeError(f"ck_linear_bf16 rc={rc} on {n}")
+                        raise RuntimeError(f"cbq_linear_bf16_ws rc={rc} on {n}")
             ms, _ = timed_graph(torch, run, max(2, args.steps // 4), 1)
             us = ms * 1e3 / len(ns)
             tf = 2.0 * T * M * K / (us * 1e-6) / 1e12
             out["shapes"][f"T{T}_{kind}"] = {"shape": f"{K}->{M}", "us_per_launch": round(us, 1),
+                                             "k_splits": max(1, nws // (4 * T * M)),
                                              "TFLOP/s": round(tf, 1),
                                              "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
     g = out["shapes"]["T2048_gate_proj"]

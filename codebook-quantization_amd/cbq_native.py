@@ -55,6 +55,9 @@ SIGNATURES = {
     "cbq_version": (ctypes.c_char_p, []),
     "ck_linear_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "ck_linear_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "cbq_linear_bf16_workspace": (ctypes.c_size_t, [_i, _i, _i]),
+    "cbq_linear_bf16_ws": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, ctypes.c_size_t,
+                                _vp]),
     "cbq_linear_affine_f32": (_i, [_vp, _vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _i, _i, _i, _i,
                                    _vp]),
     "ck_embedding_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),

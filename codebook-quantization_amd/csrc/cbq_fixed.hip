@@ -807,8 +807,10 @@ int embedding_impl(const int32_t *ids, const uint8_t *packed, const float *cb, f
 }  // namespace
 
 // bf16 MFMA prefill path (cbq_prefill.hip); -1 = shape not handled there.
+// S > 1 splits K, with S * T * M floats of workspace.
 int cbq_prefill_bf16(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
-                     int T, int M, int K, int C, int bits, hipStream_t st);
+                     int T, int M, int K, int C, int bits, hipStream_t st, int S, float *ws);
+int cbq_prefill_splits(int T, int M, int K);
 
 int cbq_num_cus()
 {
@@ -917,11 +919,37 @@ int ck_linear_bf16(const void *x_bf16, const uint8_t *packed, const float *codeb
     if (x_bf16 && packed && codebook && out_bf16 && T >= 64 && M > 0 && K > 0 && C > 0 &&
         bits >= 1 && bits <= 16) {
         const int rc = cbq_prefill_bf16((const uint16_t *)x_bf16, packed, codebook,
-                                        (uint16_t *)out_bf16, T, M, K, C, bits, stream);
+                                        (uint16_t *)out_bf16, T, M, K, C, bits, stream, 1,
+                                        nullptr);
         if (rc >= 0) return rc;
     }
     return linear_any_t<uint16_t, uint16_t>((const uint16_t *)x_bf16, packed, codebook,
                                             (uint16_t *)out_bf16, T, M, K, C, bits, stream);
+}
+
+size_t cbq_linear_bf16_workspace(int T, int M, int K)
+{
+    if (T <= 0 || M <= 0 || K <= 0) return 0;
+    const int S = cbq_prefill_splits(T, M, K);
+    return S > 1 ? (size_t)S * T * M * sizeof(float) : 0;
+}
+
+int cbq_linear_bf16_ws(const void *x_bf16, const uint8_t *packed, const float *codebook,
+                       void *out_bf16, int T, int M, int K, int C, int bits, void *workspace,
+                       size_t ws_bytes, hipStream_t stream)
+{
+    if (x_bf16 && packed && codebook && out_bf16 && T >= 64 && M > 0 && K > 0 && C > 0 &&
+        bits >= 1 && bits <= 16) {
+        const size_t need = cbq_linear_bf16_workspace(T, M, K);
+        const bool split = need > 0 && workspace && ws_bytes >= need &&
+                           ((uintptr_t)workspace & 15) == 0;
+        const int rc = cbq_prefill_bf16((const uint16_t *)x_bf16, packed, codebook,
+                                        (uint16_t *)out_bf16, T, M, K, C, bits, stream,
+                                        split ? cbq_prefill_splits(T, M, K) : 1,
+                                        split ? (float *)workspace : nullptr);
+        if (rc >= 0) return rc;
+    }
+    return ck_linear_bf16(x_bf16, packed, codebook, out_bf16, T, M, K, C, bits, stream);
 }
 
 int ck_embedding_f32(const int32_t *token_ids, const uint8_t *packed, const float *codebook,

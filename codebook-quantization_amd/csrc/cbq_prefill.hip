@@ -166,10 +166,13 @@ __device__ __forceinline__ void prefill_loop(
     }
 }
 
-template <int BITS>
+// SPLIT: block z sums only K groups [z * gs, z * gs + gs) and writes its fp32
+// partial tile to ws + z * T * M; prefill_reduce_kernel adds the partials.
+template <int BITS, bool SPLIT>
 __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     const uint16_t *__restrict__ x, const uint32_t *__restrict__ words,
-    const float *__restrict__ cb, uint16_t *__restrict__ out, int T, int M, int K, int C)
+    const float *__restrict__ cb, uint16_t *__restrict__ out, int T, int M, int K, int C,
+    float *__restrict__ ws, int gs)
 {
     __shared__ uint16_t s_cb[1 << BITS];                       // bf16 codebook (hi), padded
     __shared__ uint16_t s_cblo[1 << BITS];                     // bf16(cb - hi)
@@ -181,7 +184,9 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     const int lane = tid & (CBQ_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / CBQ_WAVE);
     const int t0 = blockIdx.x * kPT, m0 = blockIdx.y * kPM;
-    const int G = K / kPK;
+    const int G_all = K / kPK;
+    const int g_lo = SPLIT ? (int)blockIdx.z * gs : 0;
+    const int G = SPLIT ? min(G_all, g_lo + gs) - g_lo : G_all;
 
     // bf16 codebook, padded to 2^BITS (clamp semantics), split hi + lo
     int inexact = 0;
@@ -198,14 +203,14 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     // x staging: thread -> tile row tid/2, chunks 2*(tid%2) and +1 (clamped row)
     const int xr = tid >> 1, xc = (tid & 1) * 2;
     const int xt = min(t0 + xr, T - 1);
-    const uint16_t *xrow = x + (size_t)xt * K + xc * 8;
+    const uint16_t *xrow = x + (size_t)xt * K + (size_t)g_lo * kPK + xc * 8;
     // W decode: wave w takes part w % 4 (indices 8*part .. +7 of each group)
     // of tile rows 64*(w / 4) + lane, so the part is wave-uniform
     const int wr = ((wave >> 2) << 6) + lane, wp = wave & 3;
     const int wm = min(m0 + wr, M - 1);
     const int bit0 = wp * 8 * BITS;                            // within the 32-index group
     const int q0 = bit0 >> 5, sh0 = bit0 & 31;
-    const uint32_t *wrow = words + (size_t)wm * G * BITS + q0;
+    const uint32_t *wrow = words + ((size_t)wm * G_all + g_lo) * BITS + q0;
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -247,38 +252,85 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const int t = t0 + wt + a * 32 + i * 8 + (lane >> 5) * 4 + j;
-                    if (t < T) out[(size_t)t * M + m] = f32_to_bf16_rne(acc[a][b][i * 4 + j]);
+                    if (t >= T) continue;
+                    if (SPLIT)
+                        ws[((size_t)blockIdx.z * T + t) * M + m] = acc[a][b][i * 4 + j];
+                    else
+                        out[(size_t)t * M + m] = f32_to_bf16_rne(acc[a][b][i * 4 + j]);
                 }
         }
 }
 
+// out = bf16(sum over s of ws[s]), s in order.
+__global__ void prefill_reduce_kernel(const float *__restrict__ ws, int S, int64_t n,
+                                      uint16_t *__restrict__ out)
+{
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        float t = ws[i];
+        for (int s = 1; s < S; s++) t += ws[s * n + i];
+        out[i] = f32_to_bf16_rne(t);
+    }
+}
+
 template <int BITS>
 int launch_prefill(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
-                   int T, int M, int K, int C, hipStream_t st)
+                   int T, int M, int K, int C, int S, float *ws, hipStream_t st)
 {
-    dim3 grid((unsigned)((T + kPT - 1) / kPT), (unsigned)((M + kPM - 1) / kPM));
-    hipLaunchKernelGGL((fixed_prefill_kernel<BITS>), grid, dim3(kPBlock), 0, st, x,
-                       (const uint32_t *)packed, cb, out, T, M, K, C);
-    return cbq_launch_status("fixed_prefill_kernel");
+    const int G = K / kPK;
+    if (S <= 1) {
+        dim3 grid((unsigned)((T + kPT - 1) / kPT), (unsigned)((M + kPM - 1) / kPM));
+        hipLaunchKernelGGL((fixed_prefill_kernel<BITS, false>), grid, dim3(kPBlock), 0, st, x,
+                           (const uint32_t *)packed, cb, out, T, M, K, C, (float *)nullptr, G);
+        return cbq_launch_status("fixed_prefill_kernel");
+    }
+    const int gs = (G + S - 1) / S;
+    S = (G + gs - 1) / gs;                                   // no empty split
+    dim3 grid((unsigned)((T + kPT - 1) / kPT), (unsigned)((M + kPM - 1) / kPM), (unsigned)S);
+    hipLaunchKernelGGL((fixed_prefill_kernel<BITS, true>), grid, dim3(kPBlock), 0, st, x,
+                       (const uint32_t *)packed, cb, out, T, M, K, C, ws, gs);
+    int rc = cbq_launch_status("fixed_prefill_kernel");
+    if (rc) return rc;
+    const int64_t n = (int64_t)T * M;
+    const int blocks = (int)std::min<int64_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(prefill_reduce_kernel, dim3(blocks), dim3(256), 0, st, ws, S, n, out);
+    return cbq_launch_status("prefill_reduce_kernel");
 }
 
 }  // namespace
 
+// K splits for a T x M x K prefill.  Only grids of fewer tiles than half the
+// CUs split (past that the partials' extra traffic costs more than the idle
+// CUs): into enough blocks to cover the CUs once, with at least 8 K groups
+// (256 inputs) per split and at most 16 splits.
+int cbq_prefill_splits(int T, int M, int K)
+{
+    if (T < 64 || K % kPK != 0) return 1;
+    const int64_t tiles = (int64_t)((T + kPT - 1) / kPT) * ((M + kPM - 1) / kPM);
+    const int64_t cus = cbq_num_cus();
+    if (2 * tiles >= cus) return 1;
+    int S = (int)std::min<int64_t>((cus + tiles - 1) / tiles, 16);
+    S = std::min(S, (K / kPK) / 8);
+    return S < 2 ? 1 : S;
+}
+
 // Prefill dispatch used by ck_linear_bf16 (cbq_fixed.hip).  Returns -1 when
 // the shape is not handled here (the caller keeps its token-tile path).
+// S > 1 needs ws of S * T * M floats.
 int cbq_prefill_bf16(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
-                     int T, int M, int K, int C, int bits, hipStream_t st)
+                     int T, int M, int K, int C, int bits, hipStream_t st, int S, float *ws)
 {
     if (T < 64 || K % kPK != 0 || (((uintptr_t)packed | (uintptr_t)x) & 15) != 0 ||
         (K * 2) % 16 != 0 || (size_t)T > 65535ull * kPT || M > 65535 * kPM)
         return -1;
+    if (S > 1 && !ws) return -1;
     switch (bits) {
-    case 8: return launch_prefill<8>(x, packed, cb, out, T, M, K, C, st);
-    case 10: return launch_prefill<10>(x, packed, cb, out, T, M, K, C, st);
-    case 11: return launch_prefill<11>(x, packed, cb, out, T, M, K, C, st);
-    case 12: return launch_prefill<12>(x, packed, cb, out, T, M, K, C, st);
-    case 13: return launch_prefill<13>(x, packed, cb, out, T, M, K, C, st);
-    case 14: return launch_prefill<14>(x, packed, cb, out, T, M, K, C, st);
+    case 8: return launch_prefill<8>(x, packed, cb, out, T, M, K, C, S, ws, st);
+    case 10: return launch_prefill<10>(x, packed, cb, out, T, M, K, C, S, ws, st);
+    case 11: return launch_prefill<11>(x, packed, cb, out, T, M, K, C, S, ws, st);
+    case 12: return launch_prefill<12>(x, packed, cb, out, T, M, K, C, S, ws, st);
+    case 13: return launch_prefill<13>(x, packed, cb, out, T, M, K, C, S, ws, st);
+    case 14: return launch_prefill<14>(x, packed, cb, out, T, M, K, C, S, ws, st);
     default: return -1;
     }
 }

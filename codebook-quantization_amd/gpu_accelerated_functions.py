@@ -77,10 +77,16 @@ class GPUAcceleratedLinear:
         if in_dtype == torch.bfloat16:
             xc = x.reshape(T, self.K).contiguous()
             out = torch.empty(T, self.M, dtype=torch.bfloat16, device=dev)
-            rc = self._lib.ck_linear_bf16(xc.data_ptr(), self.packed.data_ptr(),
-                                          self.codebook.data_ptr(), out.data_ptr(), T, self.M,
-                                          self.K, self.C, self.bits, nat.stream_ptr(dev))
-            nat.check(rc, "ck_linear_bf16")
+            # batched tokens may split K across blocks: fp32 partials in a
+            # workspace from torch's caching allocator
+            nws = int(self._lib.cbq_linear_bf16_workspace(T, self.M, self.K)) if T >= 64 else 0
+            ws = torch.empty(max(1, nws // 4), dtype=torch.float32, device=dev) if nws else None
+            rc = self._lib.cbq_linear_bf16_ws(xc.data_ptr(), self.packed.data_ptr(),
+                                              self.codebook.data_ptr(), out.data_ptr(), T, self.M,
+                                              self.K, self.C, self.bits,
+                                              None if ws is None else ws.data_ptr(), nws,
+                                              nat.stream_ptr(dev))
+            nat.check(rc, "cbq_linear_bf16_ws")
             return out.reshape(*lead, self.M)
         xc = x.reshape(T, self.K).to(torch.float32).contiguous()
         out = torch.empty(T, self.M, dtype=torch.float32, device=dev)

@@ -15,7 +15,8 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
-def _prefill(cuda, xb, pk, cb, M, K, bits):
+def _prefill(cuda, xb, pk, cb, M, K, bits, split=False):
+    """ck_linear_bf16, or with split cbq_linear_bf16_ws with its workspace."""
     import bitpack
     import cbq_native as nat
     lib = nat.load()
@@ -24,9 +25,18 @@ def _prefill(cuda, xb, pk, cb, M, K, bits):
     cd = torch.from_numpy(np.ascontiguousarray(cb, np.float32)).to(cuda)
     xd = xb.to(cuda).contiguous()
     out = torch.full((T, M), float("nan"), dtype=torch.bfloat16, device=cuda)
-    rc = lib.ck_linear_bf16(xd.data_ptr(), pd.data_ptr(), cd.data_ptr(), out.data_ptr(), T, M, K,
-                            len(cb), bits, nat.stream_ptr(cuda))
-    nat.check(rc, "ck_linear_bf16")
+    if split:
+        nws = int(lib.cbq_linear_bf16_workspace(T, M, K))
+        assert nws > 0, "shape expected to split K"
+        ws = torch.full((nws // 4,), float("nan"), dtype=torch.float32, device=cuda)
+        rc = lib.cbq_linear_bf16_ws(xd.data_ptr(), pd.data_ptr(), cd.data_ptr(), out.data_ptr(),
+                                    T, M, K, len(cb), bits, ws.data_ptr(), nws,
+                                    nat.stream_ptr(cuda))
+        nat.check(rc, "cbq_linear_bf16_ws")
+    else:
+        rc = lib.ck_linear_bf16(xd.data_ptr(), pd.data_ptr(), cd.data_ptr(), out.data_ptr(), T,
+                                M, K, len(cb), bits, nat.stream_ptr(cuda))
+        nat.check(rc, "ck_linear_bf16")
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
 
@@ -92,3 +102,32 @@ def test_matches_token_tile_path(cuda):
     y64 = _prefill(cuda, xb, d["indices"], d["codebook"], M, K, d["bits"])
     y16 = _prefill(cuda, xb[:16].clone(), d["indices"], d["codebook"], M, K, d["bits"])
     assert rel_l2(y64[:16], y16) <= TOL
+
+
+@pytest.mark.parametrize("T,M,K", [(100, 300, 4096), (512, 136, 12288), (512, 1024, 4096),
+                                   (300, 2048, 4096)])
+def test_split_k_matches_oracle(cuda, oracle, T, M, K):
+    """Small output grids split K across blocks (fp32 partials in the
+    caller's workspace, summed in split order): the same tolerance against
+    the oracle, and the same output as the unsplit kernel within it."""
+    w = cbb.bf16_round(np.random.default_rng(T * 3 + M).standard_normal((M, K)) * 0.02)
+    d = cbb.compress_fixed(w)
+    xb = torch.randn(T, K, generator=torch.Generator().manual_seed(M)).bfloat16()
+    ys = _prefill(cuda, xb, d["indices"], d["codebook"], M, K, d["bits"], split=True)
+    ref = oracle.fixed_gemv(xb.float().numpy(), d["indices"], d["codebook"], M, K, d["bits"],
+                            chunk_rows=None)
+    _check(ys, ref)
+    y1 = _prefill(cuda, xb, d["indices"], d["codebook"], M, K, d["bits"])
+    assert rel_l2(ys, y1) <= TOL
+
+
+def test_split_k_inexact_codebook_and_clamp(cuda, oracle):
+    T, M, K, bits, C = 128, 200, 8192, 12, 3000
+    rng = np.random.default_rng(9)
+    raw = rng.integers(0, 1 << bits, size=M * K)
+    cb = (rng.standard_normal(C) * 0.05).astype(np.float32)
+    pk = oracle.pack_lsb(raw, bits)
+    xb = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).bfloat16()
+    y = _prefill(cuda, xb, pk, cb, M, K, bits, split=True)
+    ref = oracle.fixed_gemv(xb.float().numpy(), pk, cb, M, K, bits, C=C, chunk_rows=None)
+    assert rel_l2(y, ref) <= TOL
