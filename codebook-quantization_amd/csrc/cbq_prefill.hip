@@ -7,7 +7,7 @@
 // row's 32-index groups are BITS whole 32-bit words.
 //
 // Block = 8 waves, output tile 256 tokens x 128 features, K step 32.  Per K
-// step the block
+// step the block (tiles double-buffered in LDS, one barrier per step)
 //   - copies the x tile [256][32] bf16 to LDS,
 //   - decodes the W tile [128][32]: 4 threads per row, 8 indices each,
 //     gathering bf16 values from an LDS codebook padded to 2^BITS entries
@@ -98,70 +98,87 @@ __device__ __forceinline__ void prefill_loop(
 #pragma unroll
         for (int i = 0; i < NW; i++) wv[i] = ws[q0 + i < BITS ? i : BITS - 1 - q0];
     };
-    // Four K steps in flight: a register ring of x and index words, refilled
-    // right after each step's tiles are written.  The loop is unrolled by the
-    // ring depth so every ring slot is a fixed register set, and the barriers
-    // wait on LDS only, never on the prefetches.
+    // Four K steps in flight: a register ring of x and index words.  The LDS
+    // tiles are double-buffered: step g's MFMAs read buffer g & 1 while the
+    // waves decode and write step g + 1 into the other buffer, so each step
+    // needs one barrier, and the decode overlaps the matrix core.  The loop
+    // is unrolled by the ring depth (even) so ring slots and buffers are
+    // fixed registers and addresses; barriers wait on LDS only.
     constexpr int PD = 4;
     u32x4 xv[PD][2];
     uint32_t wv[PD][NW];
 #pragma unroll
     for (int d = 0; d < PD; d++) load_step(d < G ? d : G - 1, xv[d], wv[d]);
 
+    auto stage = [&](int d, int g, int buf) {
+        const bool live = g < G;
+        uint32_t *bx = s_x + buf * (kPT * 16);
+        uint32_t *bw = s_w + buf * (kPM * 16);
+        uint32_t *bl = s_wlo + buf * (kPM * 16);
+        *(u32x4 *)tile_chunk(bx, xr, xc) = live ? xv[d][0] : u32x4{0, 0, 0, 0};
+        *(u32x4 *)tile_chunk(bx, xr, xc + 1) = live ? xv[d][1] : u32x4{0, 0, 0, 0};
+        uint32_t pk[4], pl[4];
+        decode_part<BITS, WP, TWO>(wv[d], s_cb, s_cblo, pk, pl);
+        *(u32x4 *)tile_chunk(bw, wr, wp) = u32x4{pk[0], pk[1], pk[2], pk[3]};
+        if (TWO) *(u32x4 *)tile_chunk(bl, wr, wp) = u32x4{pl[0], pl[1], pl[2], pl[3]};
+    };
+    auto mfma_step = [&](int buf) {
+        const uint32_t *bx = s_x + buf * (kPT * 16);
+        const uint32_t *bw = s_w + buf * (kPM * 16);
+        const uint32_t *bl = s_wlo + buf * (kPM * 16);
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {   // two k16 halves of the 32-wide step
+            bf16x8 af[2], bfr[2], bfl[2];
+            const int c = kk * 2 + (lane >> 5);        // 16-byte chunk of the row
+#pragma unroll
+            for (int a = 0; a < 2; a++) {
+                const int r = wt + a * 32 + (lane & 31);
+                const u32x4 v = *(const u32x4 *)tile_chunk((uint32_t *)bx, r, c);
+                __builtin_memcpy(&af[a], &v, 16);
+            }
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const int r = wmo + b * 32 + (lane & 31);
+                const u32x4 v = *(const u32x4 *)tile_chunk((uint32_t *)bw, r, c);
+                __builtin_memcpy(&bfr[b], &v, 16);
+                if (TWO) {
+                    const u32x4 vl = *(const u32x4 *)tile_chunk((uint32_t *)bl, r, c);
+                    __builtin_memcpy(&bfl[b], &vl, 16);
+                }
+            }
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[b], acc[a][b],
+                                                                         0, 0, 0);
+                    if (TWO)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfl[b],
+                                                                             acc[a][b], 0, 0, 0);
+                }
+        }
+    };
+
+    stage(0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load_step(PD < G ? PD : G - 1, xv[0], wv[0]);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
     // Steps past G (G not a multiple of PD) run on zeroed x, adding nothing;
     // keeping them unconditional keeps the loop body branch-free.
     for (int g0 = 0; g0 < G; g0 += PD) {
 #pragma unroll
         for (int d = 0; d < PD; d++) {
             const int g = g0 + d;
-            {
-                const bool live = g < G;
-                lds_barrier();            // previous step's MFMA operands fully read
-                *(u32x4 *)tile_chunk(s_x, xr, xc) = live ? xv[d][0] : u32x4{0, 0, 0, 0};
-                *(u32x4 *)tile_chunk(s_x, xr, xc + 1) = live ? xv[d][1] : u32x4{0, 0, 0, 0};
-                uint32_t pk[4], pl[4];
-                decode_part<BITS, WP, TWO>(wv[d], s_cb, s_cblo, pk, pl);
-                *(u32x4 *)tile_chunk(s_w, wr, wp) = u32x4{pk[0], pk[1], pk[2], pk[3]};
-                if (TWO) *(u32x4 *)tile_chunk(s_wlo, wr, wp) = u32x4{pl[0], pl[1], pl[2], pl[3]};
-                // refill this slot (a clamped repeat past the end: never written);
-                // the scheduling barriers keep the loads here, PD steps ahead
-                __builtin_amdgcn_sched_barrier(0);
-                load_step(g + PD < G ? g + PD : G - 1, xv[d], wv[d]);
-                __builtin_amdgcn_sched_barrier(0);
-                lds_barrier();
-
-#pragma unroll
-                for (int kk = 0; kk < 2; kk++) {   // two k16 halves of the 32-wide step
-                    bf16x8 af[2], bfr[2], bfl[2];
-                    const int c = kk * 2 + (lane >> 5);        // 16-byte chunk of the row
-#pragma unroll
-                    for (int a = 0; a < 2; a++) {
-                        const int r = wt + a * 32 + (lane & 31);
-                        const u32x4 v = *(const u32x4 *)tile_chunk(s_x, r, c);
-                        __builtin_memcpy(&af[a], &v, 16);
-                    }
-#pragma unroll
-                    for (int b = 0; b < 2; b++) {
-                        const int r = wmo + b * 32 + (lane & 31);
-                        const u32x4 v = *(const u32x4 *)tile_chunk(s_w, r, c);
-                        __builtin_memcpy(&bfr[b], &v, 16);
-                        if (TWO) {
-                            const u32x4 vl = *(const u32x4 *)tile_chunk(s_wlo, r, c);
-                            __builtin_memcpy(&bfl[b], &vl, 16);
-                        }
-                    }
-#pragma unroll
-                    for (int a = 0; a < 2; a++)
-#pragma unroll
-                        for (int b = 0; b < 2; b++) {
-                            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                                af[a], bfr[b], acc[a][b], 0, 0, 0);
-                            if (TWO)
-                                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                                    af[a], bfl[b], acc[a][b], 0, 0, 0);
-                        }
-                }
-            }
+            const int dn = (d + 1) % PD;
+            mfma_step(d & 1);
+            stage(dn, g + 1, (d + 1) & 1);
+            // refill the staged slot (a clamped repeat past the end: never
+            // written); the scheduling barriers keep the loads PD steps ahead
+            __builtin_amdgcn_sched_barrier(0);
+            load_step(g + 1 + PD < G ? g + 1 + PD : G - 1, xv[dn], wv[dn]);
+            __builtin_amdgcn_sched_barrier(0);
+            lds_barrier();
         }
     }
 }
@@ -176,9 +193,9 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
 {
     __shared__ uint16_t s_cb[1 << BITS];                       // bf16 codebook (hi), padded
     __shared__ uint16_t s_cblo[1 << BITS];                     // bf16(cb - hi)
-    __shared__ __attribute__((aligned(16))) uint32_t s_x[kPT * 16];   // [256][32] bf16
-    __shared__ __attribute__((aligned(16))) uint32_t s_w[kPM * 16];   // [128][32] bf16
-    __shared__ __attribute__((aligned(16))) uint32_t s_wlo[kPM * 16];
+    __shared__ __attribute__((aligned(16))) uint32_t s_x[2 * kPT * 16];   // 2 x [256][32] bf16
+    __shared__ __attribute__((aligned(16))) uint32_t s_w[2 * kPM * 16];   // 2 x [128][32] bf16
+    __shared__ __attribute__((aligned(16))) uint32_t s_wlo[2 * kPM * 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & (CBQ_WAVE - 1);
