@@ -348,7 +348,6 @@ int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode
         return CK_ERR_ARG;
     SplitSegs segs = {};
     segs.n = n;
-    int m_max = 0;
     for (int i = 0; i < n; i++) {
         const cbq_split_matrix *m = mats[i];
         if (!m || !m->cwords || !m->row_off || !m->raw || !m->lut || !outs[i] || Ms[i] <= 0)
@@ -364,16 +363,22 @@ int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode
         g.lut = m->lut;
         g.out = outs[i];
         g.M = Ms[i];
-        m_max = std::max(m_max, Ms[i]);
     }
-    // waves per block: 16 unless that leaves CUs idle
-    const int per = m_max / cbq_num_cus();
+    // One block per CU in all (a second round of blocks would pay the table
+    // staging and the first loads again): each matrix gets blocks in
+    // proportion to its rows, with 16 waves per block unless that leaves CUs
+    // idle.
+    int64_t m_sum = 0;
+    for (int i = 0; i < n; i++) m_sum += Ms[i];
+    const int cus = cbq_num_cus();
+    const int64_t per = m_sum / cus;
     const int nw = per >= 16 ? 16 : per >= 8 ? 8 : 4;
     int blocks = 0;
     for (int i = 0; i < n; i++) {
         SplitSeg &g = segs.s[i];
         g.block0 = blocks;
-        g.nblocks = std::max(1, std::min(cbq_num_cus(), (g.M + nw - 1) / nw));
+        const int share = (int)std::max<int64_t>(1, (cus * (int64_t)g.M + m_sum / 2) / m_sum);
+        g.nblocks = std::max(1, std::min(share, (g.M + nw - 1) / nw));
         blocks += g.nblocks;
     }
 #define CBQ_SPLIT(NWV, MODE)                                                                      \
