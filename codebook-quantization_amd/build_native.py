@@ -15,8 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 SO = os.path.join(HERE, "libcbq_hip.so")
 ARCH = "gfx950"
-SOURCES = ["cbq_fixed.hip", "cbq_huffman.hip", "cbq_prefill.hip", "cbq_decode.hip",
-           "cbq_split.hip"]
+SOURCES = ["cbq_fixed.hip", "cbq_huffman.hip", "cbq_prefill.hip", "cbq_prefill_f32.hip",
+           "cbq_decode.hip", "cbq_split.hip"]
 
 
 def hipcc() -> str:

@@ -56,6 +56,9 @@ SIGNATURES = {
     "ck_linear_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "ck_linear_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "cbq_linear_bf16_workspace": (ctypes.c_size_t, [_i, _i, _i]),
+    "cbq_linear_f32_workspace": (ctypes.c_size_t, [_i, _i, _i]),
+    "cbq_linear_f32_ws": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, ctypes.c_size_t,
+                               _vp]),
     "cbq_linear_bf16_ws": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, ctypes.c_size_t,
                                 _vp]),
     "cbq_linear_affine_f32": (_i, [_vp, _vp, ctypes.c_uint32, ctypes.c_uint32, _vp, _i, _i, _i, _i,
@@ -81,6 +84,7 @@ SIGNATURES = {
     "cbq_linear_xform_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _i, _i, _i,
                                   _i, _vp]),
     "cbq_split_bits": (_i, [_vp, _i64, _vp, _i, _vp, _vp]),
+    "cbq_pack_indices": (_i, [_vp, _i64, _i, _vp, _vp]),
     "cbq_split_pack": (_i, [_vp, _i64, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
     "cbq_split_linear_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _i, _vp, _vp, _vp, _i,
                                   _vp]),

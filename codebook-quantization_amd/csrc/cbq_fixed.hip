@@ -811,6 +811,10 @@ int embedding_impl(const int32_t *ids, const uint8_t *packed, const float *cb, f
 int cbq_prefill_bf16(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
                      int T, int M, int K, int C, int bits, hipStream_t st, int S, float *ws);
 int cbq_prefill_splits(int T, int M, int K);
+// fp32 MFMA prefill path (cbq_prefill_f32.hip); -1 = shape not handled there.
+int cbq_prefill_f32(const float *x, const uint8_t *packed, const float *cb, float *out, int T,
+                    int M, int K, int C, int bits, hipStream_t st, int S, float *ws);
+int cbq_prefill_f32_splits(int T, int M, int K);
 
 int cbq_num_cus()
 {
@@ -844,7 +848,38 @@ const char *cbq_version(void) { return "cbq_hip 0.1 gfx950"; }
 int ck_linear_f32(const float *x, const uint8_t *packed, const float *codebook, float *out,
                   int T, int M, int K, int C, int bits, hipStream_t stream)
 {
+    // T >= 64: the GEMM regime, fp32 MFMA (cbq_prefill_f32.hip)
+    if (x && packed && codebook && out && T >= 64 && M > 0 && K > 0 && C > 0 && bits >= 1 &&
+        bits <= 16) {
+        const int rc = cbq_prefill_f32(x, packed, codebook, out, T, M, K, C, bits, stream, 1,
+                                       nullptr);
+        if (rc >= 0) return rc;
+    }
     return linear_any_t<float, float>(x, packed, codebook, out, T, M, K, C, bits, stream);
+}
+
+size_t cbq_linear_f32_workspace(int T, int M, int K)
+{
+    if (T <= 0 || M <= 0 || K <= 0) return 0;
+    const int S = cbq_prefill_f32_splits(T, M, K);
+    return S > 1 ? (size_t)S * T * M * sizeof(float) : 0;
+}
+
+int cbq_linear_f32_ws(const float *x, const uint8_t *packed, const float *codebook, float *out,
+                      int T, int M, int K, int C, int bits, void *workspace, size_t ws_bytes,
+                      hipStream_t stream)
+{
+    if (x && packed && codebook && out && T >= 64 && M > 0 && K > 0 && C > 0 && bits >= 1 &&
+        bits <= 16) {
+        const size_t need = cbq_linear_f32_workspace(T, M, K);
+        const bool split = need > 0 && workspace && ws_bytes >= need &&
+                           ((uintptr_t)workspace & 15) == 0;
+        const int rc = cbq_prefill_f32(x, packed, codebook, out, T, M, K, C, bits, stream,
+                                       split ? cbq_prefill_f32_splits(T, M, K) : 1,
+                                       split ? (float *)workspace : nullptr);
+        if (rc >= 0) return rc;
+    }
+    return ck_linear_f32(x, packed, codebook, out, T, M, K, C, bits, stream);
 }
 
 int cbq_linear_xform_f32(const float *x0, const float *x1, float *h_out, int mode, float eps,

@@ -307,9 +307,54 @@ __global__ void split_pack_kernel(const int32_t *__restrict__ idx, int64_t n_sub
     }
 }
 
+// LSB-first fixed-width packing (src/bitpack.py:32-95) of int32 indices,
+// clamped to [0, 2^bits - 1]: one thread per 32-index group, which is `bits`
+// whole words.
+template <int BITS>
+__global__ void pack_indices_kernel(const int32_t *__restrict__ idx, int64_t n_groups,
+                                    uint32_t *__restrict__ words)
+{
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n_groups) return;
+    const int32_t *p = idx + g * 32;
+    uint32_t *w = words + g * BITS;
+    constexpr uint32_t top = (1u << BITS) - 1u;
+    uint64_t acc = 0;
+    int nb = 0, q = 0;
+    for (int i = 0; i < 32; i++) {
+        const int32_t v = p[i];
+        const uint32_t u = v < 0 ? 0u : ((uint32_t)v > top ? top : (uint32_t)v);
+        acc |= (uint64_t)u << nb;
+        nb += BITS;
+        if (nb >= 32) {
+            w[q++] = (uint32_t)acc;
+            acc >>= 32;
+            nb -= 32;
+        }
+    }
+}
+
 }  // namespace
 
 extern "C" {
+
+int cbq_pack_indices(const int32_t *indices, int64_t n, int bits, uint8_t *packed,
+                     hipStream_t stream)
+{
+    if (!indices || !packed || n <= 0 || n % 32 != 0 || ((uintptr_t)packed & 3) != 0)
+        return CK_ERR_ARG;
+    const int64_t groups = n / 32;
+    const dim3 grid((unsigned)((groups + 255) / 256));
+    switch (bits) {
+    case 8: hipLaunchKernelGGL(pack_indices_kernel<8>, grid, dim3(256), 0, stream, indices, groups, (uint32_t *)packed); break;
+    case 10: hipLaunchKernelGGL(pack_indices_kernel<10>, grid, dim3(256), 0, stream, indices, groups, (uint32_t *)packed); break;
+    case 11: hipLaunchKernelGGL(pack_indices_kernel<11>, grid, dim3(256), 0, stream, indices, groups, (uint32_t *)packed); break;
+    case 12: hipLaunchKernelGGL(pack_indices_kernel<12>, grid, dim3(256), 0, stream, indices, groups, (uint32_t *)packed); break;
+    case 13: hipLaunchKernelGGL(pack_indices_kernel<13>, grid, dim3(256), 0, stream, indices, groups, (uint32_t *)packed); break;
+    default: return CK_ERR_ARG;
+    }
+    return cbq_launch_status("pack_indices_kernel");
+}
 
 int cbq_split_bits(const int32_t *indices, int64_t n_symbols, const uint32_t *sym_code, int n_sym,
                    uint32_t *sub_bits, hipStream_t stream)

@@ -385,8 +385,8 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
     import ctypes
     import cbq_native as nat
     import synthetic
-    from gpu_huffman_functions import (build_columns, build_split, columns_eligible,
-                                       decode_symbols)
+    from gpu_huffman_functions import (SymbolDecoder, build_columns, build_split,
+                                       columns_eligible, decode_symbols, huffman_prefill)
     lib = nat.load()
     dev = torch.device(device)
 
@@ -426,9 +426,14 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
             x = x.reshape(-1, K).contiguous()
             T = x.shape[0]
             out = torch.empty(T, M, device=dev)
-            nat.check(lib.ck_linear_f32(x.data_ptr(), t.packed.data_ptr(), t.codebook.data_ptr(),
-                                        out.data_ptr(), T, M, K, t.codebook.numel(), t.bits,
-                                        nat.stream_ptr(dev)), "ck_linear_f32")
+            # a prompt (T >= 64) may split K: fp32 partials in a torch workspace
+            nws = int(lib.cbq_linear_f32_workspace(T, M, K)) if T >= 64 else 0
+            ws = torch.empty(max(1, nws // 4), device=dev) if nws else None
+            nat.check(lib.cbq_linear_f32_ws(x.data_ptr(), t.packed.data_ptr(),
+                                            t.codebook.data_ptr(), out.data_ptr(), T, M, K,
+                                            t.codebook.numel(), t.bits,
+                                            None if ws is None else ws.data_ptr(), nws,
+                                            nat.stream_ptr(dev)), "cbq_linear_f32_ws")
             return out
 
         def xform(x0, x1, h_out, mode):
@@ -462,11 +467,19 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         elif with_cols and columns_eligible(desc, K):   # single-token GEMV on the column layout
             cols = build_columns(desc, M * K, dev, t.lengths, t.tables["codebook"].cpu().numpy())
 
+        sym = []                             # symbol tables, built on the first prompt
+
         def f(x, desc=desc, cols=cols):
             x = x.reshape(-1, K).contiguous()
             T = x.shape[0]
             if T == 1 and sp is not None:
                 return one(x)
+            if T >= 64:                      # prompt: decode + pack + matrix cores
+                if not sym:
+                    sym.append(SymbolDecoder(t.words, t.chunk_off, t.sub_len, t.lengths, dev))
+                y = huffman_prefill(sym[0], x, M, K, t.tables["codebook"])
+                if y is not None:
+                    return y
             out = torch.empty(T, M, device=dev)
             if T == 1 and cols is not None:
                 nat.check(lib.cbq_huff_linear_col_f32(x.data_ptr(), ctypes.byref(desc),

@@ -90,10 +90,14 @@ class GPUAcceleratedLinear:
             return out.reshape(*lead, self.M)
         xc = x.reshape(T, self.K).to(torch.float32).contiguous()
         out = torch.empty(T, self.M, dtype=torch.float32, device=dev)
-        rc = self._lib.ck_linear_f32(xc.data_ptr(), self.packed.data_ptr(),
-                                     self.codebook.data_ptr(), out.data_ptr(), T, self.M, self.K,
-                                     self.C, self.bits, nat.stream_ptr(dev))
-        nat.check(rc, "ck_linear_f32")
+        nws = int(self._lib.cbq_linear_f32_workspace(T, self.M, self.K)) if T >= 64 else 0
+        ws = torch.empty(max(1, nws // 4), dtype=torch.float32, device=dev) if nws else None
+        rc = self._lib.cbq_linear_f32_ws(xc.data_ptr(), self.packed.data_ptr(),
+                                         self.codebook.data_ptr(), out.data_ptr(), T, self.M,
+                                         self.K, self.C, self.bits,
+                                         None if ws is None else ws.data_ptr(), nws,
+                                         nat.stream_ptr(dev))
+        nat.check(rc, "cbq_linear_f32_ws")
         out = out.reshape(*lead, self.M)
         return out if in_dtype == torch.float32 else out.to(in_dtype)
 

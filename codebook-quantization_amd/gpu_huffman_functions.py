@@ -170,24 +170,72 @@ def split_bytes(keep) -> int:
     return sum(int(t.numel() * t.element_size()) for t in keep)
 
 
+class SymbolDecoder:
+    """Symbol-payload decode tables over a device-format stream (words,
+    chunk_off, sub_len as in _DeviceStream), built once; indices() decodes
+    every symbol to int32 with cbq_huff_decode_indices."""
+
+    def __init__(self, words: torch.Tensor, chunk_off: torch.Tensor, sub_len: torch.Tensor,
+                 lengths: np.ndarray, device):
+        lengths = np.ascontiguousarray(lengths, np.uint8)
+        lut1, lut2, canon, pay = hc.device_luts(lengths, None, int(lengths.size), False,
+                                                clamp=False)
+        self.device = device
+        self.n_sym = int(lengths.size)
+        self._keep = [words, chunk_off, sub_len,
+                      torch.from_numpy(lut1.view(np.int32)).to(device),
+                      torch.from_numpy(lut2.view(np.int32)).to(device),
+                      torch.from_numpy(canon).to(device), torch.from_numpy(pay).to(device)]
+        k = self._keep
+        self.desc = nat.HuffStream(
+            words=words.data_ptr(), n_words=int(words.numel()), chunk_off=chunk_off.data_ptr(),
+            sub_len=sub_len.data_ptr(), lut1=k[3].data_ptr(), lut2=k[4].data_ptr(),
+            n_lut2=int(lut2.size), canon=k[5].data_ptr(), canon_pay=k[6].data_ptr(),
+            value_cb=None, C=self.n_sym, stage_words=hc.stage_words_for(chunk_off.cpu().numpy()))
+
+    def indices(self, n: int) -> torch.Tensor:
+        out = torch.empty(n, dtype=torch.int32, device=self.device)
+        nat.check(nat.load().cbq_huff_decode_indices(ctypes.byref(self.desc), out.data_ptr(), n,
+                                                     nat.stream_ptr(self.device)),
+                  "cbq_huff_decode_indices")
+        return out
+
+
 def decode_symbols(words: torch.Tensor, chunk_off: torch.Tensor, sub_len: torch.Tensor,
                    lengths: np.ndarray, n: int, device) -> torch.Tensor:
-    """Decoded symbols (int32 [n]) of a device-format stream, via symbol-payload
-    tables and cbq_huff_decode_indices."""
-    lengths = np.ascontiguousarray(lengths, np.uint8)
-    lut1, lut2, canon, pay = hc.device_luts(lengths, None, int(lengths.size), False, clamp=False)
-    keep = [torch.from_numpy(a.view(np.int32) if a.dtype == np.uint32 else a).to(device)
-            for a in (lut1, lut2)] + [torch.from_numpy(canon).to(device),
-                                      torch.from_numpy(pay).to(device)]
-    desc = nat.HuffStream(words=words.data_ptr(), n_words=int(words.numel()),
-                          chunk_off=chunk_off.data_ptr(), sub_len=sub_len.data_ptr(),
-                          lut1=keep[0].data_ptr(), lut2=keep[1].data_ptr(), n_lut2=int(lut2.size),
-                          canon=keep[2].data_ptr(), canon_pay=keep[3].data_ptr(), value_cb=None,
-                          C=int(lengths.size), stage_words=hc.stage_words_for(chunk_off.cpu().numpy()))
-    out = torch.empty(n, dtype=torch.int32, device=device)
-    nat.check(nat.load().cbq_huff_decode_indices(ctypes.byref(desc), out.data_ptr(), n,
-                                                 nat.stream_ptr(device)), "cbq_huff_decode_indices")
+    """Decoded symbols (int32 [n]) of a device-format stream."""
+    out = SymbolDecoder(words, chunk_off, sub_len, lengths, device).indices(n)
     torch.cuda.synchronize(device)
+    return out
+
+
+def huffman_prefill(sym: SymbolDecoder, x: torch.Tensor, M: int, K: int,
+                    codebook: torch.Tensor) -> Optional[torch.Tensor]:
+    """y [T, M] for T >= 64 fp32 tokens: the stream is decoded to transient
+    fixed-width indices (cbq_huff_decode_indices, cbq_pack_indices) and
+    multiplied on the fp32 matrix cores (cbq_linear_f32_ws).  None when the
+    alphabet needs more than 13 bits or K % 32 != 0."""
+    T = x.shape[0]
+    C = int(codebook.numel())
+    bits = max(8, int(np.ceil(np.log2(max(sym.n_sym, C, 2)))))
+    bits = 10 if bits == 9 else bits
+    if bits > 13 or K % 32 or (M * K) % 32:
+        return None
+    lib = nat.load()
+    dev = sym.device
+    st = nat.stream_ptr(dev)
+    idx = sym.indices(M * K)
+    packed = torch.empty(M * K * bits // 8 + 16, dtype=torch.uint8, device=dev)
+    nat.check(lib.cbq_pack_indices(idx.data_ptr(), M * K, bits, packed.data_ptr(), st),
+              "cbq_pack_indices")
+    del idx
+    out = torch.empty(T, M, dtype=torch.float32, device=dev)
+    nws = int(lib.cbq_linear_f32_workspace(T, M, K))
+    ws = torch.empty(max(1, nws // 4), dtype=torch.float32, device=dev) if nws else None
+    nat.check(lib.cbq_linear_f32_ws(x.data_ptr(), packed.data_ptr(), codebook.data_ptr(),
+                                    out.data_ptr(), T, M, K, C, bits,
+                                    None if ws is None else ws.data_ptr(), nws, st),
+              "cbq_linear_f32_ws")
     return out
 
 
@@ -236,6 +284,8 @@ class HuffmanCodebookLinear:
                                  huff_sub_lens, device)
         self.device = device
         self._idx_dev = None
+        self._sym = None                  # symbol tables for the batched-token path
+        self._cb_dev = torch.from_numpy(self._cb_np).to(device)
         # single-token GEMVs read the split format when the codebook
         # is bf16-exact, else the column layout when the shape allows
         self.cols = None
@@ -265,6 +315,14 @@ class HuffmanCodebookLinear:
         xc = x.reshape(T, self.K).to(torch.float32).contiguous()
         out = torch.empty(T, self.M, dtype=torch.float32, device=self.device)
         st = nat.stream_ptr(self.device)
+        if T >= 64:
+            if self._sym is None:
+                self._sym = SymbolDecoder(self.dev.words, self.dev.chunk_off, self.dev.sub_len,
+                                          np.asarray(self._src[1], np.uint8), self.device)
+            y = huffman_prefill(self._sym, xc, self.M, self.K, self._cb_dev)
+            if y is not None:
+                out = y.reshape(*lead, self.M)
+                return out if in_dtype == torch.float32 else out.to(in_dtype)
         if T == 1 and self.split is not None:
             nat.check(self._lib.cbq_split_linear_f32(
                 xc.data_ptr(), None, None, 0, 0.0, 1,

@@ -46,6 +46,21 @@ int ck_linear_f32(const float *x, const uint8_t *packed, const float *codebook,
                   float *out, int T, int M, int K, int C, int bits,
                   hipStream_t stream);
 
+/* Workspace bytes cbq_linear_f32_ws splits K with for a T x M x K product
+ * (0: no split).  No counterpart in the reference. */
+size_t cbq_linear_f32_workspace(int T, int M, int K);
+
+/* ck_linear_f32 with a caller workspace: for T >= 64 on the fp32 MFMA path
+ * (widths 8 and 10..13), grids under two blocks per CU split K across
+ * blocks that write fp32 partials to `workspace` (>= cbq_linear_f32_workspace
+ * bytes, 16-byte aligned), summed in split order by a second kernel.  With a
+ * smaller workspace it is ck_linear_f32.  No counterpart in the reference:
+ * batched fp32 tokens through GPUAcceleratedLinear
+ * (src/gpu_accelerated_functions.py:928-950), e.g. a prompt prefill. */
+int cbq_linear_f32_ws(const float *x, const uint8_t *packed, const float *codebook, float *out,
+                      int T, int M, int K, int C, int bits, void *workspace, size_t ws_bytes,
+                      hipStream_t stream);
+
 /* Fixed-width GEMV with an implicit (affine) codebook: index i stands for
  * the bf16 value with bit pattern lo + i (i < w), 0x8000 + lo + i - w
  * (w <= i < 2w), and 0.0 for i >= 2w.  This is the load-time re-indexed
@@ -320,6 +335,15 @@ int cbq_split_linear_f32(const float *x0, const float *x1, float *h_out, int mod
  * (src/compressed_matmul.c:296-322). */
 int cbq_huff_decode_indices(const cbq_huff_stream *hs, int32_t *out,
                             int64_t n_symbols, hipStream_t stream);
+
+/* Packs n int32 indices (n % 32 == 0, clamped to [0, 2^bits - 1]) into the
+ * reference's LSB-first fixed-width stream (src/bitpack.py:32-95), bits in
+ * {8, 10, 11, 12, 13}; packed 4-byte aligned, n * bits / 8 bytes.  No
+ * counterpart on the GPU in the reference: the batched-token (prefill) path
+ * of a Huffman module decodes its stream with cbq_huff_decode_indices, packs
+ * it here and runs ck_linear_f32's matrix-core GEMM on the transient copy. */
+int cbq_pack_indices(const int32_t *indices, int64_t n, int bits, uint8_t *packed,
+                     hipStream_t stream);
 
 /* ==== library introspection ============================================== */
 
