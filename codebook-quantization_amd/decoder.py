@@ -386,15 +386,24 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
     import cbq_native as nat
     import synthetic
     from gpu_huffman_functions import (SymbolDecoder, build_columns, build_split,
-                                       columns_eligible, decode_symbols, huffman_prefill)
+                                       columns_eligible, huffman_prefill)
     lib = nat.load()
     dev = torch.device(device)
+
+    syms = {}
+
+    def sym_of(t):
+        """Symbol-payload decode tables of a tensor, built once at load (the
+        split format and the prompt path both decode the stream)."""
+        if t.name not in syms:
+            syms[t.name] = SymbolDecoder(t.words, t.chunk_off, t.sub_len, t.lengths, dev)
+        return syms[t.name]
 
     def huff_split(t):
         M, K = t.shape
         if not split or K % 4096:
             return None
-        idx = decode_symbols(t.words, t.chunk_off, t.sub_len, t.lengths, M * K, dev)
+        idx = sym_of(t).indices(M * K)
         sp = build_split(idx, t.tables["codebook"].cpu().numpy(), dev)
         del idx
         return sp
@@ -467,7 +476,7 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         elif with_cols and columns_eligible(desc, K):   # single-token GEMV on the column layout
             cols = build_columns(desc, M * K, dev, t.lengths, t.tables["codebook"].cpu().numpy())
 
-        sym = []                             # symbol tables, built on the first prompt
+        sym = sym_of(t)
 
         def f(x, desc=desc, cols=cols):
             x = x.reshape(-1, K).contiguous()
@@ -475,9 +484,7 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
             if T == 1 and sp is not None:
                 return one(x)
             if T >= 64:                      # prompt: decode + pack + matrix cores
-                if not sym:
-                    sym.append(SymbolDecoder(t.words, t.chunk_off, t.sub_len, t.lengths, dev))
-                y = huffman_prefill(sym[0], x, M, K, t.tables["codebook"])
+                y = huffman_prefill(sym, x, M, K, t.tables["codebook"])
                 if y is not None:
                     return y
             out = torch.empty(T, M, device=dev)

@@ -284,17 +284,18 @@ class HuffmanCodebookLinear:
                                  huff_sub_lens, device)
         self.device = device
         self._idx_dev = None
-        self._sym = None                  # symbol tables for the batched-token path
+        self._sym = None                  # symbol tables (split format, batched tokens)
         self._cb_dev = torch.from_numpy(self._cb_np).to(device)
         # single-token GEMVs read the split format when the codebook
         # is bf16-exact, else the column layout when the shape allows
         self.cols = None
         self.split = None
         if split_format and self.K % hc.CHUNK_SYMBOLS == 0:
-            idx = self.decode_indices().reshape(-1)
+            self._sym = SymbolDecoder(self.dev.words, self.dev.chunk_off, self.dev.sub_len,
+                                      np.asarray(huff_lengths, np.uint8), device)
+            idx = self._sym.indices(self.M * self.K)
             self.split = build_split(idx, self._cb_np, device)
             del idx
-            self._idx_dev = None
         if self.split is None and columns_eligible(self.dev.desc, self.K):
             self._col_keep, self.cols = build_columns(
                 self.dev.desc, self.M * self.K, device, np.asarray(huff_lengths, np.uint8),
