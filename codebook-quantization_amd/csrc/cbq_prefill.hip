@@ -85,7 +85,7 @@ template <int BITS, bool TWO, int WP>
 __device__ __forceinline__ void prefill_loop(
     const uint16_t *__restrict__ xrow, const uint32_t *__restrict__ wrow, int G, int q0,
     int sh0, const uint16_t *s_cb, const uint16_t *s_cblo, uint32_t *s_x, uint32_t *s_w,
-    uint32_t *s_wlo, int xr, int xc, int wr, int wp, int lane, int wt, int wmo,
+    uint32_t *s_wlo, int xr, int xc, int wr, int wp, int lane, int wt, int wmo, bool active,
     f32x16 (&acc)[2][2])
 {
     constexpr int NW = (8 * BITS + 31 + 31) / 32;             // words covering 8 fields
@@ -171,7 +171,8 @@ __device__ __forceinline__ void prefill_loop(
         for (int d = 0; d < PD; d++) {
             const int g = g0 + d;
             const int dn = (d + 1) % PD;
-            mfma_step(d & 1);
+            // waves whose 64 tokens all lie past T (a short batch) only stage
+            if (active) mfma_step(d & 1);
             stage(dn, g + 1, (d + 1) & 1);
             // refill the staged slot (a clamped repeat past the end: never
             // written); the scheduling barriers keep the loads PD steps ahead
@@ -237,9 +238,10 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     const int wt = (wave >> 1) * 64;      // wave's token offset in the tile
     const int wmo = (wave & 1) * 64;      // wave's feature offset in the tile
     // one loop instance per (split, part): the loop body itself has no branch
+    const bool active = t0 + wt < T;      // wave-uniform
 #define CBQ_PREFILL_LOOP(TW, P)                                                                  \
     prefill_loop<BITS, TW, P>(xrow, wrow, G, q0, sh0, s_cb, s_cblo, s_x, s_w, s_wlo, xr, xc, wr, \
-                              wp, lane, wt, wmo, acc)
+                              wp, lane, wt, wmo, active, acc)
     if (two) {
         switch (wp) {
         case 0: CBQ_PREFILL_LOOP(true, 0); break;

@@ -64,7 +64,7 @@ template <int BITS, int WP>
 __device__ __forceinline__ void prefill_f32_loop(
     const float *__restrict__ xrow, const uint32_t *__restrict__ wrow, int G, int q0,
     const float *s_cb, float *s_x, float *s_w, int xr, int hx, int wr, int lane, int wt, int wmo,
-    f32x16 (&acc)[2][2])
+    bool active, f32x16 (&acc)[2][2])
 {
     constexpr int NW = (8 * BITS + 31 + 31) / 32;             // words covering 8 fields
     auto load_step = [&](int g, f4 (&xv)[4], uint32_t (&wv)[NW]) {
@@ -112,6 +112,8 @@ __device__ __forceinline__ void prefill_f32_loop(
             load_step(g + PD < G ? g + PD : G - 1, xv[d], wv[d]);
             __builtin_amdgcn_sched_barrier(0);
             lds_barrier();
+            // waves whose 64 tokens all lie past T (a short batch) only stage
+            if (!active) continue;
 
             const int h = lane >> 5;
             float af[2][16], bf[2][16];
@@ -192,8 +194,10 @@ __global__ __launch_bounds__(kFBlock) void fixed_prefill_f32_kernel(
         for (int b = 0; b < 2; b++) acc[a][b] = f32x16{};
     const int wt = (wave >> 1) * 64;      // wave's token offset in the tile
     const int wmo = (wave & 1) * 64;      // wave's feature offset in the tile
+    const bool active = t0 + wt < T;      // wave-uniform
 #define CBQ_PF32_LOOP(P)                                                                          \
-    prefill_f32_loop<BITS, P>(xrow, wrow, G, q0, s_cb, s_x, s_w, xr, hx, wr, lane, wt, wmo, acc)
+    prefill_f32_loop<BITS, P>(xrow, wrow, G, q0, s_cb, s_x, s_w, xr, hx, wr, lane, wt, wmo,      \
+                              active, acc)
     switch (wp) {
     case 0: CBQ_PF32_LOOP(0); break;
     case 1: CBQ_PF32_LOOP(1); break;
