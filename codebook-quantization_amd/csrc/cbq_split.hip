@@ -106,21 +106,28 @@ __device__ __forceinline__ void split_stage(const SplitItem &it, uint32_t H, uin
 // the words (d, d+1) of the current window and word d+2, read one group
 // ahead, stay in registers and the table reads are the only LDS accesses on
 // the dependent chain.
+//
+// The stream position is kept as the plain sum of the table entries read
+// (plus a bias of 32): an entry's bits 8..15 are zero, so bits 0..15 of the
+// sum are the bits consumed so far (at most 64 * 7 + 32 < 2^16) and the
+// hi-byte fields only pile up above them.  Shifts use bits 0..4 of their
+// amount, so no masking is needed between the table read and the next
+// window.
 __device__ __forceinline__ float split_decode(const uint32_t (&raw)[16], const uint32_t *s_lds,
                                               int lane_addr, const float *xr, int xsw)
 {
     float acc = 0.f;
-    int qm = -2;                                      // stream bit position - 2
-    int d = -1;                                       // word of bit qm
+    uint32_t pos = 30;                                // (stream bit position - 2) + 32
+    uint32_t d1 = 0;                                  // (word of bit position - 2) + 1
     const char *base = (const char *)s_lds + lane_addr;
     uint32_t w0 = *(const uint32_t *)(base - 4 * kSSub);
     uint32_t w1 = *(const uint32_t *)base;
 #pragma unroll
     for (int g = 0; g < 16; g++) {
-        const uint32_t w2 = *(const uint32_t *)(base + (d + 2) * (4 * kSSub));
+        const uint32_t w2 = *(const uint32_t *)(base + (d1 + 1) * (4 * kSSub));
         const f4 xv4 = *(const f4 *)(xr + ((4 * g) ^ xsw));
         const float xv[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
-        uint32_t w = __builtin_amdgcn_alignbit(w1, w0, (uint32_t)qm);   // 30 bits in 2..31
+        uint32_t w = __builtin_amdgcn_alignbit(w1, w0, pos);   // 30 bits in 2..31
 #pragma unroll
         for (int u = 0; u < 4; u += 2) {
             const uint32_t e = *(const uint32_t *)((const char *)s_lds + (w & (4u * kSLut - 4u)));
@@ -130,12 +137,12 @@ __device__ __forceinline__ float split_decode(const uint32_t (&raw)[16], const u
             acc = fmaf(xv[u], __uint_as_float(v0), acc);
             acc = fmaf(xv[u + 1], __uint_as_float(v1), acc);
             w >>= (e & 31u);
-            qm += (int)(e & 0xffu);
+            pos += e;
         }
-        const int dn = qm >> 5;                       // d or d + 1
-        w0 = dn != d ? w1 : w0;
-        w1 = dn != d ? w2 : w1;
-        d = dn;
+        const uint32_t dn = __builtin_amdgcn_ubfe(pos, 5, 11);   // d1 or d1 + 1
+        w0 = dn != d1 ? w1 : w0;
+        w1 = dn != d1 ? w2 : w1;
+        d1 = dn;
     }
     return acc;
 }
