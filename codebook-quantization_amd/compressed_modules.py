@@ -58,7 +58,10 @@ def _resolve_codebook(data: dict, global_codebooks: dict, default_type=None):
         return torch.as_tensor(np.asarray(cb)).float()
     ttype = data.get("codebook_type") or data.get("type") or default_type
     if ttype and ttype in global_codebooks:
-        return torch.as_tensor(np.asarray(global_codebooks[ttype])).float()
+        g = global_codebooks[ttype]
+        if isinstance(g, torch.Tensor):          # e.g. bf16, as the loader returns them
+            return g.detach().to("cpu", torch.float32)
+        return torch.as_tensor(np.asarray(g)).float()
     return None
 
 
