@@ -347,6 +347,215 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rope_decode_kernel(
     asm volatile("" ::"v"(sink));                                 // keeps the warming loads
 }
 
+// The same one-token step with the cached rows split over S blocks per query
+// head (grid n_q x S, flash decoding): a lone block per head is held to one
+// CU's load bandwidth, S blocks per head spread the key/value reads over the
+// chip.  Block (h, s) takes rows [s R, (s + 1) R) of the n_old + 1 rows
+// (R = ceil((n_old + 1) / S)) in chunks of CH rows: scores, a running max and
+// sum of exponentials, and the exp-weighted sum of value rows.  It writes the
+// partial (max, sum, vector) to the workspace; attn_combine_kernel, the next
+// launch, merges the S partials of each head in order s = 0 .. S-1.  The
+// first chunk's key and value rows are requested before the head norm, so
+// their latency overlaps it.
+constexpr int kSplitThreads = 256;
+constexpr int kSplitChunk = 64;
+constexpr int kMaxSplits = 16;
+
+__host__ __device__ constexpr int attn_split_count(int max_len)
+{
+    return max_len <= kSplitChunk ? 1
+         : ((max_len + kSplitChunk - 1) / kSplitChunk > kMaxSplits
+                ? kMaxSplits : (max_len + kSplitChunk - 1) / kSplitChunk);
+}
+
+template <int HD>
+__global__ __launch_bounds__(kSplitThreads) void attn_rope_split_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    const float *__restrict__ qw, const float *__restrict__ kw, const float *__restrict__ cos_t,
+    const float *__restrict__ sin_t, const int64_t *__restrict__ pos, float *__restrict__ kc,
+    float *__restrict__ vc, float *__restrict__ part, int group, int max_len, float scale,
+    float eps)
+{
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int LPR = HD / 32;                       // lanes per key row, 32 dims each
+    constexpr int RPP = kSplitThreads / LPR;           // key rows per score pass
+    constexpr int CH = RPP < kSplitChunk ? RPP : kSplitChunk;
+    constexpr int Q4 = HD / 4;                         // float4 columns of a row
+    constexpr int NG = kSplitThreads / Q4;             // row groups of the value pass
+    constexpr int VPT = CH / NG;                       // value rows per thread per chunk
+    static_assert(CH <= CBQ_WAVE && CH % NG == 0, "chunk layout");
+
+    __shared__ float s_raw[2][HD];
+    __shared__ __attribute__((aligned(16))) float s_q[HD];
+    __shared__ float s_k[HD], s_cs[2][HD];
+    __shared__ __attribute__((aligned(16))) float s_v[HD];
+    __shared__ float s_sc[CH], s_p[CH];
+    __shared__ __attribute__((aligned(16))) float s_part[NG * HD];
+    __shared__ float s_ml[3];                          // running max, sum, chunk rescale
+
+    const int h = blockIdx.x, sp = blockIdx.y, S = gridDim.y, g = h / group;
+    const int tid = threadIdx.x, wave = tid / CBQ_WAVE, lane = tid & (CBQ_WAVE - 1);
+    const int64_t p = pos[0];
+    const bool store = p >= 0 && p < max_len;
+    const int64_t trow = store ? p : 0;
+    const int n_old = (int)(p < 0 ? 0 : (p > max_len ? max_len : p));
+    const int n_all = n_old + 1;
+    const int R = (n_all + S - 1) / S;
+    const int j0 = sp * R < n_all ? sp * R : n_all;
+    const int j1 = j0 + R < n_all ? j0 + R : n_all;
+
+    const float *K = kc + (size_t)g * max_len * HD;
+    const float *V = vc + (size_t)g * max_len * HD;
+    const int srow = tid / LPR, spart = tid % LPR;     // score pass: row, 32-dim part
+    const int d4 = tid % Q4, rg = tid / Q4;            // value pass: column, row group
+    f4 kreg[8], vreg[VPT];
+    auto load_chunk = [&](int c0) {
+        const int j = c0 + srow;
+        if (srow < CH && j < j1 && j < n_old) {
+            const f4 *kr = (const f4 *)(K + (size_t)j * HD + spart * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) kreg[i] = kr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const int jv = c0 + rg + i * NG;
+            if (jv < j1 && jv < n_old) vreg[i] = ((const f4 *)(V + (size_t)jv * HD))[d4];
+        }
+    };
+    if (j0 < j1) load_chunk(j0);
+
+    // head norm + rope of the query head and the group's new key (as
+    // attn_rope_decode_kernel), the new value row
+    float r = 0.f;
+    if (wave < 2) {
+        const float *src = wave == 0 ? q + (size_t)h * HD : k + (size_t)g * HD;
+        float ss = 0.f;
+        for (int d = lane; d < HD; d += CBQ_WAVE) {
+            const float x = src[d];
+            s_raw[wave][d] = x;
+            ss = __fadd_rn(ss, __fmul_rn(x, x));
+        }
+        r = rsqrtf(wave_sum(ss) / (float)HD + eps);
+    } else if (wave == 2) {
+        for (int d = lane; d < HD; d += CBQ_WAVE) s_v[d] = v[(size_t)g * HD + d];
+    } else {
+        for (int d = lane; d < HD; d += CBQ_WAVE) {
+            s_cs[0][d] = cos_t[trow * HD + d];
+            s_cs[1][d] = sin_t[trow * HD + d];
+        }
+    }
+    __syncthreads();
+    if (wave < 2) {
+        const float *w = wave == 0 ? qw : kw;
+        float *dst = wave == 0 ? s_q : s_k;
+        constexpr int half = HD / 2;
+        for (int d = lane; d < HD; d += CBQ_WAVE) {
+            const int dp = d < half ? d + half : d - half;
+            float xn = __fmul_rn(s_raw[wave][d], r), xp = __fmul_rn(s_raw[wave][dp], r);
+            if (w) { xn = __fmul_rn(w[d], xn); xp = __fmul_rn(w[dp], xp); }
+            const float rot = d < half ? -xp : xp;
+            dst[d] = __fadd_rn(__fmul_rn(xn, s_cs[0][d]), __fmul_rn(rot, s_cs[1][d]));
+        }
+    }
+    __syncthreads();
+    if (store && sp == 0 && h % group == 0)
+        for (int d = tid; d < HD; d += kSplitThreads) {
+            kc[((size_t)g * max_len + p) * HD + d] = s_k[d];
+            vc[((size_t)g * max_len + p) * HD + d] = s_v[d];
+        }
+
+    float m_run = -INFINITY, l_run = 0.f;              // wave 0's copies are the live ones
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = j0; c0 < j1; c0 += CH) {
+        if (c0 != j0) load_chunk(c0);
+        const int n = j1 - c0 < CH ? j1 - c0 : CH;
+        if (srow < n) {
+            const int j = c0 + srow;
+            const float *qp = s_q + spart * 32;
+            float dot = 0.f;
+            if (j < n_old) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    dot = fmaf(qp[4 * i + 0], kreg[i].x, dot);
+                    dot = fmaf(qp[4 * i + 1], kreg[i].y, dot);
+                    dot = fmaf(qp[4 * i + 2], kreg[i].z, dot);
+                    dot = fmaf(qp[4 * i + 3], kreg[i].w, dot);
+                }
+            } else {
+                for (int d = 0; d < 32; d++) dot = fmaf(qp[d], s_k[spart * 32 + d], dot);
+            }
+#pragma unroll
+            for (int o = LPR >> 1; o > 0; o >>= 1) dot = __fadd_rn(dot, __shfl_xor(dot, o, CBQ_WAVE));
+            if (spart == 0) s_sc[srow] = __fmul_rn(dot, scale);
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const float sc = lane < n ? s_sc[lane] : -INFINITY;
+            const float mn = fmaxf(m_run, wave_max(sc));
+            const float alpha = expf(__fsub_rn(m_run, mn));
+            const float pj = lane < n ? expf(__fsub_rn(sc, mn)) : 0.f;
+            if (lane < CH) s_p[lane] = pj;
+            l_run = __fadd_rn(__fmul_rn(l_run, alpha), wave_sum(pj));
+            m_run = mn;
+            if (lane == 0) s_ml[2] = alpha;
+        }
+        __syncthreads();
+        const float alpha = s_ml[2];
+        acc.x = __fmul_rn(acc.x, alpha);
+        acc.y = __fmul_rn(acc.y, alpha);
+        acc.z = __fmul_rn(acc.z, alpha);
+        acc.w = __fmul_rn(acc.w, alpha);
+#pragma unroll
+        for (int i = 0; i < VPT; i++) {
+            const int rr = rg + i * NG;
+            if (rr < n) {
+                const f4 vv = c0 + rr < n_old ? vreg[i] : ((const f4 *)s_v)[d4];
+                acc = __builtin_elementwise_fma((f4)s_p[rr], vv, acc);
+            }
+        }
+    }
+    ((f4 *)s_part)[tid] = acc;
+    if (tid == 0) {
+        s_ml[0] = m_run;
+        s_ml[1] = l_run;
+    }
+    __syncthreads();
+
+    // this block's partial: [max, sum, vector[HD]]
+    float *rec = part + ((size_t)h * S + sp) * (HD + 2);
+    for (int d = tid; d < HD; d += kSplitThreads) {
+        float t = 0.f;
+        for (int i = 0; i < NG; i++) t = __fadd_rn(t, s_part[i * HD + d]);
+        rec[2 + d] = t;
+    }
+    if (tid == 0) {
+        rec[0] = s_ml[0];
+        rec[1] = s_ml[1];
+    }
+}
+
+// out[h] = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s over the S partials
+// of head h, in order s = 0 .. S-1 (M = max_s m_s; an empty split has
+// m = -inf, l = 0, acc = 0 and adds nothing).  One block per head, one
+// thread per dimension.
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_combine_kernel(const float *__restrict__ part, int S,
+                                                          float *__restrict__ out)
+{
+    const int h = blockIdx.x, d = threadIdx.x;
+    const float *base = part + (size_t)h * S * (HD + 2);
+    float M = -INFINITY;
+    for (int t = 0; t < S; t++) M = fmaxf(M, base[(size_t)t * (HD + 2)]);
+    float L = 0.f, o = 0.f;
+    for (int t = 0; t < S; t++) {
+        const float *rt = base + (size_t)t * (HD + 2);
+        const float e = expf(__fsub_rn(rt[0], M));
+        L = __fadd_rn(L, __fmul_rn(rt[1], e));
+        o = __fadd_rn(o, __fmul_rn(rt[2 + d], e));
+    }
+    out[(size_t)h * HD + d] = __fdiv_rn(o, L);
+}
+
 // Greedy pick of a decode step in two launches: kArgBlocks blocks reduce
 // slices of the logits to (value, index) partials in the caller's workspace,
 // one block reduces those and does the step bookkeeping.  Order: first
@@ -508,6 +717,46 @@ int cbq_attn_rope_decode_f32(const float *q, const float *k, const float *v,
     }
 #undef CBQ_ATTN_ROPE
     return cbq_launch_status("attn_rope_decode_kernel");
+}
+
+size_t cbq_attn_rope_decode_workspace(int n_q, int hd, int max_len)
+{
+    if (n_q <= 0 || hd <= 0 || max_len <= 0) return 0;
+    return (size_t)n_q * attn_split_count(max_len) * (hd + 2) * sizeof(float);
+}
+
+int cbq_attn_rope_decode_ws_f32(const float *q, const float *k, const float *v,
+                                const float *q_weight, const float *k_weight,
+                                const float *cos_table, const float *sin_table,
+                                const int64_t *pos, float *k_cache, float *v_cache, float *out,
+                                int n_q, int n_kv, int hd, int max_len, float scale, float eps,
+                                void *workspace, size_t workspace_bytes, hipStream_t stream)
+{
+    if (!q || !k || !v || !cos_table || !sin_table || !pos || !k_cache || !v_cache || !out ||
+        !workspace)
+        return CK_ERR_ARG;
+    if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || max_len <= 0 || max_len > kAttnMaxLen)
+        return CK_ERR_ARG;
+    if (((uintptr_t)k_cache & 15) != 0 || ((uintptr_t)v_cache & 15) != 0 ||
+        ((uintptr_t)workspace & 3) != 0)
+        return CK_ERR_ARG;
+    if (hd != 64 && hd != 128 && hd != 256) return CK_ERR_ARG;
+    if (workspace_bytes < cbq_attn_rope_decode_workspace(n_q, hd, max_len)) return CK_ERR_ARG;
+    const int S = attn_split_count(max_len);
+    float *part = (float *)workspace;
+    const int group = n_q / n_kv;
+#define CBQ_ATTN_SPLIT(HD)                                                                      \
+    hipLaunchKernelGGL(attn_rope_split_kernel<HD>, dim3(n_q, S), dim3(kSplitThreads), 0, stream, \
+                       q, k, v, q_weight, k_weight, cos_table, sin_table, pos, k_cache, v_cache,  \
+                       part, group, max_len, scale, eps);                                          \
+    hipLaunchKernelGGL(attn_combine_kernel<HD>, dim3(n_q), dim3(HD), 0, stream, part, S, out)
+    switch (hd) {
+    case 64: CBQ_ATTN_SPLIT(64); break;
+    case 128: CBQ_ATTN_SPLIT(128); break;
+    default: CBQ_ATTN_SPLIT(256); break;
+    }
+#undef CBQ_ATTN_SPLIT
+    return cbq_launch_status("attn_combine_kernel");
 }
 
 int cbq_argmax_step(const float *logits, int n, void *workspace, int32_t *ids32, int64_t *toks,

@@ -108,15 +108,39 @@ class _Glue:
             self.nat.stream_ptr(q.device)), "cbq_head_norm_rope_f32")
         return q_out
 
+    def attn_workspace(self, device, max_len: int) -> torch.Tensor:
+        """Scratch of the split one-token attention, allocated once per device
+        and cache length (before any graph capture)."""
+        key = (torch.device(device), int(max_len))
+        if getattr(self, "_aws", None) is None or self._aws[0] != key:
+            n = self.lib.cbq_attn_rope_decode_workspace(self.cfg.n_q, self.cfg.head_dim,
+                                                        int(max_len))
+            self._aws = (key, torch.empty(n, dtype=torch.uint8, device=key[0]))
+        return self._aws[1]
+
+    # Caches at least this long take the split-over-blocks attention: one
+    # block per head is held to one CU's load bandwidth, which the longer
+    # contexts exceed; below it the single launch is cheaper than the split
+    # launch plus its merge launch.
+    SPLIT_ATTN_MIN_LEN = 2048
+
     def attend_rope1(self, q, k, v, cos, sin, pos_dev, k_cache, v_cache) -> torch.Tensor:
         """One token: head norm + rope of q and k, cache write, attention."""
         c = self.cfg
         out = torch.empty(1, c.n_q * c.head_dim, dtype=torch.float32, device=q.device)
-        self.nat.check(self.lib.cbq_attn_rope_decode_f32(
-            q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None, cos.data_ptr(), sin.data_ptr(),
-            pos_dev.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
-            c.n_q, c.n_kv, c.head_dim, k_cache.shape[1], float(c.head_dim ** -0.5), c.eps,
-            self.nat.stream_ptr(q.device)), "cbq_attn_rope_decode_f32")
+        max_len = k_cache.shape[1]
+        args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None, cos.data_ptr(),
+                sin.data_ptr(), pos_dev.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                out.data_ptr(), c.n_q, c.n_kv, c.head_dim, max_len, float(c.head_dim ** -0.5),
+                c.eps)
+        if max_len >= self.SPLIT_ATTN_MIN_LEN:
+            ws = self.attn_workspace(q.device, max_len)
+            self.nat.check(self.lib.cbq_attn_rope_decode_ws_f32(
+                *args, ws.data_ptr(), ws.numel(), self.nat.stream_ptr(q.device)),
+                "cbq_attn_rope_decode_ws_f32")
+        else:
+            self.nat.check(self.lib.cbq_attn_rope_decode_f32(
+                *args, self.nat.stream_ptr(q.device)), "cbq_attn_rope_decode_f32")
         return out
 
     def argmax_step(self, logits, ids32, toks, pos_dev, first: int) -> None:
@@ -153,6 +177,8 @@ class Qwen3Decoder:
         self.cache = torch.zeros(kv, dtype=torch.float32, device=self.device)
         self.pos = 0
         self.glue = _Glue(cfg)
+        if max_len >= _Glue.SPLIT_ATTN_MIN_LEN:
+            self.glue.attn_workspace(self.device, max_len)
         # One-token steps fold RMSNorm / SiLU into the GEMVs' x staging when
         # every linear that consumes them offers `xform` (stacked q/k/v and
         # gate/up, down, lm_head): 5 launches per layer instead of 8, with

@@ -18,6 +18,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -64,6 +65,23 @@ int cbq_attn_rope_decode_f32(const float *q, const float *k, const float *v,
                              const int64_t *pos, float *k_cache, float *v_cache,
                              float *out, int n_q, int n_kv, int hd, int max_len,
                              float scale, float eps, hipStream_t stream);
+
+/* cbq_attn_rope_decode_f32 with the cached rows split over several blocks per
+ * query head (flash decoding), then a second launch that merges the splits;
+ * same arguments, results equal to rounding (the softmax is accumulated per
+ * split and merged in split order).  workspace: device scratch of at least
+ * cbq_attn_rope_decode_workspace(n_q, hd, max_len) bytes, 4-byte aligned,
+ * overwritten by every call (no initial contents needed); calls that share a
+ * workspace must not overlap.  hd in {64, 128, 256}.  No counterpart in the
+ * reference (HF computes the attention there): decoder glue of this build. */
+size_t cbq_attn_rope_decode_workspace(int n_q, int hd, int max_len);
+int cbq_attn_rope_decode_ws_f32(const float *q, const float *k, const float *v,
+                                const float *q_weight, const float *k_weight,
+                                const float *cos_table, const float *sin_table,
+                                const int64_t *pos, float *k_cache, float *v_cache,
+                                float *out, int n_q, int n_kv, int hd, int max_len,
+                                float scale, float eps, void *workspace,
+                                size_t workspace_bytes, hipStream_t stream);
 
 /* Greedy pick of a captured decode step: tok = argmax(logits[0, n)) (first
  * maximum; NaN ranks highest, as torch.argmax); ids32[0] = tok;

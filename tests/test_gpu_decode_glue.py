@@ -172,6 +172,72 @@ def test_attn_rope_decode_matches_two_step(cuda, lib, hd, n_q, n_kv, pos0, max_l
     assert _rel(out, ref) <= 1e-6
 
 
+@pytest.mark.parametrize("hd,n_q,n_kv,pos0,max_len", [(128, 32, 8, 0, 512), (128, 32, 8, 200, 512),
+                                                      (128, 32, 8, 511, 512), (64, 4, 2, 63, 64),
+                                                      (256, 8, 2, 17, 64), (128, 8, 2, 3000, 4096),
+                                                      (128, 4, 4, 64, 64), (64, 8, 8, 700, 1000)])
+def test_attn_rope_split_matches_fused(cuda, lib, hd, n_q, n_kv, pos0, max_len):
+    """The split-over-blocks kernels (flash decoding, then a merge launch)
+    write the same cache row as the one-block kernel, give its output to
+    rounding and the float64 softmax attention to 1e-5, and repeat bit for
+    bit on a workspace left dirty by the previous call."""
+    g = torch.Generator().manual_seed(pos0 * 7 + hd + n_q)
+    q = torch.randn(n_q * hd, generator=g).to(cuda)
+    k = torch.randn(n_kv * hd, generator=g).to(cuda)
+    v = torch.randn(n_kv * hd, generator=g).to(cuda)
+    cfg = decoder.DecoderConfig(layers=1, hidden=n_q * hd, inter=64, n_q=n_q, n_kv=n_kv,
+                                head_dim=hd, vocab=16)
+    cos, sin = (torch.from_numpy(a).to(cuda) for a in decoder.rope_tables(cfg, max_len + 1))
+    kc = torch.randn(n_kv, max_len, hd, generator=g).to(cuda)
+    vc = torch.randn(n_kv, max_len, hd, generator=g).to(cuda)
+    kc2, vc2 = kc.clone(), vc.clone()
+    pos = torch.tensor([pos0], dtype=torch.int64, device=cuda)
+    st = nat.stream_ptr(cuda)
+    nbytes = lib.cbq_attn_rope_decode_workspace(n_q, hd, max_len)
+    ws = torch.full((nbytes,), 0x7f, dtype=torch.uint8, device=cuda)
+    outs = []
+    for _ in range(2):
+        kcs, vcs = kc.clone(), vc.clone()
+        out = torch.empty(n_q * hd, device=cuda)
+        nat.check(lib.cbq_attn_rope_decode_ws_f32(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None, cos.data_ptr(), sin.data_ptr(),
+            pos.data_ptr(), kcs.data_ptr(), vcs.data_ptr(), out.data_ptr(), n_q, n_kv, hd, max_len,
+            hd ** -0.5, 1e-6, ws.data_ptr(), nbytes, st), "split")
+        outs.append((out, kcs, vcs))
+    assert torch.equal(outs[0][0], outs[1][0])
+    ref = torch.empty_like(outs[0][0])
+    nat.check(lib.cbq_attn_rope_decode_f32(q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None,
+                                           cos.data_ptr(), sin.data_ptr(), pos.data_ptr(),
+                                           kc2.data_ptr(), vc2.data_ptr(), ref.data_ptr(), n_q,
+                                           n_kv, hd, max_len, hd ** -0.5, 1e-6, st), "fused")
+    out, kcs, vcs = outs[0]
+    assert torch.equal(kcs, kc2) and torch.equal(vcs, vc2)
+    assert _rel(out, ref) <= 2e-6
+    # float64 reference over the rows the kernel attends: the cached rows
+    # [0, min(pos, max_len)) and the new (normed, rotated) key/value
+    qr = torch.empty_like(q)
+    kc3, vc3 = kc.clone(), vc.clone()
+    nat.check(lib.cbq_head_norm_rope_f32(q.data_ptr(), k.data_ptr(), v.data_ptr(), None, None,
+                                         cos.data_ptr(), sin.data_ptr(), pos.data_ptr(),
+                                         qr.data_ptr(), kc3.data_ptr(), vc3.data_ptr(), 1, n_q,
+                                         n_kv, hd, max_len, 1e-6, st), "rope")
+    n_old = min(pos0, max_len)
+    rep = n_q // n_kv
+    kk = kc[:, :n_old].double().cpu()
+    vv = vc[:, :n_old].double().cpu()
+    if pos0 < max_len:
+        knew, vnew = kc3[:, pos0].double().cpu(), vc3[:, pos0].double().cpu()
+    else:
+        knew, vnew = None, None
+    if knew is not None:
+        kk = torch.cat([kk, knew[:, None]], 1)
+        vv = torch.cat([vv, vnew[:, None]], 1)
+        kk, vv = kk.repeat_interleave(rep, 0), vv.repeat_interleave(rep, 0)
+        s = torch.einsum("hd,hld->hl", qr.view(n_q, hd).double().cpu(), kk) * hd ** -0.5
+        want = torch.einsum("hl,hld->hd", torch.softmax(s, -1), vv)
+        assert _rel(out.view(n_q, hd), want) <= 1e-5
+
+
 @pytest.mark.parametrize("n", [1, 7, 151936])
 def test_argmax_step(cuda, lib, n):
     x = torch.randn(n, device=cuda)

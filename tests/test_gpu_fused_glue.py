@@ -79,3 +79,29 @@ def test_fused_decoder_identical(cuda, model):
         assert torch.equal(a, b), (kind, s, float((a - b).abs().max()))
     toks = [m.generate_graph(list(range(40, 52)), 8) for m in models]
     assert toks[0] == toks[1]
+
+
+def test_long_cache_split_attention_decoder(cuda, model, monkeypatch):
+    """A decoder whose cache is long enough for the split-over-blocks
+    attention gives the same tokens as the single-launch attention and
+    logits equal to rounding (graph replays and eager steps), and repeats
+    its own logits bit for bit."""
+    kind, dec, tensors = model
+    cfg = _cfg(dec)
+    prompt = list(range(40, 52))
+
+    def run(split):
+        monkeypatch.setattr(decoder._Glue, "SPLIT_ATTN_MIN_LEN", 2048 if split else 1 << 30)
+        m = decoder.from_synthetic(cfg, tensors, max_len=2048)
+        toks = m.generate_graph(prompt, 6)
+        m.reset()
+        m.forward(torch.tensor(prompt))
+        return toks, m.forward(torch.tensor([7]))
+
+    ta, la = run(True)
+    tb, lb = run(False)
+    assert ta == tb, (kind, ta, tb)
+    rel = float((la - lb).norm() / lb.norm())
+    assert rel <= 1e-5, (kind, rel)
+    tc, lc = run(True)
+    assert tc == ta and torch.equal(lc, la), kind
