@@ -324,6 +324,30 @@ def main():
                            f"{t.shape[1]}->{t.shape[0]}"),
                 "bytes_per_launch": b_gu, "us_per_launch": round(us_gu, 2)}
 
+    # config 2's batch 4 / 16 (and 2, 8): the same stacked gate+up launches with
+    # T tokens (every weight is read once for all T rows of x)
+    batch = {}
+    for T in (2, 4, 8, 16):
+        xT = torch.randn(T, t.shape[1], device=dev)
+        oT = torch.empty(T, t.shape[0], device=dev)
+
+        def launch_T(T=T, xT=xT, oT=oT):
+            st = nat.stream_ptr(dev)
+            for n in gus:
+                f = fixed[n]
+                rc = lib.ck_linear_f32(xT.data_ptr(), f.packed.data_ptr(), f.codebook.data_ptr(),
+                                       oT.data_ptr(), T, f.shape[0], f.shape[1],
+                                       f.codebook.numel(), f.bits, st)
+                if rc:
+                    raise RuntimeError(f"ck_linear_f32 T={T} rc={rc}")
+        ms_T, _ = timed_graph(torch, launch_T, args.steps, args.warmup)
+        us_T = ms_T * 1e3 / len(gus)
+        bT = fixed_bytes(t.shape[0], t.shape[1], t.bits, t.codebook.numel(), T)
+        batch[f"T{T}"] = {"us_per_launch": round(us_T, 2),
+                          "GB/s": round(bT / (us_T * 1e-6) / 1e9, 1),
+                          "GFLOP/s": round(2.0 * T * t.shape[0] * t.shape[1] / (us_T * 1e-6) / 1e9, 1)}
+    log(f"stacked gate+up at T=2/4/8/16: {batch}")
+
     result = {
         "metric": METRIC, "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 1), "unit": "GB/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
@@ -338,6 +362,7 @@ def main():
                    "weight_stream_tok_per_s": round(1000.0 / ms_step, 1)},
         "roofline": roofline,
         "breakdown": breakdown,
+        "batch_stacked_gate_up": batch,
     }
 
     if not args.no_prefill:

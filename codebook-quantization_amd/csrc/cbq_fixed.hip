@@ -16,6 +16,12 @@
 
 
 #include <algorithm>
+#include <type_traits>
+
+// Matrix-core path for 2..16 fp32 tokens (cbq_tiny.hip); -1 = shape not
+// handled there.
+int cbq_fixed_tiny_t(const float *x, const uint8_t *packed, const float *cb, float *out, int T,
+                     int M, int K, int C, int bits, hipStream_t st);
 
 namespace {
 
@@ -23,6 +29,7 @@ constexpr int kBlock = 1024;                // 16 waves share one LDS codebook
 constexpr int kWavesPerBlock = kBlock / CBQ_WAVE;
 constexpr int kMaxLdsBytes = 64 * 1024;     // per-workgroup budget we allow
 constexpr int kMaxLdsCodebook = 16384;      // entries of fp32 codebook in LDS
+constexpr int kTinyMinT = 5;                // fp32 token tiles of 5..16 go to the matrix cores
 // The x-in-registers path runs one block per CU, so it may use most of the
 // CU's 160 KB of LDS (codebook + padded x + row partials).
 constexpr int kMaxLdsBytesXReg = 152 * 1024;
@@ -351,13 +358,31 @@ template <> struct XStage<uint16_t> {
 // XMODE (T = 1, float x): x is staged as xform_value(XMODE, x, x1, ...) -
 // silu(x) * x1, or the RMSNorm of x (+ x1) with block 0 storing x + x1 to
 // h_out - so the decoder's separate glue launch disappears.
-template <int BITS, int TMAX, typename XT, typename OT, bool AFFINE = false, int XMODE = XF_NONE>
+template <bool KCHUNK, typename OT>
+__device__ __forceinline__ void put_out_t(OT *o, float v, int accum)
+{
+    if constexpr (KCHUNK) {
+        static_assert(sizeof(OT) == sizeof(float), "column ranges accumulate fp32 outputs");
+        *o = accum ? *o + v : v;
+    } else {
+        *o = from_f32<OT>(v);
+    }
+}
+
+//
+// KCHUNK: the launch covers index columns [k0, k0 + K) of rows Kfull long
+// (x is [T, Kfull]); accum != 0 adds the partial products to out instead of
+// writing them.  The host splits K this way when x of all T tokens does not
+// fit in LDS, one launch per column range in order.
+template <int BITS, int TMAX, typename XT, typename OT, bool AFFINE = false, int XMODE = XF_NONE,
+          bool KCHUNK = false>
 __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     const XT *__restrict__ x, const uint32_t *__restrict__ words,
     const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C,
     uint32_t aff_lo, uint32_t aff_w, const float *__restrict__ x1, float *__restrict__ h_out,
-    float eps)
+    float eps, int Kfull, int k0, int accum)
 {
+    static_assert(!KCHUNK || (XMODE == XF_NONE && !AFFINE), "column ranges: plain x only");
     constexpr bool PADDED = BITS <= 14 && !AFFINE;
     constexpr int D = kStreamD;
     __shared__ float s_cbp[PADDED ? (1 << BITS) : 1];
@@ -369,6 +394,8 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     uint32_t *s_x = (uint32_t *)(PADDED ? s_dyn : s_dyn + cb_slots);
 
     const int G = K >> 5;
+    const int Gf = KCHUNK ? (Kfull >> 5) : G;      // groups per stored row
+    const int g0 = KCHUNK ? (k0 >> 5) : 0;         // first group of this launch
     const int NGW = (G + CBQ_WAVE - 1) / CBQ_WAVE;
     const int lane = threadIdx.x & (CBQ_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CBQ_WAVE);
@@ -394,7 +421,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
             sl = sl < n_xdw ? sl : n_xdw - 1;      // tail lanes re-copy the last dword
             const int t = sl / xdw, d = sl - t * xdw;
             const int g = d / GD, p = (d % GD) >> 2;
-            const int src = t * xdw + g * GD + (XStage<XT>::chunk(p, g) << 2) + (d & 3);
+            const int src = t * (Gf * GD) + (g0 + g) * GD + (XStage<XT>::chunk(p, g) << 2) + (d & 3);
             __builtin_amdgcn_global_load_lds((const void *)(xw + src),
                                              (lds_ptr_t)(s_x + (i << 6)), 4, 0, 0);
         }
@@ -414,7 +441,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
         int g = ch * CBQ_WAVE + lane;
         g = g < G ? g : G - 1;
         const int row = rows > 0 ? wid + ri * W : 0;
-        return words + ((size_t)row * G + g) * BITS + zero;
+        return words + ((size_t)row * Gf + g0 + g) * BITS + zero;
     };
     uint32_t buf[D][BITS];
 #pragma unroll
@@ -502,7 +529,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
                     const int row = wid + (ri - 64 + lane) * W;
 #pragma unroll
                     for (int t = 0; t < TMAX; t++)
-                        if (t < T) out[(size_t)t * M + row] = from_f32<OT>(res[t]);
+                        if (t < T) put_out_t<KCHUNK>(out + (size_t)t * M + row, res[t], accum);
                 }
             }
         }
@@ -513,7 +540,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
         const int row = wid + (rb + lane) * W;
 #pragma unroll
         for (int t = 0; t < TMAX; t++)
-            if (t < T) out[(size_t)t * M + row] = from_f32<OT>(res[t]);
+            if (t < T) put_out_t<KCHUNK>(out + (size_t)t * M + row, res[t], accum);
     }
 }
 
@@ -662,7 +689,7 @@ int launch_stream(const XT *x, const uint8_t *packed, const float *cb, OT *out, 
         std::max(1, std::min(cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
     hipLaunchKernelGGL((fixed_stream_kernel<BITS, TMAX, XT, OT>), dim3(blocks),
                        dim3(kStreamBlock), dyn_lds, st, x, (const uint32_t *)packed, cb, out, T,
-                       M, K, C, 0u, 0u, (const float *)nullptr, (float *)nullptr, 0.f);
+                       M, K, C, 0u, 0u, (const float *)nullptr, (float *)nullptr, 0.f, K, 0, 0);
     return cbq_launch_status("fixed_stream_kernel");
 }
 
@@ -675,7 +702,7 @@ int launch_affine(const float *x, const uint8_t *packed, uint32_t lo, uint32_t w
     hipLaunchKernelGGL((fixed_stream_kernel<BITS, TMAX, float, float, true>), dim3(blocks),
                        dim3(kStreamBlock), dyn_lds, st, x, (const uint32_t *)packed,
                        (const float *)nullptr, out, T, M, K, 1, lo, w, (const float *)nullptr,
-                       (float *)nullptr, 0.f);
+                       (float *)nullptr, 0.f, K, 0, 0);
     return cbq_launch_status("fixed_stream_kernel<affine>");
 }
 
@@ -705,6 +732,33 @@ size_t stream_dyn_lds(int T, int K, int C)
     return cb_dyn + x_bytes;
 }
 
+// x of all T tokens too large for LDS (T = 16 at K = 4096): the columns go in
+// ranges whose x does fit, one streaming launch per range in order, the first
+// writing out and the rest adding to it.  Every weight is still read once.
+template <int BITS, int TMAX>
+int launch_stream_cols(const float *x, const uint8_t *packed, const float *cb, float *out,
+                       int T, int M, int K, int C, hipStream_t st)
+{
+    const int G = K / 32;
+    int gmax = G;
+    while (gmax > 0 && !stream_dyn_lds<BITS, float>(T, gmax * 32, C)) gmax--;
+    if (gmax == 0) return -1;
+    const int n = (G + gmax - 1) / gmax;
+    const int gc = (G + n - 1) / n;                  // balanced ranges, <= gmax groups
+    const int blocks =
+        std::max(1, std::min(cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
+    for (int i = 0; i * gc < G; i++) {
+        const int ga = i * gc, gb = std::min(G, ga + gc);
+        const int kc = (gb - ga) * 32;
+        const size_t dyn = stream_dyn_lds<BITS, float>(T, kc, C);
+        hipLaunchKernelGGL((fixed_stream_kernel<BITS, TMAX, float, float, false, XF_NONE, true>),
+                           dim3(blocks), dim3(kStreamBlock), dyn, st, x,
+                           (const uint32_t *)packed, cb, out, T, M, kc, C, 0u, 0u,
+                           (const float *)nullptr, (float *)nullptr, 0.f, K, ga * 32, i > 0);
+    }
+    return cbq_launch_status("fixed_stream_kernel<columns>");
+}
+
 template <int BITS, typename XT, typename OT>
 int dispatch_t(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T,
                int M, int K, int C, hipStream_t st)
@@ -716,6 +770,13 @@ int dispatch_t(const XT *x, const uint8_t *packed, const float *cb, OT *out, int
         if (T == 1) return launch_stream<BITS, 1>(x, packed, cb, out, T, M, K, C, dyn, st);
         if (T <= 4) return launch_stream<BITS, 4>(x, packed, cb, out, T, M, K, C, dyn, st);
         return launch_stream<BITS, 16>(x, packed, cb, out, T, M, K, C, dyn, st);
+    }
+    if constexpr (std::is_same<XT, float>::value && std::is_same<OT, float>::value) {
+        if (T > 1 && ((uintptr_t)x & 3) == 0) {
+            const int rc = T <= 4 ? launch_stream_cols<BITS, 4>(x, packed, cb, out, T, M, K, C, st)
+                                  : launch_stream_cols<BITS, 16>(x, packed, cb, out, T, M, K, C, st);
+            if (rc >= 0) return rc;
+        }
     }
     if (T == 1) return dispatch_x<BITS, 1>(x, packed, cb, out, T, M, K, C, st);
     if (T <= 4) return dispatch_x<BITS, 4>(x, packed, cb, out, T, M, K, C, st);
@@ -740,6 +801,12 @@ int linear_tile(const XT *x, const uint8_t *packed, const float *cb, OT *out, in
 {
     const bool fast = (K % 32 == 0) && C <= kMaxLdsCodebook &&
                       ((uintptr_t)packed & 3) == 0;
+    if constexpr (std::is_same<XT, float>::value && std::is_same<OT, float>::value) {
+        if (fast && T >= kTinyMinT) {
+            const int rc = cbq_fixed_tiny_t(x, packed, cb, out, T, M, K, C, bits, st);
+            if (rc >= 0) return rc;
+        }
+    }
     if (fast) {
         switch (bits) {
         case 8: return dispatch_t<8>(x, packed, cb, out, T, M, K, C, st);
@@ -899,7 +966,7 @@ int cbq_linear_xform_f32(const float *x0, const float *x1, float *h_out, int mod
 #define CBQ_XF(B, MODE)                                                                        \
     hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE>), dim3(blocks),    \
                        dim3(kStreamBlock), dyn, stream, x0, (const uint32_t *)packed, codebook, \
-                       out, 1, M, K, C, 0u, 0u, x1, h_out, eps)
+                       out, 1, M, K, C, 0u, 0u, x1, h_out, eps, K, 0, 0)
 #define CBQ_XF_MODES(B)                                                                        \
     do {                                                                                       \
         dyn = stream_dyn_lds<B, float>(1, K, C);                                               \

@@ -79,6 +79,37 @@ def test_widths_shapes_and_generic_path(cuda, oracle, M, K, bits, C):
         assert rel_l2(y, ref) <= TOL, (M, K, bits, C, T)
 
 
+@pytest.mark.parametrize("M,K,T", [(512, 4096, 16), (300, 12288, 16), (256, 12288, 5),
+                                   (200, 4096, 8), (96, 2048, 16)])
+def test_column_ranges_large_x(cuda, oracle, M, K, T):
+    """x of all T tokens does not fit in LDS: the streaming GEMV runs over
+    balanced column ranges, the first launch writing out, the rest adding."""
+    rng = np.random.default_rng(M * 7 + K + T)
+    w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
+    d = cbb.compress_fixed(w)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    y = _run_linear(cuda, x, d["indices"], d["codebook"], M, K, len(d["codebook"]), d["bits"])
+    ref = oracle.fixed_gemv(x, d["indices"], d["codebook"], M, K, d["bits"], chunk_rows=None)
+    assert rel_l2(y, ref) <= TOL, (M, K, T)
+
+
+@pytest.mark.parametrize("bits", [8, 10, 11, 12, 13, 14, 16])
+@pytest.mark.parametrize("T", [5, 16])
+def test_matrix_core_token_tiles(cuda, oracle, bits, T):
+    """5..16 fp32 tokens run on the fp32 matrix cores (cbq_tiny.hip): every
+    width it takes, indices past C clamped, rows not a multiple of 32."""
+    rng = np.random.default_rng(bits * 31 + T)
+    M, K = 200, 1024
+    C = min(1 << bits, 3000)
+    raw = rng.integers(0, 1 << bits, size=M * K)
+    cb = (rng.standard_normal(C) * 0.02).astype(np.float32)
+    pk = oracle.pack_lsb(raw, bits)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    y = _run_linear(cuda, x, pk, cb, M, K, C, bits)
+    ref = oracle.fixed_gemv(x, pk, cb, M, K, bits, C=C, chunk_rows=None)
+    assert rel_l2(y, ref) <= TOL, (bits, T)
+
+
 def test_bf16_io(cuda, oracle):
     nat, lib = _nat()
     M, K = 512, 2048
@@ -174,8 +205,11 @@ def test_embedding_clamps_ids(cuda, oracle):
 @pytest.mark.parametrize("T", [1, 3, 20])
 def test_affine_implicit_codebook_bit_exact(cuda, oracle, T):
     """cbq_linear_affine_f32 over re-indexed weights equals ck_linear_f32 over
-    the frequency-sorted codebook bit for bit (same values, same order of
-    accumulation), zeros of either sign included; and matches the oracle."""
+    the frequency-sorted codebook bit for bit at T = 1 (same values, same
+    streaming kernel and order of accumulation), zeros of either sign
+    included; at T = 20 the table path's 16-token tile runs on the matrix
+    cores (another order of accumulation), so there the two agree to
+    rounding; both match the oracle."""
     import bitpack
     import cbq_native as nat
     rng = np.random.default_rng(40 + T)
@@ -202,7 +236,11 @@ def test_affine_implicit_codebook_bit_exact(cuda, oracle, T):
                                 len(cb), bits, st), "table")
     nat.check(lib.cbq_linear_affine_f32(x.data_ptr(), pka.data_ptr(), lo, wid, ya.data_ptr(), T, M,
                                         K, bits, st), "affine")
-    assert torch.equal(y, ya)
+    if T < 5:
+        assert torch.equal(y, ya)
+    else:
+        assert rel_l2(y.cpu().numpy(), ya.cpu().numpy()) <= 2e-6
     ref = oracle.fixed_gemv(x.cpu().numpy(), packed, cb, M, K, bits)
     assert rel_l2(ya.cpu().numpy(), ref) <= 1e-5
+    assert rel_l2(y.cpu().numpy(), ref) <= 1e-5
 
