@@ -22,6 +22,8 @@
 // handled there.
 int cbq_fixed_tiny_t(const float *x, const uint8_t *packed, const float *cb, float *out, int T,
                      int M, int K, int C, int bits, hipStream_t st);
+int cbq_fixed_tiny_t_bf16(const uint16_t *x, const uint8_t *packed, const float *cb,
+                          uint16_t *out, int T, int M, int K, int C, int bits, hipStream_t st);
 
 namespace {
 
@@ -801,11 +803,13 @@ int linear_tile(const XT *x, const uint8_t *packed, const float *cb, OT *out, in
 {
     const bool fast = (K % 32 == 0) && C <= kMaxLdsCodebook &&
                       ((uintptr_t)packed & 3) == 0;
-    if constexpr (std::is_same<XT, float>::value && std::is_same<OT, float>::value) {
-        if (fast && T >= kTinyMinT) {
-            const int rc = cbq_fixed_tiny_t(x, packed, cb, out, T, M, K, C, bits, st);
-            if (rc >= 0) return rc;
-        }
+    if (fast && T >= kTinyMinT) {
+        int rc = -1;
+        if constexpr (std::is_same<XT, float>::value && std::is_same<OT, float>::value)
+            rc = cbq_fixed_tiny_t(x, packed, cb, out, T, M, K, C, bits, st);
+        if constexpr (std::is_same<XT, uint16_t>::value && std::is_same<OT, uint16_t>::value)
+            rc = cbq_fixed_tiny_t_bf16(x, packed, cb, out, T, M, K, C, bits, st);
+        if (rc >= 0) return rc;
     }
     if (fast) {
         switch (bits) {

@@ -1,6 +1,6 @@
-// Fixed-width GEMM for a few tokens (2 <= T <= 16; ck_linear_f32 sends it
-// tiles of 5..16) on the fp32 matrix cores
-// of gfx950 (v_mfma_f32_16x16x4_f32), behind ck_linear_f32
+// Fixed-width GEMM for a few tokens (2 <= T <= 16; ck_linear_f32 and
+// ck_linear_bf16 send it tiles of 5..16) on the fp32 matrix cores of gfx950
+// (v_mfma_f32_16x16x4_f32)
 // (rocm/compressed_kernel.hip:607-627 is the reference entry point; its
 // kernel runs one block per output scalar).
 //
@@ -43,10 +43,11 @@ __device__ __forceinline__ void wave_sync_lds()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int BITS>
+// x in XT (fp32, or bf16 widened exactly); out in OT (one rounding for bf16).
+template <int BITS, typename XT, typename OT>
 __global__ __launch_bounds__(kTinyThreads) void fixed_tiny_mfma_kernel(
-    const float *__restrict__ x, const uint32_t *__restrict__ words,
-    const float *__restrict__ cb, float *__restrict__ out, int T, int M, int K, int C)
+    const XT *__restrict__ x, const uint32_t *__restrict__ words,
+    const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C)
 {
     static_assert(BITS >= 8 && BITS <= 16, "widths with a 4-dword 8-index window");
     // codebook [cs], partials [8][64][4], then per wave kTinyRing slots of
@@ -74,7 +75,7 @@ __global__ __launch_bounds__(kTinyThreads) void fixed_tiny_mfma_kernel(
     const int w0 = wbit >> 5;
     const int boff = wbit & 31;
     const int lastq = ((wbit + 8 * BITS - 1) >> 5) - w0;     // last word of the window, <= 3
-    const float *xrow = x + (size_t)(tok < T ? tok : 0) * K + 8 * j;
+    const XT *xrow = x + (size_t)(tok < T ? tok : 0) * K + 8 * j;
     // loads: lane l fetches 4 words of row l / 4's group, at word
     // min(4 (l % 4), BITS - 4), so one 16-byte load per lane covers the 16
     // rows' groups and never leaves a group; they pass through LDS to the
@@ -89,9 +90,18 @@ __global__ __launch_bounds__(kTinyThreads) void fixed_tiny_mfma_kernel(
     auto load = [&](int d, int g) {
         const int gg = g < gb ? g : (gb > 0 ? gb - 1 : 0);
         __builtin_memcpy(wr[d], lsrc + (size_t)gg * BITS, sizeof(wr[d]));
-        const f4 *xp = (const f4 *)(xrow + (size_t)gg * 32);
-        xa[d] = xp[0];
-        xb[d] = xp[1];
+        if constexpr (sizeof(XT) == 4) {
+            const f4 *xp = (const f4 *)(xrow + (size_t)gg * 32);
+            xa[d] = xp[0];
+            xb[d] = xp[1];
+        } else {                                // 8 bf16 values: 16 bytes
+            uint32_t h[4];
+            __builtin_memcpy(h, xrow + (size_t)gg * 32, sizeof(h));
+            xa[d] = (f4){__uint_as_float(h[0] << 16), __uint_as_float(h[0] & 0xffff0000u),
+                         __uint_as_float(h[1] << 16), __uint_as_float(h[1] & 0xffff0000u)};
+            xb[d] = (f4){__uint_as_float(h[2] << 16), __uint_as_float(h[2] & 0xffff0000u),
+                         __uint_as_float(h[3] << 16), __uint_as_float(h[3] & 0xffff0000u)};
+        }
     };
 #pragma unroll
     for (int d = 0; d < kTinyRing; d++) load(d, ga + d);
@@ -162,18 +172,14 @@ __global__ __launch_bounds__(kTinyThreads) void fixed_tiny_mfma_kernel(
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const int m = r0 + 4 * j + v;
-            if (m < M && tok < T) out[(size_t)tok * M + m] = vals[v];
+            if (m < M && tok < T) out[(size_t)tok * M + m] = from_f32<OT>(vals[v]);
         }
     }
 }
 
-}  // namespace
-
-// 2 <= T <= 16 fp32 tokens, K % 32 == 0, widths 8 and 10-14 and 16: the
-// kernel above; returns -1 for shapes it does not take (the caller then
-// uses its other paths).
-int cbq_fixed_tiny_t(const float *x, const uint8_t *packed, const float *cb, float *out, int T,
-                     int M, int K, int C, int bits, hipStream_t st)
+template <typename XT, typename OT>
+int tiny_launch(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T, int M,
+                int K, int C, int bits, hipStream_t st)
 {
     if (T < 2 || T > 16 || M <= 0 || K <= 0 || K % 32 || C <= 0 || C > kTinyMaxCodebook)
         return -1;
@@ -182,9 +188,9 @@ int cbq_fixed_tiny_t(const float *x, const uint8_t *packed, const float *cb, flo
     const size_t lds = (size_t)cs * 4 + (size_t)kTinyWaves * CBQ_WAVE * 16 +
                        (size_t)kTinyWaves * kTinyRing * 16 * 16 * 4;
     const int blocks = (M + 31) / 32;
-#define CBQ_TINY(B)                                                                          \
-    hipLaunchKernelGGL(fixed_tiny_mfma_kernel<B>, dim3(blocks), dim3(kTinyThreads), lds, st, x, \
-                       (const uint32_t *)packed, cb, out, T, M, K, C)
+#define CBQ_TINY(B)                                                                            \
+    hipLaunchKernelGGL((fixed_tiny_mfma_kernel<B, XT, OT>), dim3(blocks), dim3(kTinyThreads),  \
+                       lds, st, x, (const uint32_t *)packed, cb, out, T, M, K, C)
     switch (bits) {
     case 8: CBQ_TINY(8); break;
     case 10: CBQ_TINY(10); break;
@@ -197,4 +203,21 @@ int cbq_fixed_tiny_t(const float *x, const uint8_t *packed, const float *cb, flo
     }
 #undef CBQ_TINY
     return cbq_launch_status("fixed_tiny_mfma_kernel");
+}
+
+}  // namespace
+
+// 2 <= T <= 16 tokens (fp32, or bf16 x and out), K % 32 == 0, widths 8,
+// 10-14 and 16: the kernel above; returns -1 for shapes it does not take
+// (the caller then uses its other paths).
+int cbq_fixed_tiny_t(const float *x, const uint8_t *packed, const float *cb, float *out, int T,
+                     int M, int K, int C, int bits, hipStream_t st)
+{
+    return tiny_launch<float, float>(x, packed, cb, out, T, M, K, C, bits, st);
+}
+
+int cbq_fixed_tiny_t_bf16(const uint16_t *x, const uint8_t *packed, const float *cb,
+                          uint16_t *out, int T, int M, int K, int C, int bits, hipStream_t st)
+{
+    return tiny_launch<uint16_t, uint16_t>(x, packed, cb, out, T, M, K, C, bits, st);
 }

@@ -110,14 +110,17 @@ def test_matrix_core_token_tiles(cuda, oracle, bits, T):
     assert rel_l2(y, ref) <= TOL, (bits, T)
 
 
-def test_bf16_io(cuda, oracle):
+@pytest.mark.parametrize("K,Ts", [(2048, (1, 5)), (4096, (16, 3, 9))])
+def test_bf16_io(cuda, oracle, K, Ts):
+    """ck_linear_bf16: streaming kernel (T <= 4) and matrix cores (5..16
+    tokens, x of 16 tokens at K = 4096 larger than LDS)."""
     nat, lib = _nat()
-    M, K = 512, 2048
+    M = 512
     w = cbb.bf16_round(np.random.default_rng(2).standard_normal((M, K)) * 0.02)
     d = cbb.compress_fixed(w)
-    bits = d["bits"]                      # 3581 unique values -> 12-bit indices
+    bits = d["bits"]                      # 12-bit indices at K = 2048, 13 at 4096
     assert d["indices"].size >= (M * K * bits + 7) // 8
-    for T in (1, 5):
+    for T in Ts:
         xb = torch.randn(T, K).bfloat16()
         x32 = xb.float().numpy()
         ref = oracle.fixed_gemv(x32, d["indices"], d["codebook"], M, K, bits, chunk_rows=None)
