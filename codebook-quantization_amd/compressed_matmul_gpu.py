@@ -1,0 +1,165 @@
+"""The reference's functional entry points, on the GPU.
+
+Same names, arguments and results as src/compressed_matmul_cpu.py
+(compressed_matmul :279-343, huffman_matmul :446-507, huffman_embedding
+:509-561, huffman_decode_weights :563-609): numpy (or torch) in, float32 numpy
+out, outputs written rather than accumulated, indices clamped to C - 1.  The
+work runs on this package's gfx950 kernels (libcbq_hip.so); there is no CPU
+fallback, and a call without a visible GPU raises.
+
+`huff_data` is the dict the reference's modules keep for their Huffman layers
+(src/compressed_modules.py:240-249): huff_stream (MSB-first, 4 zero pad
+bytes), lut_sym / lut_len (12-bit prefix table), sl_first_code /
+sl_base_offset / sl_sym (codes longer than 12 bits), row_bit_starts and
+sl_max_len.  It carries no code lengths, so they are read back from the two
+tables (lengths_from_tables), which fix the canonical code exactly.
+
+`chunk_rows` is accepted for signature compatibility and ignored: a call is
+one launch over all rows.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+import torch
+
+import bitpack
+import cbq_native as nat
+import huffman_codebook as hc
+
+LUT_BITS = 12
+
+
+def _device() -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError("compressed_matmul_gpu needs a ROCm GPU (none visible); the "
+                           "compressed path has no CPU fallback")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _f32(a) -> np.ndarray:
+    if isinstance(a, torch.Tensor):
+        return a.detach().to("cpu", torch.float32).numpy()
+    return np.asarray(a, np.float32)
+
+
+def _codebook(codebook_np, C: Optional[int]) -> np.ndarray:
+    cb = np.ascontiguousarray(_f32(codebook_np).reshape(-1))
+    n = len(cb) if C is None else int(C)
+    if n <= 0 or n > len(cb):
+        raise ValueError(f"codebook size C={n} outside 1..{len(cb)}")
+    return cb[:n]
+
+
+def lengths_from_tables(huff_data: dict, n_symbols: Optional[int] = None) -> np.ndarray:
+    """Code length of every symbol, from the reference's decode tables: a
+    code of L <= 12 bits fills the 2^(12-L) lut entries of its prefix with
+    (symbol, L) (src/huffman_codebook.py:394-423); longer codes are listed per
+    length in sl_sym[sl_base_offset[L]:sl_base_offset[L+1]]
+    (src/huffman_codebook.py:353-391).  Symbols with no code get length 0."""
+    lut_sym = np.asarray(huff_data["lut_sym"]).astype(np.int64).reshape(-1)
+    lut_len = np.asarray(huff_data["lut_len"]).astype(np.int64).reshape(-1)
+    # the GPU tables mark a miss with lut_sym = -1, the CPU copies with
+    # lut_len = 0 (and lut_sym = 0xFFFF)
+    hit = (lut_len > 0) & (lut_sym >= 0) & (lut_sym != 0xFFFF)
+    first = np.asarray(huff_data["sl_first_code"]).astype(np.int64).reshape(-1)
+    base = np.asarray(huff_data["sl_base_offset"]).astype(np.int64).reshape(-1)
+    sl_sym = np.asarray(huff_data["sl_sym"]).astype(np.int64).reshape(-1)
+    top = 0
+    if hit.any():
+        top = max(top, int(lut_sym[hit].max()) + 1)
+    if sl_sym.size:
+        top = max(top, int(sl_sym.max()) + 1)
+    n = top if n_symbols is None else max(int(n_symbols), top)
+    lengths = np.zeros(n, np.uint8)
+    lengths[lut_sym[hit]] = lut_len[hit]
+    for L in range(LUT_BITS + 1, len(base) - 1):
+        if L < len(first) and first[L] >= 0:
+            lengths[sl_sym[base[L]:base[L + 1]]] = L
+    return lengths
+
+
+def compressed_matmul(x_np, packed_np, codebook_np, M, K, bits, chunk_rows=None, C=None):
+    """y = x @ W^T with W the LSB-first `bits`-wide indices in packed_np
+    (no pad needed) into codebook_np; x (..., K) -> (..., M) float32 numpy."""
+    dev = _device()
+    lib = nat.load()
+    M, K, bits = int(M), int(K), int(bits)
+    x = _f32(x_np)
+    lead = x.shape[:-1]
+    x2 = np.ascontiguousarray(x.reshape(-1, K))
+    T = x2.shape[0]
+    cb = _codebook(codebook_np, C)
+    pk = np.asarray(packed_np, np.uint8).reshape(-1)
+    need = (M * K * bits + 7) // 8
+    if pk.size < need:
+        raise ValueError(f"packed stream holds {pk.size} bytes, {need} needed")
+    out = torch.empty(T, M, dtype=torch.float32, device=dev)
+    if T:
+        xd = torch.from_numpy(x2).to(dev)
+        pd = torch.from_numpy(bitpack.device_padded(pk[:need])).to(dev)
+        cd = torch.from_numpy(cb).to(dev)
+        nat.check(lib.ck_linear_f32(xd.data_ptr(), pd.data_ptr(), cd.data_ptr(), out.data_ptr(),
+                                    T, M, K, len(cb), bits, nat.stream_ptr(dev)), "ck_linear_f32")
+    return out.cpu().numpy().reshape(*lead, M)
+
+
+def _huff_linear(huff_data, cb: np.ndarray, M: int, K: int):
+    from gpu_huffman_functions import HuffmanCodebookLinear
+    lengths = lengths_from_tables(huff_data, len(cb))
+    stream = np.asarray(huff_data["huff_stream"], np.uint8)
+    rbs = huff_data.get("row_bit_starts")
+    return HuffmanCodebookLinear(
+        "huffman_matmul", stream, lengths, M * K, torch.from_numpy(cb), (M, K),
+        max(1, int(np.ceil(np.log2(max(len(cb), 2))))),
+        huff_row_bit_starts=None if rbs is None else np.asarray(rbs, np.int64))
+
+
+def huffman_matmul(x_np, huff_data, codebook_np, M, K, chunk_rows=None, C=None):
+    """y = x @ W^T with W the Huffman stream of huff_data (M x K symbols);
+    x (..., K) -> (..., M) float32 numpy."""
+    dev = _device()
+    M, K = int(M), int(K)
+    x = _f32(x_np)
+    lead = x.shape[:-1]
+    x2 = np.ascontiguousarray(x.reshape(-1, K))
+    lin = _huff_linear(huff_data, _codebook(codebook_np, C), M, K)
+    if x2.shape[0] == 0:
+        return np.zeros((*lead, M), np.float32)
+    y = lin(torch.from_numpy(x2).to(dev))
+    return y.float().cpu().numpy().reshape(*lead, M)
+
+
+def huffman_embedding(token_ids_np, huff_data, codebook_np, H, C=None):
+    """Rows of the Huffman-coded table for token_ids (T,) -> (T, H) float32
+    numpy; row_bit_starts covers the whole vocabulary (one entry per row)."""
+    from gpu_huffman_functions import HuffmanCodebookEmbedding
+    dev = _device()
+    H = int(H)
+    ids = token_ids_np.detach().cpu().numpy() if isinstance(token_ids_np, torch.Tensor) \
+        else np.asarray(token_ids_np)
+    ids = np.ascontiguousarray(ids.reshape(-1).astype(np.int64))
+    cb = _codebook(codebook_np, C)
+    rbs = np.asarray(huff_data["row_bit_starts"], np.int64)
+    vocab = len(rbs)
+    if ids.size == 0:
+        return np.zeros((0, H), np.float32)
+    emb = HuffmanCodebookEmbedding(
+        "huffman_embedding", np.asarray(huff_data["huff_stream"], np.uint8),
+        lengths_from_tables(huff_data, len(cb)), vocab * H, torch.from_numpy(cb), (vocab, H),
+        max(1, int(np.ceil(np.log2(max(len(cb), 2))))), huff_row_bit_starts=rbs)
+    out = emb(torch.from_numpy(ids).to(dev))
+    return out.float().cpu().numpy().reshape(len(ids), H)
+
+
+def huffman_decode_weights(huff_data, codebook_np, M, K, C=None):
+    """The dense float32 [M, K] matrix of a Huffman-coded tensor
+    (codebook[min(symbol, C - 1)]), decoded on the GPU."""
+    _device()
+    M, K = int(M), int(K)
+    cb = _codebook(codebook_np, C)
+    lin = _huff_linear(huff_data, cb, M, K)
+    idx = lin.decode_indices().long().clamp_(0, len(cb) - 1)
+    w = torch.from_numpy(cb).to(idx.device)[idx]
+    return w.reshape(M, K).cpu().numpy()
