@@ -255,6 +255,89 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
     }
 }
 
+// ---- split format -> fixed-width indices (batched tokens) ------------------
+
+// The 64 weights of this lane's sub-block as bf16 bit patterns, mapped to
+// codebook indices through inv (65536 entries): split_decode's walk with the
+// table value instead of the product.
+__device__ __forceinline__ void split_decode_index(const uint32_t (&raw)[16], const uint32_t *s_lds,
+                                                   int lane_addr, const uint16_t *__restrict__ inv,
+                                                   uint32_t (&idx)[64])
+{
+    uint32_t pos = 30;
+    uint32_t d1 = 0;
+    const char *base = (const char *)s_lds + lane_addr;
+    uint32_t w0 = *(const uint32_t *)(base - 4 * kSSub);
+    uint32_t w1 = *(const uint32_t *)base;
+#pragma unroll
+    for (int g = 0; g < 16; g++) {
+        const uint32_t w2 = *(const uint32_t *)(base + (d1 + 1) * (4 * kSSub));
+        uint32_t w = __builtin_amdgcn_alignbit(w1, w0, pos);
+#pragma unroll
+        for (int u = 0; u < 4; u += 2) {
+            const uint32_t e = *(const uint32_t *)((const char *)s_lds + (w & (4u * kSLut - 4u)));
+            // high byte from the entry, low byte raw: the weight's bf16 bits
+            const uint32_t b0 = __builtin_amdgcn_perm(e, raw[g], 0x0c0c0700u | u);
+            const uint32_t b1 = __builtin_amdgcn_perm(e, raw[g], 0x0c0c0600u | (u + 1));
+            idx[4 * g + u] = inv[b0];
+            idx[4 * g + u + 1] = inv[b1];
+            w >>= (e & 31u);
+            pos += e;
+        }
+        const uint32_t dn = __builtin_amdgcn_ubfe(pos, 5, 11);
+        w0 = dn != d1 ? w1 : w0;
+        w1 = dn != d1 ? w2 : w1;
+        d1 = dn;
+    }
+}
+
+constexpr int kPackWaves = 4;
+
+// One wave per chunk (waves stride over the chunks): lane l decodes
+// sub-block l and writes its 64 indices as the 2 BITS words they occupy in
+// the LSB-first stream (src/bitpack.py:32-95): chunk c, sub-block l starts at
+// word 128 BITS c + 2 BITS l.
+template <int BITS>
+__global__ __launch_bounds__(kPackWaves * CBQ_WAVE) void split_to_packed_kernel(
+    SplitSeg S, int64_t n_chunks, const uint16_t *__restrict__ inv, uint32_t *__restrict__ packed)
+{
+    __shared__ __attribute__((aligned(16))) uint32_t s_lds[kSLut + kPackWaves * kSSlotWords];
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CBQ_WAVE);
+    uint32_t *const s_slot = s_lds + kSLut + wave * kSSlotWords;
+    const int lane_addr =
+        __builtin_amdgcn_readfirstlane(4 * (kSLut + wave * kSSlotWords)) + 4 * lane;
+    for (int i = wave; i < kSLut / (4 * CBQ_WAVE); i += kPackWaves)
+        __builtin_amdgcn_global_load_lds(S.lut + i * 4 * CBQ_WAVE + 4 * lane,
+                                         (__attribute__((address_space(3))) void *)(s_lds + i * 4 * CBQ_WAVE),
+                                         16, 0, 0);
+    __syncthreads();                                  // table staged
+    const int64_t W = (int64_t)gridDim.x * kPackWaves;
+    for (int64_t c = (int64_t)blockIdx.x * kPackWaves + wave; c < n_chunks; c += W) {
+        const uint32_t r0 = S.row_off[c];
+        uint32_t H = S.row_off[c + 1] - r0;
+        H = H < (uint32_t)kSRows ? H : (uint32_t)kSRows;
+        SplitItem it;
+        split_load(it, S, c, r0, H, lane);
+        split_stage(it, H, s_slot, lane);
+        uint32_t idx[64];
+        split_decode_index(it.raw, s_lds, lane_addr, inv, idx);
+        uint32_t *dst = packed + (size_t)c * (128 * BITS) + lane * (2 * BITS);
+        uint64_t acc = 0;
+        int nb = 0, q = 0;
+#pragma unroll
+        for (int i = 0; i < 64; i++) {
+            acc |= (uint64_t)idx[i] << nb;
+            nb += BITS;
+            if (nb >= 32) {
+                dst[q++] = (uint32_t)acc;
+                acc >>= 32;
+                nb -= 32;
+            }
+        }
+    }
+}
+
 // ---- build ------------------------------------------------------------------
 
 // sym_code[i]: bit-reversed high-byte code | len << 24 of symbol i.
@@ -387,6 +470,37 @@ int cbq_split_pack(const int32_t *indices, int64_t n_symbols, const uint32_t *sy
     hipLaunchKernelGGL(split_pack_kernel, dim3((unsigned)((n_sub + 255) / 256)), dim3(256), 0,
                        stream, indices, n_sub, sym_code, sym_raw, n_sym, row_off, cwords, raw);
     return cbq_launch_status("split_pack_kernel");
+}
+
+int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits, uint8_t *packed,
+                        hipStream_t stream)
+{
+    if (!m || !m->cwords || !m->row_off || !m->raw || !m->lut || !inv || !packed ||
+        m->n_chunks <= 0)
+        return CK_ERR_ARG;
+    if (((uintptr_t)m->raw & 15) != 0 || ((uintptr_t)m->lut & 15) != 0 ||
+        ((uintptr_t)m->cwords & 15) != 0 || ((uintptr_t)packed & 3) != 0)
+        return CK_ERR_ARG;
+    SplitSeg g = {};
+    g.cwords = m->cwords;
+    g.row_off = m->row_off;
+    g.raw = m->raw;
+    g.lut = m->lut;
+    const int64_t want = (m->n_chunks + kPackWaves - 1) / kPackWaves;
+    const int blocks = (int)(want < (int64_t)cbq_num_cus() * 2 ? want : (int64_t)cbq_num_cus() * 2);
+#define CBQ_S2P(B)                                                                             \
+    hipLaunchKernelGGL(split_to_packed_kernel<B>, dim3(blocks), dim3(kPackWaves * CBQ_WAVE), 0, \
+                       stream, g, m->n_chunks, inv, (uint32_t *)packed)
+    switch (bits) {
+    case 8: CBQ_S2P(8); break;
+    case 10: CBQ_S2P(10); break;
+    case 11: CBQ_S2P(11); break;
+    case 12: CBQ_S2P(12); break;
+    case 13: CBQ_S2P(13); break;
+    default: return CK_ERR_ARG;
+    }
+#undef CBQ_S2P
+    return cbq_launch_status("split_to_packed_kernel");
 }
 
 int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode, float eps, int n,

@@ -412,7 +412,8 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
     import cbq_native as nat
     import synthetic
     from gpu_huffman_functions import (SymbolDecoder, build_columns, build_split,
-                                       columns_eligible, huffman_prefill)
+                                       columns_eligible, huffman_prefill, split_inverse,
+                                       split_prefill)
     lib = nat.load()
     dev = torch.device(device)
 
@@ -492,11 +493,15 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                               canon_pay=tb["pay"].data_ptr(), value_cb=None,
                               C=tb["codebook"].numel(), stage_words=tb["stage_words"])
 
-    def huff_linear(t, with_cols=True):
+    def huff_linear(t, with_cols=True, sp_prompt=None):
+        """sp_prompt: the tensor's split format when a grouped launch owns
+        its one-token GEMV and this callable serves the multi-token calls."""
         M, K = t.shape
         desc = huff_desc(t)
         cols = None
         sp = huff_split(t) if with_cols else None
+        sp_p = sp if sp is not None else sp_prompt
+        inv = split_inverse(t.tables["codebook"].cpu().numpy(), dev) if sp_p is not None else None
         if sp is not None:
             one, sxform = split_fns([sp], [M], K)
         elif with_cols and columns_eligible(desc, K):   # single-token GEMV on the column layout
@@ -509,8 +514,12 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
             T = x.shape[0]
             if T == 1 and sp is not None:
                 return one(x)
-            if T >= 64:                      # prompt: decode + pack + matrix cores
-                y = huffman_prefill(sym, x, M, K, t.tables["codebook"])
+            if T >= 64:                      # prompt: transient packed stream + matrix cores
+                y = None
+                if sp_p is not None:
+                    y = split_prefill(sp_p, inv, x, M, K, t.tables["codebook"])
+                if y is None:
+                    y = huffman_prefill(sym, x, M, K, t.tables["codebook"])
                 if y is not None:
                     return y
             out = torch.empty(T, M, device=dev)
@@ -558,7 +567,8 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         if all(sp is not None for sp in sps):
             Ms = [t.shape[0] for t in ts]
             one, sxform = split_fns(sps, Ms, K)
-            singles = [huff_linear(t, with_cols=False) for t in ts]   # multi-token calls
+            singles = [huff_linear(t, with_cols=False, sp_prompt=sp)      # multi-token calls
+                       for t, sp in zip(ts, sps)]
 
             def g(x):
                 x = x.reshape(-1, K).contiguous()

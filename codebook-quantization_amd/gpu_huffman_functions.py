@@ -239,6 +239,52 @@ def huffman_prefill(sym: SymbolDecoder, x: torch.Tensor, M: int, K: int,
     return out
 
 
+def prefill_bits(C: int) -> int:
+    """Index width of the transient fixed-width stream (8, 10..13; 9 packs
+    as 10), or 0 when C needs more than 13 bits."""
+    bits = max(8, int(np.ceil(np.log2(max(C, 2)))))
+    bits = 10 if bits == 9 else bits
+    return bits if bits <= 13 else 0
+
+
+def split_inverse(codebook: np.ndarray, device) -> torch.Tensor:
+    """uint16 [65536]: bf16 bit pattern -> an index of the codebook holding
+    that value (the split format stores bf16 values; any index of an equal
+    value gives the same product)."""
+    cb = np.ascontiguousarray(codebook, np.float32).reshape(-1)
+    pats = (cb.view(np.uint32) >> 16).astype(np.int64)
+    inv = np.zeros(1 << 16, np.uint16)
+    inv[pats[::-1]] = np.arange(len(cb), dtype=np.uint16)[::-1]     # first index wins
+    return torch.from_numpy(inv.view(np.int16)).to(device)
+
+
+def split_prefill(split, inv: torch.Tensor, x: torch.Tensor, M: int, K: int,
+                  codebook: torch.Tensor) -> Optional[torch.Tensor]:
+    """y [T, M] for T >= 64 fp32 tokens from the split format: decoded straight
+    to a transient fixed-width stream (cbq_split_to_packed, one table read per
+    two weights) and multiplied on the fp32 matrix cores (cbq_linear_f32_ws).
+    None when the codebook needs more than 13 bits."""
+    T = x.shape[0]
+    C = int(codebook.numel())
+    bits = prefill_bits(C)
+    if not bits or K % 32 or (M * K) % 32:
+        return None
+    lib = nat.load()
+    dev = x.device
+    st = nat.stream_ptr(dev)
+    packed = torch.empty(M * K * bits // 8 + 16, dtype=torch.uint8, device=dev)
+    nat.check(lib.cbq_split_to_packed(ctypes.byref(split[1]), inv.data_ptr(), bits,
+                                      packed.data_ptr(), st), "cbq_split_to_packed")
+    out = torch.empty(T, M, dtype=torch.float32, device=dev)
+    nws = int(lib.cbq_linear_f32_workspace(T, M, K))
+    ws = torch.empty(max(1, nws // 4), dtype=torch.float32, device=dev) if nws else None
+    nat.check(lib.cbq_linear_f32_ws(x.data_ptr(), packed.data_ptr(), codebook.data_ptr(),
+                                    out.data_ptr(), T, M, K, C, bits,
+                                    None if ws is None else ws.data_ptr(), nws, st),
+              "cbq_linear_f32_ws")
+    return out
+
+
 def columns_eligible(desc: "nat.HuffStream", K: int) -> bool:
     """The column GEMV serves T = 1 rows of whole 4096-symbol chunks with
     bf16-value payloads and a second table level that fits its LDS."""
@@ -290,6 +336,7 @@ class HuffmanCodebookLinear:
         # is bf16-exact, else the column layout when the shape allows
         self.cols = None
         self.split = None
+        self._inv = None
         if split_format and self.K % hc.CHUNK_SYMBOLS == 0:
             self._sym = SymbolDecoder(self.dev.words, self.dev.chunk_off, self.dev.sub_len,
                                       np.asarray(huff_lengths, np.uint8), device)
@@ -316,6 +363,13 @@ class HuffmanCodebookLinear:
         xc = x.reshape(T, self.K).to(torch.float32).contiguous()
         out = torch.empty(T, self.M, dtype=torch.float32, device=self.device)
         st = nat.stream_ptr(self.device)
+        if T >= 64 and self.split is not None:
+            if self._inv is None:
+                self._inv = split_inverse(self._cb_np, self.device)
+            y = split_prefill(self.split, self._inv, xc, self.M, self.K, self._cb_dev)
+            if y is not None:
+                out = y.reshape(*lead, self.M)
+                return out if in_dtype == torch.float32 else out.to(in_dtype)
         if T >= 64:
             if self._sym is None:
                 self._sym = SymbolDecoder(self.dev.words, self.dev.chunk_off, self.dev.sub_len,

@@ -345,6 +345,17 @@ int cbq_huff_decode_indices(const cbq_huff_stream *hs, int32_t *out,
 int cbq_pack_indices(const int32_t *indices, int64_t n, int bits, uint8_t *packed,
                      hipStream_t stream);
 
+/* Decodes a split-format matrix (cbq_split_matrix, n_chunks chunks of 4096
+ * weights) straight to the LSB-first fixed-width stream of its codebook
+ * indices, bits in {8, 10, 11, 12, 13}: inv maps every bf16 bit pattern of
+ * the codebook to an index holding that value (65536 uint16 entries);
+ * packed (4-byte aligned) receives n_chunks * 4096 * bits / 8 bytes.  No
+ * counterpart in the reference: the batched-token path of a Huffman module
+ * whose split format exists (one table read per two weights instead of the
+ * stream decode to int32 and cbq_pack_indices). */
+int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits,
+                        uint8_t *packed, hipStream_t stream);
+
 /* ==== library introspection ============================================== */
 
 /* Version string of the library build. */

@@ -95,6 +95,34 @@ def test_huffman_module_batched_tokens(cuda, oracle, M, K):
     assert rel_l2(y, ref) <= TOL, rel_l2(y, ref)
 
 
+@pytest.mark.parametrize("M,K", [(96, 8192), (33, 4096)])
+def test_split_to_packed(cuda, oracle, M, K):
+    """cbq_split_to_packed turns the split format back into the reference's
+    LSB-first index stream bit for bit, and the module's batched-token path
+    on it equals the stream-decode path exactly."""
+    import ctypes
+    import cbq_native as nat
+    import huffman_codebook as hc
+    from gpu_huffman_functions import prefill_bits, split_inverse
+    from test_gpu_huffman import _lin
+    rng = np.random.default_rng(M + K)
+    w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
+    cb, idx = cbb.frequency_sorted_codebook(w)
+    enc = hc.huffman_encode_indices(idx, shape=(M, K))
+    lin = _lin(enc, cb, M, K)
+    assert lin.split is not None
+    bits = prefill_bits(len(cb))
+    inv = split_inverse(cb, cuda)
+    out = torch.zeros(M * K * bits // 8 + 16, dtype=torch.uint8, device=cuda)
+    nat.check(nat.load().cbq_split_to_packed(ctypes.byref(lin.split[1]), inv.data_ptr(), bits,
+                                             out.data_ptr(), nat.stream_ptr(cuda)), "s2p")
+    want = oracle.pack_lsb(idx.reshape(-1), bits)
+    assert np.array_equal(out.cpu().numpy()[:want.size], want)
+    x = torch.from_numpy(rng.standard_normal((80, K)).astype(np.float32)).to(cuda)
+    lin_stream = _lin(enc, cb, M, K, split_format=False)
+    assert torch.equal(lin(x), lin_stream(x))
+
+
 def test_pack_indices_layout(cuda, oracle):
     """cbq_pack_indices writes the reference's LSB-first stream bit for bit,
     clamping to 2^bits - 1."""
