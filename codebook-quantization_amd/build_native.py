@@ -2,8 +2,8 @@
 
     python codebook-quantization_amd/build_native.py
 
-Compiles csrc/*.hip with hipcc straight into a shared library next to this
-file.  Packed-fp32 VALU ops are disabled (-packed-fp32-ops): the kernels are
+Compiles each csrc/*.hip with hipcc (in parallel) and links them into a
+shared library next to this file.  Packed-fp32 VALU ops are disabled (-packed-fp32-ops): the kernels are
 written for scalar fp32 FMAs.
 """
 import os
@@ -26,23 +26,50 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libcbq_hip.so)")
 
 
+FLAGS = [f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         "-Wno-unused-command-line-argument"]
+
+
+def sources():
+    return [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+
+
 def command(out: str = SO):
-    srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    return [hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
-            "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-            "-Wno-unused-command-line-argument", "-pthread", "-o", out] + srcs
+    """One hipcc line that compiles every source and links the library."""
+    return [hipcc()] + FLAGS + ["-shared", "-pthread", "-o", out] + sources()
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every time it is called; write atomically next to this file."""
-    tmp = SO + ".tmp"
-    cmd = command(tmp)
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + res.stderr[-4000:])
-    os.replace(tmp, SO)
+def build(verbose: bool = False, jobs: int = 0) -> str:
+    """Compile every time it is called (one hipcc per source, in parallel, in
+    a temporary directory), link, and move the library next to this file."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+    srcs = sources()
+    jobs = jobs or min(len(srcs), max(1, os.cpu_count() or 1))
+    with tempfile.TemporaryDirectory(prefix="cbq_build_") as tmpd:
+        objs = [os.path.join(tmpd, os.path.basename(s) + ".o") for s in srcs]
+
+        def compile_one(so):
+            src, obj = so
+            cmd = [hipcc()] + FLAGS + ["-c", "-o", obj, src]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            return subprocess.run(cmd, capture_output=True, text=True)
+
+        with ThreadPoolExecutor(jobs) as ex:
+            for src, res in zip(srcs, ex.map(compile_one, zip(srcs, objs))):
+                if res.returncode != 0:
+                    raise RuntimeError(f"hipcc failed on {src}:\n" + res.stderr[-4000:])
+        tmp = os.path.join(tmpd, "libcbq_hip.so")
+        cmd = [hipcc()] + FLAGS + ["-shared", "-pthread", "-o", tmp] + objs
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError("hipcc link failed:\n" + res.stderr[-4000:])
+        shutil.copyfile(tmp, SO + ".tmp")
+    os.replace(SO + ".tmp", SO)
     return SO
 
 

@@ -1,10 +1,13 @@
 """Synthetic compressed decoders built on the GPU (bench and e2e workloads).
 
-Weights are N(0, std) rounded to bf16 (torch's nearest-even cast), drawn per
-tensor from a seeded CUDA generator, so every tensor can be regenerated
-bit-identically.  Lossless codebooks are shared per category (attention /
-mlp_ffn / embedding) and frequency-sorted; fixed-width tensors are packed
-LSB-first; Huffman tensors get their own 24-bit-limited canonical code
+Weights are N(0, std) bf16 values drawn per tensor by a counter-based
+integer generator (make_bf16): a 32-bit hash of (tensor seed, element index)
+picks the bf16 value through an inverse-CDF table of the normal distribution
+over bf16 rounding intervals.  Only integer operations touch the samples, so
+the CPU (numpy or torch) and the GPU produce the same bits, and a CPU oracle
+can rebuild exactly the model the GPU runs.  Lossless codebooks are shared
+per category (attention / mlp_ffn / embedding) and frequency-sorted;
+fixed-width tensors are packed LSB-first; Huffman tensors get their own 24-bit-limited canonical code
 (lengths from that tensor's symbol counts, as the reference codes each
 tensor, src/adaptive_compressor.py:111-127) and the chunk index.
 """
@@ -45,11 +48,77 @@ def tensor_seed(name: str, base: int = 0) -> int:
     return (zlib.crc32(name.encode()) ^ (base * 0x9E3779B1)) & 0x7FFFFFFF
 
 
+_M32 = 0xFFFFFFFF
+_GEN_CHUNK = 1 << 26
+
+
+def _mul32(x, c: int):
+    """(x * c) mod 2^32 for x in [0, 2^32) held in int64 (torch or numpy):
+    the constant is split in 16-bit halves so no product exceeds 2^49."""
+    return (x * (c & 0xFFFF) + (((x * (c >> 16)) & 0xFFFF) << 16)) & _M32
+
+
+def mix32(x):
+    """Chris Wellons' "lowbias32" 32-bit integer hash (hash-prospector):
+    x ^= x>>16; x *= 0x7feb352d; x ^= x>>15; x *= 0x846ca68b; x ^= x>>16."""
+    x = x ^ (x >> 16)
+    x = _mul32(x, 0x7FEB352D)
+    x = x ^ (x >> 15)
+    x = _mul32(x, 0x846CA68B)
+    return x ^ (x >> 16)
+
+
+def uniform32(i, seed: int):
+    """Uniform 32-bit integers for element indices i (int64, < 2^32) of the
+    stream `seed`: two hash rounds keyed by the seed."""
+    a = (i + ((seed * 0x9E3779B9) & _M32)) & _M32
+    return mix32(mix32(a) ^ ((seed * 0x85EBCA6B) & _M32))
+
+
+_TABLES: Dict[float, Tuple[np.ndarray, np.ndarray]] = {}
+
+
+def normal_bf16_table(std: float = 0.02) -> Tuple[np.ndarray, np.ndarray]:
+    """(pats uint16 [n], thr int64 [n-1]): the bf16 values with nonzero
+    probability under N(0, std) rounded to nearest bf16, in ascending order,
+    and the upper ends of their intervals on the 2^32 grid.  A uniform u in
+    [0, 2^32) draws pats[searchsorted(thr, u, side='right')].  Value j's
+    interval is bounded by the midpoints to its neighbours (its rounding
+    interval), so its probability is Phi(mid_hi/std) - Phi(mid_lo/std) to
+    within 2^-32."""
+    if std in _TABLES:
+        return _TABLES[std]
+    from scipy.special import ndtr
+    pos = np.arange(1, 0x7F80, dtype=np.uint32)              # positive finite bf16
+    pv = (pos << 16).view(np.float32).astype(np.float64)
+    vals = np.concatenate([-pv[::-1], [0.0], pv])
+    pats = np.concatenate([pos[::-1] | 0x8000, [0], pos]).astype(np.uint16)
+    mids = 0.5 * (vals[1:] + vals[:-1])
+    thr = np.floor(ndtr(mids / std) * 2.0 ** 32).astype(np.int64)
+    lo = np.concatenate([[0], thr])
+    hi = np.concatenate([thr, [1 << 32]])
+    keep = hi > lo
+    _TABLES[std] = (pats[keep], hi[keep][:-1].copy())
+    return _TABLES[std]
+
+
 def make_bf16(shape, name: str, std: float = 0.02, base_seed: int = 0,
               device="cuda") -> torch.Tensor:
-    g = torch.Generator(device=device)
-    g.manual_seed(tensor_seed(name, base_seed))
-    return (torch.randn(*shape, generator=g, device=device, dtype=torch.float32) * std).bfloat16()
+    """N(0, std) bf16 weights of one tensor, identical bits on every device
+    (see normal_bf16_table and uniform32)."""
+    pats, thr = normal_bf16_table(std)
+    dev = torch.device(device)
+    pats_t = torch.from_numpy(pats.view(np.int16)).to(dev)
+    thr_t = torch.from_numpy(thr).to(dev)
+    seed = tensor_seed(name, base_seed)
+    n = int(np.prod(shape))
+    out = torch.empty(n, dtype=torch.int16, device=dev)
+    step = n if dev.type == "cuda" else _GEN_CHUNK
+    for s0 in range(0, n, step):
+        s1 = min(n, s0 + step)
+        u = uniform32(torch.arange(s0, s1, dtype=torch.int64, device=dev), seed)
+        out[s0:s1] = pats_t[torch.searchsorted(thr_t, u, right=True)]
+    return out.view(torch.bfloat16).reshape(shape)
 
 
 @dataclass

@@ -141,11 +141,13 @@ def fixed_gemv(x, packed, codebook, M, K, bits, C=None, chunk_rows=CHUNK_ROWS,
     x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, K)
     cb = np.ascontiguousarray(codebook, dtype=np.float32)
     pk = np.ascontiguousarray(packed, dtype=np.uint8)
-    if len(pk) < (M * K * bits + 7) // 8 + 2:
+    need = (M * K * bits + 7) // 8
+    if len(pk) < need + 4:
+        if len(pk) < need + 2:
+            pk = np.concatenate([pk, np.zeros(2, np.uint8)])
+        # The C read is a 4-byte window, one byte past the wrapper's 2-byte pad
+        # for b <= 7 (src/compressed_matmul.c:330-347); keep that byte readable.
         pk = np.concatenate([pk, np.zeros(2, np.uint8)])
-    # The C read is a 4-byte window, one byte past the wrapper's 2-byte pad for
-    # b <= 7 (src/compressed_matmul.c:330-347); keep that byte readable here.
-    pk = np.concatenate([pk, np.zeros(2, np.uint8)])
     T = x.shape[0]
     out = np.zeros((T, M), np.float32)
     C = len(cb) if C is None else int(C)
@@ -175,7 +177,9 @@ def fixed_embedding(ids, packed, codebook, H, bits, C=None):
     """out[t, h] = codebook[min(idx[ids[t]*H + h], C-1)] (float32)."""
     ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
     cb = np.ascontiguousarray(codebook, dtype=np.float32)
-    pk = np.concatenate([np.asarray(packed, np.uint8), np.zeros(4, np.uint8)])
+    pk = np.ascontiguousarray(packed, np.uint8)
+    if len(ids) and len(pk) < ((int(ids.max()) + 1) * H * bits + 7) // 8 + 4:
+        pk = np.concatenate([pk, np.zeros(4, np.uint8)])
     out = np.zeros((len(ids), H), np.float32)
     lib("oracle").lib.oracle_fixed_embedding(
         _p(ids, _i32p), _p(pk, _u8p), _p(cb, _f32p), _p(out, _f32p), len(ids), H,

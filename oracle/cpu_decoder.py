@@ -33,10 +33,13 @@ def rope_tables(head_dim: int, theta: float, max_len: int):
 
 
 class CpuQwen3:
-    def __init__(self, cfg, comp: dict, max_len: int = 256, threads=None):
+    def __init__(self, cfg, comp: dict, max_len: int = 256, threads=None, kind: str = "oracle"):
+        """kind: "oracle" (the C restatement) or "ref" (the reference's own
+        compiled kernel, oracle/_ref) for the fixed-width GEMVs."""
         self.cfg = cfg
         self.comp = comp
         self.threads = threads
+        self.kind = kind
         self.cos, self.sin = rope_tables(cfg.head_dim, cfg.rope_theta, max_len)
         self.max_len = max_len
         self.reset()
@@ -54,7 +57,7 @@ class CpuQwen3:
         if d.get("encoding") == "huffman":
             return O.huff_gemv(x, d, cb, M, K, chunk_rows=None, threads=self.threads)
         return O.fixed_gemv(x, d["indices"], cb, M, K, int(d["bits"]), chunk_rows=None,
-                            threads=self.threads)
+                            threads=self.threads, kind=self.kind)
 
     def embed(self, ids: np.ndarray) -> np.ndarray:
         d = self.comp["model.embed_tokens"]
