@@ -97,6 +97,8 @@ SIGNATURES = {
     "cbq_attn_rope_decode_workspace": (ctypes.c_size_t, [_i, _i, _i]),
     "cbq_attn_rope_decode_ws_f32": (_i, [_vp] * 11 + [_i] * 4 + [ctypes.c_float] * 2
                                     + [_vp, ctypes.c_size_t, _vp]),
+    "cbq_attn_rope_decode_noalloc_f32": (_i, [_vp] * 11 + [_i] * 4 + [ctypes.c_float] * 2
+                                         + [_vp]),
     "cbq_argmax_step": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "cbq_silu_mul_f32": (_i, [_vp, _vp, _vp, _i64, _vp]),
 }

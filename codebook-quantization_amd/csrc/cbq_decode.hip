@@ -10,6 +10,9 @@
 #include "../../include/cbq_decode.h"
 
 #include <math.h>
+#include <stdio.h>
+
+#include <mutex>
 
 // hipcc contracts a * b + c into an fma by default; the glue rounds each
 // product and sum on its own (explicit fmaf calls stay fused).
@@ -635,6 +638,84 @@ __global__ __launch_bounds__(kGlueBlock) void silu_mul_kernel(const float *__res
 
 }  // namespace
 
+// Static split-partials scratch of cbq_attn_rope_decode_noalloc_f32, one
+// copy per device, held for the life of the process.  Host code never passes
+// the array's name to a kernel (in host code it names a host-side stand-in):
+// scratch_address() resolves the device's own copy once per device with
+// hipGetSymbolAddress and every launch uses that pointer.
+constexpr size_t kAttnScratchBytes = CBQ_ATTN_SCRATCH_BYTES;
+static __device__ __align__(256) float scratch[kAttnScratchBytes / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float *g_scratch_ptr[kMaxDevices];
+
+// The current device's copy of `scratch`.
+int scratch_address(float **out)
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        fprintf(stderr, "[cbq_hip] scratch: no usable current device (%d)\n", dev);
+        return CK_ERR_HIP;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            fprintf(stderr, "[cbq_hip] scratch: hipGetSymbolAddress failed on device %d: %s\n",
+                    dev, hipGetErrorString(e));
+            return CK_ERR_HIP;
+        }
+        g_scratch_ptr[dev] = (float *)p;
+    }
+    *out = g_scratch_ptr[dev];
+    return CK_SUCCESS;
+}
+
+// Argument checks shared by the split one-token attention entry points.
+int attn_split_check(const float *q, const float *k, const float *v, const float *cos_table,
+                     const float *sin_table, const int64_t *pos, const float *k_cache,
+                     const float *v_cache, const float *out, int n_q, int n_kv, int hd,
+                     int max_len)
+{
+    if (!q || !k || !v || !cos_table || !sin_table || !pos || !k_cache || !v_cache || !out)
+        return CK_ERR_ARG;
+    if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || max_len <= 0 || max_len > kAttnMaxLen)
+        return CK_ERR_ARG;
+    if (((uintptr_t)k_cache & 15) != 0 || ((uintptr_t)v_cache & 15) != 0) return CK_ERR_ARG;
+    if (hd != 64 && hd != 128 && hd != 256) return CK_ERR_ARG;
+    return CK_SUCCESS;
+}
+
+// Split launch + merge launch with the partials at `part`
+// (attn_split_count(max_len) * n_q * (hd + 2) floats).
+int attn_split_launch(const float *q, const float *k, const float *v, const float *q_weight,
+                      const float *k_weight, const float *cos_table, const float *sin_table,
+                      const int64_t *pos, float *k_cache, float *v_cache, float *out, int n_q,
+                      int n_kv, int hd, int max_len, float scale, float eps, float *part,
+                      hipStream_t stream)
+{
+    const int S = attn_split_count(max_len);
+    const int group = n_q / n_kv;
+#define CBQ_ATTN_SPLIT(HD)                                                                      \
+    hipLaunchKernelGGL(attn_rope_split_kernel<HD>, dim3(n_q, S), dim3(kSplitThreads), 0, stream, \
+                       q, k, v, q_weight, k_weight, cos_table, sin_table, pos, k_cache, v_cache,  \
+                       part, group, max_len, scale, eps);                                          \
+    hipLaunchKernelGGL(attn_combine_kernel<HD>, dim3(n_q), dim3(HD), 0, stream, part, S, out)
+    switch (hd) {
+    case 64: CBQ_ATTN_SPLIT(64); break;
+    case 128: CBQ_ATTN_SPLIT(128); break;
+    default: CBQ_ATTN_SPLIT(256); break;
+    }
+#undef CBQ_ATTN_SPLIT
+    return cbq_launch_status("attn_combine_kernel");
+}
+
+}  // namespace
+
 extern "C" {
 
 int cbq_add_rmsnorm_f32(float *h, const float *delta, const float *weight, float *out, int T,
@@ -732,31 +813,40 @@ int cbq_attn_rope_decode_ws_f32(const float *q, const float *k, const float *v,
                                 int n_q, int n_kv, int hd, int max_len, float scale, float eps,
                                 void *workspace, size_t workspace_bytes, hipStream_t stream)
 {
-    if (!q || !k || !v || !cos_table || !sin_table || !pos || !k_cache || !v_cache || !out ||
-        !workspace)
-        return CK_ERR_ARG;
-    if (n_q <= 0 || n_kv <= 0 || n_q % n_kv || max_len <= 0 || max_len > kAttnMaxLen)
-        return CK_ERR_ARG;
-    if (((uintptr_t)k_cache & 15) != 0 || ((uintptr_t)v_cache & 15) != 0 ||
-        ((uintptr_t)workspace & 3) != 0)
-        return CK_ERR_ARG;
-    if (hd != 64 && hd != 128 && hd != 256) return CK_ERR_ARG;
+    if (!workspace || ((uintptr_t)workspace & 3) != 0) return CK_ERR_ARG;
+    const int rc = attn_split_check(q, k, v, cos_table, sin_table, pos, k_cache, v_cache, out,
+                                    n_q, n_kv, hd, max_len);
+    if (rc) return rc;
     if (workspace_bytes < cbq_attn_rope_decode_workspace(n_q, hd, max_len)) return CK_ERR_ARG;
-    const int S = attn_split_count(max_len);
-    float *part = (float *)workspace;
-    const int group = n_q / n_kv;
-#define CBQ_ATTN_SPLIT(HD)                                                                      \
-    hipLaunchKernelGGL(attn_rope_split_kernel<HD>, dim3(n_q, S), dim3(kSplitThreads), 0, stream, \
-                       q, k, v, q_weight, k_weight, cos_table, sin_table, pos, k_cache, v_cache,  \
-                       part, group, max_len, scale, eps);                                          \
-    hipLaunchKernelGGL(attn_combine_kernel<HD>, dim3(n_q), dim3(HD), 0, stream, part, S, out)
-    switch (hd) {
-    case 64: CBQ_ATTN_SPLIT(64); break;
-    case 128: CBQ_ATTN_SPLIT(128); break;
-    default: CBQ_ATTN_SPLIT(256); break;
+    return attn_split_launch(q, k, v, q_weight, k_weight, cos_table, sin_table, pos, k_cache,
+                             v_cache, out, n_q, n_kv, hd, max_len, scale, eps,
+                             (float *)workspace, stream);
+}
+
+int cbq_attn_rope_decode_noalloc_f32(const float *q, const float *k, const float *v,
+                                     const float *q_weight, const float *k_weight,
+                                     const float *cos_table, const float *sin_table,
+                                     const int64_t *pos, float *k_cache, float *v_cache,
+                                     float *out, int n_q, int n_kv, int hd, int max_len,
+                                     float scale, float eps, hipStream_t stream)
+{
+    int rc = attn_split_check(q, k, v, cos_table, sin_table, pos, k_cache, v_cache, out, n_q,
+                              n_kv, hd, max_len);
+    if (rc) return rc;
+    const size_t need = cbq_attn_rope_decode_workspace(n_q, hd, max_len);
+    if (need > sizeof(scratch)) {
+        fprintf(stderr,
+                "[cbq_hip] cbq_attn_rope_decode_noalloc_f32: n_q=%d hd=%d max_len=%d needs %zu "
+                "bytes of split partials, above the %zu-byte static scratch; use "
+                "cbq_attn_rope_decode_ws_f32 with a workspace\n",
+                n_q, hd, max_len, need, sizeof(scratch));
+        return CK_ERR_ARG;
     }
-#undef CBQ_ATTN_SPLIT
-    return cbq_launch_status("attn_combine_kernel");
+    float *part = nullptr;
+    rc = scratch_address(&part);
+    if (rc) return rc;
+    return attn_split_launch(q, k, v, q_weight, k_weight, cos_table, sin_table, pos, k_cache,
+                             v_cache, out, n_q, n_kv, hd, max_len, scale, eps, part, stream);
 }
 
 int cbq_argmax_step(const float *logits, int n, void *workspace, int32_t *ids32, int64_t *toks,

@@ -83,6 +83,28 @@ int cbq_attn_rope_decode_ws_f32(const float *q, const float *k, const float *v,
                                 float scale, float eps, void *workspace,
                                 size_t workspace_bytes, hipStream_t stream);
 
+/* cbq_attn_rope_decode_ws_f32 for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  It has no counterpart in the reference.  Same
+ * arguments as cbq_attn_rope_decode_f32, results bit-identical to
+ * cbq_attn_rope_decode_ws_f32.  The split partials live in a static device
+ * array of CBQ_ATTN_SCRATCH_BYTES (1 MiB) that the library holds on every
+ * GPU it runs on until the process ends; shapes whose partials,
+ * cbq_attn_rope_decode_workspace(n_q, hd, max_len) bytes, exceed it return
+ * CK_ERR_ARG with a message (e.g. n_q * (hd + 2) > 16384 once max_len >
+ * 960).  The first call on a device resolves the array's address
+ * (hipGetSymbolAddress): make it outside stream capture.  Every call on a
+ * GPU uses that GPU's one array, so calls that overlap on one GPU (other
+ * streams, other host threads) race; the partials are fully rewritten by
+ * each call, nothing needs clearing.  Allocates nothing. */
+#define CBQ_ATTN_SCRATCH_BYTES (1u << 20)
+int cbq_attn_rope_decode_noalloc_f32(const float *q, const float *k, const float *v,
+                                     const float *q_weight, const float *k_weight,
+                                     const float *cos_table, const float *sin_table,
+                                     const int64_t *pos, float *k_cache, float *v_cache,
+                                     float *out, int n_q, int n_kv, int hd, int max_len,
+                                     float scale, float eps, hipStream_t stream);
+
 /* Greedy pick of a captured decode step: tok = argmax(logits[0, n)) (first
  * maximum; NaN ranks highest, as torch.argmax); ids32[0] = tok;
  * toks[pos[0] - first] = tok when that index lies in [0, n_toks);
