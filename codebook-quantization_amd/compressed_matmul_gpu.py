@@ -105,15 +105,39 @@ def compressed_matmul(x_np, packed_np, codebook_np, M, K, bits, chunk_rows=None,
     return out.cpu().numpy().reshape(*lead, M)
 
 
+_LINEARS: "OrderedDict" = None
+_CACHE_SIZE = 4
+
+
 def _huff_linear(huff_data, cb: np.ndarray, M: int, K: int):
+    """The device format of a Huffman tensor, built once per (stream,
+    codebook, shape) and reused by later calls on the same data (the
+    reference's functional calls take the arrays anew each time; here the
+    last few device formats stay cached, keyed by a CRC of the stream and
+    the codebook)."""
+    import zlib
+    from collections import OrderedDict
     from gpu_huffman_functions import HuffmanCodebookLinear
-    lengths = lengths_from_tables(huff_data, len(cb))
-    stream = np.asarray(huff_data["huff_stream"], np.uint8)
+    global _LINEARS
+    if _LINEARS is None:
+        _LINEARS = OrderedDict()
+    stream = np.ascontiguousarray(huff_data["huff_stream"], np.uint8)
     rbs = huff_data.get("row_bit_starts")
-    return HuffmanCodebookLinear(
+    key = (M, K, stream.size, zlib.crc32(stream), zlib.crc32(np.ascontiguousarray(cb)),
+           None if rbs is None else zlib.crc32(np.ascontiguousarray(rbs, np.int64)))
+    lin = _LINEARS.get(key)
+    if lin is not None:
+        _LINEARS.move_to_end(key)
+        return lin
+    lengths = lengths_from_tables(huff_data, len(cb))
+    lin = HuffmanCodebookLinear(
         "huffman_matmul", stream, lengths, M * K, torch.from_numpy(cb), (M, K),
         max(1, int(np.ceil(np.log2(max(len(cb), 2))))),
         huff_row_bit_starts=None if rbs is None else np.asarray(rbs, np.int64))
+    _LINEARS[key] = lin
+    while len(_LINEARS) > _CACHE_SIZE:
+        _LINEARS.popitem(last=False)
+    return lin
 
 
 def huffman_matmul(x_np, huff_data, codebook_np, M, K, chunk_rows=None, C=None):

@@ -147,7 +147,15 @@ __device__ __forceinline__ float split_decode(const uint32_t (&raw)[16], const u
     return acc;
 }
 
-template <int NW, int XMODE>
+// Row groups: the flat symbol stream is cut into 4096-symbol chunks, so with
+// K % 4096 != 0 a chunk holds parts of several rows.  The GEMV therefore
+// walks groups of GR = 4096 / gcd(K, 4096) rows, which are exactly
+// R = GR * K / 4096 whole chunks; chunk p of every group covers the same x
+// columns, (p * 4096 + i) mod K, so the block stages one 4096-float x tile
+// per phase p as before.  Lane l's sub-block lies in row (p * 4096 + 64 l) / K
+// of the group (K % 64 == 0), and a chunk's dot products are summed per row
+// with masked wave sums.  GR = 1 (K % 4096 == 0) is the plain row walk.
+template <int NW, int XMODE, int GR>
 __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *__restrict__ x,
                                                                    SplitSegs segs, int K,
                                                                    const float *__restrict__ x1,
@@ -169,12 +177,13 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
     const int lane_addr =
         __builtin_amdgcn_readfirstlane(4 * (kSLut + kSChunk + wave * kSSlotWords)) + 4 * lane;
 
-    const int R = K / kSChunk;
+    const int R = K * GR / kSChunk;                    // chunks per row group
+    const int Mg = M / GR;                              // row groups
     const int W = S.nblocks * NW;
     const int wid = bid * NW + wave;
-    const int rows = wid < M ? (M - wid + W - 1) / W : 0;
+    const int rows = wid < Mg ? (Mg - wid + W - 1) / W : 0;
     const int b0 = bid * NW;
-    const int rows_max = b0 < M ? (M - b0 + W - 1) / W : 0;
+    const int rows_max = b0 < Mg ? (Mg - b0 + W - 1) / W : 0;
     const int n_seg = (rows_max + 63) >> 6;
     const float *const xr = s_x + lane * 64;
     const int xsw = (lane & 15) << 2;
@@ -207,22 +216,35 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
     const bool store_h = XMODE == XF_ADD_RMS && blockIdx.x == 0 && h_out != nullptr;
 
     for (int seg = 0; seg < n_seg; seg++) {
-        float res = 0.f;
+        float res[GR];
+#pragma unroll
+        for (int q = 0; q < GR; q++) res[q] = 0.f;
         const int seg_rows = min(64, rows - seg * 64);
         for (int p = 0; p < R; p++) {
             __syncthreads();
-            if constexpr (XMODE == XF_NONE) {
-                for (int r = wave; r < 64; r += NW) {
-                    const float v = x[(size_t)p * kSChunk + (r << 6) + (lane ^ ((r & 15) << 2))];
-                    s_x[(r << 6) + lane] = v;
-                }
-            } else {
-                for (int r = wave; r < 64; r += NW)
-                    s_x[(r << 6) + lane] =
-                        xform_value(XMODE, x, x1, h_out, store_h,
-                                    p * kSChunk + (r << 6) + (lane ^ ((r & 15) << 2)), xr_scale);
+            for (int r = wave; r < 64; r += NW) {
+                int t = p * kSChunk + (r << 6) + (lane ^ ((r & 15) << 2));
+                if constexpr (GR > 1) t %= K;
+                if constexpr (XMODE == XF_NONE) s_x[(r << 6) + lane] = x[t];
+                else s_x[(r << 6) + lane] = xform_value(XMODE, x, x1, h_out, store_h, t, xr_scale);
             }
             __syncthreads();
+            // rows of the group that chunk p touches, and this lane's row
+            const int q_lo = p * kSChunk / K, q_hi = (p * kSChunk + kSChunk - 1) / K;
+            const int q_me = (p * kSChunk + lane * kSSub) / K;
+            auto add_rows = [&](float acc, int b) {
+                if constexpr (GR == 1) {
+                    const float s = wave_sum(acc);
+                    if (lane == b) res[0] += s;
+                } else {
+#pragma unroll
+                    for (int q = 0; q < GR; q++)
+                        if (q >= q_lo && q <= q_hi) {
+                            const float s = wave_sum(q_me == q ? acc : 0.f);
+                            if (lane == b) res[q] += s;
+                        }
+                }
+            };
             // The slot is rewritten only after the previous item's reads (LDS
             // operations of a wave complete in order).
             if (seg_rows > 0 && (seg > 0 || p > 0)) {
@@ -235,23 +257,21 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
                     split_load(B, S, c, rB, hB, lane);
                 }
                 split_stage(A, hA, s_slot, lane);
-                {
-                    const float s = wave_sum(split_decode(A.raw, s_lds, lane_addr, xr, xsw));
-                    if (lane == b) res += s;
-                }
+                add_rows(split_decode(A.raw, s_lds, lane_addr, xr, xsw), b);
                 if (b + 1 >= seg_rows) break;
                 if (b + 2 < seg_rows) {
                     const int64_t c = chunk_of(seg, p, b + 2, rA, hA);
                     split_load(A, S, c, rA, hA, lane);
                 }
                 split_stage(B, hB, s_slot, lane);
-                {
-                    const float s = wave_sum(split_decode(B.raw, s_lds, lane_addr, xr, xsw));
-                    if (lane == b + 1) res += s;
-                }
+                add_rows(split_decode(B.raw, s_lds, lane_addr, xr, xsw), b + 1);
             }
         }
-        if (lane < seg_rows) S.out[wid + (int64_t)(seg * 64 + lane) * W] = res;
+        if (lane < seg_rows) {
+            const int64_t g = wid + (int64_t)(seg * 64 + lane) * W;
+#pragma unroll
+            for (int q = 0; q < GR; q++) S.out[g * GR + q] = res[q];
+        }
     }
 }
 
@@ -497,6 +517,8 @@ int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits
     case 11: CBQ_S2P(11); break;
     case 12: CBQ_S2P(12); break;
     case 13: CBQ_S2P(13); break;
+    case 16: CBQ_S2P(16); break;
+    case 32: CBQ_S2P(32); break;
     default: return CK_ERR_ARG;
     }
 #undef CBQ_S2P
@@ -507,8 +529,9 @@ int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode
                          const cbq_split_matrix *const *mats, float *const *outs, const int *Ms,
                          int K, hipStream_t stream)
 {
-    if (!x || n < 1 || n > kSMaxSeg || !mats || !outs || !Ms || K <= 0 || K % kSChunk != 0)
+    if (!x || n < 1 || n > kSMaxSeg || !mats || !outs || !Ms || K <= 0 || K % 1024 != 0)
         return CK_ERR_ARG;
+    const int GR = K % kSChunk == 0 ? 1 : K % 2048 == 0 ? 2 : 4;   // 4096 / gcd(K, 4096)
     if (mode < XF_NONE || mode > XF_RMS || ((mode == XF_SILU || mode == XF_ADD_RMS) && !x1) ||
         (mode >= XF_ADD_RMS && K > 16384))
         return CK_ERR_ARG;
@@ -518,7 +541,7 @@ int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode
         const cbq_split_matrix *m = mats[i];
         if (!m || !m->cwords || !m->row_off || !m->raw || !m->lut || !outs[i] || Ms[i] <= 0)
             return CK_ERR_ARG;
-        if (m->n_chunks != (int64_t)Ms[i] * (K / kSChunk)) return CK_ERR_ARG;
+        if (Ms[i] % GR != 0 || m->n_chunks * kSChunk != (int64_t)Ms[i] * K) return CK_ERR_ARG;
         if (((uintptr_t)m->raw & 15) != 0 || ((uintptr_t)m->lut & 15) != 0 ||
             ((uintptr_t)m->cwords & 15) != 0)
             return CK_ERR_ARG;
@@ -534,22 +557,30 @@ int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode
     // staging and the first loads again): each matrix gets blocks in
     // proportion to its rows, with 16 waves per block unless that leaves CUs
     // idle.
+    // (in row groups: a group of GR rows is one unit of work)
     int64_t m_sum = 0;
-    for (int i = 0; i < n; i++) m_sum += Ms[i];
+    for (int i = 0; i < n; i++) m_sum += Ms[i] / GR;
     const int cus = cbq_num_cus();
     const int64_t per = m_sum / cus;
     const int nw = per >= 16 ? 16 : per >= 8 ? 8 : 4;
     int blocks = 0;
     for (int i = 0; i < n; i++) {
         SplitSeg &g = segs.s[i];
+        const int Mg = g.M / GR;
         g.block0 = blocks;
-        const int share = (int)std::max<int64_t>(1, (cus * (int64_t)g.M + m_sum / 2) / m_sum);
-        g.nblocks = std::max(1, std::min(share, (g.M + nw - 1) / nw));
+        const int share = (int)std::max<int64_t>(1, (cus * (int64_t)Mg + m_sum / 2) / m_sum);
+        g.nblocks = std::max(1, std::min(share, (Mg + nw - 1) / nw));
         blocks += g.nblocks;
     }
-#define CBQ_SPLIT(NWV, MODE)                                                                      \
-    hipLaunchKernelGGL((split_gemv_kernel<NWV, MODE>), dim3(blocks), dim3(NWV * CBQ_WAVE), 0,     \
+#define CBQ_SPLIT_GR(NWV, MODE, G)                                                                \
+    hipLaunchKernelGGL((split_gemv_kernel<NWV, MODE, G>), dim3(blocks), dim3(NWV * CBQ_WAVE), 0,  \
                        stream, x, segs, K, x1, h_out, eps)
+#define CBQ_SPLIT(NWV, MODE)                                                                      \
+    do {                                                                                          \
+        if (GR == 1) CBQ_SPLIT_GR(NWV, MODE, 1);                                                  \
+        else if (GR == 2) CBQ_SPLIT_GR(NWV, MODE, 2);                                             \
+        else CBQ_SPLIT_GR(NWV, MODE, 4);                                                          \
+    } while (0)
 #define CBQ_SPLIT_MODES(NWV)                                                                      \
     do {                                                                                          \
         if (mode == XF_SILU) CBQ_SPLIT(NWV, XF_SILU);                                             \
@@ -562,6 +593,7 @@ int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode
     else CBQ_SPLIT_MODES(16);
 #undef CBQ_SPLIT_MODES
 #undef CBQ_SPLIT
+#undef CBQ_SPLIT_GR
     return cbq_launch_status("split_gemv_kernel");
 }
 

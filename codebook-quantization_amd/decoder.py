@@ -405,34 +405,38 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
     directly on torch's current stream.  With stack, each layer's q/k/v and
     gate/up run as one GEMV launch each instead of three / two: fixed-width
     rows are stacked into one matrix, Huffman matrices (one code each) share
-    a grouped launch.  With split, Huffman single-token GEMVs run on the
-    split format (built from each matrix's decoded stream) where it
-    applies, else on the column layout."""
+    a grouped launch.  With split, every Huffman linear whose shape and
+    codebook allow it is re-encoded into the split format (built from its
+    decoded stream) and keeps only that format: closures hold the split
+    format alone, so the caller may drop the HuffTensors' streams.  Others
+    keep their stream.  model.linear_bytes maps each launched matrix to its
+    device bytes."""
     import ctypes
     import cbq_native as nat
     import synthetic
-    from gpu_huffman_functions import (SymbolDecoder, build_columns, build_split,
-                                       columns_eligible, huffman_prefill, split_inverse,
+    from gpu_huffman_functions import (SymbolDecoder, build_split, huffman_prefill,
+                                       split_bytes, split_eligible, split_inverse,
                                        split_prefill)
     lib = nat.load()
     dev = torch.device(device)
-
-    syms = {}
+    resident: Dict[str, int] = {}               # device bytes of each matrix's format
 
     def sym_of(t):
-        """Symbol-payload decode tables of a tensor, built once at load (the
-        split format and the prompt path both decode the stream)."""
-        if t.name not in syms:
-            syms[t.name] = SymbolDecoder(t.words, t.chunk_off, t.sub_len, t.lengths, dev)
-        return syms[t.name]
+        """Symbol-payload decode tables of a stream (for the split build and
+        the stream path's batched tokens)."""
+        return SymbolDecoder(t.words, t.chunk_off, t.sub_len, t.lengths, dev)
 
     def huff_split(t):
+        """The split format of a Huffman tensor, or None when it does not
+        apply (then the stream stays the matrix's format)."""
         M, K = t.shape
-        if not split or K % 4096:
+        if not split or not split_eligible(M, K):
             return None
         idx = sym_of(t).indices(M * K)
         sp = build_split(idx, t.tables["codebook"].cpu().numpy(), dev)
         del idx
+        if sp is not None:
+            resident[t.name] = split_bytes(sp[0])
         return sp
 
     def split_fns(sps, Ms, K):
@@ -493,42 +497,41 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                               canon_pay=tb["pay"].data_ptr(), value_cb=None,
                               C=tb["codebook"].numel(), stage_words=tb["stage_words"])
 
-    def huff_linear(t, with_cols=True, sp_prompt=None):
-        """sp_prompt: the tensor's split format when a grouped launch owns
-        its one-token GEMV and this callable serves the multi-token calls."""
+    def split_linear(sp, M, K, cbt):
+        """A split-format matrix: one token on the split GEMV, batched tokens
+        through its transient fixed-width stream.  Captures only the split
+        format, so the tensor's stream can be freed."""
+        inv = split_inverse(cbt.cpu().numpy(), dev)
+        one, sxform = split_fns([sp], [M], K)
+
+        def f(x):
+            x = x.reshape(-1, K).contiguous()
+            if x.shape[0] == 1:
+                return one(x)
+            return split_prefill(sp, inv, x, M, K, cbt)
+        f.xform = sxform
+        f.split = sp
+        return f
+
+    def huff_linear(t):
+        """One Huffman matrix: the split format where it applies, else the
+        stream (every token count on the fused stream kernels; batched
+        tokens >= 64 through a transient fixed-width stream)."""
         M, K = t.shape
-        desc = huff_desc(t)
-        cols = None
-        sp = huff_split(t) if with_cols else None
-        sp_p = sp if sp is not None else sp_prompt
-        inv = split_inverse(t.tables["codebook"].cpu().numpy(), dev) if sp_p is not None else None
+        cbt = t.tables["codebook"]
+        sp = huff_split(t)
         if sp is not None:
-            one, sxform = split_fns([sp], [M], K)
-        elif with_cols and columns_eligible(desc, K):   # single-token GEMV on the column layout
-            cols = build_columns(desc, M * K, dev, t.lengths, t.tables["codebook"].cpu().numpy())
+            return split_linear(sp, M, K, cbt)
+        resident[t.name] = t.nbytes
+        desc = huff_desc(t)
 
-        sym = sym_of(t)
-
-        def f(x, desc=desc, cols=cols):
+        def f(x, desc=desc, keep=(t.words, t.chunk_off, t.sub_len, t.tables, t.lengths)):
             x = x.reshape(-1, K).contiguous()
             T = x.shape[0]
-            if T == 1 and sp is not None:
-                return one(x)
-            if T >= 64:                      # prompt: transient packed stream + matrix cores
-                y = None
-                if sp_p is not None:
-                    y = split_prefill(sp_p, inv, x, M, K, t.tables["codebook"])
-                if y is None:
-                    y = huffman_prefill(sym, x, M, K, t.tables["codebook"])
-                if y is not None:
-                    return y
+            if T >= 64:
+                return huffman_prefill(SymbolDecoder(keep[0], keep[1], keep[2], keep[4], dev),
+                                       x, M, K, cbt)
             out = torch.empty(T, M, device=dev)
-            if T == 1 and cols is not None:
-                nat.check(lib.cbq_huff_linear_col_f32(x.data_ptr(), ctypes.byref(desc),
-                                                      ctypes.byref(cols[1]), out.data_ptr(), M, K,
-                                                      nat.stream_ptr(dev)),
-                          "cbq_huff_linear_col_f32")
-                return out
             for t0 in range(0, T, 16):
                 tt = min(16, T - t0)
                 nat.check(lib.cbq_huff_linear_f32(x.data_ptr() + t0 * K * 4, ctypes.byref(desc),
@@ -536,93 +539,31 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                                                   nat.stream_ptr(dev)), "cbq_huff_linear_f32")
             return out
         f.desc = desc
-        if sp is not None:
-            f.xform = sxform
-            f.split = sp
-        elif cols is not None and cols[1].ulut1:
-            hs1 = (ctypes.POINTER(nat.HuffStream) * 1)(ctypes.pointer(desc))
-            col1 = (ctypes.POINTER(nat.HuffColumns) * 1)(ctypes.pointer(cols[1]))
-            m1 = (ctypes.c_int * 1)(M)
-
-            def xform(x0, x1, h_out, mode, keep=(hs1, col1, m1)):
-                """One token, x = transform(x0, x1) staged by the GEMV."""
-                out = torch.empty(1, M, device=dev)
-                nat.check(lib.cbq_huff_linear_col_xform_f32(
-                    x0.data_ptr(), None if x1 is None else x1.data_ptr(),
-                    None if h_out is None else h_out.data_ptr(), mode, cfg.eps, 1, hs1, col1,
-                    (ctypes.c_void_p * 1)(out.data_ptr()), m1, K, nat.stream_ptr(dev)),
-                    "cbq_huff_linear_col_xform_f32")
-                return out
-            f.xform = xform
         return f
 
     def huff_group(ts, name):
-        """One grouped column-GEMV launch for matrices sharing x (q/k/v,
-        gate/up), each with its own code; None when a part does not
-        qualify for the column layout."""
+        """One grouped split-GEMV launch for matrices sharing x (q/k/v,
+        gate/up), each with its own code; None when a part has no split
+        format (the parts then run one by one)."""
         K = ts[0].shape[1]
-        if any(t.shape[1] != K for t in ts):
+        if any(t.shape[1] != K for t in ts) or not split:
             return None
         sps = [huff_split(t) for t in ts]
-        if all(sp is not None for sp in sps):
-            Ms = [t.shape[0] for t in ts]
-            one, sxform = split_fns(sps, Ms, K)
-            singles = [huff_linear(t, with_cols=False, sp_prompt=sp)      # multi-token calls
-                       for t, sp in zip(ts, sps)]
-
-            def g(x):
-                x = x.reshape(-1, K).contiguous()
-                if x.shape[0] > 1:
-                    return torch.cat([h(x) for h in singles], dim=1)
-                return one(x)
-            g.xform = sxform
-            g.name = name
-            return g
-        descs = [huff_desc(t) for t in ts]
-        if not all(columns_eligible(d, K) for d in descs):
+        if not all(sp is not None for sp in sps):
             return None
-        cols = [build_columns(d, t.shape[0] * K, dev, t.lengths, t.tables["codebook"].cpu().numpy())
-                for d, t in zip(descs, ts)]
         Ms = [t.shape[0] for t in ts]
-        n = len(ts)
-        hs_arr = (ctypes.POINTER(nat.HuffStream) * n)(*[ctypes.pointer(d) for d in descs])
-        col_arr = (ctypes.POINTER(nat.HuffColumns) * n)(*[ctypes.pointer(c[1]) for c in cols])
-        m_arr = (ctypes.c_int * n)(*Ms)
-        singles = [huff_linear(t, with_cols=False) for t in ts]   # multi-token calls, per part
+        one, sxform = split_fns(sps, Ms, K)
+        singles = [split_linear(sp, t.shape[0], K, t.tables["codebook"])   # batched tokens
+                   for t, sp in zip(ts, sps)]
 
-        def f(x, keep=(descs, cols, hs_arr, col_arr, m_arr)):
+        def g(x):
             x = x.reshape(-1, K).contiguous()
-            T = x.shape[0]
-            if T > 1:
-                return torch.cat([g(x) for g in singles], dim=1)
-            out = torch.empty(1, sum(Ms), device=dev)
-            offs, o = [], 0
-            for M in Ms:
-                offs.append(out.data_ptr() + 4 * o)
-                o += M
-            out_arr = (ctypes.c_void_p * n)(*offs)
-            nat.check(lib.cbq_huff_linear_col_multi_f32(
-                x.data_ptr(), n, hs_arr, col_arr, out_arr, m_arr, K, nat.stream_ptr(dev)),
-                "cbq_huff_linear_col_multi_f32")
-            return out
-
-        def xform(x0, x1, h_out, mode, keep=(descs, cols, hs_arr, col_arr, m_arr)):
-            """One token, x = transform(x0, x1) staged by the grouped GEMV."""
-            out = torch.empty(1, sum(Ms), device=dev)
-            offs, o = [], 0
-            for M in Ms:
-                offs.append(out.data_ptr() + 4 * o)
-                o += M
-            nat.check(lib.cbq_huff_linear_col_xform_f32(
-                x0.data_ptr(), None if x1 is None else x1.data_ptr(),
-                None if h_out is None else h_out.data_ptr(), mode, cfg.eps, n, hs_arr, col_arr,
-                (ctypes.c_void_p * n)(*offs), m_arr, K, nat.stream_ptr(dev)),
-                "cbq_huff_linear_col_xform_f32")
-            return out
-        f.name = name
-        if all(c[1].ulut1 for c in cols):
-            f.xform = xform
-        return f
+            if x.shape[0] > 1:
+                return torch.cat([h(x) for h in singles], dim=1)
+            return one(x)
+        g.xform = sxform
+        g.name = name
+        return g
 
     def embed_fn(t):
         V, H = t.shape
@@ -661,6 +602,7 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                 st = synthetic.stack_fixed(ts, p + fused)
                 if st is not None:
                     linears[p + fused] = fixed_linear(st)
+                    resident[p + fused] = st.nbytes
             elif all(isinstance(t, synthetic.HuffTensor) for t in ts):
                 g = huff_group(ts, p + fused)
                 if g is not None:
@@ -672,6 +614,15 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                  "gate_proj": "gate_up_proj", "up_proj": "gate_up_proj"}.get(leaf)
         if fused is not None and f"{stem}.{fused}" in linears:
             continue
-        linears[n] = huff_linear(t) if isinstance(t, synthetic.HuffTensor) else fixed_linear(t)
-    return Qwen3Decoder(cfg, linears, embed_fn(tensors["model.embed_tokens"]), dev, max_len,
-                        fuse_glue=fuse_glue)
+        if isinstance(t, synthetic.HuffTensor):
+            linears[n] = huff_linear(t)
+        else:
+            linears[n] = fixed_linear(t)
+            resident[n] = t.nbytes
+    emb = tensors["model.embed_tokens"]
+    model = Qwen3Decoder(cfg, linears, embed_fn(emb), dev, max_len, fuse_glue=fuse_glue)
+    # device bytes of every linear's format (what a decode step streams) and
+    # of the embedding (read one row per token)
+    model.linear_bytes = dict(resident)
+    model.embed_bytes = int(emb.nbytes)
+    return model

@@ -11,15 +11,17 @@ Same classes and constructor signatures as the reference
 plus two optional keys written by this package's encoder,
 `huff_chunk_offsets` and `huff_sub_lens`.  Where the reference decodes every
 row into a transient int32 [M*K] buffer and then runs a GEMV (and decodes the
-whole vocabulary for each embedding call), this backend keeps only the
-stream in HBM and decodes it chunk-parallel straight into the dot product or
-into the requested embedding rows.
+whole vocabulary for each embedding call), this backend keeps one compressed
+format per matrix in HBM and decodes it chunk-parallel straight into the dot
+product (one token) or into the requested embedding rows.
 
 At construction the reference stream is turned into the device format: bytes
 bit-reversed into LSB-first words, decode tables rebuilt from `huff_lengths`
 (the reference's huff_lut_* / huff_sl_* arrays are derived from the same
 lengths and are not needed), and - when the chunk index is absent - one host
-pass over the stream (split at `huff_row_bit_starts`) computes it.
+pass over the stream (split at `huff_row_bit_starts`) computes it.  A linear
+whose codebook allows it is then re-encoded on the device into the split
+format and the stream is freed (HuffmanCodebookLinear's `layout`).
 """
 from __future__ import annotations
 
@@ -126,15 +128,17 @@ def build_columns(desc: "nat.HuffStream", n_sym: int, device, lengths=None,
     return keep, cols
 
 
-def build_split(indices: torch.Tensor, codebook: np.ndarray, device):
+def build_split(indices: torch.Tensor, codebook: np.ndarray, device, counts=None):
     """Split format (struct cbq_split_matrix) of decoded symbols
     (int32 [n], n % 4096 == 0), built on the device; None when a codebook
     value is not bf16 or the exponents need codes longer than 7 bits.
-    Returns the device tensors to keep alive and the descriptor."""
+    counts: the symbols' histogram when the caller has it.  Returns the
+    device tensors to keep alive and the descriptor."""
     n = int(indices.numel())
     if n == 0 or n % hc.CHUNK_SYMBOLS:
         return None
-    counts = torch.bincount(indices.reshape(-1).clamp_min(0).to(torch.int64)).cpu().numpy()
+    if counts is None:
+        counts = torch.bincount(indices.reshape(-1).clamp_min(0).to(torch.int64)).cpu().numpy()
     t = hc.split_tables(codebook, counts)
     if t is None:
         return None
@@ -168,6 +172,24 @@ def build_split(indices: torch.Tensor, codebook: np.ndarray, device):
 def split_bytes(keep) -> int:
     """Bytes the split GEMV streams: column words, row offsets, raw bytes, table."""
     return sum(int(t.numel() * t.element_size()) for t in keep)
+
+
+def split_eligible(M: int, K: int) -> bool:
+    """Shapes the split GEMV serves: K % 1024 == 0 and whole 4096-symbol
+    chunks (cbq_split_linear_f32)."""
+    return M > 0 and K > 0 and K % 1024 == 0 and (M * K) % hc.CHUNK_SYMBOLS == 0
+
+
+def index_exact(codebook: np.ndarray, counts: np.ndarray) -> bool:
+    """True when the split format's values name their indices uniquely: every
+    symbol that occurs is < C and the codebook's bf16 values are distinct, so
+    decoding through split_inverse returns the stored indices exactly."""
+    cb = np.ascontiguousarray(codebook, np.float32).reshape(-1)
+    counts = np.asarray(counts).reshape(-1)
+    if counts.size > cb.size and counts[cb.size:].any():
+        return False
+    pats = cb.view(np.uint32) >> 16
+    return np.unique(pats).size == pats.size
 
 
 class SymbolDecoder:
@@ -209,36 +231,6 @@ def decode_symbols(words: torch.Tensor, chunk_off: torch.Tensor, sub_len: torch.
     return out
 
 
-def huffman_prefill(sym: SymbolDecoder, x: torch.Tensor, M: int, K: int,
-                    codebook: torch.Tensor) -> Optional[torch.Tensor]:
-    """y [T, M] for T >= 64 fp32 tokens: the stream is decoded to transient
-    fixed-width indices (cbq_huff_decode_indices, cbq_pack_indices) and
-    multiplied on the fp32 matrix cores (cbq_linear_f32_ws).  None when the
-    alphabet needs more than 13 bits or K % 32 != 0."""
-    T = x.shape[0]
-    C = int(codebook.numel())
-    bits = max(8, int(np.ceil(np.log2(max(sym.n_sym, C, 2)))))
-    bits = 10 if bits == 9 else bits
-    if bits > 13 or K % 32 or (M * K) % 32:
-        return None
-    lib = nat.load()
-    dev = sym.device
-    st = nat.stream_ptr(dev)
-    idx = sym.indices(M * K)
-    packed = torch.empty(M * K * bits // 8 + 16, dtype=torch.uint8, device=dev)
-    nat.check(lib.cbq_pack_indices(idx.data_ptr(), M * K, bits, packed.data_ptr(), st),
-              "cbq_pack_indices")
-    del idx
-    out = torch.empty(T, M, dtype=torch.float32, device=dev)
-    nws = int(lib.cbq_linear_f32_workspace(T, M, K))
-    ws = torch.empty(max(1, nws // 4), dtype=torch.float32, device=dev) if nws else None
-    nat.check(lib.cbq_linear_f32_ws(x.data_ptr(), packed.data_ptr(), codebook.data_ptr(),
-                                    out.data_ptr(), T, M, K, C, bits,
-                                    None if ws is None else ws.data_ptr(), nws, st),
-              "cbq_linear_f32_ws")
-    return out
-
-
 def prefill_bits(C: int) -> int:
     """Index width of the transient fixed-width stream (8, 10..13; 9 packs
     as 10), or 0 when C needs more than 13 bits."""
@@ -247,41 +239,102 @@ def prefill_bits(C: int) -> int:
     return bits if bits <= 13 else 0
 
 
+_INVERSE: dict = {}
+
+
 def split_inverse(codebook: np.ndarray, device) -> torch.Tensor:
     """uint16 [65536]: bf16 bit pattern -> an index of the codebook holding
     that value (the split format stores bf16 values; any index of an equal
-    value gives the same product)."""
+    value gives the same product).  One device copy per (device, codebook),
+    shared by every matrix of that codebook."""
     cb = np.ascontiguousarray(codebook, np.float32).reshape(-1)
+    key = (str(torch.device(device)), cb.size, hash(cb.tobytes()))
+    hit = _INVERSE.get(key)
+    if hit is not None and np.array_equal(hit[0], cb):
+        return hit[1]
     pats = (cb.view(np.uint32) >> 16).astype(np.int64)
     inv = np.zeros(1 << 16, np.uint16)
     inv[pats[::-1]] = np.arange(len(cb), dtype=np.uint16)[::-1]     # first index wins
-    return torch.from_numpy(inv.view(np.int16)).to(device)
+    t = torch.from_numpy(inv.view(np.int16)).to(device)
+    _INVERSE[key] = (cb.copy(), t)
+    return t
 
 
-def split_prefill(split, inv: torch.Tensor, x: torch.Tensor, M: int, K: int,
-                  codebook: torch.Tensor) -> Optional[torch.Tensor]:
-    """y [T, M] for T >= 64 fp32 tokens from the split format: decoded straight
-    to a transient fixed-width stream (cbq_split_to_packed, one table read per
-    two weights) and multiplied on the fp32 matrix cores (cbq_linear_f32_ws).
-    None when the codebook needs more than 13 bits."""
-    T = x.shape[0]
-    C = int(codebook.numel())
-    bits = prefill_bits(C)
-    if not bits or K % 32 or (M * K) % 32:
-        return None
+
+
+def _packed_for_gemm(idx_or_split, n: int, C: int, dev, inv: Optional[torch.Tensor] = None):
+    """(packed uint8 stream, bits) of n indices for ck_linear_f32: the
+    LSB-first fixed-width stream (8, 10..13 bits; 16 bits = little-endian
+    uint16 when C needs more), with the zero padding the GEMV's wide reads
+    need.  idx_or_split: int32 indices on the device, or a split-format
+    descriptor pair decoded through inv (cbq_split_to_packed)."""
+    lib = nat.load()
+    st = nat.stream_ptr(dev)
+    bits = prefill_bits(C) or 16
+    nb = (n * bits + 7) // 8
+    packed = torch.zeros(((nb + 15) // 16) * 16 + 16, dtype=torch.uint8, device=dev)
+    if inv is not None:
+        nat.check(lib.cbq_split_to_packed(ctypes.byref(idx_or_split[1]), inv.data_ptr(), bits,
+                                          packed.data_ptr(), st), "cbq_split_to_packed")
+        return packed, bits
+    idx = idx_or_split
+    if bits == 16:
+        packed[:2 * n] = idx.clamp(0, 0xFFFF).to(torch.int32).to(torch.int16).view(torch.uint8)
+        return packed, bits
+    n32 = (n + 31) // 32 * 32
+    if n32 != n:                                   # whole 32-index groups for the packer
+        idx = torch.cat([idx, idx.new_zeros(n32 - n)])
+    nat.check(lib.cbq_pack_indices(idx.data_ptr(), n32, bits, packed.data_ptr(), st),
+              "cbq_pack_indices")
+    return packed, bits
+
+
+def linear_from_packed(x: torch.Tensor, packed: torch.Tensor, bits: int, M: int, K: int,
+                       codebook: torch.Tensor) -> torch.Tensor:
+    """y [T, M] = x [T, K] (fp32) @ W^T over a transient packed index stream:
+    ck_linear_f32's kernels for every T (the fp32 matrix cores for T >= 64,
+    with split K in a torch workspace)."""
     lib = nat.load()
     dev = x.device
-    st = nat.stream_ptr(dev)
-    packed = torch.empty(M * K * bits // 8 + 16, dtype=torch.uint8, device=dev)
-    nat.check(lib.cbq_split_to_packed(ctypes.byref(split[1]), inv.data_ptr(), bits,
-                                      packed.data_ptr(), st), "cbq_split_to_packed")
+    T = x.shape[0]
+    C = int(codebook.numel())
     out = torch.empty(T, M, dtype=torch.float32, device=dev)
-    nws = int(lib.cbq_linear_f32_workspace(T, M, K))
+    nws = int(lib.cbq_linear_f32_workspace(T, M, K)) if T >= 64 else 0
     ws = torch.empty(max(1, nws // 4), dtype=torch.float32, device=dev) if nws else None
     nat.check(lib.cbq_linear_f32_ws(x.data_ptr(), packed.data_ptr(), codebook.data_ptr(),
                                     out.data_ptr(), T, M, K, C, bits,
-                                    None if ws is None else ws.data_ptr(), nws, st),
-              "cbq_linear_f32_ws")
+                                    None if ws is None else ws.data_ptr(), nws,
+                                    nat.stream_ptr(dev)), "cbq_linear_f32_ws")
+    return out
+
+
+def huffman_prefill(sym: "SymbolDecoder", x: torch.Tensor, M: int, K: int,
+                    codebook: torch.Tensor) -> torch.Tensor:
+    """y [T, M] for batched fp32 tokens from the stream: decoded to transient
+    fixed-width indices (cbq_huff_decode_indices, cbq_pack_indices) and
+    multiplied by ck_linear_f32's kernels."""
+    idx = sym.indices(M * K)
+    packed, bits = _packed_for_gemm(idx, M * K, int(codebook.numel()), x.device)
+    del idx
+    return linear_from_packed(x, packed, bits, M, K, codebook)
+
+
+def split_prefill(split, inv: torch.Tensor, x: torch.Tensor, M: int, K: int,
+                  codebook: torch.Tensor) -> torch.Tensor:
+    """y [T, M] for batched fp32 tokens from the split format: decoded
+    straight to a transient fixed-width stream (cbq_split_to_packed, one
+    table read per two weights) and multiplied by ck_linear_f32's kernels."""
+    packed, bits = _packed_for_gemm(split, M * K, int(codebook.numel()), x.device, inv)
+    return linear_from_packed(x, packed, bits, M, K, codebook)
+
+
+def split_indices(split, inv: torch.Tensor, n: int, device) -> torch.Tensor:
+    """int32 [n] codebook indices of a split-format matrix (exact when
+    index_exact held at build time)."""
+    out = torch.empty(n, dtype=torch.int32, device=device)
+    nat.check(nat.load().cbq_split_to_packed(ctypes.byref(split[1]), inv.data_ptr(), 32,
+                                             out.data_ptr(), nat.stream_ptr(device)),
+              "cbq_split_to_packed")
     return out
 
 
@@ -298,7 +351,25 @@ def _cb_numpy(codebook) -> np.ndarray:
 
 
 class HuffmanCodebookLinear:
-    """y = x @ W^T with W Huffman-coded in HBM; decode fused into the GEMV."""
+    """y = x @ W^T with W Huffman-coded in HBM.
+
+    One device format per matrix (`layout`):
+
+    - "split" (the default wherever it applies: a bf16 codebook with distinct
+      values, every symbol < C, K % 1024 == 0, whole 4096-symbol chunks): the
+      split format alone, ~11.5 bits per weight, built on the device from the
+      stream, after which the stream is freed.  One token runs the split
+      GEMV; batched tokens decode it to a transient fixed-width stream for
+      ck_linear_f32's kernels; decode_indices() maps the values back to their
+      indices.
+    - "stream": the reference stream in device words plus its chunk index
+      (~10.8 bits per weight).  Every call runs the fused stream kernels
+      (cbq_huff_linear_f32); T >= 64, and every T when K % 64 != 0, decode
+      to a transient fixed-width stream for ck_linear_f32.
+    - "columns": the stream plus its column layout (two formats resident),
+      for comparing the column GEMV; one token runs cbq_huff_linear_col_f32.
+
+    layout="auto" picks "split" when it applies, else "stream"."""
 
     def __init__(self, name: str, huff_stream, huff_lengths, huff_n: int,
                  codebook, shape, bits: int,
@@ -310,48 +381,66 @@ class HuffmanCodebookLinear:
                  huff_sl_sym: Optional[np.ndarray] = None,
                  huff_chunk_offsets: Optional[np.ndarray] = None,
                  huff_sub_lens: Optional[np.ndarray] = None,
-                 split_format: bool = True):
+                 layout: str = "auto"):
         if not torch.cuda.is_available():
             raise RuntimeError("the compressed GPU path needs a ROCm GPU (none visible)")
+        if layout not in ("auto", "split", "stream", "columns"):
+            raise ValueError(f"{name}: unknown layout {layout!r}")
         self.name = name
         self.shape = tuple(int(s) for s in shape)
         self.M, self.K = self.shape
         self.bits = int(bits)
-        if self.K % hc.SUB_SYMBOLS:
-            raise ValueError(f"{name}: in_features {self.K} must be a multiple of "
-                             f"{hc.SUB_SYMBOLS}")
         self._lib = nat.load()
         device = codebook.device if isinstance(codebook, torch.Tensor) and codebook.is_cuda \
             else torch.device("cuda")
-        self._cb_np = _cb_numpy(codebook)
-        self._src = (huff_stream, huff_lengths, int(huff_n), huff_row_bit_starts)
-        self.dev = _DeviceStream(name, huff_stream, huff_lengths, huff_n, self._cb_np,
-                                 self.shape, huff_row_bit_starts, huff_chunk_offsets,
-                                 huff_sub_lens, device)
         self.device = device
-        self._idx_dev = None
-        self._sym = None                  # symbol tables (split format, batched tokens)
+        self._cb_np = _cb_numpy(codebook)
         self._cb_dev = torch.from_numpy(self._cb_np).to(device)
-        # single-token GEMVs read the split format when the codebook
-        # is bf16-exact, else the column layout when the shape allows
-        self.cols = None
+        self._lengths = np.ascontiguousarray(huff_lengths, np.uint8)
+        dev = _DeviceStream(name, huff_stream, huff_lengths, huff_n, self._cb_np,
+                            self.shape, huff_row_bit_starts, huff_chunk_offsets,
+                            huff_sub_lens, device)
         self.split = None
+        self.cols = None
         self._inv = None
-        if split_format and self.K % hc.CHUNK_SYMBOLS == 0:
-            self._sym = SymbolDecoder(self.dev.words, self.dev.chunk_off, self.dev.sub_len,
-                                      np.asarray(huff_lengths, np.uint8), device)
-            idx = self._sym.indices(self.M * self.K)
-            self.split = build_split(idx, self._cb_np, device)
+        if layout in ("auto", "split") and split_eligible(self.M, self.K):
+            idx = SymbolDecoder(dev.words, dev.chunk_off, dev.sub_len, self._lengths,
+                                device).indices(self.M * self.K)
+            counts = torch.bincount(idx.clamp_min(0).to(torch.int64)).cpu().numpy()
+            if index_exact(self._cb_np, counts):
+                self.split = build_split(idx, self._cb_np, device, counts=counts)
             del idx
-        if self.split is None and columns_eligible(self.dev.desc, self.K):
-            self._col_keep, self.cols = build_columns(
-                self.dev.desc, self.M * self.K, device, np.asarray(huff_lengths, np.uint8),
-                self._cb_np)
-            self._cwords, self._row_off = self._col_keep[0], self._col_keep[1]
+        if layout == "split" and self.split is None:
+            raise ValueError(f"{name}: the split format does not apply to this matrix")
+        if self.split is not None:
+            self.dev = None                       # one resident format: the stream is freed
+            self._inv = split_inverse(self._cb_np, device)
+        else:
+            self.dev = dev
+            if self.K % hc.SUB_SYMBOLS == 0 and layout == "columns":
+                if not columns_eligible(dev.desc, self.K):
+                    raise ValueError(f"{name}: the column layout does not apply")
+                self._col_keep, self.cols = build_columns(dev.desc, self.M * self.K, device,
+                                                          self._lengths, self._cb_np)
+                self._cwords, self._row_off = self._col_keep[0], self._col_keep[1]
+
+    @property
+    def resident_bytes(self) -> int:
+        """Device bytes of the matrix's format(s), tables included."""
+        if self.split is not None:
+            return split_bytes(self.split[0])
+        n = self.dev.stream_bytes + self.dev.table_bytes
+        if self.cols is not None:
+            n += split_bytes(self._col_keep)
+        return n
 
     @property
     def compressed_bytes(self) -> int:
-        return self.dev.stream_bytes + self.dev.table_bytes
+        return self.resident_bytes
+
+    def _symbols(self) -> "SymbolDecoder":
+        return SymbolDecoder(self.dev.words, self.dev.chunk_off, self.dev.sub_len,
+                             self._lengths, self.device)
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         in_dtype = x.dtype
@@ -361,54 +450,44 @@ class HuffmanCodebookLinear:
             raise ValueError(f"{self.name}: expected last dim {self.K}, got {x.shape[-1]}")
         T = int(x.numel() // self.K)
         xc = x.reshape(T, self.K).to(torch.float32).contiguous()
-        out = torch.empty(T, self.M, dtype=torch.float32, device=self.device)
         st = nat.stream_ptr(self.device)
-        if T >= 64 and self.split is not None:
-            if self._inv is None:
-                self._inv = split_inverse(self._cb_np, self.device)
-            y = split_prefill(self.split, self._inv, xc, self.M, self.K, self._cb_dev)
-            if y is not None:
-                out = y.reshape(*lead, self.M)
-                return out if in_dtype == torch.float32 else out.to(in_dtype)
-        if T >= 64:
-            if self._sym is None:
-                self._sym = SymbolDecoder(self.dev.words, self.dev.chunk_off, self.dev.sub_len,
-                                          np.asarray(self._src[1], np.uint8), self.device)
-            y = huffman_prefill(self._sym, xc, self.M, self.K, self._cb_dev)
-            if y is not None:
-                out = y.reshape(*lead, self.M)
-                return out if in_dtype == torch.float32 else out.to(in_dtype)
-        if T == 1 and self.split is not None:
+        if T == 0:
+            out = torch.empty(0, self.M, dtype=torch.float32, device=self.device)
+        elif self.split is not None and T == 1:
+            out = torch.empty(1, self.M, dtype=torch.float32, device=self.device)
             nat.check(self._lib.cbq_split_linear_f32(
                 xc.data_ptr(), None, None, 0, 0.0, 1,
                 (ctypes.POINTER(nat.SplitMatrix) * 1)(ctypes.pointer(self.split[1])),
                 (ctypes.c_void_p * 1)(out.data_ptr()), (ctypes.c_int * 1)(self.M), self.K, st),
                 "cbq_split_linear_f32")
-            T = 0
+        elif self.split is not None:
+            out = split_prefill(self.split, self._inv, xc, self.M, self.K, self._cb_dev)
+        elif T >= 64 or self.K % hc.SUB_SYMBOLS:
+            out = huffman_prefill(self._symbols(), xc, self.M, self.K, self._cb_dev)
         elif T == 1 and self.cols is not None:
+            out = torch.empty(1, self.M, dtype=torch.float32, device=self.device)
             nat.check(self._lib.cbq_huff_linear_col_f32(
                 xc.data_ptr(), ctypes.byref(self.dev.desc), ctypes.byref(self.cols),
                 out.data_ptr(), self.M, self.K, st), "cbq_huff_linear_col_f32")
-            T = 0
-        for t0 in range(0, T, 16):
-            tt = min(16, T - t0)
-            rc = self._lib.cbq_huff_linear_f32(
-                xc.data_ptr() + t0 * self.K * 4, ctypes.byref(self.dev.desc),
-                out.data_ptr() + t0 * self.M * 4, tt, self.M, self.K, st)
-            nat.check(rc, "cbq_huff_linear_f32")
+        else:
+            out = torch.empty(T, self.M, dtype=torch.float32, device=self.device)
+            for t0 in range(0, T, 16):
+                tt = min(16, T - t0)
+                rc = self._lib.cbq_huff_linear_f32(
+                    xc.data_ptr() + t0 * self.K * 4, ctypes.byref(self.dev.desc),
+                    out.data_ptr() + t0 * self.M * 4, tt, self.M, self.K, st)
+                nat.check(rc, "cbq_huff_linear_f32")
         out = out.reshape(*lead, self.M)
         return out if in_dtype == torch.float32 else out.to(in_dtype)
 
     def decode_indices(self) -> torch.Tensor:
-        """All M*K decoded symbols (int32, unclamped) with the chunked kernel."""
-        if self._idx_dev is None:
-            s, l, n, rbs = self._src
-            self._idx_dev = _DeviceStream(self.name, s, l, n, self._cb_np, self.shape, rbs,
-                                          None, None, self.device, raw_symbols=True)
-        out = torch.empty(self.M * self.K, dtype=torch.int32, device=self.device)
-        rc = self._lib.cbq_huff_decode_indices(ctypes.byref(self._idx_dev.desc), out.data_ptr(),
-                                               self.M * self.K, nat.stream_ptr(self.device))
-        nat.check(rc, "cbq_huff_decode_indices")
+        """All M*K decoded symbols (int32, unclamped): from the split format
+        through the inverse table, or from the stream with the chunked
+        decoder; bit-exact either way."""
+        if self.split is not None:
+            out = split_indices(self.split, self._inv, self.M * self.K, self.device)
+        else:
+            out = self._symbols().indices(self.M * self.K)
         return out.reshape(self.M, self.K)
 
 
@@ -431,22 +510,30 @@ class HuffmanCodebookEmbedding:
         self.shape = tuple(int(s) for s in shape)
         self.vocab, self.hidden = self.shape
         self.bits = int(bits)
-        if self.hidden % hc.SUB_SYMBOLS:
-            raise ValueError(f"{name}: hidden {self.hidden} must be a multiple of "
-                             f"{hc.SUB_SYMBOLS}")
         self._lib = nat.load()
         device = codebook.device if isinstance(codebook, torch.Tensor) and codebook.is_cuda \
             else torch.device("cuda")
-        self.dev = _DeviceStream(name, huff_stream, huff_lengths, huff_n, _cb_numpy(codebook),
+        cb = _cb_numpy(codebook)
+        self.dev = _DeviceStream(name, huff_stream, huff_lengths, huff_n, cb,
                                  self.shape, huff_row_bit_starts, huff_chunk_offsets,
                                  huff_sub_lens, device)
         self.device = device
+        self._lengths = np.ascontiguousarray(huff_lengths, np.uint8)
+        self._cb_dev = torch.from_numpy(cb).to(device)
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         ids = x.to(self.device).reshape(-1).to(torch.int32).contiguous()
         T = int(ids.numel())
         out = torch.empty(T, self.hidden, dtype=torch.float32, device=self.device)
-        if T:
+        if T and self.hidden % hc.SUB_SYMBOLS:
+            # rows that do not start on a 64-symbol sub-block: decode the
+            # whole table (as the reference does per call) and gather
+            idx = SymbolDecoder(self.dev.words, self.dev.chunk_off, self.dev.sub_len,
+                                self._lengths, self.device).indices(self.vocab * self.hidden)
+            rows = ids.to(torch.int64).clamp(0, self.vocab - 1)
+            sym = idx.view(self.vocab, self.hidden)[rows].to(torch.int64)
+            out = self._cb_dev[sym.clamp(0, self._cb_dev.numel() - 1)]
+        elif T:
             rc = self._lib.cbq_huff_embedding_f32(ids.data_ptr(), ctypes.byref(self.dev.desc),
                                                   out.data_ptr(), T, self.vocab, self.hidden,
                                                   nat.stream_ptr(self.device))

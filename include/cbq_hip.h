@@ -322,9 +322,12 @@ int cbq_split_pack(const int32_t *indices, int64_t n_symbols, const uint32_t *sy
                    uint8_t *raw, hipStream_t stream);
 
 /* y_i[M_i] = W_i @ x for up to four split-format matrices sharing x (T = 1,
- * K % 4096 == 0), with x = transform(x0, x1) as cbq_linear_xform_f32 (mode
- * 0: x0 itself).  Outputs equal cbq_huff_linear_col_f32's on the same
- * weights bit for bit. */
+ * K % 1024 == 0, M_i * K % 4096 == 0), with x = transform(x0, x1) as
+ * cbq_linear_xform_f32 (mode 0: x0 itself).  With K % 4096 == 0 the outputs
+ * equal cbq_huff_linear_col_f32's on the same weights bit for bit; other K
+ * walk groups of 4096 / gcd(K, 4096) rows (whole chunks).  Replaces the
+ * T = 1 decode + GEMV of HuffmanCodebookLinear.__call__
+ * (src/gpu_huffman_functions.py:834-855). */
 int cbq_split_linear_f32(const float *x0, const float *x1, float *h_out, int mode, float eps, int n,
                          const cbq_split_matrix *const *mats, float *const *outs, const int *Ms,
                          int K, hipStream_t stream);
@@ -347,12 +350,15 @@ int cbq_pack_indices(const int32_t *indices, int64_t n, int bits, uint8_t *packe
 
 /* Decodes a split-format matrix (cbq_split_matrix, n_chunks chunks of 4096
  * weights) straight to the LSB-first fixed-width stream of its codebook
- * indices, bits in {8, 10, 11, 12, 13}: inv maps every bf16 bit pattern of
- * the codebook to an index holding that value (65536 uint16 entries);
- * packed (4-byte aligned) receives n_chunks * 4096 * bits / 8 bytes.  No
- * counterpart in the reference: the batched-token path of a Huffman module
- * whose split format exists (one table read per two weights instead of the
- * stream decode to int32 and cbq_pack_indices). */
+ * indices, bits in {8, 10, 11, 12, 13, 16, 32} (16: little-endian uint16,
+ * 32: int32 indices): inv maps every bf16 bit pattern of the codebook to an
+ * index holding that value (65536 uint16 entries); packed (4-byte aligned)
+ * receives n_chunks * 4096 * bits / 8 bytes.  No counterpart in the
+ * reference: the batched-token path of a Huffman module whose split format
+ * exists (one table read per two weights instead of the stream decode to
+ * int32 and cbq_pack_indices), and, with bits = 32, its index decode
+ * (huffman_decode_to_weights_f32 with an identity codebook,
+ * src/compressed_matmul.c:296-322) when the codebook's values are distinct. */
 int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits,
                         uint8_t *packed, hipStream_t stream);
 

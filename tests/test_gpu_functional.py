@@ -62,3 +62,40 @@ def test_huffman_functions(cuda, oracle, C_cut):
     assert np.array_equal(wd, oracle.huff_decode_weights(enc, cb, M, K, C=C_cut))
     if C_cut is None:
         assert np.array_equal(wd, w)
+
+
+@pytest.mark.parametrize("M,K", [(16, 32), (7, 100), (40, 1536)])
+def test_huffman_functions_any_k(cuda, oracle, M, K):
+    """Shapes whose rows are not whole 64-symbol sub-blocks (the reference
+    decodes a 16 x 32 tensor in tests/test_compressed_roundtrip.py:747-756):
+    the flat stream is decoded to transient indices, then gathered (decode,
+    embedding) or multiplied by ck_linear_f32's kernels."""
+    rng = np.random.default_rng(M * K)
+    w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
+    cb, idx = cbb.frequency_sorted_codebook(w)
+    enc = oracle.huffman_encode(idx.reshape(-1), shape=(M, K))
+    hd = _huff_data(enc)
+    wd = cmg.huffman_decode_weights(hd, cb, M, K)
+    assert np.array_equal(wd, w)
+    assert np.array_equal(wd, oracle.huff_decode_weights(enc, cb, M, K))
+    for T in (1, 5):
+        x = rng.standard_normal((T, K)).astype(np.float32)
+        y = cmg.huffman_matmul(x, hd, cb, M, K)
+        assert rel_l2(y, oracle.huff_gemv(x, enc, cb, M, K)) <= 1e-5, T
+    ids = np.array([M - 1, 0, 3 % M])
+    assert np.array_equal(cmg.huffman_embedding(ids, hd, cb, K), w[ids])
+
+
+def test_functional_reuses_device_format(cuda):
+    """Repeated calls on the same Huffman data reuse one device format."""
+    rng = np.random.default_rng(2)
+    M, K = 64, 4096
+    w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
+    cb, idx = cbb.frequency_sorted_codebook(w)
+    import huffman_codebook as hc
+    hd = _huff_data(hc.huffman_encode_indices(idx, shape=(M, K)))
+    a = cmg._huff_linear(hd, cb, M, K)
+    assert cmg._huff_linear(dict(hd), cb.copy(), M, K) is a
+    cb2 = cb.copy()
+    cb2[0] = 0.5
+    assert cmg._huff_linear(hd, cb2, M, K) is not a

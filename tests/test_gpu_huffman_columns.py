@@ -30,7 +30,7 @@ def test_columns_hold_sub_block_bits(cuda):
     w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
     cb, idx = cbb.frequency_sorted_codebook(w)
     enc = hc.huffman_encode_indices(idx, shape=(M, K))
-    lin = _lin(enc, cb, M, K, split_format=False)
+    lin = _lin(enc, cb, M, K, layout="columns")
     assert lin.cols is not None
     stream_bits = _bits(lin.dev.words.cpu().numpy().view(np.uint32))
     cw = lin._cwords.cpu().numpy().view(np.uint32)
@@ -58,7 +58,7 @@ def test_column_gemv_equals_packed(cuda, oracle, M, K):
     w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
     cb, idx = cbb.frequency_sorted_codebook(w)
     enc = hc.huffman_encode_indices(idx, shape=(M, K))
-    lin = _lin(enc, cb, M, K, split_format=False)
+    lin = _lin(enc, cb, M, K, layout="columns")
     assert lin.cols is not None
     assert lin.cols.ulut1, "unified tables expected for a 24-bit code"
     x = torch.from_numpy(rng.standard_normal((1, K)).astype(np.float32)).to(cuda)
@@ -85,7 +85,7 @@ def test_column_gemv_tall_chunks(cuda, oracle):
     cb = cbb.bf16_round(rng.standard_normal(4096) * 0.02).astype(np.float32)
     enc = hc.huffman_encode_indices(idx, shape=(M, K))
     assert int(np.asarray(enc["huff_lengths"]).max()) == 12
-    lin = _lin(enc, cb, M, K, split_format=False)
+    lin = _lin(enc, cb, M, K, layout="columns")
     assert lin.cols is not None
     H = np.diff(lin._row_off.cpu().numpy())
     assert (H >= 24).all()
@@ -109,7 +109,7 @@ def test_column_gemv_long_codes(cuda, oracle):
     idx = rng.choice(31, size=M * K, p=p / p.sum())
     enc = oracle.huffman_encode(idx, shape=(M, K), lengths=lengths)
     cb = cbb.bf16_round(rng.standard_normal(31) * 0.02).astype(np.float32)
-    lin = _lin(enc, cb, M, K, split_format=False)
+    lin = _lin(enc, cb, M, K, layout="columns")
     assert lin.cols is not None and not lin.cols.ulut1     # no unified tables past 24 bits
     x = rng.standard_normal((1, K)).astype(np.float32)
     y = lin(torch.from_numpy(x).to(cuda)).cpu().numpy()

@@ -79,20 +79,23 @@ def test_matches_token_tile_path(cuda):
 
 @pytest.mark.parametrize("M,K", [(300, 4096), (70, 12288)])
 def test_huffman_module_batched_tokens(cuda, oracle, M, K):
-    """HuffmanCodebookLinear with T >= 64 decodes its stream to transient
-    fixed-width indices (cbq_huff_decode_indices + cbq_pack_indices) and runs
-    the fp32 matrix-core GEMM; against the reference C kernel."""
+    """HuffmanCodebookLinear with T >= 64 decodes its format to transient
+    fixed-width indices (the split format through cbq_split_to_packed, the
+    stream through cbq_huff_decode_indices + cbq_pack_indices) and runs the
+    fp32 matrix-core GEMM; both layouts against the reference C kernel."""
     import huffman_codebook as hc
     from test_gpu_huffman import _lin
     rng = np.random.default_rng(M)
     w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
     cb, idx = cbb.frequency_sorted_codebook(w)
     enc = hc.huffman_encode_indices(idx, shape=(M, K))
-    lin = _lin(enc, cb, M, K)
     x = rng.standard_normal((96, K)).astype(np.float32)
-    y = lin(torch.from_numpy(x).to(cuda)).cpu().numpy()
     ref = oracle.huff_gemv(x, enc, cb, M, K, chunk_rows=None)
-    assert rel_l2(y, ref) <= TOL, rel_l2(y, ref)
+    for layout in ("auto", "stream"):
+        lin = _lin(enc, cb, M, K, layout=layout)
+        assert (lin.split is not None) == (layout == "auto")
+        y = lin(torch.from_numpy(x).to(cuda)).cpu().numpy()
+        assert rel_l2(y, ref) <= TOL, (layout, rel_l2(y, ref))
 
 
 @pytest.mark.parametrize("M,K", [(96, 8192), (33, 4096)])
@@ -119,7 +122,7 @@ def test_split_to_packed(cuda, oracle, M, K):
     want = oracle.pack_lsb(idx.reshape(-1), bits)
     assert np.array_equal(out.cpu().numpy()[:want.size], want)
     x = torch.from_numpy(rng.standard_normal((80, K)).astype(np.float32)).to(cuda)
-    lin_stream = _lin(enc, cb, M, K, split_format=False)
+    lin_stream = _lin(enc, cb, M, K, layout="stream")
     assert torch.equal(lin(x), lin_stream(x))
 
 

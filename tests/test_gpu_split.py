@@ -159,12 +159,100 @@ def test_module_split_equals_columns(cuda, oracle, M, K):
     cb, idx = cbb.frequency_sorted_codebook(w)
     enc = hc.huffman_encode_indices(idx, shape=(M, K))
     a = _lin(enc, cb, M, K)
-    b = _lin(enc, cb, M, K, split_format=False)
+    b = _lin(enc, cb, M, K, layout="columns")
     assert a.split is not None and b.split is None and b.cols is not None
     x = torch.from_numpy(rng.standard_normal((1, K)).astype(np.float32)).to(cuda)
     ya, yb = a(x), b(x)
     assert torch.equal(ya, yb)
     ref = oracle.huff_gemv(x.cpu().numpy(), enc, cb, M, K, chunk_rows=None)
     assert rel_l2(ya.cpu().numpy(), ref) <= 1e-5
-    y3 = a(torch.cat([x, x, x]))                           # T > 1 stays on the stream kernel
+    y3 = a(torch.cat([x, x, x]))                   # T > 1: transient fixed-width stream
     assert rel_l2(y3[1:2].cpu().numpy(), ref) <= 1e-5
+
+
+def _split_of(cuda, w):
+    """(codebook, indices, split format) of bf16 weights w [M, K]."""
+    import codebook_builder as cbb
+    cb, idx = cbb.frequency_sorted_codebook(w)
+    sp = build_split(torch.from_numpy(idx.astype(np.int32)).to(cuda), cb, cuda)
+    assert sp is not None
+    return cb, idx, sp
+
+
+@pytest.mark.parametrize("Ms,K", [((2048, 1024, 1024), 2048), ((6144,), 2048),
+                                  ((2048,), 6144), ((96, 40), 1024), ((64, 128), 3072),
+                                  ((512,), 5120)])
+def test_row_groups_against_oracle(cuda, oracle, Ms, K):
+    """K % 4096 != 0: the split GEMV walks groups of 4096 / gcd(K, 4096) rows
+    (2 for K = 2048, 6144; 4 for K = 1024, 3072, 5120).  Each matrix against
+    the reference C kernel on the same indices (rel-L2 <= 1e-5), the grouped
+    launch equal to one launch per matrix bit for bit."""
+    import codebook_builder as cbb
+    from conftest import rel_l2
+    lib = nat.load()
+    rng = np.random.default_rng(K + sum(Ms))
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    xd = torch.from_numpy(x).to(cuda)
+    built, singles = [], []
+    for i, M in enumerate(Ms):
+        w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
+        cb, idx, sp = _split_of(cuda, w)
+        y = _split(lib, xd, [sp], [M], K)
+        packed = oracle.pack_lsb(idx.reshape(-1).astype(np.int64), cbb.bits_for(len(cb)))
+        ref = oracle.fixed_gemv(x, packed, cb, M, K, cbb.bits_for(len(cb)), chunk_rows=None)
+        assert rel_l2(y.cpu().numpy(), ref) <= 1e-5, (M, K)
+        built.append(sp)
+        singles.append(y)
+    if len(Ms) > 1:
+        got = _split(lib, xd, built, list(Ms), K)
+        assert torch.equal(got, torch.cat(singles, dim=1))
+
+
+@pytest.mark.parametrize("K", [2048, 6144, 1024])
+def test_row_groups_folded_glue(cuda, K):
+    """The folded RMSNorm / SiLU staging with row groups equals the glue
+    kernel followed by the plain split GEMV bit for bit."""
+    import codebook_builder as cbb
+    lib = nat.load()
+    rng = np.random.default_rng(K)
+    M = 4096 // K * 96 if K < 4096 else 64
+    w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
+    _, _, sp = _split_of(cuda, w)
+    cfg = decoder.DecoderConfig(layers=1, hidden=K, inter=K, n_q=1, n_kv=1, head_dim=64,
+                                vocab=16)
+    g = decoder._Glue(cfg)
+    gen = torch.Generator(device=cuda).manual_seed(K)
+    h = torch.randn(1, K, device=cuda, generator=gen) * 2
+    dl = torch.randn(1, K, device=cuda, generator=gen)
+    want = _split(lib, g.add_rms(h.clone(), None), [sp], [M], K)
+    assert torch.equal(_split(lib, h, [sp], [M], K, nat.XF_RMS), want)
+    hc_ = h.clone()
+    want = _split(lib, g.add_rms(hc_, dl), [sp], [M], K)
+    h2 = torch.full_like(h, float("nan"))
+    assert torch.equal(_split(lib, h, [sp], [M], K, nat.XF_ADD_RMS, dl, h2), want)
+    assert torch.equal(h2, hc_)
+    want = _split(lib, g.silu_mul(h, dl), [sp], [M], K)
+    assert torch.equal(_split(lib, h, [sp], [M], K, nat.XF_SILU, dl), want)
+
+
+def test_split_decode_indices_exact(cuda, oracle):
+    """decode_indices() of a split-only module (stream freed) returns the
+    stored indices bit for bit, against the reference C decoder; T = 2..63
+    and T >= 64 run through the transient fixed-width stream."""
+    import codebook_builder as cbb
+    from conftest import rel_l2
+    from test_gpu_huffman import _lin
+    rng = np.random.default_rng(21)
+    M, K = 200, 6144
+    w = cbb.bf16_round(rng.standard_normal((M, K)) * 0.02)
+    cb, idx = cbb.frequency_sorted_codebook(w)
+    enc = hc.huffman_encode_indices(idx, shape=(M, K))
+    lin = _lin(enc, cb, M, K)
+    assert lin.split is not None and lin.dev is None
+    kind = "ref" if oracle.ref_available() else "oracle"
+    want = oracle.huff_decode_indices(enc, M, K, kind=kind)
+    assert np.array_equal(lin.decode_indices().cpu().numpy(), want)
+    for T in (1, 3, 17, 70):
+        x = rng.standard_normal((T, K)).astype(np.float32)
+        y = lin(torch.from_numpy(x).to(cuda)).cpu().numpy()
+        assert rel_l2(y, oracle.huff_gemv(x, enc, cb, M, K, chunk_rows=None)) <= 1e-5, T
