@@ -10,24 +10,36 @@ rows stacked into one matrix and gate/up into one (same codebook, so the
 packed streams concatenate exactly), o and down, then the lm_head: 145
 launches, captured once into a HIP graph and replayed.
 
-value = algorithmic compressed bytes per step / step time (GB/s).  The same
-sweep is also run with canonical-Huffman streams (24-bit codes, 4096-symbol
-chunks; q/k/v and gate/up as grouped launches, one code per matrix) and
-reported under "huffman".  "roofline" is the dominant kernel (the stacked
-gate+up GEMV): algorithmic bytes per launch / its mean launch time from HIP
-events around back-to-back launches over all 36 layers' distinct weights (so
-the 256 MB MALL cannot serve repeats).  "breakdown" times every unstacked
-shape the same way.  "prefill" is the bf16 MFMA GEMM (T = 512, 2048) and
-"e2e" the greedy decode of the whole model.  "cpu_baseline" times the
-reference's own C kernel (oracle/_ref, compiled from src/compressed_matmul.c)
-on one gate_proj matrix on the host cores.
+value = algorithmic compressed bytes per step / step time (GB/s).  "roofline"
+is the dominant kernel (the stacked gate+up GEMV): algorithmic bytes per
+launch / its mean launch time from HIP events around back-to-back launches
+over all 36 layers' distinct weights (so the 256 MB MALL cannot serve
+repeats).  Further keys:
+
+- "breakdown": every unstacked 9B shape timed the same way;
+- "batch_stacked_gate_up": the stacked gate+up launch with 2..16 tokens;
+- "huffman": the same sweep with canonical-Huffman weights held in the split
+  format alone (the decoder's format; each matrix's stream is decoded on the
+  GPU, re-encoded and freed), with its resident bits per weight;
+- "qwen3_1_7b": BASELINE configs 2 and 3, the 28-layer 1.7B shapes at 1, 4
+  and 16 tokens, fixed-width and Huffman;
+- "prefill": the bf16 MFMA GEMM at T = 512 and 2048 (config 4);
+- "e2e": greedy decode of the whole 36-layer model (config 5), both encodings,
+  tokens checked against the CPU oracle's golden run when the prompt matches;
+- "cpu_baseline": the reference's own C kernels (oracle/_ref, compiled from
+  src/compressed_matmul.c) on config 1 on the host cores.
 """
-import argparse
-import json
 import os
-import re
-import sys
-import time
+
+# The CPU baseline's OpenMP team binds to neighbouring cores; set before any
+# OpenMP runtime is loaded (torch loads one).
+os.environ.setdefault("OMP_PROC_BIND", "close")
+
+import argparse  # noqa: E402
+import json  # noqa: E402
+import re  # noqa: E402
+import sys  # noqa: E402
+import time  # noqa: E402
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "codebook-quantization_amd"))
@@ -35,6 +47,7 @@ sys.path.insert(0, os.path.join(ROOT, "codebook-quantization_amd"))
 METRIC = "compressed GEMV HBM GB/s (% of peak) + decode tok/s, batch 1, 9B-scale shapes"
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16
+GOLDEN_E2E = os.path.join(ROOT, "tests", "golden", "e2e_qwen3_8b_golden.npz")
 
 
 def log(*a):
@@ -43,13 +56,6 @@ def log(*a):
 
 def fixed_bytes(M, K, bits, C, T=1):
     return (M * K * bits + 7) // 8 + 4 * C + T * K * 4 + T * M * 4
-
-
-def huff_bytes(t, T=1):
-    M, K = t.shape
-    tabs = t.tables
-    aux = 4 * tabs["lut1"].numel() + 4 * tabs["lut2"].numel() + 4 * tabs["codebook"].numel()
-    return t.nbytes + aux + T * K * 4 + T * M * 4
 
 
 def timed_graph(torch, fn, reps, warmup):
@@ -87,32 +93,132 @@ def read_traffic(name):
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(np, packed, cb, x, M, K, bits, seconds):
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import cbq_oracle as O
-    kind = "reference" if O.ref_available() else "port"
-    lib_kind = "ref" if kind == "reference" else "oracle"
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
-    threads = min(threads, os.cpu_count() or threads)
-    nbytes = fixed_bytes(M, K, bits, len(cb))
-    O.fixed_gemv(x, packed, cb, M, K, bits, kind=lib_kind, chunk_rows=None, threads=threads)
-    times = []
-    t_end = time.time() + seconds
-    while time.time() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        O.fixed_gemv(x, packed, cb, M, K, bits, kind=lib_kind, chunk_rows=None, threads=threads)
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    t0 = time.perf_counter()
-    O.fixed_gemv(x, packed, cb, M, K, bits, kind=lib_kind, chunk_rows=256, threads=threads)
-    as_called = time.perf_counter() - t0
-    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": (f"gate_proj {K}->{M} 13-bit fixed-width GEMV, T=1, one call over all rows "
-                       f"(src/compressed_matmul.c compressed_matmul_f32_chunk, gcc -O3 -fopenmp), "
-                       f"median of {len(times)} runs = {med * 1e3:.2f} ms; as called by the "
-                       f"reference wrapper (256-row chunks) {as_called * 1e3:.2f} ms = "
-                       f"{nbytes / as_called / 1e9:.3f} GB/s")}
+# ---- decoder launch lists ----------------------------------------------------
 
+def step_plan(dec, with_head=True):
+    """The decoder's launches for one token: per layer the stacked q/k/v,
+    o, the stacked gate/up and down; then the lm_head.  Entries are a
+    name or a tuple of part names (one stacked / grouped launch)."""
+    plan = []
+    for i in range(dec.cfg["layers"]):
+        p = f"model.layers.{i}."
+        plan.append(tuple(p + n for n in ("self_attn.q_proj", "self_attn.k_proj",
+                                          "self_attn.v_proj")))
+        plan.append(p + "self_attn.o_proj")
+        plan.append(tuple(p + n for n in ("mlp.gate_proj", "mlp.up_proj")))
+        plan.append(p + "mlp.down_proj")
+    if with_head:
+        plan.append("lm_head")
+    return plan
+
+
+def fixed_launches(torch, nat, lib, dev, synthetic, fixed, plan):
+    """(launch list, outputs) of a step plan over fixed-width tensors, the
+    stacked parts concatenated into one matrix (synthetic.stack_fixed)."""
+    mats = []
+    for e in plan:
+        if isinstance(e, tuple):
+            st = synthetic.stack_fixed([fixed[n] for n in e], e[0] + "+stacked")
+            if st is None:
+                mats += [fixed[n] for n in e]
+            else:
+                mats.append(st)
+        else:
+            mats.append(fixed[e])
+    return mats
+
+
+def run_fixed(torch, nat, lib, dev, mats, xs, outs, T=1):
+    st = nat.stream_ptr(dev)
+    for t in mats:
+        M, K = t.shape
+        rc = lib.ck_linear_f32(xs[K].data_ptr(), t.packed.data_ptr(), t.codebook.data_ptr(),
+                               outs[id(t)].data_ptr(), T, M, K, t.codebook.numel(), t.bits, st)
+        if rc:
+            raise RuntimeError(f"ck_linear_f32 rc={rc} on {t.name}")
+
+
+def fixed_sweep(torch, nat, lib, dev, mats, T, steps, warmup):
+    """Graph-replayed step over `mats` with T tokens -> (ms, algorithmic bytes)."""
+    xs, outs = {}, {}
+    for t in mats:
+        M, K = t.shape
+        if K not in xs:
+            xs[K] = torch.randn(T, K, device=dev)
+        outs[id(t)] = torch.empty(T, M, device=dev)
+    ms, _ = timed_graph(torch, lambda: run_fixed(torch, nat, lib, dev, mats, xs, outs, T),
+                        steps, warmup)
+    nbytes = sum(fixed_bytes(t.shape[0], t.shape[1], t.bits, t.codebook.numel(), T)
+                 for t in mats)
+    return ms, nbytes
+
+
+# ---- Huffman: split format only ------------------------------------------------
+
+def build_split_formats(torch, dev, huff, names):
+    """The split format of every Huffman tensor in `names`, decoded from its
+    stream on the GPU; the stream is then dropped (the split format is the
+    matrix's only resident format).  Returns {name: (keep, desc)} and the
+    streams' byte counts (reference stream + chunk index)."""
+    from gpu_huffman_functions import build_split, decode_symbols, split_eligible
+    splits, stream_bytes = {}, {}
+    for n in names:
+        t = huff[n]
+        M, K = t.shape
+        stream_bytes[n] = t.nbytes
+        if split_eligible(M, K):
+            idx = decode_symbols(t.words, t.chunk_off, t.sub_len, t.lengths, M * K, dev)
+            sp = build_split(idx, t.tables["codebook"].cpu().numpy(), dev)
+            del idx
+            if sp is not None:
+                splits[n] = sp
+                t.words = t.chunk_off = t.sub_len = None     # stream freed
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return splits, stream_bytes
+
+
+def split_launch_args(nat, splits, huff, ns, outs):
+    import ctypes
+    k = len(ns)
+    return (k, (ctypes.POINTER(nat.SplitMatrix) * k)(*[ctypes.pointer(splits[n][1]) for n in ns]),
+            (ctypes.c_void_p * k)(*[outs[n].data_ptr() for n in ns]),
+            (ctypes.c_int * k)(*[huff[n].shape[0] for n in ns]), huff[ns[0]].shape[1])
+
+
+def huffman_sweep(torch, nat, lib, dev, huff, splits, plan, steps, warmup):
+    """Graph-replayed split-format step (grouped q/k/v and gate/up) ->
+    (ms, bytes the kernels stream, per-launch args)."""
+    from gpu_huffman_functions import split_bytes
+    outs, xs, launches = {}, {}, []
+    for e in plan:
+        ns = list(e) if isinstance(e, tuple) else [e]
+        missing = [n for n in ns if n not in splits]
+        if missing:
+            raise RuntimeError(f"no split format for {missing}")
+        for n in ns:
+            M, K = huff[n].shape
+            outs[n] = torch.empty(1, M, device=dev)
+            if K not in xs:
+                xs[K] = torch.randn(1, K, device=dev)
+        launches.append(split_launch_args(nat, splits, huff, ns, outs))
+
+    def run():
+        for k, mats, out_a, m_a, K in launches:
+            rc = lib.cbq_split_linear_f32(xs[K].data_ptr(), None, None, 0, 0.0, k, mats, out_a,
+                                          m_a, K, nat.stream_ptr(dev))
+            if rc:
+                raise RuntimeError(f"split GEMV rc={rc}")
+    ms, _ = timed_graph(torch, run, steps, warmup)
+    nbytes = 0
+    for e in plan:
+        ns = list(e) if isinstance(e, tuple) else [e]
+        nbytes += sum(split_bytes(splits[n][0]) + 4 * huff[n].shape[0] for n in ns)
+        nbytes += 4 * huff[ns[0]].shape[1]
+    return ms, nbytes
+
+
+# ---- sections ------------------------------------------------------------------
 
 def prefill_section(torch, nat, lib, dev, fixed, kinds, args):
     """bf16 MFMA prefill over the same fixed-width weights,
@@ -152,31 +258,219 @@ def prefill_section(torch, nat, lib, dev, fixed, kinds, args):
     return out
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(np, seconds):
+    """BASELINE config 1 on the host cores with the reference's own C kernels
+    (oracle/_ref; the restatement when that is not built): W [6144, 2048]
+    N(0, 0.02) bf16 (synthetic.make_bf16, seed "config1"), frequency-sorted
+    lossless codebook, 13-bit fixed-width indices and the canonical-Huffman
+    stream of the same indices; T = 1, 4, 16; each timed as the reference
+    wrapper calls it (256-row chunks, stream copied to pad it every call,
+    src/compressed_matmul_cpu.py:276-343, 446-507) and as one call over all
+    rows (tables prepared once).  Median of >= 7 runs after one warm-up, with
+    the box's CPU share of OpenMP threads bound close.  GB/s on the same
+    algorithmic bytes as the GPU figures."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import cbq_oracle as O
+    import codebook_builder as cbb
+    import huffman_codebook as hc
+    import synthetic
+    kind = "reference" if O.ref_available() else "port"
+    lk = "ref" if kind == "reference" else "oracle"
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    threads = min(threads, os.cpu_count() or threads)
+    M, K = 6144, 2048
+    w = synthetic.make_bf16((M, K), "config1", device="cpu").float().numpy()
+    cb, idx = cbb.frequency_sorted_codebook(w)
+    bits = cbb.bits_for(len(cb))
+    import bitpack
+    packed = bitpack.pack_any_bits(idx, bits)
+    enc = hc.huffman_encode_indices(idx, shape=(M, K))
+    C = len(cb)
+    L = O.lib(lk)
+    pk_pad = np.concatenate([packed, np.zeros(4, np.uint8)])
+    tabs = O.huff_cpu_tables(enc)
+    stream_b = len(enc["huff_stream"])
+    rng = np.random.default_rng(1)
+    budget = max(1.0, seconds) / 12.0                  # per (mode, encoding, T) cell
+    res = {}
+
+    def timed(fn):
+        fn()
+        ts = []
+        t_end = time.perf_counter() + budget
+        while len(ts) < 7 or (time.perf_counter() < t_end and len(ts) < 200):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)), len(ts)
+
+    for T in (1, 4, 16):
+        x = rng.standard_normal((T, K)).astype(np.float32)
+        out = np.zeros((T, M), np.float32)
+        fb = fixed_bytes(M, K, bits, C, T)
+        hb = stream_b + 8 * M + 4 * C + T * K * 4 + T * M * 4   # + row starts (reference tables)
+
+        def fixed_single():
+            out[:] = 0
+            with O._omp_threads(threads):
+                L.fixed_rows(O._p(x, O._f32p), O._p(pk_pad, O._u8p), O._p(cb, O._f32p),
+                             O._p(out, O._f32p), T, M, K, C, bits, 0, M)
+
+        def huff_single():
+            out[:] = 0
+            with O._omp_threads(threads):
+                L.huff_rows(O._p(x, O._f32p), *O._tab_args(tabs), O._p(cb, O._f32p),
+                            O._p(out, O._f32p), T, M, K, C, 0, M, tabs["max_len"])
+
+        cells = {
+            "fixed_single": (fixed_single, fb),
+            "fixed_as_called": (lambda: O.fixed_gemv(x, packed, cb, M, K, bits, kind=lk,
+                                                     chunk_rows=256, threads=threads), fb),
+            "huffman_single": (huff_single, hb),
+            "huffman_as_called": (lambda: O.huff_gemv(x, enc, cb, M, K, kind=lk, chunk_rows=256,
+                                                      threads=threads), hb),
+        }
+        for name, (fn, nb) in cells.items():
+            med, n = timed(fn)
+            res[f"T{T}_{name}"] = {"ms": round(med * 1e3, 3), "GB/s": round(nb / med / 1e9, 3),
+                                   "runs": n}
+    head = res["T1_fixed_single"]
+    return {"value": head["GB/s"], "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": (f"config 1 (K={K} -> M={M}, 13-bit fixed width, T=1): one call over all "
+                       f"rows of src/compressed_matmul.c compressed_matmul_f32_chunk "
+                       f"(gcc -O3 -fopenmp, {threads} threads, OMP_PROC_BIND="
+                       f"{os.environ.get('OMP_PROC_BIND')}), median of {head['runs']} runs = "
+                       f"{head['ms']} ms on {cpu_model()}; every mode, encoding and T in "
+                       f"cpu_baseline_detail")}, \
+        {"cpu": cpu_model(), "threads": threads, "omp_proc_bind": os.environ.get("OMP_PROC_BIND"),
+         "kind": kind, "codebook": C, "bits": bits,
+         "huffman_bits_per_weight": round(8.0 * stream_b / (M * K), 3), "cells": res}
+
+
+def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
+    """BASELINE configs 2 and 3: every layer linear of the 28-layer 1.7B-shape
+    decoder (no lm_head), decoder launch order, at 1, 4 and 16 tokens;
+    fixed-width 13-bit indices, and the same weights Huffman-coded in the
+    split format (one token on the split GEMV; 4 and 16 tokens through the
+    transient fixed-width stream and ck_linear_f32)."""
+    from gpu_huffman_functions import split_bytes, split_inverse, split_prefill
+    dec = synthetic.SyntheticDecoder("qwen3-1.7b", log=log)
+    names = dec.all_linears(with_head=False)
+    plan = step_plan(dec, with_head=False)
+    out = {"layers": dec.cfg["layers"], "shapes": "q 2048->2048, k/v 2048->1024, o 2048->2048, "
+                                                   "gate/up 2048->6144, down 6144->2048"}
+    fixed = dec.build_fixed(names)
+    mats = fixed_launches(torch, nat, lib, dev, synthetic, fixed, plan)
+    fx = {}
+    for T in (1, 4, 16):
+        ms, nb = fixed_sweep(torch, nat, lib, dev, mats, T, args.steps, args.warmup)
+        fx[f"T{T}"] = {"ms_per_step": round(ms, 4), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+                       "pct_of_hbm_peak": round(100 * nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1)}
+    per = {}
+    for kind, sel in (("q_proj", "self_attn.q_proj"), ("k_proj", "self_attn.k_proj"),
+                      ("o_proj", "self_attn.o_proj"), ("gate_proj", "mlp.gate_proj"),
+                      ("down_proj", "mlp.down_proj")):
+        ms_k = [fixed[n] for n, _, _ in names if n.endswith(sel)]
+        ms, nb = fixed_sweep(torch, nat, lib, dev, ms_k, 1, max(3, args.steps // 2), 1)
+        t = ms_k[0]
+        per[kind] = {"shape": f"{t.shape[1]}->{t.shape[0]}",
+                     "us_per_launch": round(ms * 1e3 / len(ms_k), 2),
+                     "GB/s": round(nb / (ms * 1e-3) / 1e9, 1)}
+    out["fixed"] = {"sweep": fx, "per_shape_T1": per}
+    del fixed, mats
+    torch.cuda.empty_cache()
+
+    huff = dec.build_huffman(names)
+    splits, stream_bytes = build_split_formats(torch, dev, huff, names)
+    ms1, nb1 = huffman_sweep(torch, nat, lib, dev, huff, splits, plan, args.steps, args.warmup)
+    n_w = sum(huff[n].shape[0] * huff[n].shape[1] for n in names)
+    res_b = sum(split_bytes(splits[n][0]) for n in names)
+    hu = {"T1": {"ms_per_step": round(ms1, 4), "GB/s": round(nb1 / (ms1 * 1e-3) / 1e9, 1),
+                 "pct_of_hbm_peak": round(100 * nb1 / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1),
+                 "stream_equivalent_GB/s": round(sum(stream_bytes.values()) / (ms1 * 1e-3) / 1e9,
+                                                 1)}}
+    invs = {}
+    for T in (4, 16):
+        xs = {}
+        for n in names:
+            K = huff[n].shape[1]
+            if K not in xs:
+                xs[K] = torch.randn(T, K, device=dev)
+            cbt = huff[n].tables["codebook"]
+            if id(cbt) not in invs:
+                invs[id(cbt)] = split_inverse(cbt.cpu().numpy(), dev)
+
+        def run(T=T, xs=xs):
+            for n in names:
+                t = huff[n]
+                M, K = t.shape
+                split_prefill(splits[n], invs[id(t.tables["codebook"])], xs[K], M, K,
+                              t.tables["codebook"])
+        run()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        reps = max(2, args.steps // 4)
+        for _ in range(reps):
+            run()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+        hu[f"T{T}"] = {"ms_per_step": round(ms, 3),
+                       "note": "transient fixed-width decode + ck_linear_f32 per matrix, "
+                               "eager launches with allocations (not graph-captured)"}
+    out["huffman"] = {"sweep": hu, "bits_per_weight_resident": round(8.0 * res_b / n_w, 3),
+                      "bits_per_weight_stream_incl_index":
+                          round(8.0 * sum(stream_bytes.values()) / n_w, 3)}
+    del huff, splits
+    torch.cuda.empty_cache()
+    return out
+
+
 def e2e_section(torch, dec, args):
     """always-compressed greedy decode of the random-init
     36-layer Qwen3-8B-shape decoder at batch 1: all linears, the lm_head and
-    the embedding Huffman-coded (24-bit canonical codes, 4096-symbol chunks);
-    128-token uniform random prompt, then args.e2e_tokens greedy tokens (EOS
-    ignored).  tok/s over the decode steps, which are captured once as a HIP
-    graph and replayed.  The same model with fixed-width 13-bit indices (the
-    same weights) runs too; its tokens must agree."""
+    the embedding Huffman-coded (24-bit canonical codes, 4096-symbol chunks;
+    linears re-encoded to the split format, their streams freed); 128-token
+    uniform random prompt, then args.e2e_tokens greedy tokens (EOS ignored).
+    tok/s over the decode steps, which are captured once as a HIP graph and
+    replayed.  The same model with fixed-width 13-bit indices (the same
+    weights) runs too; both encodings' tokens are compared with the CPU
+    oracle's golden tokens (tests/golden/e2e_qwen3_8b_golden.npz) when the
+    prompt is the golden's."""
     import numpy as np
     import decoder as D
-    import synthetic
     c = dec.cfg
     cfg = D.DecoderConfig(layers=c["layers"], hidden=c["hidden"], inter=c["inter"], n_q=c["n_q"],
                           n_kv=c["n_kv"], head_dim=c["head_dim"], vocab=c["vocab"])
     names = dec.all_linears() + [dec.embed]
     prompt = [int(t) for t in np.random.default_rng(2).integers(0, cfg.vocab, 128)]
+    golden = None
+    if os.path.exists(GOLDEN_E2E):
+        g = np.load(GOLDEN_E2E, allow_pickle=False)
+        if [int(t) for t in g["prompt"]] == prompt and c["layers"] == 36:
+            golden = [int(t) for t in g["tokens"]]
     n_new = args.e2e_tokens
     out = {"prompt_tokens": len(prompt), "new_tokens": n_new, "batch": 1}
     toks = {}
+    n_w = sum(M * K for n, M, K in dec.all_linears())
     for enc in ("huffman", "fixed"):
         t0 = time.time()
         tensors = dec.build_huffman(names) if enc == "huffman" else dec.build_fixed(names)
         torch.cuda.synchronize()
-        build_s = time.time() - t0
         model = D.from_synthetic(cfg, tensors, max_len=len(prompt) + n_new)
+        del tensors                                # the model holds what it streams
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        build_s = time.time() - t0
         prefill = []                         # first call (allocator and module warm-up), then steady
         for _ in range(2):
             torch.cuda.synchronize()
@@ -188,22 +482,24 @@ def e2e_section(torch, dec, args):
         prefill_s = prefill[1]
         timing = {}
         toks[enc] = model.generate_graph(prompt, n_new, timing)
-        step_bytes = sum((t.nbytes if enc == "huffman" else t.nbytes) for n, t in tensors.items()
-                         if n != dec.embed[0])
+        step_bytes = sum(model.linear_bytes.values())
         tps = timing["decode_steps"] / timing["decode_s"]
         out[enc] = {"decode_tok_per_s": round(tps, 2),
                     "ms_per_token": round(1e3 / tps, 3),
                     "weight_GB_per_token": round(step_bytes / 1e9, 3),
                     "weight_GB/s": round(step_bytes * tps / 1e9, 1),
+                    "bits_per_weight_resident": round(8.0 * step_bytes / n_w, 3),
                     "prefill_ms_128_tokens": round(prefill_s * 1e3, 1),
                     "prefill_ms_first_call": round(prefill[0] * 1e3, 1),
                     "build_s": round(build_s, 1), "first_tokens": toks[enc][:8]}
+        if golden is not None:
+            k = min(len(golden), n_new)
+            out[enc]["tokens_equal_oracle_golden"] = toks[enc][:k] == golden[:k]
+            out[enc]["golden_tokens_compared"] = k
         log(f"e2e {enc}: {tps:.1f} tok/s")
-        del tensors, model
+        del model
         torch.cuda.empty_cache()
     out["tokens_equal_huffman_vs_fixed"] = toks["huffman"] == toks["fixed"]
-    out["token_agreement"] = round(sum(a == b for a, b in zip(toks["huffman"], toks["fixed"])) /
-                                   max(1, n_new), 4)
     return out
 
 
@@ -217,9 +513,10 @@ def main():
     ap.add_argument("--no-huffman", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--no-1p7b", action="store_true")
     ap.add_argument("--e2e-tokens", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only run a plain device copy of this many MiB (PMC calibration)")
     args = ap.parse_args()
@@ -247,73 +544,38 @@ def main():
 
     dec = synthetic.SyntheticDecoder(args.config, layers=args.layers, log=log)
     tensors = dec.all_linears()
+    names = [n for n, _, _ in tensors]
     t0 = time.time()
     fixed = dec.build_fixed(tensors)
     torch.cuda.synchronize()
     log(f"built {len(fixed)} fixed-width tensors in {time.time() - t0:.1f}s")
 
-    xs, outs = {}, {}
-    for name, M, K in tensors:
-        if K not in xs:
-            xs[K] = torch.randn(1, K, device=dev)
-        outs[name] = torch.empty(1, M, device=dev)
-
-    def launch_fixed(names):
-        st = nat.stream_ptr(dev)
-        for n in names:
-            t = fixed[n]
-            M, K = t.shape
-            rc = lib.ck_linear_f32(xs[K].data_ptr(), t.packed.data_ptr(), t.codebook.data_ptr(),
-                                   outs[n].data_ptr(), 1, M, K, t.codebook.numel(), t.bits, st)
-            if rc:
-                raise RuntimeError(f"ck_linear_f32 rc={rc} on {n}")
-
-    # The decode step's launches, as the decoder makes them: per layer the
-    # q/k/v rows stacked into one matrix and gate/up into one (same codebook
-    # and index width, so the packed bytes concatenate exactly), o, down; and
-    # the lm_head.
-    import synthetic
-    stacked = {}
-    step_names = []
-    for i in range(dec.cfg["layers"]):
-        p = f"model.layers.{i}."
-        for fused, parts in (("self_attn.qkv_proj", ("self_attn.q_proj", "self_attn.k_proj",
-                                                     "self_attn.v_proj")),
-                             ("mlp.gate_up_proj", ("mlp.gate_proj", "mlp.up_proj"))):
-            st = synthetic.stack_fixed([fixed[p + n] for n in parts], p + fused)
-            if st is None:
-                step_names += [p + n for n in parts]
-                continue
-            stacked[p + fused] = st
-            outs[p + fused] = torch.empty(1, st.shape[0], device=dev)
-            step_names.append(p + fused)
-        step_names += [p + "self_attn.o_proj", p + "mlp.down_proj"]
-    step_names += [n for n, _, _ in tensors if "layers" not in n]
-    fixed.update(stacked)
-    names = [n for n, _, _ in tensors]
-    step_bytes = sum(fixed_bytes(fixed[n].shape[0], fixed[n].shape[1], fixed[n].bits,
-                                 fixed[n].codebook.numel()) for n in step_names)
-    ms_step, _ = timed_graph(torch, lambda: launch_fixed(step_names), args.steps, args.warmup)
+    plan = step_plan(dec)
+    mats = fixed_launches(torch, nat, lib, dev, synthetic, fixed, plan)
+    ms_step, step_bytes = fixed_sweep(torch, nat, lib, dev, mats, 1, args.steps, args.warmup)
     log(f"fixed sweep: {ms_step:.3f} ms/step, {step_bytes / 1e9:.2f} GB/step, "
-        f"{len(step_names)} launches")
+        f"{len(mats)} launches")
 
     # per-shape mean launch time (each shape over all layers' distinct weights)
     kinds = {}
-    for n in names + list(stacked):
+    for n in names:
         kinds.setdefault(n.split(".")[-1] if "layers" in n else n, []).append(n)
+    stacked = {"qkv_proj": [m for m in mats if m.shape[0] == dec.cfg["n_q"] * dec.cfg["head_dim"]
+                            + 2 * dec.cfg["n_kv"] * dec.cfg["head_dim"] and "+stacked" in m.name],
+               "gate_up_proj": [m for m in mats if m.shape[0] == 2 * dec.cfg["inter"]
+                                and "+stacked" in m.name]}
     breakdown = {}
-    for kind, ns in kinds.items():
-        ms, _ = timed_graph(torch, lambda ns=ns: launch_fixed(ns), max(3, args.steps // 2), 1)
-        t = fixed[ns[0]]
-        per = ms / len(ns)
-        b = fixed_bytes(t.shape[0], t.shape[1], t.bits, t.codebook.numel())
+    groups = {k: [fixed[n] for n in ns] for k, ns in kinds.items()}
+    groups.update({k: v for k, v in stacked.items() if v})
+    for kind, ts in groups.items():
+        ms, nb = fixed_sweep(torch, nat, lib, dev, ts, 1, max(3, args.steps // 2), 1)
+        t = ts[0]
         breakdown[kind] = {"shape": f"{t.shape[1]}->{t.shape[0]}", "bits": t.bits,
-                           "us_per_launch": round(per * 1e3, 2),
-                           "GB/s": round(b / (per * 1e-3) / 1e9, 1)}
-    gu = kinds.get("gate_proj", []) + kinds.get("up_proj", [])
-    gus = kinds.get("gate_up_proj", []) or gu          # the decoder's stacked launch
-    ms_gu, _ = timed_graph(torch, lambda: launch_fixed(gus), args.steps, args.warmup)
-    t = fixed[gus[0]]
+                           "us_per_launch": round(ms * 1e3 / len(ts), 2),
+                           "GB/s": round(nb / (ms * 1e-3) / 1e9, 1)}
+    gus = stacked["gate_up_proj"] or groups["gate_proj"] + groups["up_proj"]
+    ms_gu, _ = fixed_sweep(torch, nat, lib, dev, gus, 1, args.steps, args.warmup)
+    t = gus[0]
     b_gu = fixed_bytes(t.shape[0], t.shape[1], t.bits, t.codebook.numel())
     us_gu = ms_gu * 1e3 / len(gus)
     achieved = b_gu / (us_gu * 1e-6) / 1e9
@@ -324,38 +586,28 @@ def main():
                            f"{t.shape[1]}->{t.shape[0]}"),
                 "bytes_per_launch": b_gu, "us_per_launch": round(us_gu, 2)}
 
-    # config 2's batch 4 / 16 (and 2, 8): the same stacked gate+up launches with
-    # T tokens (every weight is read once for all T rows of x)
+    # config 2's batch 4 / 16 (and 2, 8) on the 9B stacked gate+up: every
+    # weight is read once for all T rows of x
     batch = {}
     for T in (2, 4, 8, 16):
-        xT = torch.randn(T, t.shape[1], device=dev)
-        oT = torch.empty(T, t.shape[0], device=dev)
-
-        def launch_T(T=T, xT=xT, oT=oT):
-            st = nat.stream_ptr(dev)
-            for n in gus:
-                f = fixed[n]
-                rc = lib.ck_linear_f32(xT.data_ptr(), f.packed.data_ptr(), f.codebook.data_ptr(),
-                                       oT.data_ptr(), T, f.shape[0], f.shape[1],
-                                       f.codebook.numel(), f.bits, st)
-                if rc:
-                    raise RuntimeError(f"ck_linear_f32 T={T} rc={rc}")
-        ms_T, _ = timed_graph(torch, launch_T, args.steps, args.warmup)
+        ms_T, nb = fixed_sweep(torch, nat, lib, dev, gus, T, args.steps, args.warmup)
         us_T = ms_T * 1e3 / len(gus)
-        bT = fixed_bytes(t.shape[0], t.shape[1], t.bits, t.codebook.numel(), T)
         batch[f"T{T}"] = {"us_per_launch": round(us_T, 2),
-                          "GB/s": round(bT / (us_T * 1e-6) / 1e9, 1),
-                          "GFLOP/s": round(2.0 * T * t.shape[0] * t.shape[1] / (us_T * 1e-6) / 1e9, 1)}
+                          "GB/s": round(nb / len(gus) / (us_T * 1e-6) / 1e9, 1),
+                          "vs_T1": round(us_T / us_gu, 3),
+                          "GFLOP/s": round(2.0 * T * t.shape[0] * t.shape[1] / (us_T * 1e-6) / 1e9,
+                                           1)}
     log(f"stacked gate+up at T=2/4/8/16: {batch}")
 
     result = {
         "metric": METRIC, "value": round(step_bytes / (ms_step * 1e-3) / 1e9, 1), "unit": "GB/s",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic: random-init N(0,0.02) bf16 weights, lossless per-category codebooks",
+        "data": "synthetic: random-init N(0,0.02) bf16 weights (counter-based generator, "
+                "identical on CPU and GPU), lossless per-category codebooks",
         "config": {"workload": f"{args.config} decode-step GEMV sweep, batch 1, fixed-width",
                    "layers": dec.cfg["layers"], "linears_per_step": len(names),
-                   "launches_per_step": len(step_names),
+                   "launches_per_step": len(mats),
                    "stacking": "per layer q/k/v rows in one matrix, gate/up in one",
                    "bytes_per_step": step_bytes, "pct_of_hbm_peak":
                        round(100 * step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1),
@@ -367,165 +619,61 @@ def main():
 
     if not args.no_prefill:
         result["prefill"] = prefill_section(torch, nat, lib, dev, fixed, kinds, args)
+    del fixed, mats, gus, groups, stacked
+    torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
-        n0 = gu[0]
-        t = fixed[n0]
-        M, K = t.shape
-        packed = t.packed.cpu().numpy()[:(M * K * t.bits + 7) // 8]
-        result["cpu_baseline"] = cpu_baseline(np, packed, t.codebook.cpu().numpy(),
-                                              xs[K].cpu().numpy(), M, K, t.bits, args.cpu_seconds)
+        result["cpu_baseline"], result["cpu_baseline_detail"] = cpu_baseline(np, args.cpu_seconds)
+        log(f"cpu baseline: {result['cpu_baseline']['value']} GB/s")
 
     if not args.no_huffman:
-        del fixed
-        torch.cuda.empty_cache()
+        from gpu_huffman_functions import split_bytes
         t0 = time.time()
         huff = dec.build_huffman(tensors)
-        torch.cuda.synchronize()
-        log(f"built {len(huff)} Huffman tensors in {time.time() - t0:.1f}s")
-        descs = {}
-        for n, t in huff.items():
-            tb = t.tables
-            descs[n] = nat.HuffStream(
-                words=t.words.data_ptr(), n_words=t.words.numel(),
-                chunk_off=t.chunk_off.data_ptr(), sub_len=t.sub_len.data_ptr(),
-                lut1=tb["lut1"].data_ptr(), lut2=tb["lut2"].data_ptr(), n_lut2=tb["lut2"].numel(),
-                canon=tb["canon"].data_ptr(), canon_pay=tb["pay"].data_ptr(), value_cb=None,
-                C=tb["codebook"].numel(), stage_words=tb["stage_words"])
-        import ctypes
-        from gpu_huffman_functions import (build_columns, build_split, columns_eligible,
-                                           decode_symbols, split_bytes)
-        # split format (the single-token GEMV's format), decoded from
-        # each matrix's own stream; column layout for the gate/up comparison
-        splits = {}
-        for n, t in huff.items():
-            M, K = t.shape
-            if K % 4096 == 0:
-                idx = decode_symbols(t.words, t.chunk_off, t.sub_len, t.lengths, M * K, dev)
-                sp = build_split(idx, t.tables["codebook"].cpu().numpy(), dev)
-                del idx
-                if sp is not None:
-                    splits[n] = sp
-        cols = {}
-        for n in gu:
-            t = huff[n]
-            if columns_eligible(descs[n], t.shape[1]):
-                cols[n] = build_columns(descs[n], t.shape[0] * t.shape[1], dev, t.lengths,
-                                        t.tables["codebook"].cpu().numpy())
-        torch.cuda.synchronize()
-        log(f"split format for {len(splits)} of {len(huff)} Huffman tensors")
-
-        def split_args(ns):
-            k = len(ns)
-            return (k, (ctypes.POINTER(nat.SplitMatrix) * k)(*[ctypes.pointer(splits[n][1])
-                                                               for n in ns]),
-                    (ctypes.c_void_p * k)(*[outs[n].data_ptr() for n in ns]),
-                    (ctypes.c_int * k)(*[huff[n].shape[0] for n in ns]), huff[ns[0]].shape[1])
-
-        def launch_split(a):
-            k, mats, out_a, m_a, K = a
-            rc = lib.cbq_split_linear_f32(xs[K].data_ptr(), None, None, 0, 0.0, k, mats, out_a,
-                                          m_a, K, nat.stream_ptr(dev))
-            if rc:
-                raise RuntimeError(f"split GEMV rc={rc}")
-
-        def launch_huff(ns):
-            st = nat.stream_ptr(dev)
-            for n in ns:
-                M, K = huff[n].shape
-                if n in splits:
-                    launch_split(single[n])
-                    continue
-                rc = lib.cbq_huff_linear_f32(xs[K].data_ptr(), ctypes.byref(descs[n]),
-                                             outs[n].data_ptr(), 1, M, K, st)
-                if rc:
-                    raise RuntimeError(f"Huffman GEMV rc={rc} on {n}")
-
-        def launch_cols(ns):
-            st = nat.stream_ptr(dev)
-            for n in ns:
-                M, K = huff[n].shape
-                rc = lib.cbq_huff_linear_col_f32(xs[K].data_ptr(), ctypes.byref(descs[n]),
-                                                 ctypes.byref(cols[n][1]), outs[n].data_ptr(),
-                                                 M, K, st)
-                if rc:
-                    raise RuntimeError(f"column GEMV rc={rc} on {n}")
-
-        single = {n: split_args([n]) for n in splits}
-        # the decoder's launches: per layer q/k/v and gate/up grouped (one code
-        # each, one launch), o, down; then the lm_head
-        n_arr = {}
-        groups = []
-        for i in range(dec.cfg["layers"]):
-            p = f"model.layers.{i}."
-            for parts in (("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj"),
-                          ("mlp.gate_proj", "mlp.up_proj")):
-                ns = [p + n for n in parts]
-                if all(n in splits for n in ns):
-                    n_arr[ns[0]] = split_args(ns)
-                    groups.append(ns[0])
-                else:
-                    groups += ns
-            groups += [p + "self_attn.o_proj", p + "mlp.down_proj"]
-        groups += [n for n in names if "layers" not in n]
-
-        def launch_huff_step():
-            for n in groups:
-                if n in n_arr:
-                    launch_split(n_arr[n])
-                else:
-                    launch_huff([n])
-
-        hbytes = sum(huff_bytes(t) for t in huff.values())
-        sbytes = sum(split_bytes(splits[n][0]) + 4 * (huff[n].shape[0] + huff[n].shape[1])
-                     if n in splits else huff_bytes(huff[n]) for n in huff)
-        ms_h, _ = timed_graph(torch, launch_huff_step, args.steps, args.warmup)
-        ms_hgu, _ = timed_graph(torch, lambda: launch_huff(gu), args.steps, args.warmup)
-        us_hgu = ms_hgu * 1e3 / len(gu)
-        g0 = huff[gu[0]]
-        sb_gu = split_bytes(splits[gu[0]][0]) + 4 * (g0.shape[0] + g0.shape[1])
-        us_cgu = None
-        if all(n in cols for n in gu):
-            ms_cgu, _ = timed_graph(torch, lambda: launch_cols(gu), args.steps, args.warmup)
-            us_cgu = ms_cgu * 1e3 / len(gu)
-        # the decoder's gate/up launch: both matrices in one grouped launch
-        # (timed last, after the column-layout comparison)
-        gug = [n for n in n_arr if n.endswith("mlp.gate_proj")]
-        us_gg = b_gg = None
-        if gug:
-            ms_gg, _ = timed_graph(torch, lambda: [launch_split(n_arr[n]) for n in gug],
-                                   args.steps, args.warmup)
-            us_gg = ms_gg * 1e3 / len(gug)
-            up0 = gug[0].replace("gate_proj", "up_proj")
-            b_gg = (split_bytes(splits[gug[0]][0]) + split_bytes(splits[up0][0])
-                    + 4 * (g0.shape[0] + huff[up0].shape[0] + g0.shape[1]))
+        splits, stream_bytes = build_split_formats(torch, dev, huff, names)
+        log(f"built {len(huff)} Huffman tensors, {len(splits)} split formats, in "
+            f"{time.time() - t0:.1f}s")
+        ms_h, sbytes = huffman_sweep(torch, nat, lib, dev, huff, splits, plan, args.steps,
+                                     args.warmup)
+        hbytes = sum(stream_bytes.values())
         n_w = sum(h.shape[0] * h.shape[1] for h in huff.values())
+        res_b = sum(split_bytes(splits[n][0]) for n in names)
+        gate_up = [e for e in plan if isinstance(e, tuple) and e[0].endswith("mlp.gate_proj")]
+        ms_gg, b_gg = huffman_sweep(torch, nat, lib, dev, huff, splits, gate_up, args.steps,
+                                    args.warmup)
+        us_gg = ms_gg * 1e3 / len(gate_up)
+        b_gg //= len(gate_up)
+        s_gg = sum(stream_bytes[n] for n in gate_up[0]) + 4 * (
+            sum(huff[n].shape[0] for n in gate_up[0]) + huff[gate_up[0][0]].shape[1])
+        ach = b_gg / (us_gg * 1e-6) / 1e9
         result["huffman"] = {
             "value": round(sbytes / (ms_h * 1e-3) / 1e9, 1), "unit": "GB/s",
             "ms_per_step": round(ms_h, 4), "bytes_per_step": sbytes,
             "format": "split (raw low byte of bf16, <=7-bit Huffman code of the high byte), "
-                      "built on the GPU from each matrix's canonical-Huffman index stream",
+                      "built on the GPU from each matrix's canonical-Huffman index stream, "
+                      "which is then freed: the only resident format",
             "stream_bytes_per_step": hbytes,
             "stream_equivalent_GB/s": round(hbytes / (ms_h * 1e-3) / 1e9, 1),
-            "launches_per_step": len(groups),
-            "bits_per_weight_split": round(8.0 * sbytes / n_w, 3),
-            "bits_per_weight_stream_incl_index": round(
-                8.0 * sum(h.nbytes for h in huff.values()) / n_w, 3),
+            "launches_per_step": len(plan),
+            "bits_per_weight_resident": round(8.0 * res_b / n_w, 3),
+            "bits_per_weight_stream_incl_index": round(8.0 * hbytes / n_w, 3),
             "weight_stream_tok_per_s": round(1000.0 / ms_h, 1),
-            "column_kernel_gate_up_us_per_launch": None if us_cgu is None else round(us_cgu, 2),
-            "single_matrix_gate_up": {"us_per_launch": round(us_hgu, 2), "bytes_per_launch": sb_gu,
-                                      "GB/s": round(sb_gu / (us_hgu * 1e-6) / 1e9, 1)}}
-        if us_gg is not None:
-            ach = b_gg / (us_gg * 1e-6) / 1e9
-            result["huffman"]["roofline"] = {
+            "roofline": {
                 "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(ach / HBM_PEAK_GBPS, 4),
+                "stream_equivalent_achieved": round(s_gg / (us_gg * 1e-6) / 1e9, 1),
+                "stream_equivalent_frac": round(s_gg / (us_gg * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
                 "traffic": read_traffic("split_gemv_kernel_gate_up_qwen3-8b_pmc.md"),
                 "kernel": "split_gemv_kernel<16> grouped gate+up, 2 x 4096->12288 in one launch",
-                "bytes_per_launch": b_gg, "us_per_launch": round(us_gg, 2)}
-        log(f"huffman sweep (split format): {ms_h:.3f} ms/step, {sbytes / 1e9:.2f} GB/step, "
-            f"{len(groups)} launches; gate/up {us_hgu:.2f} us (column kernel {us_cgu} us), "
-            f"grouped gate+up {us_gg} us")
+                "bytes_per_launch": b_gg, "us_per_launch": round(us_gg, 2)}}
+        log(f"huffman sweep (split format): {ms_h:.3f} ms/step, {sbytes / 1e9:.2f} GB/step; "
+            f"grouped gate+up {us_gg:.2f} us; {8.0 * res_b / n_w:.3f} bits/weight resident")
+        del huff, splits
+        torch.cuda.empty_cache()
+
+    if not args.no_1p7b and args.config == "qwen3-8b" and args.layers is None:
+        result["qwen3_1_7b"] = sweep_1p7b(torch, nat, lib, dev, synthetic, args)
+        log(f"1.7B sweeps: {result['qwen3_1_7b']['fixed']['sweep']}")
 
     if not args.no_e2e:
         result["e2e"] = e2e_section(torch, dec, args)

@@ -18,6 +18,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 SO_PATH = os.path.join(HERE, "libcbq_hip.so")
 
 CK_SUCCESS, CK_ERR_HIP, CK_ERR_ARG = 0, 1, 2
+ARGMAX_WORKSPACE = 8192                          # CBQ_ARGMAX_WORKSPACE of include/cbq_hip.h
 XF_SILU, XF_ADD_RMS, XF_RMS = 1, 2, 3            # CBQ_XF_* of include/cbq_hip.h
 
 _vp = ctypes.c_void_p
@@ -89,6 +90,12 @@ SIGNATURES = {
     "cbq_split_pack": (_i, [_vp, _i64, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
     "cbq_split_linear_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _i, _vp, _vp, _vp, _i,
                                   _vp]),
+    "cbq_linear_xform_argmax_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _i,
+                                         _i, _i, _i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _i64,
+                                         _i64, _vp]),
+    "cbq_split_linear_argmax_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float,
+                                         ctypes.POINTER(SplitMatrix), _vp, _i, _i, _vp,
+                                         ctypes.c_size_t, _vp, _vp, _vp, _i64, _i64, _vp]),
     # include/cbq_decode.h
     "cbq_add_rmsnorm_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, ctypes.c_float, _vp]),
     "cbq_head_norm_rope_f32": (_i, [_vp] * 11 + [_i] * 5 + [ctypes.c_float, _vp]),

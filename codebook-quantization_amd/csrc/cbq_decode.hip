@@ -566,13 +566,6 @@ __global__ __launch_bounds__(HD) void attn_combine_kernel(const float *__restric
 constexpr int kArgThreads = 512;
 constexpr int kArgBlocks = 128;
 
-__device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib)
-{
-    const bool na = a != a, nb = b != b;
-    if (na || nb) return na && (!nb || ia < ib);
-    return a > b || (a == b && ia < ib);
-}
-
 __device__ __forceinline__ void arg_block_reduce(float &best, int &bi, float *s_v, int *s_i)
 {
     for (int o = CBQ_WAVE >> 1; o > 0; o >>= 1) {
@@ -625,6 +618,32 @@ __global__ __launch_bounds__(kArgBlocks) void argmax_final_kernel(
     }
 }
 
+// Merge of the (value, index) pairs a fused GEMV + pick wrote (one per
+// block), then the step bookkeeping of argmax_final_kernel.
+constexpr int kMergeThreads = 1024;
+
+__global__ __launch_bounds__(kMergeThreads) void argmax_merge_kernel(
+    const float *__restrict__ part_v, const int *__restrict__ part_i, int n_part, int n,
+    int32_t *__restrict__ ids32, int64_t *__restrict__ toks, int64_t *__restrict__ pos,
+    int64_t first, int64_t n_toks)
+{
+    __shared__ float s_v[kMergeThreads / CBQ_WAVE];
+    __shared__ int s_i[kMergeThreads / CBQ_WAVE];
+    float best = -INFINITY;
+    int bi = kArgNone;
+    for (int i = threadIdx.x; i < n_part; i += kMergeThreads)
+        if (arg_better(part_v[i], part_i[i], best, bi)) { best = part_v[i]; bi = part_i[i]; }
+    arg_block_reduce(best, bi, s_v, s_i);
+    if (threadIdx.x == 0) {
+        const int tok = bi < n ? bi : 0;
+        ids32[0] = tok;
+        const int64_t p = pos[0];
+        const int64_t kk = p - first;
+        if (kk >= 0 && kk < n_toks) toks[kk] = tok;
+        pos[0] = p + 1;
+    }
+}
+
 __global__ __launch_bounds__(kGlueBlock) void silu_mul_kernel(const float *__restrict__ g,
                                                              const float *__restrict__ u,
                                                              float *__restrict__ out, int64_t n)
@@ -637,6 +656,15 @@ __global__ __launch_bounds__(kGlueBlock) void silu_mul_kernel(const float *__res
 }
 
 }  // namespace
+
+int cbq_argmax_merge(const float *part_v, const int *part_i, int n_part, int n, int32_t *ids32,
+                     int64_t *toks, int64_t *pos, int64_t first, int64_t n_toks,
+                     hipStream_t stream)
+{
+    hipLaunchKernelGGL(argmax_merge_kernel, dim3(1), dim3(kMergeThreads), 0, stream, part_v,
+                       part_i, n_part, n, ids32, toks, pos, first, n_toks);
+    return cbq_launch_status("argmax_merge_kernel");
+}
 
 // Static split-partials scratch of cbq_attn_rope_decode_noalloc_f32, one
 // copy per device, held for the life of the process.  Host code never passes

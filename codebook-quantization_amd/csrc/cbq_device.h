@@ -24,6 +24,57 @@ static inline int cbq_launch_status(const char *what)
 // Number of compute units of the current device (cached per device id).
 int cbq_num_cus();
 
+// ---- greedy pick (argmax) ----------------------------------------------------
+// Order of (value, index) candidates: the larger value, then the smaller
+// index; NaN ranks highest (the first NaN wins), as torch.argmax.  An empty
+// candidate is (-inf, kArgNone): it loses to every real index.
+constexpr int kArgNone = 0x7fffffff;
+
+__device__ __forceinline__ bool arg_better(float a, int ia, float b, int ib)
+{
+    const bool na = a != a, nb = b != b;
+    if (na || nb) return na && (!nb || ia < ib);
+    return a > b || (a == b && ia < ib);
+}
+
+__device__ __forceinline__ void arg_wave_reduce(float &best, int &bi)
+{
+    for (int o = CBQ_WAVE >> 1; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, CBQ_WAVE);
+        const int oi = __shfl_xor(bi, o, CBQ_WAVE);
+        if (arg_better(ov, oi, best, bi)) { best = ov; bi = oi; }
+    }
+}
+
+// The block's best candidate into part_v / part_i [blockIdx.x]; every thread
+// of the block calls it.  s_v / s_i: one slot per wave.
+__device__ __forceinline__ void arg_block_store(float best, int bi, float *s_v, int *s_i,
+                                                float *part_v, int *part_i)
+{
+    arg_wave_reduce(best, bi);
+    if ((threadIdx.x & (CBQ_WAVE - 1)) == 0) {
+        s_v[threadIdx.x / CBQ_WAVE] = best;
+        s_i[threadIdx.x / CBQ_WAVE] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x / CBQ_WAVE); w++)
+            if (arg_better(s_v[w], s_i[w], best, bi)) { best = s_v[w]; bi = s_i[w]; }
+        part_v[blockIdx.x] = best;
+        part_i[blockIdx.x] = bi;
+    }
+}
+
+// Second launch of a fused greedy pick (cbq_decode.hip): merges n_part
+// (value, index) pairs, then ids32[0] = tok; toks[pos[0] - first] = tok when
+// that index lies in [0, n_toks); pos[0] += 1 (tok = 0 when no candidate
+// is below n).
+int cbq_argmax_merge(const float *part_v, const int *part_i, int n_part, int n, int32_t *ids32,
+                     int64_t *toks, int64_t *pos, int64_t first, int64_t n_toks,
+                     hipStream_t stream);
+// Bytes of the pairs a fused GEMV + pick writes: one per block, at most 1024.
+constexpr int kArgMaxParts = 1024;
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t h)
 {
     return __uint_as_float((uint32_t)h << 16);

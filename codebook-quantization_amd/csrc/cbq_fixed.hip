@@ -382,9 +382,13 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     const XT *__restrict__ x, const uint32_t *__restrict__ words,
     const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C,
     uint32_t aff_lo, uint32_t aff_w, const float *__restrict__ x1, float *__restrict__ h_out,
-    float eps, int Kfull, int k0, int accum)
+    float eps, int Kfull, int k0, int accum, float *__restrict__ arg_v = nullptr,
+    int *__restrict__ arg_i = nullptr)
 {
     static_assert(!KCHUNK || (XMODE == XF_NONE && !AFFINE), "column ranges: plain x only");
+    // arg_v / arg_i (T = 1): besides writing out (when out is not null), the
+    // block reduces its rows to one (max, first index) pair of the greedy
+    // pick, written to arg_v / arg_i [blockIdx.x].
     constexpr bool PADDED = BITS <= 14 && !AFFINE;
     constexpr int D = kStreamD;
     __shared__ float s_cbp[PADDED ? (1 << BITS) : 1];
@@ -475,6 +479,8 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     float acc[TMAX], res[TMAX];
 #pragma unroll
     for (int t = 0; t < TMAX; t++) acc[t] = res[t] = 0.f;
+    float a_best = -INFINITY;                      // greedy-pick candidate of this lane
+    int a_idx = kArgNone;
     int ri = 0, ch = 0, base = 0;
     do {
 #pragma unroll
@@ -529,9 +535,15 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
                 ri++;
                 if ((ri & 63) == 0 && ri <= rows) {
                     const int row = wid + (ri - 64 + lane) * W;
+                    if (out) {
 #pragma unroll
-                    for (int t = 0; t < TMAX; t++)
-                        if (t < T) put_out_t<KCHUNK>(out + (size_t)t * M + row, res[t], accum);
+                        for (int t = 0; t < TMAX; t++)
+                            if (t < T) put_out_t<KCHUNK>(out + (size_t)t * M + row, res[t], accum);
+                    }
+                    if (arg_v && arg_better(res[0], row, a_best, a_idx)) {
+                        a_best = res[0];
+                        a_idx = row;
+                    }
                 }
             }
         }
@@ -540,9 +552,20 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     const int rb = rows & ~63;
     if (lane < rows - rb) {
         const int row = wid + (rb + lane) * W;
+        if (out) {
 #pragma unroll
-        for (int t = 0; t < TMAX; t++)
-            if (t < T) put_out_t<KCHUNK>(out + (size_t)t * M + row, res[t], accum);
+            for (int t = 0; t < TMAX; t++)
+                if (t < T) put_out_t<KCHUNK>(out + (size_t)t * M + row, res[t], accum);
+        }
+        if (arg_v && arg_better(res[0], row, a_best, a_idx)) {
+            a_best = res[0];
+            a_idx = row;
+        }
+    }
+    if (arg_v) {                                   // uniform: every thread takes part
+        __shared__ float s_av[kStreamWaves];
+        __shared__ int s_ai[kStreamWaves];
+        arg_block_store(a_best, a_idx, s_av, s_ai, arg_v, arg_i);
     }
 }
 
@@ -991,6 +1014,56 @@ int cbq_linear_xform_f32(const float *x0, const float *x1, float *h_out, int mod
 #undef CBQ_XF_MODES
 #undef CBQ_XF
     return cbq_launch_status("fixed_stream_kernel<xform>");
+}
+
+int cbq_linear_xform_argmax_f32(const float *x0, const float *x1, float *h_out, int mode,
+                                float eps, const uint8_t *packed, const float *codebook,
+                                float *out, int M, int K, int C, int bits, void *workspace,
+                                size_t workspace_bytes, int32_t *ids32, int64_t *toks,
+                                int64_t *pos, int64_t first, int64_t n_toks, hipStream_t stream)
+{
+    if (!x0 || !packed || !codebook || M <= 0 || K <= 0 || K % 32 != 0 || C <= 0 ||
+        C > kMaxLdsCodebook || !workspace || !ids32 || !toks || !pos || n_toks <= 0)
+        return CK_ERR_ARG;
+    if (mode < XF_NONE || mode > XF_RMS || ((mode == XF_SILU || mode == XF_ADD_RMS) && !x1))
+        return CK_ERR_ARG;
+    if (mode >= XF_ADD_RMS && K > 16384) return CK_ERR_ARG;
+    if (((uintptr_t)packed & 3) != 0 || ((uintptr_t)x0 & 3) != 0 ||
+        ((uintptr_t)workspace & 3) != 0 || workspace_bytes < CBQ_ARGMAX_WORKSPACE)
+        return CK_ERR_ARG;
+    const int blocks =
+        std::max(1, std::min(cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
+    if (blocks > kArgMaxParts) return CK_ERR_ARG;
+    float *part_v = (float *)workspace;
+    int *part_i = (int *)(part_v + kArgMaxParts);
+    size_t dyn = 0;
+#define CBQ_XA(B, MODE)                                                                        \
+    hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE>), dim3(blocks),    \
+                       dim3(kStreamBlock), dyn, stream, x0, (const uint32_t *)packed, codebook, \
+                       out, 1, M, K, C, 0u, 0u, x1, h_out, eps, K, 0, 0, part_v, part_i)
+#define CBQ_XA_MODES(B)                                                                        \
+    do {                                                                                       \
+        dyn = stream_dyn_lds<B, float>(1, K, C);                                               \
+        if (!dyn) return CK_ERR_ARG;                                                           \
+        if (mode == XF_SILU) CBQ_XA(B, XF_SILU);                                               \
+        else if (mode == XF_ADD_RMS) CBQ_XA(B, XF_ADD_RMS);                                    \
+        else if (mode == XF_RMS) CBQ_XA(B, XF_RMS);                                            \
+        else CBQ_XA(B, XF_NONE);                                                               \
+    } while (0)
+    switch (bits) {
+    case 8: CBQ_XA_MODES(8); break;
+    case 10: CBQ_XA_MODES(10); break;
+    case 11: CBQ_XA_MODES(11); break;
+    case 12: CBQ_XA_MODES(12); break;
+    case 13: CBQ_XA_MODES(13); break;
+    case 14: CBQ_XA_MODES(14); break;
+    default: return CK_ERR_ARG;
+    }
+#undef CBQ_XA_MODES
+#undef CBQ_XA
+    const int rc = cbq_launch_status("fixed_stream_kernel<argmax>");
+    if (rc) return rc;
+    return cbq_argmax_merge(part_v, part_i, blocks, M, ids32, toks, pos, first, n_toks, stream);
 }
 
 int cbq_linear_affine_f32(const float *x, const uint8_t *packed, uint32_t lo, uint32_t w,

@@ -160,7 +160,9 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
                                                                    SplitSegs segs, int K,
                                                                    const float *__restrict__ x1,
                                                                    float *__restrict__ h_out,
-                                                                   float eps)
+                                                                   float eps,
+                                                                   float *__restrict__ arg_v,
+                                                                   int *__restrict__ arg_i)
 {
     int sidx = 0;
 #pragma unroll
@@ -214,6 +216,8 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
     if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS)
         xr_scale = tile.finish(K, eps, s_x);      // s_x is staged after the next barrier
     const bool store_h = XMODE == XF_ADD_RMS && blockIdx.x == 0 && h_out != nullptr;
+    float a_best = -INFINITY;                      // greedy-pick candidate of this lane
+    int a_idx = kArgNone;
 
     for (int seg = 0; seg < n_seg; seg++) {
         float res[GR];
@@ -270,8 +274,19 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
         if (lane < seg_rows) {
             const int64_t g = wid + (int64_t)(seg * 64 + lane) * W;
 #pragma unroll
-            for (int q = 0; q < GR; q++) S.out[g * GR + q] = res[q];
+            for (int q = 0; q < GR; q++) {
+                if (S.out) S.out[g * GR + q] = res[q];
+                if (arg_v && arg_better(res[q], (int)(g * GR + q), a_best, a_idx)) {
+                    a_best = res[q];
+                    a_idx = (int)(g * GR + q);
+                }
+            }
         }
+    }
+    if (arg_v) {                                   // one matrix per launch (checked on the host)
+        __shared__ float s_av[NW];
+        __shared__ int s_ai[NW];
+        arg_block_store(a_best, a_idx, s_av, s_ai, arg_v, arg_i);
     }
 }
 
@@ -525,12 +540,19 @@ int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits
     return cbq_launch_status("split_to_packed_kernel");
 }
 
-int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode, float eps, int n,
-                         const cbq_split_matrix *const *mats, float *const *outs, const int *Ms,
-                         int K, hipStream_t stream)
+}  // extern "C"
+
+namespace {
+
+// cbq_split_linear_f32, with the greedy-pick pairs of every block written to
+// arg_v / arg_i when those are not null (one matrix; outs[0] may be null).
+int split_linear(const float *x, const float *x1, float *h_out, int mode, float eps, int n,
+                 const cbq_split_matrix *const *mats, float *const *outs, const int *Ms, int K,
+                 float *arg_v, int *arg_i, int *n_blocks, hipStream_t stream)
 {
     if (!x || n < 1 || n > kSMaxSeg || !mats || !outs || !Ms || K <= 0 || K % 1024 != 0)
         return CK_ERR_ARG;
+    if (arg_v && n != 1) return CK_ERR_ARG;
     const int GR = K % kSChunk == 0 ? 1 : K % 2048 == 0 ? 2 : 4;   // 4096 / gcd(K, 4096)
     if (mode < XF_NONE || mode > XF_RMS || ((mode == XF_SILU || mode == XF_ADD_RMS) && !x1) ||
         (mode >= XF_ADD_RMS && K > 16384))
@@ -539,7 +561,8 @@ int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode
     segs.n = n;
     for (int i = 0; i < n; i++) {
         const cbq_split_matrix *m = mats[i];
-        if (!m || !m->cwords || !m->row_off || !m->raw || !m->lut || !outs[i] || Ms[i] <= 0)
+        if (!m || !m->cwords || !m->row_off || !m->raw || !m->lut || (!outs[i] && !arg_v) ||
+            Ms[i] <= 0)
             return CK_ERR_ARG;
         if (Ms[i] % GR != 0 || m->n_chunks * kSChunk != (int64_t)Ms[i] * K) return CK_ERR_ARG;
         if (((uintptr_t)m->raw & 15) != 0 || ((uintptr_t)m->lut & 15) != 0 ||
@@ -574,7 +597,7 @@ int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode
     }
 #define CBQ_SPLIT_GR(NWV, MODE, G)                                                                \
     hipLaunchKernelGGL((split_gemv_kernel<NWV, MODE, G>), dim3(blocks), dim3(NWV * CBQ_WAVE), 0,  \
-                       stream, x, segs, K, x1, h_out, eps)
+                       stream, x, segs, K, x1, h_out, eps, arg_v, arg_i)
 #define CBQ_SPLIT(NWV, MODE)                                                                      \
     do {                                                                                          \
         if (GR == 1) CBQ_SPLIT_GR(NWV, MODE, 1);                                                  \
@@ -594,7 +617,39 @@ int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode
 #undef CBQ_SPLIT_MODES
 #undef CBQ_SPLIT
 #undef CBQ_SPLIT_GR
+    if (n_blocks) *n_blocks = blocks;
     return cbq_launch_status("split_gemv_kernel");
+}
+
+}  // namespace
+
+extern "C" {
+
+int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode, float eps, int n,
+                         const cbq_split_matrix *const *mats, float *const *outs, const int *Ms,
+                         int K, hipStream_t stream)
+{
+    return split_linear(x, x1, h_out, mode, eps, n, mats, outs, Ms, K, nullptr, nullptr, nullptr,
+                        stream);
+}
+
+int cbq_split_linear_argmax_f32(const float *x0, const float *x1, float *h_out, int mode,
+                                float eps, const cbq_split_matrix *m, float *out, int M, int K,
+                                void *workspace, size_t workspace_bytes, int32_t *ids32,
+                                int64_t *toks, int64_t *pos, int64_t first, int64_t n_toks,
+                                hipStream_t stream)
+{
+    if (!m || !workspace || ((uintptr_t)workspace & 3) != 0 ||
+        workspace_bytes < CBQ_ARGMAX_WORKSPACE || !ids32 || !toks || !pos || n_toks <= 0)
+        return CK_ERR_ARG;
+    if (cbq_num_cus() > kArgMaxParts) return CK_ERR_ARG;
+    float *part_v = (float *)workspace;
+    int *part_i = (int *)(part_v + kArgMaxParts);
+    int blocks = 0;
+    const int rc = split_linear(x0, x1, h_out, mode, eps, 1, &m, &out, &M, K, part_v, part_i,
+                                &blocks, stream);
+    if (rc) return rc;
+    return cbq_argmax_merge(part_v, part_i, blocks, M, ids32, toks, pos, first, n_toks, stream);
 }
 
 }  // extern "C"

@@ -256,7 +256,9 @@ class Qwen3Decoder:
         c = self.cfg
         h = self.embed(ids_buf).reshape(1, c.hidden).to(torch.float32)
         if self.fused:
-            logits = self._forward1_fused(h, pos_buf)
+            logits = self._forward1_fused(h, pos_buf, pick=(ids_buf, toks, pos_buf, first_pos))
+            if logits is None:                      # the lm_head GEMV picked the token itself
+                return
         else:
             x = self.glue.add_rms(h, None)
             for i in range(c.layers):
@@ -264,10 +266,13 @@ class Qwen3Decoder:
             logits = self.linears["lm_head"](x).reshape(-1)
         self.glue.argmax_step(logits, ids_buf, toks, pos_buf, first_pos)
 
-    def _forward1_fused(self, h: torch.Tensor, pos_dev: torch.Tensor) -> torch.Tensor:
+    def _forward1_fused(self, h: torch.Tensor, pos_dev: torch.Tensor, pick=None):
         """One token through every layer with the norms and the SiLU product
         applied by the GEMVs that consume them; h [1, hidden] is the
-        embedding.  Returns the logits [vocab]."""
+        embedding.  Returns the logits [vocab]; with pick = (ids32, toks,
+        pos, first) and an lm_head that fuses the greedy pick
+        (`xform_argmax`), the pick is made in the lm_head GEMV instead
+        (cbq_argmax_step's bookkeeping) and None is returned."""
         import cbq_native as nat
         c = self.cfg
         L = self.linears
@@ -289,9 +294,12 @@ class Qwen3Decoder:
             h = h2
             delta = L[p + "mlp.down_proj"].xform(gu[:, :c.inter], gu[:, c.inter:], None,
                                                  nat.XF_SILU)
-        if delta is None:
-            return L["lm_head"].xform(h, None, None, nat.XF_RMS).reshape(-1)
-        return L["lm_head"].xform(h, delta, None, nat.XF_ADD_RMS).reshape(-1)
+        head = L["lm_head"]
+        mode = nat.XF_RMS if delta is None else nat.XF_ADD_RMS
+        if pick is not None and callable(getattr(head, "xform_argmax", None)):
+            head.xform_argmax(h, delta, mode, *pick)
+            return None
+        return head.xform(h, delta, None, mode).reshape(-1)
 
     @torch.no_grad()
     def generate_graph(self, prompt: List[int], n_new: int, timing: Optional[dict] = None):
@@ -420,6 +428,9 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
     lib = nat.load()
     dev = torch.device(device)
     resident: Dict[str, int] = {}               # device bytes of each matrix's format
+    # (max, index) pairs of the lm_head's fused greedy pick, allocated before
+    # any graph capture
+    argmax_ws = torch.empty(nat.ARGMAX_WORKSPACE, dtype=torch.uint8, device=dev)
 
     def sym_of(t):
         """Symbol-payload decode tables of a stream (for the split build and
@@ -485,7 +496,17 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                 t.codebook.data_ptr(), out.data_ptr(), M, K, t.codebook.numel(), t.bits,
                 nat.stream_ptr(dev)), "cbq_linear_xform_f32")
             return out
+
+        def xform_argmax(x0, x1, mode, ids32, toks, pos, first, out=None):
+            """One token, then the greedy pick in the GEMV's epilogue."""
+            nat.check(lib.cbq_linear_xform_argmax_f32(
+                x0.data_ptr(), None if x1 is None else x1.data_ptr(), None, mode, cfg.eps,
+                t.packed.data_ptr(), t.codebook.data_ptr(), nat.ptr(out), M, K,
+                t.codebook.numel(), t.bits, argmax_ws.data_ptr(), argmax_ws.numel(),
+                ids32.data_ptr(), toks.data_ptr(), pos.data_ptr(), first, toks.numel(),
+                nat.stream_ptr(dev)), "cbq_linear_xform_argmax_f32")
         f.xform = xform
+        f.xform_argmax = xform_argmax
         return f
 
     def huff_desc(t):
@@ -509,7 +530,16 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
             if x.shape[0] == 1:
                 return one(x)
             return split_prefill(sp, inv, x, M, K, cbt)
+
+        def xform_argmax(x0, x1, mode, ids32, toks, pos, first, out=None, keep=sp):
+            """One token, then the greedy pick in the GEMV's epilogue."""
+            nat.check(lib.cbq_split_linear_argmax_f32(
+                x0.data_ptr(), None if x1 is None else x1.data_ptr(), None, mode, cfg.eps,
+                ctypes.byref(sp[1]), nat.ptr(out), M, K, argmax_ws.data_ptr(), argmax_ws.numel(),
+                ids32.data_ptr(), toks.data_ptr(), pos.data_ptr(), first, toks.numel(),
+                nat.stream_ptr(dev)), "cbq_split_linear_argmax_f32")
         f.xform = sxform
+        f.xform_argmax = xform_argmax
         f.split = sp
         return f
 
@@ -570,7 +600,8 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         if isinstance(t, synthetic.HuffTensor):
             desc = huff_desc(t)
 
-            def e(ids, desc=desc):
+            # desc holds raw device pointers: keep the tensors they point at
+            def e(ids, desc=desc, keep=(t.words, t.chunk_off, t.sub_len, t.tables)):
                 ids = ids.reshape(-1).to(torch.int32)
                 out = torch.empty(ids.numel(), H, device=dev)
                 nat.check(lib.cbq_huff_embedding_f32(ids.data_ptr(), ctypes.byref(desc),

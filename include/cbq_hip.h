@@ -367,6 +367,34 @@ int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits
 /* Version string of the library build. */
 const char *cbq_version(void);
 
+/* ---- lm_head GEMV with the greedy pick fused ------------------------------
+ * The one-token GEMV of the decoder's last matrix (vocabulary rows) and the
+ * greedy pick of the next token in two launches: the GEMV's epilogue reduces
+ * each block's rows to one (max, first index) pair in `workspace`
+ * (>= CBQ_ARGMAX_WORKSPACE bytes, 4-byte aligned, overwritten by every
+ * call), and one merge block picks the token: ids32[0] = tok;
+ * toks[pos[0] - first] = tok when that index lies in [0, n_toks);
+ * pos[0] += 1.  Order as torch.argmax: first maximum, NaN highest.  out
+ * (the logits) is written when not NULL.  No counterpart in the reference,
+ * whose HF generate loop reads the logits back for the pick
+ * (chat.py:264-315); the logits never make a second trip through HBM and
+ * the separate reduction launch of cbq_argmax_step is saved.
+ * cbq_linear_xform_argmax_f32: fixed width, x = transform(x0, x1) as
+ * cbq_linear_xform_f32 (mode 0: x0 itself).
+ * cbq_split_linear_argmax_f32: one split-format matrix (Huffman), as
+ * cbq_split_linear_f32 with n = 1. */
+#define CBQ_ARGMAX_WORKSPACE 8192
+int cbq_linear_xform_argmax_f32(const float *x0, const float *x1, float *h_out, int mode,
+                                float eps, const uint8_t *packed, const float *codebook,
+                                float *out, int M, int K, int C, int bits, void *workspace,
+                                size_t workspace_bytes, int32_t *ids32, int64_t *toks,
+                                int64_t *pos, int64_t first, int64_t n_toks, hipStream_t stream);
+int cbq_split_linear_argmax_f32(const float *x0, const float *x1, float *h_out, int mode,
+                                float eps, const cbq_split_matrix *m, float *out, int M, int K,
+                                void *workspace, size_t workspace_bytes, int32_t *ids32,
+                                int64_t *toks, int64_t *pos, int64_t first, int64_t n_toks,
+                                hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
