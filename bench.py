@@ -365,11 +365,12 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
     transient fixed-width stream and ck_linear_f32)."""
     from gpu_huffman_functions import split_bytes, split_inverse, split_prefill
     dec = synthetic.SyntheticDecoder("qwen3-1.7b", log=log)
-    names = dec.all_linears(with_head=False)
+    tensors = dec.all_linears(with_head=False)
+    names = [n for n, _, _ in tensors]
     plan = step_plan(dec, with_head=False)
     out = {"layers": dec.cfg["layers"], "shapes": "q 2048->2048, k/v 2048->1024, o 2048->2048, "
                                                    "gate/up 2048->6144, down 6144->2048"}
-    fixed = dec.build_fixed(names)
+    fixed = dec.build_fixed(tensors)
     mats = fixed_launches(torch, nat, lib, dev, synthetic, fixed, plan)
     fx = {}
     for T in (1, 4, 16):
@@ -380,7 +381,7 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
     for kind, sel in (("q_proj", "self_attn.q_proj"), ("k_proj", "self_attn.k_proj"),
                       ("o_proj", "self_attn.o_proj"), ("gate_proj", "mlp.gate_proj"),
                       ("down_proj", "mlp.down_proj")):
-        ms_k = [fixed[n] for n, _, _ in names if n.endswith(sel)]
+        ms_k = [fixed[n] for n in names if n.endswith(sel)]
         ms, nb = fixed_sweep(torch, nat, lib, dev, ms_k, 1, max(3, args.steps // 2), 1)
         t = ms_k[0]
         per[kind] = {"shape": f"{t.shape[1]}->{t.shape[0]}",
@@ -390,7 +391,7 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
     del fixed, mats
     torch.cuda.empty_cache()
 
-    huff = dec.build_huffman(names)
+    huff = dec.build_huffman(tensors)
     splits, stream_bytes = build_split_formats(torch, dev, huff, names)
     ms1, nb1 = huffman_sweep(torch, nat, lib, dev, huff, splits, plan, args.steps, args.warmup)
     n_w = sum(huff[n].shape[0] * huff[n].shape[1] for n in names)
