@@ -84,6 +84,18 @@ def timed_graph(torch, fn, reps, warmup):
     return e0.elapsed_time(e1) / reps, g
 
 
+PREFILL_PROFILE = "fixed_prefill_kernel_qwen3-8b_T512_T2048.md"
+
+
+def read_profile_value(name, pattern, scale=1.0):
+    """A figure from a committed rocprofv3 summary, if any."""
+    p = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(p):
+        return None
+    m = re.search(pattern, open(p).read())
+    return round(float(m.group(1)) * scale, 4) if m else None
+
+
 def read_traffic(name):
     """HBM bytes per launch from a committed rocprofv3 PMC summary, if any."""
     p = os.path.join(ROOT, "profiles", name)
@@ -254,7 +266,10 @@ def prefill_section(torch, nat, lib, dev, fixed, kinds, args):
     g = out["shapes"]["T2048_gate_proj"]
     out["roofline"] = {"bound": "mfma", "achieved": g["TFLOP/s"], "peak": MFMA_BF16_PEAK_TFLOPS,
                        "unit": "TFLOP/s", "frac": g["frac"],
-                       "kernel": "fixed_prefill_kernel<13> gate/up 4096->12288, T=2048"}
+                       "kernel": "fixed_prefill_kernel<13> gate/up 4096->12288, T=2048",
+                       "mfma_busy_rocprof": read_profile_value(
+                           PREFILL_PROFILE, r"\*\*MFMA busy ([0-9.]+) %\*\*", 0.01),
+                       "profile": "profiles/" + PREFILL_PROFILE}
     return out
 
 
@@ -517,6 +532,9 @@ def main():
     ap.add_argument("--no-1p7b", action="store_true")
     ap.add_argument("--e2e-tokens", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="build the fixed-width weights, run only the prefill section and "
+                         "print its JSON (for counter runs)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only run a plain device copy of this many MiB (PMC calibration)")
@@ -550,6 +568,14 @@ def main():
     fixed = dec.build_fixed(tensors)
     torch.cuda.synchronize()
     log(f"built {len(fixed)} fixed-width tensors in {time.time() - t0:.1f}s")
+
+    if args.prefill_only:
+        kinds = {}
+        for n in names:
+            kinds.setdefault(n.split(".")[-1] if "layers" in n else n, []).append(n)
+        print(json.dumps({"prefill": prefill_section(torch, nat, lib, dev, fixed, kinds, args)}),
+              flush=True)
+        return
 
     plan = step_plan(dec)
     mats = fixed_launches(torch, nat, lib, dev, synthetic, fixed, plan)
