@@ -451,6 +451,72 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
     return out
 
 
+def image_roundtrip(torch, tensors, enc, meta):
+    """The direct-to-device load path on the e2e model: write `tensors` as a
+    device image under $TMPDIR, empty `tensors` (the caller's dict: its
+    device memory is freed), drop the file from the page cache
+    (fsync + POSIX_FADV_DONTNEED), load it back (cold: from the disk), free
+    that copy, load again (warm: from the page cache).  Returns the warm
+    load's tensors and the timings."""
+    import shutil
+    import tempfile
+    import cbq_image
+    dev = torch.device("cuda:0")
+    d = tempfile.mkdtemp(prefix="cbq_img_", dir=os.environ.get("TMPDIR", "/tmp"))
+    path = os.path.join(d, f"{enc}.cbq")
+    try:
+        need = sum(int(t.numel() * t.element_size()) for t in torch_tensors_of(tensors))
+        if shutil.disk_usage(d).free < 1.5 * need:
+            return tensors, {"skipped": f"less than 1.5 x {need} bytes free under {d}"}
+        t0 = time.perf_counter()
+        hdr = cbq_image.write_image(path, tensors, meta)
+        fd = os.open(path, os.O_RDONLY)
+        os.fsync(fd)
+        write_s = time.perf_counter() - t0
+        tensors.clear()
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        os.posix_fadvise(fd, 0, 0, os.POSIX_FADV_DONTNEED)
+        os.close(fd)
+        _, _, cold = cbq_image.load_image(path, dev, threads=8)
+        torch.cuda.empty_cache()
+        loaded, _, warm = cbq_image.load_image(path, dev, threads=8)
+        size = hdr["data_offset"] + hdr["payload_bytes"]
+        kinds = {}
+        for e in hdr["tensors"].values():
+            kinds[e["kind"]] = kinds.get(e["kind"], 0) + 1
+        log(f"image {enc}: {size / 1e9:.2f} GB, write+fsync {write_s:.1f}s, cold load "
+            f"{cold['total_s']:.2f}s ({cold['upload_GB/s']:.1f} GB/s), warm "
+            f"{warm['total_s']:.2f}s ({warm['upload_GB/s']:.1f} GB/s)")
+        return loaded, {"image_GB": round(size / 1e9, 3), "tensor_kinds": kinds,
+                        "write_fsync_s": round(write_s, 2),
+                        "cold_load_s": round(cold["total_s"], 3),
+                        "cold_upload_GB/s": round(cold["upload_GB/s"], 2),
+                        "warm_load_s": round(warm["total_s"], 3),
+                        "warm_upload_GB/s": round(warm["upload_GB/s"], 2),
+                        "threads": warm["threads"], "chunk_MiB": warm["chunk_mb"],
+                        "note": "cold: file dropped from the page cache after fsync, read "
+                                "from the box's disk; warm: the same file again from the page "
+                                "cache; load = header + one device allocation + "
+                                "cbq_file_upload + descriptor set-up, no host decode"}
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
+def torch_tensors_of(tensors):
+    """Every device tensor the image would store for `tensors`."""
+    import synthetic
+    out = []
+    for t in tensors.values():
+        if isinstance(t, synthetic.FixedTensor):
+            out.append(t.packed)
+        elif isinstance(t, synthetic.SplitTensor):
+            out += list(t.keep)
+        elif isinstance(t, synthetic.HuffTensor):
+            out += [t.words, t.chunk_off, t.sub_len]
+    return out
+
+
 def e2e_section(torch, dec, args):
     """always-compressed greedy decode of the random-init
     36-layer Qwen3-8B-shape decoder at batch 1: all linears, the lm_head and
@@ -461,9 +527,12 @@ def e2e_section(torch, dec, args):
     replayed.  The same model with fixed-width 13-bit indices (the same
     weights) runs too; both encodings' tokens are compared with the CPU
     oracle's golden tokens (tests/golden/e2e_qwen3_8b_golden.npz) when the
-    prompt is the golden's."""
+    prompt is the golden's.  Unless --no-load, each model is written as a
+    device image and the decoder runs from the image loaded back
+    (image_roundtrip)."""
     import numpy as np
     import decoder as D
+    import synthetic
     c = dec.cfg
     cfg = D.DecoderConfig(layers=c["layers"], hidden=c["hidden"], inter=c["inter"], n_q=c["n_q"],
                           n_kv=c["n_kv"], head_dim=c["head_dim"], vocab=c["vocab"])
@@ -481,12 +550,19 @@ def e2e_section(torch, dec, args):
     for enc in ("huffman", "fixed"):
         t0 = time.time()
         tensors = dec.build_huffman(names) if enc == "huffman" else dec.build_fixed(names)
+        if enc == "huffman":                # linears in the split format, embedding's stream
+            tensors = {n: t if n == dec.embed[0] else (synthetic.to_split(t) or t)
+                       for n, t in tensors.items()}
         torch.cuda.synchronize()
+        build_s = time.time() - t0
+        load = None
+        if not args.no_load:
+            tensors, load = image_roundtrip(torch, tensors, enc, {"config": dict(c),
+                                                                  "encoding": enc})
         model = D.from_synthetic(cfg, tensors, max_len=len(prompt) + n_new)
         del tensors                                # the model holds what it streams
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
-        build_s = time.time() - t0
         prefill = []                         # first call (allocator and module warm-up), then steady
         for _ in range(2):
             torch.cuda.synchronize()
@@ -508,6 +584,8 @@ def e2e_section(torch, dec, args):
                     "prefill_ms_128_tokens": round(prefill_s * 1e3, 1),
                     "prefill_ms_first_call": round(prefill[0] * 1e3, 1),
                     "build_s": round(build_s, 1), "first_tokens": toks[enc][:8]}
+        if load is not None:
+            out[enc]["load_from_device_image"] = load
         if golden is not None:
             k = min(len(golden), n_new)
             out[enc]["tokens_equal_oracle_golden"] = toks[enc][:k] == golden[:k]
@@ -529,6 +607,8 @@ def main():
     ap.add_argument("--no-huffman", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-e2e", action="store_true")
+    ap.add_argument("--no-load", action="store_true",
+                    help="e2e: skip the device-image write / load round trip")
     ap.add_argument("--no-1p7b", action="store_true")
     ap.add_argument("--e2e-tokens", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -16,7 +16,7 @@ CSRC = os.path.join(HERE, "csrc")
 SO = os.path.join(HERE, "libcbq_hip.so")
 ARCH = "gfx950"
 SOURCES = ["cbq_fixed.hip", "cbq_huffman.hip", "cbq_prefill.hip", "cbq_prefill_f32.hip",
-           "cbq_decode.hip", "cbq_split.hip", "cbq_tiny.hip"]
+           "cbq_decode.hip", "cbq_split.hip", "cbq_tiny.hip", "cbq_io.hip"]
 
 
 def hipcc() -> str:

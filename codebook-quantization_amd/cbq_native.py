@@ -50,6 +50,11 @@ class SplitMatrix(ctypes.Structure):
                 ("n_chunks", _i64)]
 
 
+class UploadPart(ctypes.Structure):
+    """struct cbq_upload_part (include/cbq_hip.h)."""
+    _fields_ = [("file_offset", _i64), ("nbytes", _i64), ("dst", _vp)]
+
+
 # name -> (restype, argtypes); every symbol declared in include/*.h
 SIGNATURES = {
     "ck_error_string": (ctypes.c_char_p, [_i]),
@@ -96,6 +101,8 @@ SIGNATURES = {
     "cbq_split_linear_argmax_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float,
                                          ctypes.POINTER(SplitMatrix), _vp, _i, _i, _vp,
                                          ctypes.c_size_t, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "cbq_file_upload": (_i, [ctypes.c_char_p, ctypes.POINTER(UploadPart), _i, ctypes.c_size_t,
+                             _i]),
     # include/cbq_decode.h
     "cbq_add_rmsnorm_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, ctypes.c_float, _vp]),
     "cbq_head_norm_rope_f32": (_i, [_vp] * 11 + [_i] * 5 + [ctypes.c_float, _vp]),

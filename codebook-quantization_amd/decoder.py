@@ -408,8 +408,9 @@ def from_compressed(cfg: DecoderConfig, comp: Dict[str, dict], device="cuda",
 def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda",
                    max_len: int = 512, stack: bool = True, fuse_glue: bool = True,
                    split: bool = True) -> Qwen3Decoder:
-    """Decoder over device-resident synthetic tensors (synthetic.FixedTensor /
-    HuffTensor, built on the GPU for the 9B-shape bench); calls the C ABI
+    """Decoder over device-resident tensors (device_formats.FixedTensor /
+    HuffTensor / SplitTensor: built on the GPU for the 9B-shape bench, or
+    loaded from a device image by cbq_image.load_image); calls the C ABI
     directly on torch's current stream.  With stack, each layer's q/k/v and
     gate/up run as one GEMV launch each instead of three / two: fixed-width
     rows are stacked into one matrix, Huffman matrices (one code each) share
@@ -417,7 +418,8 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
     codebook allow it is re-encoded into the split format (built from its
     decoded stream) and keeps only that format: closures hold the split
     format alone, so the caller may drop the HuffTensors' streams.  Others
-    keep their stream.  model.linear_bytes maps each launched matrix to its
+    keep their stream.  SplitTensors run in the split format whatever
+    `split` says.  model.linear_bytes maps each launched matrix to its
     device bytes."""
     import ctypes
     import cbq_native as nat
@@ -437,9 +439,16 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         the stream path's batched tokens)."""
         return SymbolDecoder(t.words, t.chunk_off, t.sub_len, t.lengths, dev)
 
+    def cb_of(t):
+        return t.codebook if isinstance(t, synthetic.SplitTensor) else t.tables["codebook"]
+
     def huff_split(t):
         """The split format of a Huffman tensor, or None when it does not
-        apply (then the stream stays the matrix's format)."""
+        apply (then the stream stays the matrix's format).  A SplitTensor
+        (loaded already in that format) is used as it is."""
+        if isinstance(t, synthetic.SplitTensor):
+            resident[t.name] = t.nbytes
+            return t.split
         M, K = t.shape
         if not split or not split_eligible(M, K):
             return None
@@ -548,7 +557,7 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         stream (every token count on the fused stream kernels; batched
         tokens >= 64 through a transient fixed-width stream)."""
         M, K = t.shape
-        cbt = t.tables["codebook"]
+        cbt = cb_of(t)
         sp = huff_split(t)
         if sp is not None:
             return split_linear(sp, M, K, cbt)
@@ -576,14 +585,15 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         gate/up), each with its own code; None when a part has no split
         format (the parts then run one by one)."""
         K = ts[0].shape[1]
-        if any(t.shape[1] != K for t in ts) or not split:
+        presplit = all(isinstance(t, synthetic.SplitTensor) for t in ts)
+        if any(t.shape[1] != K for t in ts) or not (split or presplit):
             return None
         sps = [huff_split(t) for t in ts]
         if not all(sp is not None for sp in sps):
             return None
         Ms = [t.shape[0] for t in ts]
         one, sxform = split_fns(sps, Ms, K)
-        singles = [split_linear(sp, t.shape[0], K, t.tables["codebook"])   # batched tokens
+        singles = [split_linear(sp, t.shape[0], K, cb_of(t))   # batched tokens
                    for t, sp in zip(ts, sps)]
 
         def g(x):
@@ -634,7 +644,7 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                 if st is not None:
                     linears[p + fused] = fixed_linear(st)
                     resident[p + fused] = st.nbytes
-            elif all(isinstance(t, synthetic.HuffTensor) for t in ts):
+            elif all(isinstance(t, (synthetic.HuffTensor, synthetic.SplitTensor)) for t in ts):
                 g = huff_group(ts, p + fused)
                 if g is not None:
                     linears[p + fused] = g
@@ -645,7 +655,7 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                  "gate_proj": "gate_up_proj", "up_proj": "gate_up_proj"}.get(leaf)
         if fused is not None and f"{stem}.{fused}" in linears:
             continue
-        if isinstance(t, synthetic.HuffTensor):
+        if isinstance(t, (synthetic.HuffTensor, synthetic.SplitTensor)):
             linears[n] = huff_linear(t)
         else:
             linears[n] = fixed_linear(t)

@@ -32,9 +32,20 @@ def _device_for(codebook: torch.Tensor) -> torch.device:
     return codebook.device if codebook.is_cuda else torch.device("cuda")
 
 
-def _upload_packed(indices_np, device) -> torch.Tensor:
-    arr = (np.ascontiguousarray(indices_np, dtype=np.uint8) if isinstance(indices_np, np.ndarray)
-           else indices_np.detach().cpu().numpy().astype(np.uint8))
+def index_bytes(indices, bits: int) -> np.ndarray:
+    """The packed index bytes of a stored 'indices' array.  The reference
+    keeps 8- and 16-bit indices unpacked as uint16 arrays
+    (src/adaptive_compressor.py:128-131): 8-bit values are the bytes
+    themselves, 16-bit values their little-endian byte pairs (the 16-bit
+    layout of src/bitpack.py).  Every other array already holds the bytes."""
+    arr = indices if isinstance(indices, np.ndarray) else indices.detach().cpu().numpy()
+    arr = np.ascontiguousarray(arr).reshape(-1)
+    if arr.dtype in (np.uint16, np.int16) and bits == 16:
+        return arr.astype("<u2", copy=False).view(np.uint8)
+    return arr.astype(np.uint8, copy=False)
+
+
+def _upload_packed(arr: np.ndarray, device) -> torch.Tensor:
     return torch.from_numpy(bitpack.device_padded(arr.reshape(-1))).to(device)
 
 
@@ -53,12 +64,11 @@ class GPUAcceleratedLinear:
         self.codebook = codebook.detach().to(device=device, dtype=torch.float32).contiguous()
         self.C = int(self.codebook.numel())
         need = bitpack.calculate_packed_size(self.M * self.K, self.bits)
-        src_len = (indices_np.size if isinstance(indices_np, np.ndarray)
-                   else int(indices_np.numel()))
-        if src_len < need:
-            raise ValueError(f"{name}: {src_len} packed bytes < {need} needed for "
+        raw = index_bytes(indices_np, self.bits)
+        if raw.size < need:
+            raise ValueError(f"{name}: {raw.size} packed bytes < {need} needed for "
                              f"{self.M}x{self.K} at {self.bits} bits")
-        self.packed = _upload_packed(indices_np, device)
+        self.packed = _upload_packed(raw, device)
 
     @property
     def compressed_bytes(self) -> int:
@@ -116,7 +126,7 @@ class GPUAcceleratedEmbedding:
         device = _device_for(codebook)
         self.codebook = codebook.detach().to(device=device, dtype=torch.float32).contiguous()
         self.C = int(self.codebook.numel())
-        self.packed = _upload_packed(indices_np, device)
+        self.packed = _upload_packed(index_bytes(indices_np, self.bits), device)
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         dev = self.codebook.device

@@ -14,7 +14,6 @@ tensor, src/adaptive_compressor.py:111-127) and the chunk index.
 from __future__ import annotations
 
 import zlib
-from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Tuple
 
 import numpy as np
@@ -22,6 +21,8 @@ import torch
 
 import codebook_builder as cbb
 import huffman_codebook as hc
+from device_formats import (FixedTensor, HuffTensor, SplitTensor, encode_fixed,  # noqa: F401
+                            encode_huffman, huffman_encode_torch, stack_fixed, to_split)
 
 # (name, out_features, in_features) per decoder layer
 def layer_shapes(hidden: int, inter: int, n_q: int, n_kv: int, head_dim: int):
@@ -121,88 +122,6 @@ def make_bf16(shape, name: str, std: float = 0.02, base_seed: int = 0,
     return out.view(torch.bfloat16).reshape(shape)
 
 
-@dataclass
-class FixedTensor:
-    name: str
-    shape: Tuple[int, int]
-    bits: int
-    category: str
-    packed: torch.Tensor            # uint8, device, padded
-    codebook: torch.Tensor          # float32, device
-
-    @property
-    def nbytes(self) -> int:
-        return (self.shape[0] * self.shape[1] * self.bits + 7) // 8
-
-
-def stack_fixed(parts, name: str) -> Optional[FixedTensor]:
-    """Row-stack fixed-width tensors that share K, the index width and the
-    codebook (q/k/v, gate/up): when every part's index stream ends on a byte
-    boundary, the concatenated bytes are exactly the packed stream of the
-    stacked [sum M, K] matrix, so one GEMV launch computes all parts.
-    None when the parts do not qualify."""
-    K, bits, cb = parts[0].shape[1], parts[0].bits, parts[0].codebook
-    for t in parts:
-        if (t.shape[1] != K or t.bits != bits or t.codebook.data_ptr() != cb.data_ptr()
-                or t.codebook.numel() != cb.numel() or (t.shape[0] * K * bits) % 8):
-            return None
-    M = sum(t.shape[0] for t in parts)
-    nb = (M * K * bits) // 8
-    packed = torch.zeros(((nb + 15) // 16) * 16 + 16, dtype=torch.uint8, device=cb.device)
-    o = 0
-    for t in parts:
-        packed[o:o + t.nbytes] = t.packed[:t.nbytes]
-        o += t.nbytes
-    return FixedTensor(name, (M, K), bits, parts[0].category, packed, cb)
-
-
-@dataclass
-class HuffTensor:
-    name: str
-    shape: Tuple[int, int]
-    category: str
-    lengths: np.ndarray
-    words: torch.Tensor             # int32 view of LSB-first words
-    chunk_off: torch.Tensor         # int64 (uint64 values)
-    sub_len: torch.Tensor           # int16 (uint16 values)
-    total_bits: int
-    tables: dict = field(default_factory=dict)
-
-    @property
-    def nbytes(self) -> int:
-        """Stream bytes + chunk table + sub-block table."""
-        return (self.total_bits + 7) // 8 + self.chunk_off.numel() * 8 + self.sub_len.numel() * 2
-
-
-def huffman_encode_torch(idx: torch.Tensor, lengths: np.ndarray):
-    """GPU canonical-Huffman encoder -> (int32 words, chunk_off, sub_len, bits).
-
-    Codes are bit-reversed and scattered LSB-first into 64-bit words; code
-    fields never overlap, so integer adds of the shifted fields equal their OR.
-    """
-    dev = idx.device
-    codes = hc.canonical_codes(lengths)
-    rev = hc._bitrev(codes, lengths.astype(np.int64)).astype(np.int64)
-    L_tab = torch.from_numpy(lengths.astype(np.int64)).to(dev)
-    R_tab = torch.from_numpy(rev).to(dev)
-    flat = idx.reshape(-1).to(torch.int64)
-    L = L_tab[flat]
-    starts = torch.cumsum(L, 0) - L
-    total = int(starts[-1] + L[-1])
-    words = torch.zeros(total // 64 + 3, dtype=torch.int64, device=dev)
-    w = starts >> 6
-    sh = starts & 63
-    r = R_tab[flat]
-    words.index_add_(0, w, r << sh)
-    spill = (sh + L) > 64
-    if bool(spill.any()):
-        words.index_add_(0, w[spill] + 1, r[spill] >> (64 - sh[spill]))
-    tot = torch.tensor([total], dtype=torch.int64, device=dev)
-    chunk_off = torch.cat([starts[::hc.CHUNK_SYMBOLS], tot])
-    sub_len = torch.diff(torch.cat([starts[::hc.SUB_SYMBOLS], tot])).to(torch.int16)
-    return words.view(torch.int32), chunk_off, sub_len, total
-
-
 class SyntheticDecoder:
     """All linear weights of a decoder (+ lm_head and embedding), compressed."""
 
@@ -241,13 +160,8 @@ class SyntheticDecoder:
         for name, M, K in tensors:
             cat = cbb.classify_tensor(name)
             cb, lut = books[cat]
-            bits = cbb.bits_for(cb.numel())
             idx = lut[cbb.patterns_torch(self._gen(name, M, K)).reshape(-1).to(torch.int64)]
-            pk = cbb.pack_torch(idx, bits)
-            padded = torch.zeros(((pk.numel() + 15) // 16) * 16 + 16, dtype=torch.uint8,
-                                 device=self.device)
-            padded[:pk.numel()] = pk
-            out[name] = FixedTensor(name, (M, K), bits, cat, padded, cb.contiguous())
+            out[name] = encode_fixed(name, idx, cb, (M, K), cat)
         return out
 
     def build_huffman(self, tensors, max_len: int = hc.DEFAULT_MAX_LEN) -> Dict[str, HuffTensor]:
@@ -257,20 +171,7 @@ class SyntheticDecoder:
             cat = cbb.classify_tensor(name)
             cb, lut = books[cat]
             idx = lut[cbb.patterns_torch(self._gen(name, M, K)).reshape(-1).to(torch.int64)]
-            C = cb.numel()
-            counts = torch.bincount(idx, minlength=C).cpu().numpy()
-            lengths = hc.length_limited_code_lengths(counts, max_len)
-            words, chunk_off, sub_len, total = huffman_encode_torch(idx, lengths)
-            cb_np = cb.cpu().numpy()
-            lut1, lut2, canon, pay = hc.device_luts(lengths, cb_np, C, value_payload=True)
-            t = HuffTensor(name, (M, K), cat, lengths, words, chunk_off, sub_len, total)
-            t.tables = dict(lut1=torch.from_numpy(lut1.view(np.int32)).to(self.device),
-                            lut2=torch.from_numpy(lut2.view(np.int32)).to(self.device),
-                            canon=torch.from_numpy(canon).to(self.device),
-                            pay=torch.from_numpy(pay).to(self.device),
-                            stage_words=hc.stage_words_for(chunk_off.cpu().numpy()),
-                            codebook=cb)
-            out[name] = t
+            out[name] = encode_huffman(name, idx, cb, (M, K), cat, max_len)
         return out
 
 

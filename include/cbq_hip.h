@@ -395,6 +395,30 @@ int cbq_split_linear_argmax_f32(const float *x0, const float *x1, float *h_out, 
                                 int64_t *toks, int64_t *pos, int64_t first, int64_t n_toks,
                                 hipStream_t stream);
 
+/* ==== direct-to-device load ============================================== */
+
+/* One byte range of a file and its device destination. */
+typedef struct cbq_upload_part {
+    int64_t file_offset;
+    int64_t nbytes;
+    void *dst;                   /* device memory, >= nbytes */
+} cbq_upload_part;
+
+/* Copy every part's bytes from the file at `path` to its device
+ * destination and return when all copies have completed.  n_threads reader
+ * threads (1..64) pread pieces of chunk_bytes (4 KiB .. 1 GiB) into two
+ * pinned host buffers each and hand each piece to the device with
+ * hipMemcpyAsync on the thread's own stream, so reads and copies overlap.
+ * The staging buffers and streams live for the call only; no device memory
+ * is allocated.  Destinations must not be in use by pending device work.
+ * CK_ERR_ARG for bad arguments, a file that cannot be opened or a range
+ * past its end (message on stderr), CK_ERR_HIP for runtime errors.
+ * No counterpart in the reference: it replaces the gzip .npz thread-pool
+ * preload (src/compressor.py:347-361) and the .idx mmap
+ * (src/compressed_matmul_cpu.py:23-63) on the way to the device. */
+int cbq_file_upload(const char *path, const cbq_upload_part *parts, int n_parts,
+                    size_t chunk_bytes, int n_threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -89,6 +89,15 @@ def test_argument_validation_before_launch(lib):
     assert hxf(p, p, None, 5, 1e-6, 1, one, one, one, m1, 4096, None) == 2      # unknown mode
     assert hxf(p, None, None, 3, 1e-6, 1, one, one, one, m1, 20480, None) == 2  # norm K > 16384
     assert hxf(p, None, None, 3, 1e-6, 5, one, one, one, m1, 4096, None) == 2   # > 4 matrices
+    # direct-to-device load: argument and file checks come before any HIP call
+    part = (cbq_native.UploadPart * 1)(cbq_native.UploadPart(0, 64, p))
+    up = lib.cbq_file_upload
+    assert up(b"/nonexistent/cbq.img", part, 1, 1 << 20, 2) == 2
+    assert up(__file__.encode(), part, 1, 100, 2) == 2                          # chunk < 4 KiB
+    assert up(__file__.encode(), part, 1, 1 << 20, 0) == 2                      # no threads
+    bad = (cbq_native.UploadPart * 1)(cbq_native.UploadPart(-1, 64, p))
+    assert up(__file__.encode(), bad, 1, 1 << 20, 2) == 2                       # negative offset
+    assert up(__file__.encode(), part, 0, 1 << 20, 2) == 0                      # nothing to copy
 
 
 def test_build_luts_rejects_overfull(lib):
