@@ -277,3 +277,54 @@ def replace_modules(model: nn.Module, cache: Dict[str, dict], global_codebooks: 
 
     walk(model, "")
     return replaced
+
+
+def replace_modules_from_image(model: nn.Module, image_path, device="cuda", threads: int = 8,
+                               resolve=lambda n: n, load_dense: bool = True):
+    """replace_modules over a device image (cbq_image): every nn.Linear /
+    nn.Embedding whose weight the image holds becomes an
+    AdaptiveCodebookLinear / AdaptiveCodebookEmbedding bound to the loaded
+    device tensors (no host decode, no re-encoding); an lm_head without its
+    own tensor uses model.embed_tokens' (tied weights); a Linear's bias is
+    kept.  With load_dense, every other image tensor whose name is a
+    parameter of the model (norm weights and the like) replaces that
+    parameter's data.  Returns (modules replaced, load statistics)."""
+    import cbq_image
+    from compressed_modules import AdaptiveCodebookEmbedding, AdaptiveCodebookLinear
+
+    tensors, _, stats = cbq_image.load_image(image_path, device, threads=threads)
+    replaced = 0
+
+    def walk(mod: nn.Module, prefix: str):
+        nonlocal replaced
+        for attr, child in list(mod.named_children()):
+            full = f"{prefix}.{attr}" if prefix else attr
+            wname = f"{full}.weight"
+            if isinstance(child, (nn.Linear, nn.Embedding)):
+                t = tensors.get(resolve(wname))
+                if t is None and isinstance(child, nn.Linear) and "lm_head" in full:
+                    t = tensors.get(resolve("model.embed_tokens.weight"))
+                if t is not None and not isinstance(t, torch.Tensor):
+                    if isinstance(child, nn.Linear):
+                        new = AdaptiveCodebookLinear.from_device(wname, t)
+                        if child.bias is not None:
+                            new.bias = child.bias.data.clone().detach()
+                    else:
+                        new = AdaptiveCodebookEmbedding.from_device(wname, t)
+                        if "scaled" in type(child).__name__.lower():
+                            dim = getattr(child, "embedding_dim", None)
+                            if dim and dim > 1:
+                                new.embed_scale = float(dim ** 0.5)
+                    setattr(mod, attr, new)
+                    replaced += 1
+                    continue
+            walk(child, full)
+
+    walk(model, "")
+    if load_dense:
+        params = dict(model.named_parameters())
+        for name, t in tensors.items():
+            p = params.get(resolve(name)) if isinstance(t, torch.Tensor) else None
+            if p is not None and tuple(p.shape) == tuple(t.shape):
+                p.data = t
+    return replaced, stats

@@ -29,8 +29,9 @@ directory name, compress.py:87-94) or --out:
   tensors/<safe name>.idx   raw packed indices (--export-idx, fixed width)
   device.cbq                the device image (cbq_image): every matrix in
                             the format the kernels read (fixed-width bytes;
-                            Huffman matrices in the split format where it
-                            applies, else the stream), loaded by
+                            Huffman linears in the split format where it
+                            applies, else the stream; embedding tables as
+                            streams), loaded by
                             cbq_image.load_image without host decode
 
 Codebooks, indices and streams are computed with torch integer ops on
@@ -185,7 +186,10 @@ def compress_checkpoint(model_dir, out_dir=None, entropy_code: bool = False,
             if write_npz:
                 cache_io.save_cached_tensor(tdir / f"{cache_io.safe_name(name)}.npz", name,
                                             npz_huffman(ht, row_starts, bits, cat))
-            st = dfm.to_split(ht, indices=idx) if dev.type == "cuda" else None
+            # embedding tables stay streams: rows are decoded on demand by the
+            # embedding kernel, which reads the stream's chunk index
+            table = "embed" in name.lower()
+            st = dfm.to_split(ht, indices=idx) if dev.type == "cuda" and not table else None
             image[name] = st if st is not None else ht
             summary["huffman"] += 1
             summary["split"] += st is not None

@@ -151,6 +151,29 @@ class AdaptiveCodebookLinear(nn.Module):
         return layer
 
 
+    @classmethod
+    def from_device(cls, name: str, t) -> "AdaptiveCodebookLinear":
+        """A weight already in HBM: a device_formats FixedTensor,
+        SplitTensor or HuffTensor (e.g. from cbq_image.load_image; bound to
+        the kernels as it is, nothing uploaded or re-encoded), or a dense
+        tensor (mode 'exact')."""
+        import device_formats as dfm
+        if isinstance(t, torch.Tensor):
+            layer = cls(name, tuple(t.shape), "exact")
+            layer.weight = nn.Parameter(t, requires_grad=False)
+            return layer
+        layer = cls(name, t.shape, "direct_codebook")
+        if isinstance(t, dfm.FixedTensor):
+            layer._gpu_func = GPUAcceleratedLinear.from_device(name, t)
+            cb = t.codebook
+        else:
+            layer._gpu_func = HuffmanCodebookLinear.from_device(name, t)
+            cb = layer._gpu_func._cb_dev
+        layer.bits = int(layer._gpu_func.bits)
+        layer.register_buffer("codebook", cb, persistent=False)
+        return layer
+
+
 class AdaptiveCodebookEmbedding(nn.Module):
     """Embedding whose table stays codebook-compressed."""
 
@@ -205,4 +228,26 @@ class AdaptiveCodebookEmbedding(nn.Module):
                     layer.bits)
         else:
             raise ValueError(f"Unsupported mode: {mode}")
+        return layer
+
+    @classmethod
+    def from_device(cls, name: str, t) -> "AdaptiveCodebookEmbedding":
+        """A table already in HBM: a device_formats FixedTensor or HuffTensor
+        (stream), or a dense tensor (mode 'exact')."""
+        import device_formats as dfm
+        if isinstance(t, torch.Tensor):
+            layer = cls(name, tuple(t.shape), "exact")
+            layer.weight = nn.Parameter(t, requires_grad=False)
+            return layer
+        layer = cls(name, t.shape, "direct_codebook")
+        if isinstance(t, dfm.FixedTensor):
+            layer._gpu_func = GPUAcceleratedEmbedding.from_device(name, t)
+            cb = t.codebook
+        elif isinstance(t, dfm.HuffTensor):
+            layer._gpu_func = HuffmanCodebookEmbedding.from_device(name, t)
+            cb = t.tables["codebook"]
+        else:
+            raise TypeError(f"{name}: no embedding over a {type(t).__name__}")
+        layer.bits = int(layer._gpu_func.bits)
+        layer.register_buffer("codebook", cb, persistent=False)
         return layer

@@ -70,6 +70,21 @@ class GPUAcceleratedLinear:
                              f"{self.M}x{self.K} at {self.bits} bits")
         self.packed = _upload_packed(raw, device)
 
+    @classmethod
+    def from_device(cls, name: str, t) -> "GPUAcceleratedLinear":
+        """A device_formats.FixedTensor already in HBM (padded packed bytes
+        and codebook, e.g. from cbq_image.load_image): no host copy."""
+        self = cls.__new__(cls)
+        self.name = name
+        self.shape = tuple(int(s) for s in t.shape)
+        self.M, self.K = self.shape
+        self.bits = int(t.bits)
+        self._lib = nat.load()
+        self.codebook = t.codebook
+        self.C = int(t.codebook.numel())
+        self.packed = t.packed
+        return self
+
     @property
     def compressed_bytes(self) -> int:
         return bitpack.calculate_packed_size(self.M * self.K, self.bits)
@@ -127,6 +142,20 @@ class GPUAcceleratedEmbedding:
         self.codebook = codebook.detach().to(device=device, dtype=torch.float32).contiguous()
         self.C = int(self.codebook.numel())
         self.packed = _upload_packed(index_bytes(indices_np, self.bits), device)
+
+    @classmethod
+    def from_device(cls, name: str, t) -> "GPUAcceleratedEmbedding":
+        """A device_formats.FixedTensor already in HBM: no host copy."""
+        self = cls.__new__(cls)
+        self.name = name
+        self.shape = tuple(int(s) for s in t.shape)
+        self.vocab, self.hidden = self.shape
+        self.bits = int(t.bits)
+        self._lib = nat.load()
+        self.codebook = t.codebook
+        self.C = int(t.codebook.numel())
+        self.packed = t.packed
+        return self
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         dev = self.codebook.device

@@ -94,6 +94,28 @@ class _DeviceStream:
             C=self.C, stage_words=hc.stage_words_for(chunk_offsets))
 
 
+def stream_from_device(t) -> _DeviceStream:
+    """_DeviceStream over a device_formats.HuffTensor's device arrays (the
+    stream and chunk index already in HBM, e.g. loaded from a device image):
+    no host stream, no host indexing."""
+    tb = t.tables
+    d = _DeviceStream.__new__(_DeviceStream)
+    d.name = t.name
+    d.C = int(tb["codebook"].numel())
+    d.value_payload = True
+    d.words, d.chunk_off, d.sub_len = t.words, t.chunk_off, t.sub_len
+    d.lut1, d.lut2, d.canon, d.canon_pay = tb["lut1"], tb["lut2"], tb["canon"], tb["pay"]
+    d.value_cb = None
+    d.stream_bytes = (int(t.total_bits) + 7) // 8
+    d.table_bytes = int(t.chunk_off.numel() * 8 + t.sub_len.numel() * 2)
+    d.desc = nat.HuffStream(
+        words=d.words.data_ptr(), n_words=int(d.words.numel()), chunk_off=d.chunk_off.data_ptr(),
+        sub_len=d.sub_len.data_ptr(), lut1=d.lut1.data_ptr(), lut2=d.lut2.data_ptr(),
+        n_lut2=int(d.lut2.numel()), canon=d.canon.data_ptr(), canon_pay=d.canon_pay.data_ptr(),
+        value_cb=None, C=d.C, stage_words=int(tb["stage_words"]))
+    return d
+
+
 def build_columns(desc: "nat.HuffStream", n_sym: int, device, lengths=None,
                   codebook: Optional[np.ndarray] = None):
     """Column layout of a device stream (struct cbq_huff_columns): chunk c's
@@ -424,6 +446,36 @@ class HuffmanCodebookLinear:
                                                           self._lengths, self._cb_np)
                 self._cwords, self._row_off = self._col_keep[0], self._col_keep[1]
 
+    @classmethod
+    def from_device(cls, name: str, t, bits: Optional[int] = None) -> "HuffmanCodebookLinear":
+        """A matrix already in HBM in its device format: a
+        device_formats.SplitTensor (split layout) or HuffTensor (stream
+        layout), e.g. from cbq_image.load_image.  Nothing is re-encoded."""
+        import device_formats as dfm
+        self = cls.__new__(cls)
+        self.name = name
+        self.shape = tuple(int(s) for s in t.shape)
+        self.M, self.K = self.shape
+        cb = t.codebook if isinstance(t, dfm.SplitTensor) else t.tables["codebook"]
+        self.bits = int(bits) if bits is not None else int(np.ceil(np.log2(max(cb.numel(), 2))))
+        self._lib = nat.load()
+        self.device = cb.device
+        self._cb_dev = cb
+        self._cb_np = cb.cpu().numpy()
+        self._lengths = np.ascontiguousarray(t.lengths, np.uint8)
+        self.cols = None
+        if isinstance(t, dfm.SplitTensor):
+            self.split = t.split
+            self.dev = None
+            self._inv = split_inverse(self._cb_np, self.device)
+        elif isinstance(t, dfm.HuffTensor):
+            self.split = None
+            self._inv = None
+            self.dev = stream_from_device(t)
+        else:
+            raise TypeError(f"{name}: not a Huffman device tensor ({type(t).__name__})")
+        return self
+
     @property
     def resident_bytes(self) -> int:
         """Device bytes of the matrix's format(s), tables included."""
@@ -520,6 +572,23 @@ class HuffmanCodebookEmbedding:
         self.device = device
         self._lengths = np.ascontiguousarray(huff_lengths, np.uint8)
         self._cb_dev = torch.from_numpy(cb).to(device)
+
+    @classmethod
+    def from_device(cls, name: str, t, bits: Optional[int] = None) -> "HuffmanCodebookEmbedding":
+        """A table already in HBM as a device_formats.HuffTensor (e.g. from
+        cbq_image.load_image)."""
+        self = cls.__new__(cls)
+        self.name = name
+        self.shape = tuple(int(s) for s in t.shape)
+        self.vocab, self.hidden = self.shape
+        cb = t.tables["codebook"]
+        self.bits = int(bits) if bits is not None else int(np.ceil(np.log2(max(cb.numel(), 2))))
+        self._lib = nat.load()
+        self.device = cb.device
+        self.dev = stream_from_device(t)
+        self._lengths = np.ascontiguousarray(t.lengths, np.uint8)
+        self._cb_dev = cb
+        return self
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         ids = x.to(self.device).reshape(-1).to(torch.int32).contiguous()

@@ -126,3 +126,66 @@ def test_decoder_from_image_tokens(cuda, tmp_path):
         assert m.generate_graph(prompt, 8) == want, enc
         del m, loaded
         torch.cuda.empty_cache()
+
+
+class _Tiny(torch.nn.Module):
+    """HF-style parameter names: embed_tokens, layers.0.{self_attn,mlp}, norm,
+    lm_head tied to the embedding (no tensor of its own)."""
+
+    def __init__(self, vocab=300, hidden=1024):
+        super().__init__()
+        nn = torch.nn
+        self.model = nn.Module()
+        self.model.embed_tokens = nn.Embedding(vocab, hidden)
+        layer = nn.Module()
+        layer.self_attn = nn.Module()
+        layer.self_attn.q_proj = nn.Linear(hidden, 512, bias=False)
+        layer.self_attn.k_proj = nn.Linear(hidden, 96, bias=True)
+        layer.mlp = nn.Module()
+        layer.mlp.down_proj = nn.Linear(2048, hidden, bias=False)
+        self.model.layers = nn.ModuleList([layer])
+        self.model.norm = nn.Module()
+        self.model.norm.weight = nn.Parameter(torch.ones(hidden))
+        self.lm_head = nn.Linear(hidden, vocab, bias=False)
+
+    def forward(self, ids):
+        h = self.model.embed_tokens(ids).float() * self.model.norm.weight.float()
+        att = self.model.layers[0].self_attn
+        q = att.q_proj(h)
+        k = att.k_proj(h)
+        d = self.model.layers[0].mlp.down_proj(torch.cat([q, q, q, q], -1))
+        return q, k, d, self.lm_head(h)
+
+
+@pytest.mark.parametrize("enc", [False, True])
+def test_replace_modules_from_image(cuda, tmp_path, enc):
+    """A model's Linear / Embedding modules swapped for compressed modules
+    bound to a loaded device image give the dense bf16 model's outputs
+    (fp32 arithmetic both sides, rel-L2 <= 1e-5); the tied lm_head uses the
+    embedding's tensor; dense tensors (the norm) are loaded too."""
+    from safetensors.torch import save_file
+    torch.manual_seed(0)
+    dense = _Tiny()
+    sd = {k: (v.detach() * (0.02 if "norm" not in k else 1.0) + (0.5 if "norm" in k else 0.0))
+          .bfloat16().contiguous() for k, v in dense.state_dict().items() if "lm_head" not in k}
+    d = tmp_path / "ckpt"
+    d.mkdir()
+    save_file(sd, str(d / "model.safetensors"))
+    cbq_compress.compress_checkpoint(d, tmp_path / "out", entropy_code=enc, device="cuda",
+                                     write_npz=False, log=lambda *a: None)
+    dense.load_state_dict({k: v.float() for k, v in sd.items()}, strict=False)
+    dense.lm_head.weight = dense.model.embed_tokens.weight
+    dense = dense.to(cuda)
+    comp = _Tiny()
+    n, stats = cache_io.replace_modules_from_image(comp, tmp_path / "out" / "device.cbq", cuda)
+    assert n == 5 and stats["bytes"] > 0                  # embed, q, k, down, tied lm_head
+    comp.model.layers[0].self_attn.k_proj.bias.data = \
+        dense.model.layers[0].self_attn.k_proj.bias.data.clone()
+    comp = comp.to(cuda)
+    assert comp.model.norm.weight.dtype == torch.bfloat16
+    ids = torch.tensor([[3, 17, 299, 0, 150]], device=cuda)
+    with torch.no_grad():
+        want = dense(ids)
+        got = comp(ids)
+    for a, b in zip(got, want):
+        assert rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy()) <= 1e-5
