@@ -167,6 +167,80 @@ def read_header(path) -> dict:
     return h
 
 
+_ELEM = {"uint8": 1, "int16": 2, "int32": 4, "int64": 8, "float32": 4, "bfloat16": 2,
+         "float16": 2}
+
+
+def validate_header(h: dict, file_size: int) -> None:
+    """Check an image header against its file and the invariants the kernels
+    rely on (the descriptors built from it are trusted by the kernels):
+    sections aligned, typed and inside the payload, sized for the tensor's
+    shape and format.  Raises ValueError.  The values inside the arrays
+    (row offsets, chunk offsets) are checked after upload by load_image."""
+    import huffman_codebook as hc
+    D, P = int(h.get("data_offset", -1)), int(h.get("payload_bytes", -1))
+    if D < 16 or D % ALIGN or P < 0 or D + P != file_size:
+        raise ValueError(f"image payload [{D}, {D + P}) does not match the file size {file_size}")
+
+    def sec(where, s, dtype=None, at_least=0, exact=None):
+        if not (isinstance(s, list) and len(s) == 3):
+            raise ValueError(f"{where}: malformed section {s!r}")
+        off, n, dt = s
+        if dt not in _ELEM or (dtype is not None and dt != dtype):
+            raise ValueError(f"{where}: dtype {dt!r}, expected {dtype}")
+        if off < 0 or off % ALIGN or n < 0 or n % _ELEM[dt] or off + n > P:
+            raise ValueError(f"{where}: section [{off}, {off + n}) outside the payload")
+        cnt = n // _ELEM[dt]
+        if cnt < at_least or (exact is not None and cnt != exact):
+            raise ValueError(f"{where}: {cnt} elements, expected "
+                             f"{exact if exact is not None else '>= %d' % at_least}")
+        return cnt
+
+    cbn = {}
+    for cid, c in h.get("codebooks", {}).items():
+        cbn[cid] = sec(f"codebook {cid}", [c.get("offset"), c.get("nbytes"), "float32"],
+                       "float32", at_least=1)
+    for name, e in h.get("tensors", {}).items():
+        kind, shape, s = e.get("kind"), e.get("shape"), e.get("sections", {})
+        if kind == "dense":
+            cnt = sec(f"{name}.data", s.get("data"))
+            if cnt != int(np.prod(shape)):
+                raise ValueError(f"{name}: {cnt} values for shape {shape}")
+            continue
+        if not (isinstance(shape, list) and len(shape) == 2 and min(shape) > 0):
+            raise ValueError(f"{name}: bad shape {shape!r}")
+        M, K = int(shape[0]), int(shape[1])
+        n = M * K
+        if e.get("codebook") not in cbn:
+            raise ValueError(f"{name}: unknown codebook {e.get('codebook')!r}")
+        if kind == "fixed":
+            bits = int(e.get("bits", 0))
+            if not 1 <= bits <= 16:
+                raise ValueError(f"{name}: bits {bits}")
+            sec(f"{name}.packed", s.get("packed"), "uint8", at_least=(n * bits + 7) // 8 + 4)
+        elif kind == "split":
+            nch = int(e.get("n_chunks", -1))
+            if n % hc.CHUNK_SYMBOLS or nch != n // hc.CHUNK_SYMBOLS:
+                raise ValueError(f"{name}: {nch} chunks for {M}x{K}")
+            sec(f"{name}.row_off", s.get("row_off"), "int32", exact=nch + 1)
+            sec(f"{name}.raw", s.get("raw"), "uint8", exact=n)
+            sec(f"{name}.lut", s.get("lut"), "int32", exact=1 << 14)
+            sec(f"{name}.cwords", s.get("cwords"), "int32", at_least=3 * hc.SUB_SYMBOLS)
+            sec(f"{name}.lengths", s.get("lengths"), "uint8", at_least=1)
+        elif kind == "stream":
+            tb = int(e.get("total_bits", -1))
+            sec(f"{name}.chunk_off", s.get("chunk_off"), "int64",
+                exact=(n + hc.CHUNK_SYMBOLS - 1) // hc.CHUNK_SYMBOLS + 1)
+            sec(f"{name}.sub_len", s.get("sub_len"), "int16",
+                exact=(n + hc.SUB_SYMBOLS - 1) // hc.SUB_SYMBOLS)
+            sec(f"{name}.words", s.get("words"), "int32", at_least=max(tb, 0) // 32 + 2)
+            nl = sec(f"{name}.lengths", s.get("lengths"), "uint8", at_least=1)
+            if tb < 0 or nl > cbn[e["codebook"]] + (1 << 16):
+                raise ValueError(f"{name}: total_bits {tb}, {nl} code lengths")
+        else:
+            raise ValueError(f"{name}: unknown kind {kind!r}")
+
+
 def _host_array(path, h: dict, off: int, n: int, dtype) -> np.ndarray:
     with open(path, "rb") as f:
         f.seek(h["data_offset"] + off)
@@ -179,18 +253,17 @@ def load_image(path, device="cuda", threads: int = 8, chunk_mb: int = 64):
     cbq_file_upload; tensors are views into it (kept alive by them).
     stats: upload seconds, total seconds, bytes and upload GB/s."""
     import cbq_native as nat
+    import huffman_codebook as hc
     t0 = time.perf_counter()
     h = read_header(path)
     dev = torch.device(device)
     total = int(h["payload_bytes"])
-    file_size = os.path.getsize(path)
-    if h["data_offset"] + total > file_size + ALIGN:
-        raise ValueError(f"{path}: payload of {total} bytes past the end of the file")
+    validate_header(h, os.path.getsize(path))
     buf = torch.empty(max(total, 1), dtype=torch.uint8, device=dev)
     # the allocation may reuse memory that queued work still touches: the
     # upload's own streams must not overtake it
     torch.cuda.synchronize(dev)
-    n_copy = min(total, file_size - h["data_offset"])
+    n_copy = total
     t1 = time.perf_counter()
     part = (nat.UploadPart * 1)(nat.UploadPart(h["data_offset"], n_copy, buf.data_ptr()))
     with torch.cuda.device(dev):
@@ -206,6 +279,7 @@ def load_image(path, device="cuda", threads: int = 8, chunk_mb: int = 64):
     cbs = {cid: buf[c["offset"]:c["offset"] + c["nbytes"]].view(torch.float32)
            for cid, c in h["codebooks"].items()}
     out: Dict[str, object] = {}
+    checks = []                                    # (name, device bool) of the array values
     for name, e in h["tensors"].items():
         shape = tuple(e["shape"])
         s = e["sections"]
@@ -218,14 +292,28 @@ def load_image(path, device="cuda", threads: int = 8, chunk_mb: int = 64):
                                         view(s["packed"]), cb)
         elif e["kind"] == "split":
             lengths = _host_array(path, h, s["lengths"][0], s["lengths"][1], np.uint8)
-            out[name] = dfm.split_from_arrays(name, shape, e["category"], lengths,
-                                              view(s["cwords"]), view(s["row_off"]),
+            ro, cw = view(s["row_off"]), view(s["cwords"])
+            # rows per chunk in [1, 14] (the kernels' slot), 3 readable rows after
+            d = ro[1:] - ro[:-1]
+            checks.append((name, (ro[0] == 0) & (d.min() >= 1) & (d.max() <= 14)
+                           & ((ro[-1] + 3) * 64 <= cw.numel())))
+            out[name] = dfm.split_from_arrays(name, shape, e["category"], lengths, cw, ro,
                                               view(s["raw"]), view(s["lut"]), cb,
                                               int(e["n_chunks"]))
         elif e["kind"] == "stream":
             lengths = _host_array(path, h, s["lengths"][0], s["lengths"][1], np.uint8)
             t = dfm.HuffTensor(name, shape, e["category"], lengths, view(s["words"]),
                                view(s["chunk_off"]), view(s["sub_len"]), int(e["total_bits"]))
+            # chunk offsets from 0 to total_bits, each chunk's sub-block
+            # lengths adding up to it, the words covering the stream
+            co, sl = t.chunk_off, t.sub_len.to(torch.int64) & 0xFFFF
+            nch = co.numel() - 1
+            per = torch.zeros(nch * hc.SUB_SYMBOLS, dtype=torch.int64, device=dev)
+            per[:sl.numel()] = sl
+            per = per.view(nch, hc.SUB_SYMBOLS).sum(1)
+            checks.append((name, (co[0] == 0) & (co[-1] == t.total_bits)
+                           & (co[1:] - co[:-1] == per).all()
+                           & (t.total_bits + 64 <= 32 * t.words.numel())))
             c = h["codebooks"][e["codebook"]]
             t.tables = dfm.huff_tables_host(
                 lengths, _host_array(path, h, c["offset"], c["nbytes"], np.float32), cb,
@@ -233,6 +321,11 @@ def load_image(path, device="cuda", threads: int = 8, chunk_mb: int = 64):
             out[name] = t
         else:
             raise ValueError(f"{path}: {name} has unknown kind {e['kind']!r}")
+    if checks:
+        ok = torch.stack([c for _, c in checks]).cpu()
+        bad = [n for (n, _), v in zip(checks, ok.tolist()) if not v]
+        if bad:
+            raise ValueError(f"{path}: inconsistent format arrays in {bad[:4]}")
     t3 = time.perf_counter()
     stats = {"bytes": n_copy, "upload_s": t2 - t1, "total_s": t3 - t0,
              "upload_GB/s": n_copy / max(t2 - t1, 1e-9) / 1e9, "threads": int(threads),

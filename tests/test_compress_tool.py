@@ -185,3 +185,42 @@ def test_cli(ckpt, tmp_path, capsys):
     assert cbq_compress.main([str(d), "--device", "cpu", "--out", str(out)]) == 0
     assert "already holds" in capsys.readouterr().out
     assert cbq_compress.main([str(tmp_path / "missing")]) == 1
+
+
+def test_image_validation_rejects_corrupt_headers(ckpt, tmp_path):
+    """The header checks that guard the kernels' descriptors: truncated
+    payload, sections out of range or of the wrong size, unknown kinds."""
+    import copy
+    d, _ = ckpt
+    for enc in (False, True):
+        out = tmp_path / f"v{int(enc)}"
+        cbq_compress.compress_checkpoint(d, out, entropy_code=enc, device="cpu",
+                                         write_npz=False, log=lambda *a: None)
+        path = out / "device.cbq"
+        h = cbq_image.read_header(path)
+        size = os.path.getsize(path)
+        cbq_image.validate_header(h, size)                       # the writer's own image passes
+        with pytest.raises(ValueError):
+            cbq_image.validate_header(h, size - 1)                # truncated file
+        name = "model.layers.0.self_attn.q_proj.weight"
+        key = "packed" if not enc else "chunk_off"
+        bad = copy.deepcopy(h)
+        off, nb, dt = bad["tensors"][name]["sections"][key]
+        M, K = SHAPES[name]
+        e = h["tensors"][name]
+        short = (M * K * e.get("bits", 0) + 7) // 8 if not enc else nb - 8   # no pad / one fewer
+        bad["tensors"][name]["sections"][key] = [off, short, dt]
+        with pytest.raises(ValueError):
+            cbq_image.validate_header(bad, size)
+        bad = copy.deepcopy(h)
+        bad["tensors"][name]["sections"][key] = [h["payload_bytes"], nb, dt]   # past the end
+        with pytest.raises(ValueError):
+            cbq_image.validate_header(bad, size)
+        bad = copy.deepcopy(h)
+        bad["tensors"][name]["shape"] = [64, 256]                 # more weights than stored
+        with pytest.raises(ValueError):
+            cbq_image.validate_header(bad, size)
+        bad = copy.deepcopy(h)
+        bad["tensors"][name]["kind"] = "columns"
+        with pytest.raises(ValueError):
+            cbq_image.validate_header(bad, size)

@@ -189,3 +189,38 @@ def test_replace_modules_from_image(cuda, tmp_path, enc):
         got = comp(ids)
     for a, b in zip(got, want):
         assert rel_l2(a.float().cpu().numpy(), b.float().cpu().numpy()) <= 1e-5
+
+
+def test_load_rejects_inconsistent_arrays(cuda, ckpt, tmp_path):
+    """Array values the kernels trust (split row offsets, stream chunk
+    offsets) are checked after the upload: a tampered image raises before
+    any descriptor reaches a kernel; so does a truncated file."""
+    import struct
+    d, _ = ckpt
+    cbq_compress.compress_checkpoint(d, tmp_path, entropy_code=True, device="cuda",
+                                     write_npz=False, log=lambda *a: None)
+    path = tmp_path / "device.cbq"
+    h = cbq_image.read_header(path)
+    raw = bytearray(path.read_bytes())
+    e = h["tensors"]["model.layers.0.self_attn.q_proj.weight"]
+    assert e["kind"] == "split"
+    off = h["data_offset"] + e["sections"]["row_off"][0]
+    good = bytes(raw)
+    raw[off + 4 * 3:off + 4 * 4] = struct.pack("<i", 1 << 20)      # a chunk of 2^20 rows
+    bad = tmp_path / "bad.cbq"
+    bad.write_bytes(bytes(raw))
+    with pytest.raises(ValueError):
+        cbq_image.load_image(bad, cuda)
+    e = h["tensors"]["model.layers.0.mlp.up_proj.weight"]           # K = 1000: a stream
+    assert e["kind"] == "stream"
+    raw = bytearray(good)
+    off = h["data_offset"] + e["sections"]["chunk_off"][0]
+    raw[off + 8:off + 16] = struct.pack("<q", 1 << 40)              # a chunk past the stream
+    bad.write_bytes(bytes(raw))
+    with pytest.raises(ValueError):
+        cbq_image.load_image(bad, cuda)
+    bad.write_bytes(good[:-4096])
+    with pytest.raises(ValueError):
+        cbq_image.load_image(bad, cuda)
+    tensors, _, _ = cbq_image.load_image(path, cuda)                 # the untouched image loads
+    assert len(tensors) == len(h["tensors"])
