@@ -415,6 +415,19 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
                  "pct_of_hbm_peak": round(100 * nb1 / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1),
                  "stream_equivalent_GB/s": round(sum(stream_bytes.values()) / (ms1 * 1e-3) / 1e9,
                                                  1)}}
+    per_h = {}
+    for kind, sel in (("qkv_grouped", "self_attn.q_proj"), ("o_proj", "self_attn.o_proj"),
+                      ("gate_up_grouped", "mlp.gate_proj"), ("down_proj", "mlp.down_proj")):
+        sub = [e for e in plan if (e[0] if isinstance(e, tuple) else e).endswith(sel)]
+        ms_k, nb_k = huffman_sweep(torch, nat, lib, dev, huff, splits, sub,
+                                   max(3, args.steps // 2), 1)
+        e0 = sub[0]
+        ns0 = list(e0) if isinstance(e0, tuple) else [e0]
+        per_h[kind] = {"shape": " + ".join(f"{huff[n].shape[1]}->{huff[n].shape[0]}"
+                                           for n in ns0),
+                       "us_per_launch": round(ms_k * 1e3 / len(sub), 2),
+                       "GB/s": round(nb_k / (ms_k * 1e-3) / 1e9, 1)}
+    hu["per_shape_T1"] = per_h
     invs = {}
     for T in (4, 16):
         xs = {}

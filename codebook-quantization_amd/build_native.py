@@ -40,9 +40,14 @@ def command(out: str = SO):
     return [hipcc()] + FLAGS + ["-shared", "-pthread", "-o", out] + sources()
 
 
-def build(verbose: bool = False, jobs: int = 0) -> str:
+TIMELINE_SO = os.path.join(HERE, "libcbq_hip_timeline.so")
+
+
+def build(verbose: bool = False, jobs: int = 0, out: str = SO, defines=()) -> str:
     """Compile every time it is called (one hipcc per source, in parallel, in
-    a temporary directory), link, and move the library next to this file."""
+    a temporary directory), link, and move the library to `out` (next to
+    this file by default).  defines: extra -D macros (CBQ_TIMELINE builds the
+    diagnostic variant)."""
     import tempfile
     from concurrent.futures import ThreadPoolExecutor
     srcs = sources()
@@ -52,7 +57,7 @@ def build(verbose: bool = False, jobs: int = 0) -> str:
 
         def compile_one(so):
             src, obj = so
-            cmd = [hipcc()] + FLAGS + ["-c", "-o", obj, src]
+            cmd = [hipcc()] + FLAGS + [f"-D{d}" for d in defines] + ["-c", "-o", obj, src]
             if verbose:
                 print(" ".join(cmd), flush=True)
             return subprocess.run(cmd, capture_output=True, text=True)
@@ -68,10 +73,14 @@ def build(verbose: bool = False, jobs: int = 0) -> str:
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError("hipcc link failed:\n" + res.stderr[-4000:])
-        shutil.copyfile(tmp, SO + ".tmp")
-    os.replace(SO + ".tmp", SO)
-    return SO
+        shutil.copyfile(tmp, out + ".tmp")
+    os.replace(out + ".tmp", out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    if "--timeline" in sys.argv:
+        # the diagnostic library (per-wave timeline of the streaming GEMV)
+        print(build(verbose="-v" in sys.argv, out=TIMELINE_SO, defines=("CBQ_TIMELINE",)))
+    else:
+        print(build(verbose="-v" in sys.argv))

@@ -273,6 +273,18 @@ __global__ __launch_bounds__(kBlock) void fixed_gemv_kernel(
 
 constexpr int kStreamWaves = 8;
 constexpr int kStreamBlock = kStreamWaves * CBQ_WAVE;
+
+// Diagnostic build (-DCBQ_TIMELINE): every wave of a one-token plain
+// streaming launch records the 100 MHz s_memrealtime clock at entry, after
+// the staging, after its first ring of items, after its loop and at exit,
+// plus its item count, into cbq_timeline_wave (read by cbq_timeline_read).
+// The product build has none of it.
+constexpr int kTimelineWaves = 4096;
+constexpr int kTimelineFields = 6;
+#ifdef CBQ_TIMELINE
+__device__ unsigned long long cbq_timeline_wave[kTimelineWaves * kTimelineFields];
+#define CBQ_TS(var) const unsigned long long var = __builtin_amdgcn_s_memrealtime()
+#endif
 constexpr int kStreamD = 2;
 constexpr int kStreamLds = 152 * 1024;      // codebook + staged x, per block
 
@@ -391,6 +403,11 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     // pick, written to arg_v / arg_i [blockIdx.x].
     constexpr bool PADDED = BITS <= 14 && !AFFINE;
     constexpr int D = kStreamD;
+#ifdef CBQ_TIMELINE
+    constexpr bool kTimed = TMAX == 1 && XMODE == XF_NONE && !KCHUNK && !AFFINE;
+    CBQ_TS(ts_entry);
+    unsigned long long ts_first = 0;
+#endif
     __shared__ float s_cbp[PADDED ? (1 << BITS) : 1];
     __shared__ float s_red16[XMODE >= XF_ADD_RMS ? 16 : 1];
     extern __shared__ float s_dyn[];
@@ -476,6 +493,9 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
         lds_barrier();
     }
 
+#ifdef CBQ_TIMELINE
+    CBQ_TS(ts_staged);
+#endif
     float acc[TMAX], res[TMAX];
 #pragma unroll
     for (int t = 0; t < TMAX; t++) acc[t] = res[t] = 0.f;
@@ -548,7 +568,13 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
             }
         }
         base += D;
+#ifdef CBQ_TIMELINE
+        if (base == D) ts_first = __builtin_amdgcn_s_memrealtime();
+#endif
     } while (base < n_items);
+#ifdef CBQ_TIMELINE
+    CBQ_TS(ts_loop);
+#endif
     const int rb = rows & ~63;
     if (lane < rows - rb) {
         const int row = wid + (rb + lane) * W;
@@ -567,6 +593,20 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
         __shared__ int s_ai[kStreamWaves];
         arg_block_store(a_best, a_idx, s_av, s_ai, arg_v, arg_i);
     }
+#ifdef CBQ_TIMELINE
+    if constexpr (kTimed) {
+        CBQ_TS(ts_exit);
+        if (lane == 0 && wid < kTimelineWaves) {
+            unsigned long long *tl = cbq_timeline_wave + (size_t)wid * kTimelineFields;
+            tl[0] = ts_entry;
+            tl[1] = ts_staged;
+            tl[2] = ts_first;
+            tl[3] = ts_loop;
+            tl[4] = ts_exit;
+            tl[5] = (unsigned long long)n_items;
+        }
+    }
+#endif
 }
 
 // Any width, any K, codebook read through the cache: per-element 4-byte
@@ -1146,3 +1186,26 @@ int cbq_embedding_f32(const int32_t *token_ids, const uint8_t *packed, const flo
 }
 
 }  // extern "C"
+
+// Per-wave timeline of the last one-token plain streaming launch, in a
+// -DCBQ_TIMELINE build: kTimelineWaves x 6 uint64 (entry, staged, first
+// ring done, loop done, exit in 10 ns ticks; item count).  CK_ERR_ARG in
+// the product build or when dst_bytes is short.
+extern "C" int cbq_timeline_read(void *dst, size_t dst_bytes)
+{
+#ifdef CBQ_TIMELINE
+    const size_t n = sizeof(unsigned long long) * kTimelineWaves * kTimelineFields;
+    if (!dst || dst_bytes < n) return CK_ERR_ARG;
+    const hipError_t e = hipMemcpyFromSymbol(dst, HIP_SYMBOL(cbq_timeline_wave), n, 0,
+                                             hipMemcpyDeviceToHost);
+    if (e != hipSuccess) {
+        fprintf(stderr, "cbq_timeline_read: %s\n", hipGetErrorString(e));
+        return CK_ERR_HIP;
+    }
+    return CK_SUCCESS;
+#else
+    (void)dst;
+    (void)dst_bytes;
+    return CK_ERR_ARG;
+#endif
+}

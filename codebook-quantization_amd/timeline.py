@@ -1,0 +1,104 @@
+#!/usr/bin/env python3
+"""Per-wave timeline of the one-token fixed-width streaming GEMV on the
+9B-scale decode shapes, from the diagnostic library build.
+
+    python codebook-quantization_amd/build_native.py --timeline   # once, on the build host
+    python codebook-quantization_amd/timeline.py [--lib PATH]      # on the GPU
+
+Each shape: N(0, 0.02) bf16 weights (synthetic.make_bf16), the tensor's own
+frequency-sorted codebook, 13-bit packed indices, four copies; one second of
+back-to-back launches to bring the clocks up, then one launch timed with HIP
+events whose per-wave timestamps (cbq_timeline_read) are summarised: the
+dispatch skew, the staging of codebook and x, the first ring of items, the
+per-item time after it, when the waves finish their loops (and how that
+differs between the first and the second wave of each SIMD), and the whole
+in-kernel span.  Prints a markdown report.
+"""
+import argparse
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+if HERE not in sys.path:
+    sys.path.insert(0, HERE)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+SHAPES = (("stacked gate+up", 24576, 4096), ("gate_proj", 12288, 4096),
+          ("down_proj", 4096, 12288), ("stacked q/k/v", 6144, 4096), ("o_proj", 4096, 4096))
+
+
+def pct(a, ps=(0, 10, 50, 90, 100)):
+    return " / ".join(f"{np.percentile(a, p):.2f}" for p in ps)
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--lib", default=os.path.join(HERE, "libcbq_hip_timeline.so"))
+    ap.add_argument("--warm", type=float, default=1.0)
+    args = ap.parse_args(argv)
+    import cbq_native as nat
+    import codebook_builder as cbb
+    import synthetic
+    lib = nat.load(args.lib)
+    probe = np.zeros(4096 * 6, np.uint64)
+    if lib.cbq_timeline_read(probe.ctypes.data, probe.nbytes) == nat.CK_ERR_ARG:
+        raise SystemExit(f"{args.lib} is not a timeline build (build_native.py --timeline)")
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream().cuda_stream
+    print("| shape | event µs | in-kernel span µs | staged after entry µs | first ring µs | "
+          "µs per item after it (p0/p10/p50/p90/p100) | loop end µs (p0/p10/p50/p90/p100) | "
+          "waves 0-3 / 4-7 loop end µs | MB | span GB/s |")
+    print("|---|---|---|---|---|---|---|---|---|---|")
+    for name, M, K in SHAPES:
+        w = synthetic.make_bf16((M, K), f"timeline.{name}", device=dev)
+        cb, lut = cbb.codebook_from_counts_torch(cbb.counts_torch(w))
+        idx = lut[cbb.patterns_torch(w).reshape(-1).to(torch.int64)]
+        del w
+        C, bits = cb.numel(), cbb.bits_for(cb.numel())
+        pk = cbb.pack_torch(idx, bits)
+        nb = pk.numel()
+        mats = []
+        for _ in range(4):
+            p = torch.zeros(nb + 32, dtype=torch.uint8, device=dev)
+            p[:nb] = pk
+            mats.append(p)
+        del idx, pk
+        x = torch.randn(1, K, device=dev)
+        out = torch.empty(1, M, device=dev)
+        t0 = time.time()
+        while time.time() - t0 < args.warm:
+            for p in mats:
+                nat.check(lib.ck_linear_f32(x.data_ptr(), p.data_ptr(), cb.data_ptr(),
+                                            out.data_ptr(), 1, M, K, C, bits, st), "warm-up")
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        nat.check(lib.ck_linear_f32(x.data_ptr(), mats[1].data_ptr(), cb.data_ptr(),
+                                    out.data_ptr(), 1, M, K, C, bits, st), "timed launch")
+        e1.record()
+        torch.cuda.synchronize()
+        ev_us = e0.elapsed_time(e1) * 1e3
+        tl = np.zeros(4096 * 6, np.uint64)
+        nat.check(lib.cbq_timeline_read(tl.ctypes.data, tl.nbytes), "cbq_timeline_read")
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
+        W = min(4096, 8 * min(cus, (M + 7) // 8))                # waves of the launch
+        tl = tl.reshape(4096, 6)[:W].astype(np.int64)
+        r = (tl[:, :5] - tl[:, 0].min()) * 0.01                 # µs from the first entry
+        items = tl[:, 5]
+        per_item = (r[:, 3] - r[:, 2]) / np.maximum(items - 2, 1)
+        half = (np.arange(W) % 8) < 4
+        span = float(r[:, 4].max())
+        mb = (M * K * bits + 7) // 8 / 1e6
+        print(f"| {name} {K}->{M} | {ev_us:.1f} | {span:.1f} | {np.median(r[:, 1] - r[:, 0]):.2f} | "
+              f"{np.median(r[:, 2] - r[:, 1]):.2f} | {pct(per_item)} | {pct(r[:, 3])} | "
+              f"{r[half, 3].mean():.2f} / {r[~half, 3].mean():.2f} | {mb:.1f} | "
+              f"{mb / span * 1e3:.0f} |", flush=True)
+        del mats
+        torch.cuda.empty_cache()
+
+
+if __name__ == "__main__":
+    main()

@@ -367,6 +367,15 @@ int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits
 /* Version string of the library build. */
 const char *cbq_version(void);
 
+/* Diagnostics: in a library built with -DCBQ_TIMELINE
+ * (build_native.py --timeline), copies the per-wave timeline of the last
+ * one-token fixed-width streaming launch: 4096 waves x 6 uint64 (clock at
+ * entry, after staging, after the first ring of items, after the loop, at
+ * exit, in 10 ns ticks of s_memrealtime; then the wave's item count) to
+ * host memory.  CK_ERR_ARG in the normal build or when dst_bytes <
+ * 4096 * 6 * 8.  No counterpart in the reference. */
+int cbq_timeline_read(void *dst, size_t dst_bytes);
+
 /* ---- lm_head GEMV with the greedy pick fused ------------------------------
  * The one-token GEMV of the decoder's last matrix (vocabulary rows) and the
  * greedy pick of the next token in two launches: the GEMV's epilogue reduces

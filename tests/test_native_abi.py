@@ -98,6 +98,7 @@ def test_argument_validation_before_launch(lib):
     bad = (cbq_native.UploadPart * 1)(cbq_native.UploadPart(-1, 64, p))
     assert up(__file__.encode(), bad, 1, 1 << 20, 2) == 2                       # negative offset
     assert up(__file__.encode(), part, 0, 1 << 20, 2) == 0                      # nothing to copy
+    assert lib.cbq_timeline_read(None, 0) == 2               # diagnostics: product build / no buffer
 
 
 def test_build_luts_rejects_overfull(lib):
