@@ -941,10 +941,13 @@ int embedding_impl(const int32_t *ids, const uint8_t *packed, const float *cb, f
 }  // namespace
 
 // bf16 MFMA prefill path (cbq_prefill.hip); -1 = shape not handled there.
-// S > 1 splits K, with S * T * M floats of workspace.
+// S > 1 splits K, with S * T * M floats of workspace; xf: room for x in
+// fragment order (cbq_prefill_xf_bytes) or nullptr.
 int cbq_prefill_bf16(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
-                     int T, int M, int K, int C, int bits, hipStream_t st, int S, float *ws);
+                     int T, int M, int K, int C, int bits, hipStream_t st, int S, float *ws,
+                     uint16_t *xf);
 int cbq_prefill_splits(int T, int M, int K);
+size_t cbq_prefill_xf_bytes(int T, int K);
 // fp32 MFMA prefill path (cbq_prefill_f32.hip); -1 = shape not handled there.
 int cbq_prefill_f32(const float *x, const uint8_t *packed, const float *cb, float *out, int T,
                     int M, int K, int C, int bits, hipStream_t st, int S, float *ws);
@@ -1139,7 +1142,7 @@ int ck_linear_bf16(const void *x_bf16, const uint8_t *packed, const float *codeb
         bits >= 1 && bits <= 16) {
         const int rc = cbq_prefill_bf16((const uint16_t *)x_bf16, packed, codebook,
                                         (uint16_t *)out_bf16, T, M, K, C, bits, stream, 1,
-                                        nullptr);
+                                        nullptr, nullptr);
         if (rc >= 0) return rc;
     }
     return linear_any_t<uint16_t, uint16_t>((const uint16_t *)x_bf16, packed, codebook,
@@ -1149,8 +1152,10 @@ int ck_linear_bf16(const void *x_bf16, const uint8_t *packed, const float *codeb
 size_t cbq_linear_bf16_workspace(int T, int M, int K)
 {
     if (T <= 0 || M <= 0 || K <= 0) return 0;
+    const size_t xf = cbq_prefill_xf_bytes(T, K);
+    if (xf == 0) return 0;
     const int S = cbq_prefill_splits(T, M, K);
-    return S > 1 ? (size_t)S * T * M * sizeof(float) : 0;
+    return xf + (S > 1 ? (size_t)S * T * M * sizeof(float) : 0);
 }
 
 int cbq_linear_bf16_ws(const void *x_bf16, const uint8_t *packed, const float *codebook,
@@ -1159,14 +1164,17 @@ int cbq_linear_bf16_ws(const void *x_bf16, const uint8_t *packed, const float *c
 {
     if (x_bf16 && packed && codebook && out_bf16 && T >= 64 && M > 0 && K > 0 && C > 0 &&
         bits >= 1 && bits <= 16) {
+        // workspace = [x in fragment order][fp32 split partials]
         const size_t need = cbq_linear_bf16_workspace(T, M, K);
-        const bool split = need > 0 && workspace && ws_bytes >= need &&
-                           ((uintptr_t)workspace & 15) == 0;
-        const int rc = cbq_prefill_bf16((const uint16_t *)x_bf16, packed, codebook,
-                                        (uint16_t *)out_bf16, T, M, K, C, bits, stream,
-                                        split ? cbq_prefill_splits(T, M, K) : 1,
-                                        split ? (float *)workspace : nullptr);
-        if (rc >= 0) return rc;
+        if (need > 0 && workspace && ws_bytes >= need && ((uintptr_t)workspace & 255) == 0) {
+            const size_t xf = cbq_prefill_xf_bytes(T, K);
+            const int S = cbq_prefill_splits(T, M, K);
+            const int rc = cbq_prefill_bf16((const uint16_t *)x_bf16, packed, codebook,
+                                            (uint16_t *)out_bf16, T, M, K, C, bits, stream, S,
+                                            S > 1 ? (float *)((char *)workspace + xf) : nullptr,
+                                            (uint16_t *)workspace);
+            if (rc >= 0) return rc;
+        }
     }
     return ck_linear_bf16(x_bf16, packed, codebook, out_bf16, T, M, K, C, bits, stream);
 }

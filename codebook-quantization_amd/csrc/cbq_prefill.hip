@@ -6,42 +6,71 @@
 // reference's LSB-first stream (src/bitpack.py:32-95); K % 32 == 0, so each
 // row's 32-index groups are BITS whole 32-bit words.
 //
-// Block = 8 waves, output tile 256 tokens x 128 features, K step 32.  Per K
-// step the block (tiles double-buffered in LDS, one barrier per step)
-//   - copies the x tile [256][32] bf16 to LDS,
-//   - decodes the W tile [128][32]: 4 threads per row, 8 indices each,
-//     gathering bf16 values from an LDS codebook padded to 2^BITS entries
-//     (entries >= C repeat codebook[C-1], which is the reference's clamp),
-//   - runs v_mfma_f32_32x32x16_bf16: each wave owns a 64 x 64 sub-tile
-//     (2 x 2 MFMA blocks), A = x rows, B = W rows (both K-contiguous).
-// A codebook that is not exactly bf16 (found while staging it) is split
-// into bf16 hi + lo halves, each run through the MFMA.
-// x and index words of the next four K steps are held in registers, so
-// global latency hides behind the MFMAs.  LDS rows are 4 chunks of 16
-// bytes stored at chunk ^ ((row >> 1) & 3): the ds_read_b128 of 8
-// neighbouring rows then hit distinct bank groups.
+// Block = 8 waves (two per SIMD), output tile 512 tokens x 128 features, K
+// step 32 (one index group per row).  Wave w owns tokens 64 w .. 64 w + 63
+// and all 128 features: 4 x 8 blocks of v_mfma_f32_16x16x32_bf16, 32 MFMAs a
+// step.
+//   - x does not pass through LDS.  The A operand of a 16-token block is lane
+//     l's 8 bf16 at row l % 16, k 8 (l / 16) .. +7.  With a caller workspace
+//     (cbq_linear_bf16_ws) x is first copied to that fragment order
+//     (prefill_x_frag_kernel), so every operand load is 1 KiB contiguous;
+//     without one (ck_linear_bf16) each lane reads its own row, which the L2
+//     serves at about a third of the rate.
+//   - The W tile's index words (128 rows x BITS words per step) are loaded by
+//     dword loads, consecutive lanes on consecutive words of a row, three
+//     steps ahead into registers, then stored to a double-buffered LDS slot.
+//   - Each step the 512 threads decode the W tile of step + 2 once for the
+//     block: thread -> (row, 8 indices), bf16 values gathered from an LDS
+//     codebook padded to 2^BITS entries (entries >= C repeat codebook[C-1],
+//     which is the reference's clamp), into a triple-buffered bf16 tile whose
+//     fragments the MFMAs read as their B operand.  One barrier per step.
+// A weight is decoded once per 512 tokens: the random codebook gathers
+// (about 8 per clock per CU on gfx950) stay below the matrix core's time.
+// A codebook that is not exactly bf16 (found while staging it) is split into
+// bf16 hi + lo halves, each run through the MFMA.  The output leaves through
+// LDS: each wave transposes 16 tokens at a time into a padded row-major tile
+// and stores whole rows, 16 bytes a lane.
 #include "cbq_device.h"
 
 #include <algorithm>
 
 namespace {
 
-constexpr int kPT = 256;          // tokens per block tile
-constexpr int kPM = 128;          // features per block tile
-constexpr int kPK = 32;           // K step (one index group)
-constexpr int kPBlock = 512;      // 8 waves: 4 along T x 2 along M, 64 x 64 each
+constexpr int kPT = 512;               // tokens per block tile
+constexpr int kPM = 128;               // features per block tile
+constexpr int kPK = 32;                // K step (one index group)
+constexpr int kPWaves = 8;            // two per SIMD: one hides the other's waits
+constexpr int kPBlock = kPWaves * CBQ_WAVE;
+constexpr int kWT = kPT / kPWaves;     // tokens per wave (64)
+constexpr int kTB = kWT / 16;          // 16-token MFMA blocks per wave
+constexpr int kNB = kPM / 16;          // 16-feature MFMA blocks
+constexpr int kXD = 2;                 // x register ring (steps)
+constexpr int kRD = 3;                 // index-word register ring (steps)
+constexpr int kUnroll = 6;             // K loop unroll: every ring index compile-time
+constexpr int kWBuf = kPM * 4;         // 16-byte chunks per W tile buffer
+// Index words of one step: kPM rows x BITS words, moved by kRawLoads dword
+// loads per thread (load j of thread t: slot dword j * 512 + t = word s % BITS
+// of tile row s / BITS; dwords past kPM * BITS are loaded and stored but
+// never read).
+template <int BITS> constexpr int kRawLoads = (kPM * BITS + kPBlock - 1) / kPBlock;
+template <int BITS> constexpr int kRawSlot = kRawLoads<BITS> * kPBlock;
+// The W tiles (hi and lo, three buffers each) share one LDS array with the
+// epilogue, which reuses it after the K loop: per wave kEpiRows rows of kPM
+// fp32 or bf16 outputs, rows padded by 16 bytes.
+template <bool SPLIT> constexpr int kEpiRow = kPM * (SPLIT ? 4 : 2) + 16;
+constexpr int kEpiRows = 16;
+constexpr int kLdsEpi = kPWaves * kEpiRows * kEpiRow<true>;
+constexpr int kWtChunks = (6 * kWBuf * 16 > kLdsEpi ? 6 * kWBuf * 16 : kLdsEpi) / 16;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 3); }
-
-// 16-byte chunk `c` of tile row `r` (rows of 32 bf16 = 64 bytes).
-__device__ __forceinline__ uint32_t *tile_chunk(uint32_t *tile, int r, int c)
-{
-    return tile + r * 16 + (swz(r, c) << 2);
-}
+// W tile row r (32 bf16) is four 16-byte chunks; chunk c sits at 16-byte
+// slot r * 4 + (c ^ ((r >> 2) & 3)).  The 16 lanes of a B-fragment read that
+// share a chunk take 16 consecutive rows and so 16 distinct bank groups; so
+// do 16 consecutive decode threads writing one chunk.
+__device__ __forceinline__ int wslot(int r, int c) { return (r << 2) + (c ^ ((r >> 2) & 3)); }
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f)
 {
@@ -50,135 +79,174 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f)
     return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
-// Decode the 8 indices of part WP (indices 8*WP .. 8*WP+7 of a 32-index
-// group) from the words loaded from word 8*WP*BITS/32 on, into 8 bf16 (and
-// their lo halves when TWO).  All offsets are compile-time.
-template <int BITS, int WP, bool TWO, int NW>
-__device__ __forceinline__ void decode_part(const uint32_t (&wv)[NW], const uint16_t *s_cb,
-                                            const uint16_t *s_cblo, uint32_t (&pk)[4],
-                                            uint32_t (&pl)[4])
+// Main K loop of one wave; HP = which part (of kPWaves / 2) of each
+// 32-index group this thread decodes (wave-uniform).  Steps past G clamp their loads to the last
+// group and skip their MFMAs.
+//
+// Per step g (one barrier), in issue order:
+//   - the words of step g + 3 (in registers since step g - 3) go to LDS
+//     slot (g + 1) & 1, whose words (step g + 1) were decoded during step
+//     g - 1, and the words of step g + 6 are loaded in their place;
+//   - the 32 MFMAs of step g run on B fragments already in registers; after
+//     the last MFMA of each 16-feature block its fragment of step g + 1 is
+//     read from W buffer (g + 1) % 3 (decoded during step g - 1);
+//   - between the MFMA blocks the threads decode step g + 2 (slot g & 1)
+//     into W buffer (g + 2) % 3, whose fragments were read during step g - 2:
+//     index words, then the codebook gathers, then the tile store;
+//   - x of step g + 2 is loaded.
+// So the MFMAs wait on no LDS read of their own step: the fragment reads,
+// gathers and stores run while the matrix core works.
+template <int BITS, bool TWO, int HP, bool XF>
+__device__ __forceinline__ void prefill_loop(
+    const uint16_t *__restrict__ xb, const uint32_t (&xoff)[kTB], const uint32_t *__restrict__ wb,
+    const uint32_t (&doff)[kRawLoads<BITS>], int G, const uint16_t *s_cb, const uint16_t *s_cblo,
+    u32x4 *s_w, u32x4 *s_wlo, uint32_t *s_raw, int wave, int lane, bool active,
+    f32x4 (&acc)[kTB][kNB])
 {
+    constexpr int NF = 64 / kPWaves;                     // indices a thread decodes
+    constexpr int NW = (NF * BITS + 31 + 31) / 32;       // words covering them
+    constexpr int q0 = (HP * NF * BITS) >> 5;
+    constexpr int sh0 = (HP * NF * BITS) & 31;
     constexpr uint32_t mask = (1u << BITS) - 1u;
-    constexpr int sh0 = (WP * 8 * BITS) & 31;
+    constexpr int ND = kRawLoads<BITS>;
+    constexpr int kSlot = kRawSlot<BITS>;
+    const int tid = wave * CBQ_WAVE + lane;
+    const int wr = ((wave / (kPWaves / 2)) << 6) + lane;  // decoded tile row
+    const int fo = wslot(lane & 15, lane >> 4);          // this lane's B-fragment chunk
+    // (row nb * 16 + lane % 16 has slot fo + nb * 64: (r >> 2) & 3 is unchanged by + 16)
+
+    auto load_raw = [&](int g, uint32_t (&rr)[ND]) {     // step g's index words
+        const int gc = g < G ? g : G - 1;
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-        uint32_t v[2], vl[2];
+        for (int j = 0; j < ND; j++) rr[j] = wb[(uint32_t)(doff[j] + (uint32_t)gc * BITS)];
+    };
+    auto store_raw = [&](int slot_i, const uint32_t (&rr)[ND]) {
+        uint32_t *slot = s_raw + slot_i * kSlot + tid;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int o = sh0 + (j + h) * BITS;
+        for (int j = 0; j < ND; j++) slot[j * kPBlock] = rr[j];
+    };
+    auto load_x = [&](int g, bf16x8 (&xr)[kTB]) {
+        const int gc = g < G ? g : G - 1;
+#pragma unroll
+        for (int tb = 0; tb < kTB; tb++)
+            xr[tb] = *(const bf16x8 *)(xb + (uint32_t)(xoff[tb] + (uint32_t)gc * (XF ? 512 : kPK)));
+    };
+    auto read_words = [&](int slot_i, uint32_t (&wv)[NW]) {
+        const uint32_t *rw = s_raw + slot_i * kSlot + wr * BITS;
+#pragma unroll
+        for (int i = 0; i < NW; i++) wv[i] = rw[q0 + i < BITS ? q0 + i : BITS - 1];
+    };
+    auto gather = [&](const uint32_t (&wv)[NW], uint32_t (&v)[NF], uint32_t (&vl)[NF]) {
+#pragma unroll
+        for (int j = 0; j < NF; j++) {
+            const int o = sh0 + j * BITS;
             const int q = o >> 5, sh = o & 31;
             uint32_t f;
             if (sh + BITS <= 32) f = (wv[q] >> sh) & mask;
             else f = __builtin_amdgcn_alignbit(wv[q + 1], wv[q], (uint32_t)sh) & mask;
-            v[h] = s_cb[f];
-            if (TWO) vl[h] = s_cblo[f];
+            v[j] = s_cb[f];
+            if (TWO) vl[j] = s_cblo[f];
         }
-        pk[j >> 1] = v[0] | (v[1] << 16);
-        if (TWO) pl[j >> 1] = vl[0] | (vl[1] << 16);
-    }
-}
-
-// Main K loop.  TWO: the codebook is not bf16-exact, so each weight is
-// split as hi + lo (both bf16, lo = bf16(w - hi)) and both halves go through
-// the MFMA, which keeps ~16 mantissa bits of the fp32 codebook.
-template <int BITS, bool TWO, int WP>
-__device__ __forceinline__ void prefill_loop(
-    const uint16_t *__restrict__ xrow, const uint32_t *__restrict__ wrow, int G, int q0,
-    int sh0, const uint16_t *s_cb, const uint16_t *s_cblo, uint32_t *s_x, uint32_t *s_w,
-    uint32_t *s_wlo, int xr, int xc, int wr, int wp, int lane, int wt, int wmo, bool active,
-    f32x16 (&acc)[2][2])
-{
-    constexpr int NW = (8 * BITS + 31 + 31) / 32;             // words covering 8 fields
-    auto load_step = [&](int g, u32x4 (&xv)[2], uint32_t (&wv)[NW]) {
-        const u32x4 *xs = (const u32x4 *)(xrow + (size_t)g * kPK);
-        xv[0] = xs[0];
-        xv[1] = xs[1];
-        const uint32_t *ws = wrow + (size_t)g * BITS;
-        // words past the group's last one are never used: clamp them in
-#pragma unroll
-        for (int i = 0; i < NW; i++) wv[i] = ws[q0 + i < BITS ? i : BITS - 1 - q0];
     };
-    // Four K steps in flight: a register ring of x and index words.  The LDS
-    // tiles are double-buffered: step g's MFMAs read buffer g & 1 while the
-    // waves decode and write step g + 1 into the other buffer, so each step
-    // needs one barrier, and the decode overlaps the matrix core.  The loop
-    // is unrolled by the ring depth (even) so ring slots and buffers are
-    // fixed registers and addresses; barriers wait on LDS only.
-    constexpr int PD = 4;
-    u32x4 xv[PD][2];
-    uint32_t wv[PD][NW];
+    auto store_w = [&](int buf, const uint32_t (&v)[NF], const uint32_t (&vl)[NF]) {
 #pragma unroll
-    for (int d = 0; d < PD; d++) load_step(d < G ? d : G - 1, xv[d], wv[d]);
-
-    auto stage = [&](int d, int g, int buf) {
-        const bool live = g < G;
-        uint32_t *bx = s_x + buf * (kPT * 16);
-        uint32_t *bw = s_w + buf * (kPM * 16);
-        uint32_t *bl = s_wlo + buf * (kPM * 16);
-        *(u32x4 *)tile_chunk(bx, xr, xc) = live ? xv[d][0] : u32x4{0, 0, 0, 0};
-        *(u32x4 *)tile_chunk(bx, xr, xc + 1) = live ? xv[d][1] : u32x4{0, 0, 0, 0};
-        uint32_t pk[4], pl[4];
-        decode_part<BITS, WP, TWO>(wv[d], s_cb, s_cblo, pk, pl);
-        *(u32x4 *)tile_chunk(bw, wr, wp) = u32x4{pk[0], pk[1], pk[2], pk[3]};
-        if (TWO) *(u32x4 *)tile_chunk(bl, wr, wp) = u32x4{pl[0], pl[1], pl[2], pl[3]};
+        for (int h = 0; h < NF / 8; h++) {
+            const int o = buf * kWBuf + wslot(wr, (NF / 8) * HP + h);
+            const int e = 8 * h;
+            s_w[o] = u32x4{v[e] | (v[e + 1] << 16), v[e + 2] | (v[e + 3] << 16),
+                           v[e + 4] | (v[e + 5] << 16), v[e + 6] | (v[e + 7] << 16)};
+            if (TWO)
+                s_wlo[o] = u32x4{vl[e] | (vl[e + 1] << 16), vl[e + 2] | (vl[e + 3] << 16),
+                                 vl[e + 4] | (vl[e + 5] << 16), vl[e + 6] | (vl[e + 7] << 16)};
+        }
     };
-    auto mfma_step = [&](int buf) {
-        const uint32_t *bx = s_x + buf * (kPT * 16);
-        const uint32_t *bw = s_w + buf * (kPM * 16);
-        const uint32_t *bl = s_wlo + buf * (kPM * 16);
+    auto read_frag = [&](int buf, int nb, bf16x8 &b, bf16x8 &bl) {
+        const u32x4 v = s_w[buf * kWBuf + fo + nb * 64];
+        __builtin_memcpy(&b, &v, 16);
+        if (TWO) {
+            const u32x4 vl = s_wlo[buf * kWBuf + fo + nb * 64];
+            __builtin_memcpy(&bl, &vl, 16);
+        }
+    };
+    // MFMAs of feature blocks [n0, n1) of step g.  bf16 codebook: each block
+    // is followed by the read of its fragment for step g + 1 (buffer nbuf)
+    // into the same registers.  hi + lo codebook (twice the fragments): the
+    // step's own fragments are read from buffer cbuf just before their MFMAs.
+    auto mfma_blocks = [&](int n0, int n1, bool on, const bf16x8 (&xr)[kTB], bf16x8 (&bf)[kNB],
+                           int cbuf, int nbuf) {
 #pragma unroll
-        for (int kk = 0; kk < 2; kk++) {   // two k16 halves of the 32-wide step
-            bf16x8 af[2], bfr[2], bfl[2];
-            const int c = kk * 2 + (lane >> 5);        // 16-byte chunk of the row
+        for (int nb = n0; nb < n1; nb++) {
+            bf16x8 b = bf[nb], bl;
+            if (TWO) read_frag(cbuf, nb, b, bl);
+            if (on) {
 #pragma unroll
-            for (int a = 0; a < 2; a++) {
-                const int r = wt + a * 32 + (lane & 31);
-                const u32x4 v = *(const u32x4 *)tile_chunk((uint32_t *)bx, r, c);
-                __builtin_memcpy(&af[a], &v, 16);
-            }
-#pragma unroll
-            for (int b = 0; b < 2; b++) {
-                const int r = wmo + b * 32 + (lane & 31);
-                const u32x4 v = *(const u32x4 *)tile_chunk((uint32_t *)bw, r, c);
-                __builtin_memcpy(&bfr[b], &v, 16);
-                if (TWO) {
-                    const u32x4 vl = *(const u32x4 *)tile_chunk((uint32_t *)bl, r, c);
-                    __builtin_memcpy(&bfl[b], &vl, 16);
-                }
-            }
-#pragma unroll
-            for (int a = 0; a < 2; a++)
-#pragma unroll
-                for (int b = 0; b < 2; b++) {
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[b], acc[a][b],
-                                                                         0, 0, 0);
+                for (int tb = 0; tb < kTB; tb++) {
+                    acc[tb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xr[tb], b, acc[tb][nb],
+                                                                          0, 0, 0);
                     if (TWO)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfl[b],
-                                                                             acc[a][b], 0, 0, 0);
+                        acc[tb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xr[tb], bl,
+                                                                              acc[tb][nb], 0, 0, 0);
                 }
+            }
+            if (!TWO) read_frag(nbuf, nb, bf[nb], bl);
         }
     };
 
-    stage(0, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_step(PD < G ? PD : G - 1, xv[0], wv[0]);
-    __builtin_amdgcn_sched_barrier(0);
-    lds_barrier();
-    // Steps past G (G not a multiple of PD) run on zeroed x, adding nothing;
-    // keeping them unconditional keeps the loop body branch-free.
-    for (int g0 = 0; g0 < G; g0 += PD) {
+    bf16x8 xr[kXD][kTB];
+    uint32_t rr[kRD][ND];
+    bf16x8 bf[kNB];
+    {
+        uint32_t r0[ND], r1[ND], r2[ND];
+        load_raw(0, r0);
+        load_raw(1, r1);
+        load_raw(2, r2);
 #pragma unroll
-        for (int d = 0; d < PD; d++) {
-            const int g = g0 + d;
-            const int dn = (d + 1) % PD;
-            // waves whose 64 tokens all lie past T (a short batch) only stage
-            if (active) mfma_step(d & 1);
-            stage(dn, g + 1, (d + 1) & 1);
-            // refill the staged slot (a clamped repeat past the end: never
-            // written); the scheduling barriers keep the loads PD steps ahead
+        for (int d = 0; d < kRD; d++) load_raw(d + 3, rr[d]);
+#pragma unroll
+        for (int d = 0; d < kXD; d++) load_x(d, xr[d]);
+        store_raw(0, r0);
+        store_raw(1, r1);
+        lds_barrier();
+        uint32_t wv[NW], v[NF], vl[NF];
+        read_words(0, wv);
+        gather(wv, v, vl);
+        store_w(0, v, vl);
+        lds_barrier();                                   // slot 0 free again
+        store_raw(0, r2);
+        read_words(1, wv);
+        gather(wv, v, vl);
+        store_w(1, v, vl);
+        lds_barrier();
+        if (!TWO) {
+            bf16x8 bl;
+#pragma unroll
+            for (int nb = 0; nb < kNB; nb++) read_frag(0, nb, bf[nb], bl);
+        }
+    }
+    for (int g0 = 0; g0 < G; g0 += kUnroll) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; u++) {
+            const int g = g0 + u;                        // g % kUnroll == u
+            const bool on = active && g < G;
+            store_raw((u + 1) & 1, rr[u % kRD]);         // words of step g + 3
+            load_raw(g + 3 + kRD, rr[u % kRD]);
+            uint32_t wv[NW], v[NF], vl[NF];
             __builtin_amdgcn_sched_barrier(0);
-            load_step(g + 1 + PD < G ? g + 1 + PD : G - 1, xv[dn], wv[dn]);
+            mfma_blocks(0, 2, on, xr[u % kXD], bf, u % 3, (u + 1) % 3);
             __builtin_amdgcn_sched_barrier(0);
+            read_words(u & 1, wv);                       // step g + 2's words
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_blocks(2, 4, on, xr[u % kXD], bf, u % 3, (u + 1) % 3);
+            __builtin_amdgcn_sched_barrier(0);
+            gather(wv, v, vl);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_blocks(4, 6, on, xr[u % kXD], bf, u % 3, (u + 1) % 3);
+            __builtin_amdgcn_sched_barrier(0);
+            store_w((u + 2) % 3, v, vl);
+            __builtin_amdgcn_sched_barrier(0);
+            mfma_blocks(6, kNB, on, xr[u % kXD], bf, u % 3, (u + 1) % 3);
+            __builtin_amdgcn_sched_barrier(0);
+            load_x(g + kXD, xr[u % kXD]);
             lds_barrier();
         }
     }
@@ -186,22 +254,25 @@ __device__ __forceinline__ void prefill_loop(
 
 // SPLIT: block z sums only K groups [z * gs, z * gs + gs) and writes its fp32
 // partial tile to ws + z * T * M; prefill_reduce_kernel adds the partials.
-template <int BITS, bool SPLIT>
+// Block b takes token tile b % nT of feature tile b / nT.
+template <int BITS, bool SPLIT, bool XF>
 __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     const uint16_t *__restrict__ x, const uint32_t *__restrict__ words,
     const float *__restrict__ cb, uint16_t *__restrict__ out, int T, int M, int K, int C,
-    float *__restrict__ ws, int gs)
+    float *__restrict__ ws, int gs, int nT)
 {
     __shared__ uint16_t s_cb[1 << BITS];                       // bf16 codebook (hi), padded
     __shared__ uint16_t s_cblo[1 << BITS];                     // bf16(cb - hi)
-    __shared__ __attribute__((aligned(16))) uint32_t s_x[2 * kPT * 16];   // 2 x [256][32] bf16
-    __shared__ __attribute__((aligned(16))) uint32_t s_w[2 * kPM * 16];   // 2 x [128][32] bf16
-    __shared__ __attribute__((aligned(16))) uint32_t s_wlo[2 * kPM * 16];
+    __shared__ __attribute__((aligned(16))) u32x4 s_wt[kWtChunks];   // W tiles, then the epilogue's
+    __shared__ uint32_t s_raw[2 * kRawSlot<BITS>];
+    u32x4 *s_w = s_wt;                                         // 3 x [128][32] bf16
+    u32x4 *s_wlo = s_wt + 3 * kWBuf;
 
     const int tid = threadIdx.x;
     const int lane = tid & (CBQ_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / CBQ_WAVE);
-    const int t0 = blockIdx.x * kPT, m0 = blockIdx.y * kPM;
+    const int t0 = (int)(blockIdx.x % (unsigned)nT) * kPT;
+    const int m0 = (int)(blockIdx.x / (unsigned)nT) * kPM;
     const int G_all = K / kPK;
     const int g_lo = SPLIT ? (int)blockIdx.z * gs : 0;
     const int G = SPLIT ? min(G_all, g_lo + gs) - g_lo : G_all;
@@ -218,39 +289,51 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     }
     const bool two = __syncthreads_or(inexact);        // also publishes the codebook
 
-    // x staging: thread -> tile row tid/2, chunks 2*(tid%2) and +1 (clamped row)
-    const int xr = tid >> 1, xc = (tid & 1) * 2;
-    const int xt = min(t0 + xr, T - 1);
-    const uint16_t *xrow = x + (size_t)xt * K + (size_t)g_lo * kPK + xc * 8;
-    // W decode: wave w takes part w % 4 (indices 8*part .. +7 of each group)
-    // of tile rows 64*(w / 4) + lane, so the part is wave-uniform
-    const int wr = ((wave >> 2) << 6) + lane, wp = wave & 3;
-    const int wm = min(m0 + wr, M - 1);
-    const int bit0 = wp * 8 * BITS;                            // within the 32-index group
-    const int q0 = bit0 >> 5, sh0 = bit0 & 31;
-    const uint32_t *wrow = words + ((size_t)wm * G_all + g_lo) * BITS + q0;
+    // x fragments: token block tb, lane -> row lane % 16, k chunk lane / 16.
+    // XF: x is in fragment order (prefill_x_frag_kernel), the wave's 1 KiB
+    // fragment of each step is contiguous; else row-major with rows clamped.
+    uint32_t xoff[kTB];
+#pragma unroll
+    for (int tb = 0; tb < kTB; tb++) {
+        if (XF) {
+            const int b = min(t0 + wave * kWT + tb * 16, ((T + 15) & ~15) - 16) >> 4;
+            xoff[tb] = ((uint32_t)b * (uint32_t)G_all + (uint32_t)g_lo) * 512u + (uint32_t)lane * 8u;
+        } else {
+            xoff[tb] = (uint32_t)min(t0 + wave * kWT + tb * 16 + (lane & 15), T - 1) * (uint32_t)K +
+                       (uint32_t)(g_lo * kPK + (lane >> 4) * 8);
+        }
+    }
+    // index words: load j of thread tid is dword s = j * 512 + tid of the
+    // step's slot = word s % BITS of tile row s / BITS (rows clamped)
+    const uint32_t RW = (uint32_t)G_all * BITS;
+    uint32_t doff[kRawLoads<BITS>];
+#pragma unroll
+    for (int j = 0; j < kRawLoads<BITS>; j++) {
+        const int s = j * kPBlock + tid;
+        const int row = s / BITS, w = s - row * BITS;
+        doff[j] = (uint32_t)min(m0 + row, M - 1) * RW + (uint32_t)(g_lo * BITS + w);
+    }
 
-    f32x16 acc[2][2];
+    f32x4 acc[kTB][kNB];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < kTB; a++)
 #pragma unroll
-        for (int b = 0; b < 2; b++) acc[a][b] = f32x16{};
-    const int wt = (wave >> 1) * 64;      // wave's token offset in the tile
-    const int wmo = (wave & 1) * 64;      // wave's feature offset in the tile
-    // one loop instance per (split, part): the loop body itself has no branch
-    const bool active = t0 + wt < T;      // wave-uniform
-#define CBQ_PREFILL_LOOP(TW, P)                                                                  \
-    prefill_loop<BITS, TW, P>(xrow, wrow, G, q0, sh0, s_cb, s_cblo, s_x, s_w, s_wlo, xr, xc, wr, \
-                              wp, lane, wt, wmo, active, acc)
+        for (int b = 0; b < kNB; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // waves whose 64 tokens all lie past T decode their share but skip the MFMAs
+    const bool active = t0 + wave * kWT < T;
+#define CBQ_PREFILL_LOOP(TW, H)                                                                 \
+    prefill_loop<BITS, TW, H, XF>(x, xoff, words, doff, G, s_cb, s_cblo, s_w, s_wlo, s_raw, wave, \
+                                  lane, active, acc)
+    static_assert(kPWaves == 8, "the part switch below has kPWaves / 2 cases");
     if (two) {
-        switch (wp) {
+        switch (wave & 3) {
         case 0: CBQ_PREFILL_LOOP(true, 0); break;
         case 1: CBQ_PREFILL_LOOP(true, 1); break;
         case 2: CBQ_PREFILL_LOOP(true, 2); break;
         default: CBQ_PREFILL_LOOP(true, 3); break;
         }
     } else {
-        switch (wp) {
+        switch (wave & 3) {
         case 0: CBQ_PREFILL_LOOP(false, 0); break;
         case 1: CBQ_PREFILL_LOOP(false, 1); break;
         case 2: CBQ_PREFILL_LOOP(false, 2); break;
@@ -259,25 +342,68 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     }
 #undef CBQ_PREFILL_LOOP
 
-    // acc[a][b][i*4+j] = C[tok = wt + a*32 + i*8 + (lane/32)*4 + j][feat = wmo + b*32 + lane%32]
+    // acc[tb][nb][r] = out[token t0 + 64 wave + 16 tb + 4 (lane / 16) + r]
+    //                     [feature m0 + 16 nb + lane % 16]
+    // Through LDS, kEpiRows tokens per pass: each wave writes its values into
+    // a padded row-major tile of its own and stores whole rows.
+    lds_barrier();                                    // every wave is done with the LDS above
+    constexpr int ES = SPLIT ? 4 : 2;                 // bytes per output value
+    constexpr int RS = kEpiRow<SPLIT>;
+    constexpr int LPR = kPM * ES / 16;                // lanes per row (16 bytes each)
+    constexpr int HB = kEpiRows / 16;                 // token blocks per pass
+    uint8_t *tile = (uint8_t *)s_wt + wave * kEpiRows * RS;
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int p = 0; p < kTB / HB; p++) {
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
-            const int m = m0 + wmo + b * 32 + (lane & 31);
-            if (m >= M) continue;
+        for (int h = 0; h < HB; h++)
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int nb = 0; nb < kNB; nb++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int t = t0 + wt + a * 32 + i * 8 + (lane >> 5) * 4 + j;
-                    if (t >= T) continue;
+                for (int r = 0; r < 4; r++) {
+                    const int row = h * 16 + (lane >> 4) * 4 + r, col = nb * 16 + (lane & 15);
                     if (SPLIT)
-                        ws[((size_t)blockIdx.z * T + t) * M + m] = acc[a][b][i * 4 + j];
+                        *(float *)(tile + row * RS + col * 4) = acc[HB * p + h][nb][r];
                     else
-                        out[(size_t)t * M + m] = f32_to_bf16_rne(acc[a][b][i * 4 + j]);
+                        *(uint16_t *)(tile + row * RS + col * 2) =
+                            f32_to_bf16_rne(acc[HB * p + h][nb][r]);
                 }
+#pragma unroll
+        for (int i = 0; i < kEpiRows * LPR / CBQ_WAVE; i++) {
+            const int row = i * (CBQ_WAVE / LPR) + lane / LPR, c = lane % LPR;
+            const u32x4 v = *(const u32x4 *)(tile + row * RS + c * 16);
+            const int t = t0 + wave * kWT + p * kEpiRows + row;
+            const int m = m0 + c * (16 / ES);
+            if (t >= T || m >= M) continue;
+            uint8_t *dst = SPLIT ? (uint8_t *)(ws + ((size_t)blockIdx.z * T + t) * M + m)
+                                 : (uint8_t *)(out + (size_t)t * M + m);
+            if (m + 16 / ES <= M && ((uintptr_t)dst & 15) == 0) {
+                *(u32x4 *)dst = v;
+            } else {
+                const uint8_t *src = (const uint8_t *)&v;
+                for (int e = 0; e < 16 / ES && m + e < M; e++)
+                    __builtin_memcpy(dst + e * ES, src + e * ES, ES);
+            }
         }
+    }
+}
+
+// x [T][K] bf16 row-major -> fragment order: piece i (16 bytes) of chunk
+// c = b * (K / 32) + g holds x[16 b + i % 16][32 g + 8 (i / 16) .. +7], i.e.
+// lane i's MFMA A operand for token block b at K step g; rows >= T are 0.
+// Writes are contiguous; each thread moves one 16-byte piece.
+__global__ void prefill_x_frag_kernel(const uint16_t *__restrict__ x, uint16_t *__restrict__ xf,
+                                      int T, int K)
+{
+    const uint32_t G = (uint32_t)K / kPK;
+    const uint32_t n = (uint32_t)((T + 15) >> 4) * G * CBQ_WAVE;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const uint32_t l = i & (CBQ_WAVE - 1), c = i / CBQ_WAVE;
+        const uint32_t g = c % G, b = c / G;
+        const int t = (int)(b * 16 + (l & 15));
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (t < T) v = *(const u32x4 *)(x + (size_t)t * K + g * kPK + (l >> 4) * 8);
+        *(u32x4 *)(xf + (size_t)i * 8) = v;
+    }
 }
 
 // out = bf16(sum over s of ws[s]), s in order.
@@ -292,22 +418,24 @@ __global__ void prefill_reduce_kernel(const float *__restrict__ ws, int S, int64
     }
 }
 
-template <int BITS>
-int launch_prefill(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
-                   int T, int M, int K, int C, int S, float *ws, hipStream_t st)
+template <int BITS, bool XF>
+int launch_prefill_x(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
+                     int T, int M, int K, int C, int S, float *ws, hipStream_t st)
 {
     const int G = K / kPK;
+    const int nT = (T + kPT - 1) / kPT;
+    const unsigned tiles = (unsigned)nT * (unsigned)((M + kPM - 1) / kPM);
     if (S <= 1) {
-        dim3 grid((unsigned)((T + kPT - 1) / kPT), (unsigned)((M + kPM - 1) / kPM));
-        hipLaunchKernelGGL((fixed_prefill_kernel<BITS, false>), grid, dim3(kPBlock), 0, st, x,
-                           (const uint32_t *)packed, cb, out, T, M, K, C, (float *)nullptr, G);
+        hipLaunchKernelGGL((fixed_prefill_kernel<BITS, false, XF>), dim3(tiles), dim3(kPBlock), 0,
+                           st, x, (const uint32_t *)packed, cb, out, T, M, K, C, (float *)nullptr,
+                           G, nT);
         return cbq_launch_status("fixed_prefill_kernel");
     }
     const int gs = (G + S - 1) / S;
     S = (G + gs - 1) / gs;                                   // no empty split
-    dim3 grid((unsigned)((T + kPT - 1) / kPT), (unsigned)((M + kPM - 1) / kPM), (unsigned)S);
-    hipLaunchKernelGGL((fixed_prefill_kernel<BITS, true>), grid, dim3(kPBlock), 0, st, x,
-                       (const uint32_t *)packed, cb, out, T, M, K, C, ws, gs);
+    hipLaunchKernelGGL((fixed_prefill_kernel<BITS, true, XF>), dim3(tiles, 1, (unsigned)S),
+                       dim3(kPBlock), 0, st, x, (const uint32_t *)packed, cb, out, T, M, K, C, ws,
+                       gs, nT);
     int rc = cbq_launch_status("fixed_prefill_kernel");
     if (rc) return rc;
     const int64_t n = (int64_t)T * M;
@@ -316,40 +444,65 @@ int launch_prefill(const uint16_t *x, const uint8_t *packed, const float *cb, ui
     return cbq_launch_status("prefill_reduce_kernel");
 }
 
+// xf != nullptr: x is first copied to fragment order there (prefill_x_frag_kernel)
+template <int BITS>
+int launch_prefill(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
+                   int T, int M, int K, int C, int S, float *ws, uint16_t *xf, hipStream_t st)
+{
+    if (!xf) return launch_prefill_x<BITS, false>(x, packed, cb, out, T, M, K, C, S, ws, st);
+    const uint32_t pieces = (uint32_t)((T + 15) >> 4) * (uint32_t)(K / kPK) * CBQ_WAVE;
+    const unsigned blocks = (unsigned)std::min<uint32_t>((pieces + 255) / 256, 8192);
+    hipLaunchKernelGGL(prefill_x_frag_kernel, dim3(blocks), dim3(256), 0, st, x, xf, T, K);
+    const int rc = cbq_launch_status("prefill_x_frag_kernel");
+    if (rc) return rc;
+    return launch_prefill_x<BITS, true>(xf, packed, cb, out, T, M, K, C, S, ws, st);
+}
+
 }  // namespace
 
-// K splits for a T x M x K prefill.  Only grids of fewer tiles than half the
-// CUs split (past that the partials' extra traffic costs more than the idle
-// CUs): into enough blocks to cover the CUs once, with at least 8 K groups
-// (256 inputs) per split and at most 16 splits.
+// K splits for a T x M x K prefill.  A grid of fewer tiles than CUs (one
+// 512-thread block per CU) splits K so the blocks cover the CUs at most once:
+// floor(CUs / tiles) splits, at most 16, with at least 8 K groups (256
+// inputs) per split.
 int cbq_prefill_splits(int T, int M, int K)
 {
     if (T < 64 || K % kPK != 0) return 1;
     const int64_t tiles = (int64_t)((T + kPT - 1) / kPT) * ((M + kPM - 1) / kPM);
     const int64_t cus = cbq_num_cus();
-    if (2 * tiles >= cus) return 1;
-    int S = (int)std::min<int64_t>((cus + tiles - 1) / tiles, 16);
+    if (tiles * 2 > cus) return 1;
+    int S = (int)std::min<int64_t>(cus / tiles, 16);
     S = std::min(S, (K / kPK) / 8);
     return S < 2 ? 1 : S;
 }
 
-// Prefill dispatch used by ck_linear_bf16 (cbq_fixed.hip).  Returns -1 when
-// the shape is not handled here (the caller keeps its token-tile path).
-// S > 1 needs ws of S * T * M floats.
+// Bytes of the fragment-order copy of x a T x K prefill can use (xf below).
+size_t cbq_prefill_xf_bytes(int T, int K)
+{
+    if (T < 64 || K % kPK != 0) return 0;
+    return ((size_t)((T + 15) & ~15) * K * sizeof(uint16_t) + 255) & ~(size_t)255;
+}
+
+// Prefill dispatch used by ck_linear_bf16 / cbq_linear_bf16_ws (cbq_fixed.hip).
+// Returns -1 when the shape is not handled here (the caller keeps its
+// token-tile path).  S > 1 needs ws of S * T * M floats; xf (16-byte aligned,
+// cbq_prefill_xf_bytes) holds x in fragment order, or nullptr: x is then read
+// row-major, more slowly (a lane per row).
 int cbq_prefill_bf16(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
-                     int T, int M, int K, int C, int bits, hipStream_t st, int S, float *ws)
+                     int T, int M, int K, int C, int bits, hipStream_t st, int S, float *ws,
+                     uint16_t *xf)
 {
     if (T < 64 || K % kPK != 0 || (((uintptr_t)packed | (uintptr_t)x) & 15) != 0 ||
-        (K * 2) % 16 != 0 || (size_t)T > 65535ull * kPT || M > 65535 * kPM)
-        return -1;
-    if (S > 1 && !ws) return -1;
+        (K * 2) % 16 != 0 || (uint64_t)((T + 15) & ~15) * K >= (1ull << 32) ||
+        (uint64_t)M * (K / kPK) * bits >= (1ull << 32))
+        return -1;                                       // 32-bit element and word offsets
+    if ((S > 1 && !ws) || (((uintptr_t)xf) & 15) != 0) return -1;
     switch (bits) {
-    case 8: return launch_prefill<8>(x, packed, cb, out, T, M, K, C, S, ws, st);
-    case 10: return launch_prefill<10>(x, packed, cb, out, T, M, K, C, S, ws, st);
-    case 11: return launch_prefill<11>(x, packed, cb, out, T, M, K, C, S, ws, st);
-    case 12: return launch_prefill<12>(x, packed, cb, out, T, M, K, C, S, ws, st);
-    case 13: return launch_prefill<13>(x, packed, cb, out, T, M, K, C, S, ws, st);
-    case 14: return launch_prefill<14>(x, packed, cb, out, T, M, K, C, S, ws, st);
+    case 8: return launch_prefill<8>(x, packed, cb, out, T, M, K, C, S, ws, xf, st);
+    case 10: return launch_prefill<10>(x, packed, cb, out, T, M, K, C, S, ws, xf, st);
+    case 11: return launch_prefill<11>(x, packed, cb, out, T, M, K, C, S, ws, xf, st);
+    case 12: return launch_prefill<12>(x, packed, cb, out, T, M, K, C, S, ws, xf, st);
+    case 13: return launch_prefill<13>(x, packed, cb, out, T, M, K, C, S, ws, xf, st);
+    case 14: return launch_prefill<14>(x, packed, cb, out, T, M, K, C, S, ws, xf, st);
     default: return -1;
     }
 }

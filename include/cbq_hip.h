@@ -80,17 +80,19 @@ int ck_linear_bf16(const void *x_bf16, const uint8_t *packed, const float *codeb
                    void *out_bf16, int T, int M, int K, int C, int bits,
                    hipStream_t stream);
 
-/* Workspace bytes cbq_linear_bf16_ws splits K with for a T x M x K product
- * (0: no split).  No counterpart in the reference. */
+/* Workspace bytes of cbq_linear_bf16_ws for a T x M x K product: room for a
+ * copy of x in MFMA fragment order, plus fp32 partials when K is split (0:
+ * the shape does not take the MFMA path).  No counterpart in the reference. */
 size_t cbq_linear_bf16_workspace(int T, int M, int K);
 
-/* ck_linear_bf16 with a caller workspace: for T >= 64 on the MFMA path, when
- * the output tiles alone would leave CUs idle, K is split across blocks that
- * write fp32 partials to `workspace` (>= cbq_linear_bf16_workspace bytes,
- * 16-byte aligned), summed in split order by a second kernel.  With a
- * smaller workspace it is ck_linear_bf16.  No counterpart in the reference:
- * the prefill of GPUAcceleratedLinear (src/gpu_accelerated_functions.py:928-950)
- * for batched tokens. */
+/* ck_linear_bf16 with a caller workspace (>= cbq_linear_bf16_workspace
+ * bytes, 256-byte aligned).  For T >= 64 on the MFMA path x is first copied
+ * to fragment order in the workspace (each wave's operand loads are then
+ * contiguous), and when the output tiles alone would leave CUs idle, K is
+ * split across blocks that write fp32 partials there too, summed in split
+ * order by a second kernel.  With a smaller workspace it is ck_linear_bf16.
+ * No counterpart in the reference: the prefill of GPUAcceleratedLinear
+ * (src/gpu_accelerated_functions.py:928-950) for batched tokens. */
 int cbq_linear_bf16_ws(const void *x_bf16, const uint8_t *packed, const float *codebook,
                        void *out_bf16, int T, int M, int K, int C, int bits, void *workspace,
                        size_t ws_bytes, hipStream_t stream);

@@ -16,7 +16,9 @@ TOL = 2e-3
 
 
 def _prefill(cuda, xb, pk, cb, M, K, bits, split=False):
-    """ck_linear_bf16, or with split cbq_linear_bf16_ws with its workspace."""
+    """ck_linear_bf16 (x read row-major), or with split cbq_linear_bf16_ws
+    with its workspace (x copied to fragment order, K split when the grid is
+    small)."""
     import bitpack
     import cbq_native as nat
     lib = nat.load()
@@ -27,7 +29,7 @@ def _prefill(cuda, xb, pk, cb, M, K, bits, split=False):
     out = torch.full((T, M), float("nan"), dtype=torch.bfloat16, device=cuda)
     if split:
         nws = int(lib.cbq_linear_bf16_workspace(T, M, K))
-        assert nws > 0, "shape expected to split K"
+        assert nws > 0, "shape expected to take the MFMA path"
         ws = torch.full((nws // 4,), float("nan"), dtype=torch.float32, device=cuda)
         rc = lib.cbq_linear_bf16_ws(xd.data_ptr(), pd.data_ptr(), cd.data_ptr(), out.data_ptr(),
                                     T, M, K, len(cb), bits, ws.data_ptr(), nws,
@@ -119,6 +121,24 @@ def test_split_k_matches_oracle(cuda, oracle, T, M, K):
     _check(ys, ref)
     y1 = _prefill(cuda, xb, d["indices"], d["codebook"], M, K, d["bits"])
     assert rel_l2(ys, y1) <= TOL
+
+
+@pytest.mark.parametrize("T,M,K", [(1030, 8200, 512), (2048, 12288, 128)])
+def test_workspace_path_unsplit_ragged(cuda, oracle, T, M, K):
+    """Grids large enough not to split, through cbq_linear_bf16_ws (x in
+    fragment order): T and M off every tile multiple, the padded last token
+    block and feature tile included."""
+    import cbq_native as nat
+    assert nat.load().cbq_linear_bf16_workspace(T, M, K) == ((T + 15) // 16 * 16 * K * 2 + 255) // 256 * 256
+    w = cbb.bf16_round(np.random.default_rng(T + K).standard_normal((M, K)) * 0.02)
+    d = cbb.compress_fixed(w)
+    xb = torch.randn(T, K, generator=torch.Generator().manual_seed(K)).bfloat16()
+    y = _prefill(cuda, xb, d["indices"], d["codebook"], M, K, d["bits"], split=True)
+    ref = oracle.fixed_gemv(xb.float().numpy(), d["indices"], d["codebook"], M, K, d["bits"],
+                            chunk_rows=None)
+    _check(y, ref)
+    y1 = _prefill(cuda, xb, d["indices"], d["codebook"], M, K, d["bits"])
+    assert rel_l2(y, y1) <= TOL
 
 
 def test_split_k_inexact_codebook_and_clamp(cuda, oracle):
