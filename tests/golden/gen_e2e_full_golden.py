@@ -24,9 +24,9 @@ logits are the fixed-width ones bit for bit.  Rather than decode the whole
 model twice on the CPU, this script checks that equality on layer 0's
 q_proj and gate_proj and records it.
 
-    python tests/golden/gen_e2e_full_golden.py [--tokens 64] [--prompt 128]
+    python tests/golden/gen_e2e_full_golden.py [--tokens 256] [--prompt 128]
 
-About 20 minutes on 8 cores and ~30 GB of RAM.
+About 35 minutes on 8 cores (12 for the prompt, ~5 s per generated token) and ~30 GB of RAM.
 """
 import argparse
 import os
@@ -120,7 +120,7 @@ def huffman_check(comp, x_q: np.ndarray, x_gate: np.ndarray, kind: str) -> bool:
 
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--tokens", type=int, default=64)
+    ap.add_argument("--tokens", type=int, default=256)
     ap.add_argument("--prompt", type=int, default=128)
     ap.add_argument("--threads", type=int, default=os.cpu_count() or 8)
     ap.add_argument("--out", default=OUT)
