@@ -390,19 +390,32 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
 // x [T][K] bf16 row-major -> fragment order: piece i (16 bytes) of chunk
 // c = b * (K / 32) + g holds x[16 b + i % 16][32 g + 8 (i / 16) .. +7], i.e.
 // lane i's MFMA A operand for token block b at K step g; rows >= T are 0.
-// Writes are contiguous; each thread moves one 16-byte piece.
-__global__ void prefill_x_frag_kernel(const uint16_t *__restrict__ x, uint16_t *__restrict__ xf,
-                                      int T, int K)
+// Block (b, s) moves token block b over K steps [8 s, 8 s + 8): row-contiguous
+// reads into a padded LDS tile, then fragment-order reads and contiguous
+// writes (both global sides coalesced).
+constexpr int kXfSteps = 8;
+constexpr int kXfRow = kXfSteps * kPK * 2 + 16;        // LDS bytes per token row (padded)
+__global__ __launch_bounds__(256) void prefill_x_frag_kernel(const uint16_t *__restrict__ x,
+                                                             uint16_t *__restrict__ xf, int T,
+                                                             int K)
 {
-    const uint32_t G = (uint32_t)K / kPK;
-    const uint32_t n = (uint32_t)((T + 15) >> 4) * G * CBQ_WAVE;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
-        const uint32_t l = i & (CBQ_WAVE - 1), c = i / CBQ_WAVE;
-        const uint32_t g = c % G, b = c / G;
-        const int t = (int)(b * 16 + (l & 15));
+    __shared__ __attribute__((aligned(16))) uint8_t tile[16 * kXfRow];
+    const int G = K / kPK;
+    const int b = blockIdx.x, g0 = blockIdx.y * kXfSteps;
+    const int ns = min(kXfSteps, G - g0);                // K steps in this block
+    constexpr int kRowPieces = kXfSteps * 4;            // 16-byte pieces per row
+    for (int i = threadIdx.x; i < 16 * kRowPieces; i += blockDim.x) {
+        const int r = i / kRowPieces, c = i % kRowPieces;
+        const int t = b * 16 + r;
         u32x4 v = {0u, 0u, 0u, 0u};
-        if (t < T) v = *(const u32x4 *)(x + (size_t)t * K + g * kPK + (l >> 4) * 8);
-        *(u32x4 *)(xf + (size_t)i * 8) = v;
+        if (t < T && c < ns * 4) v = *(const u32x4 *)(x + (size_t)t * K + (size_t)g0 * kPK + c * 8);
+        *(u32x4 *)(tile + r * kXfRow + c * 16) = v;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < ns * CBQ_WAVE; i += blockDim.x) {
+        const int gl = i / CBQ_WAVE, l = i % CBQ_WAVE;
+        const u32x4 v = *(const u32x4 *)(tile + (l & 15) * kXfRow + (gl * 4 + (l >> 4)) * 16);
+        *(u32x4 *)(xf + (((size_t)b * G + g0 + gl) * CBQ_WAVE + l) * 8) = v;
     }
 }
 
@@ -450,9 +463,8 @@ int launch_prefill(const uint16_t *x, const uint8_t *packed, const float *cb, ui
                    int T, int M, int K, int C, int S, float *ws, uint16_t *xf, hipStream_t st)
 {
     if (!xf) return launch_prefill_x<BITS, false>(x, packed, cb, out, T, M, K, C, S, ws, st);
-    const uint32_t pieces = (uint32_t)((T + 15) >> 4) * (uint32_t)(K / kPK) * CBQ_WAVE;
-    const unsigned blocks = (unsigned)std::min<uint32_t>((pieces + 255) / 256, 8192);
-    hipLaunchKernelGGL(prefill_x_frag_kernel, dim3(blocks), dim3(256), 0, st, x, xf, T, K);
+    const dim3 grid((unsigned)((T + 15) >> 4), (unsigned)((K / kPK + kXfSteps - 1) / kXfSteps));
+    hipLaunchKernelGGL(prefill_x_frag_kernel, grid, dim3(256), 0, st, x, xf, T, K);
     const int rc = cbq_launch_status("prefill_x_frag_kernel");
     if (rc) return rc;
     return launch_prefill_x<BITS, true>(xf, packed, cb, out, T, M, K, C, S, ws, st);
