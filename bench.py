@@ -232,10 +232,18 @@ def huffman_sweep(torch, nat, lib, dev, huff, splits, plan, steps, warmup):
 
 # ---- sections ------------------------------------------------------------------
 
+def xf_bytes(T, K):
+    """Bytes of the fragment-order copy of x at the front of the
+    cbq_linear_bf16_ws workspace (the rest holds split-K partials)."""
+    return ((T + 15) // 16 * 16 * K * 2 + 255) // 256 * 256
+
+
 def prefill_section(torch, nat, lib, dev, fixed, kinds, args):
     """bf16 MFMA prefill over the same fixed-width weights,
     T = 512 and 2048 tokens of bf16 N(0, 1) activations; per shape the mean
-    launch time over all layers' distinct weights (graph-replayed)."""
+    time of one cbq_linear_bf16_ws call (the x fragment-order copy, the GEMM
+    and, when K is split, the partial sum) over 8 layers' distinct weights
+    (graph-replayed)."""
     out = {"peak_tflops": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "shapes": {}}
     for T in (512, 2048):
         for kind in ("q_proj", "k_proj", "gate_proj", "down_proj"):
@@ -260,7 +268,7 @@ def prefill_section(torch, nat, lib, dev, fixed, kinds, args):
             us = ms * 1e3 / len(ns)
             tf = 2.0 * T * M * K / (us * 1e-6) / 1e12
             out["shapes"][f"T{T}_{kind}"] = {"shape": f"{K}->{M}", "us_per_launch": round(us, 1),
-                                             "k_splits": max(1, nws // (4 * T * M)),
+                                             "k_splits": max(1, (nws - xf_bytes(T, K)) // (4 * T * M)),
                                              "TFLOP/s": round(tf, 1),
                                              "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
     g = out["shapes"]["T2048_gate_proj"]

@@ -102,8 +102,8 @@ class GPUAcceleratedLinear:
         if in_dtype == torch.bfloat16:
             xc = x.reshape(T, self.K).contiguous()
             out = torch.empty(T, self.M, dtype=torch.bfloat16, device=dev)
-            # batched tokens may split K across blocks: fp32 partials in a
-            # workspace from torch's caching allocator
+            # batched tokens: x in MFMA fragment order (and fp32 partials when
+            # K is split) in a workspace from torch's caching allocator
             nws = int(self._lib.cbq_linear_bf16_workspace(T, self.M, self.K)) if T >= 64 else 0
             ws = torch.empty(max(1, nws // 4), dtype=torch.float32, device=dev) if nws else None
             rc = self._lib.cbq_linear_bf16_ws(xc.data_ptr(), self.packed.data_ptr(),
