@@ -234,7 +234,8 @@ def huffman_sweep(torch, nat, lib, dev, huff, splits, plan, steps, warmup):
 
 def xf_bytes(T, K):
     """Bytes of the fragment-order copy of x at the front of the
-    cbq_linear_bf16_ws workspace (the rest holds split-K partials)."""
+    cbq_linear_bf16_ws workspace (the rest holds split-K partials: whole
+    small grids, or the tiles left after the last full round of CUs)."""
     return ((T + 15) // 16 * 16 * K * 2 + 255) // 256 * 256
 
 
@@ -268,7 +269,7 @@ def prefill_section(torch, nat, lib, dev, fixed, kinds, args):
             us = ms * 1e3 / len(ns)
             tf = 2.0 * T * M * K / (us * 1e-6) / 1e12
             out["shapes"][f"T{T}_{kind}"] = {"shape": f"{K}->{M}", "us_per_launch": round(us, 1),
-                                             "k_splits": max(1, (nws - xf_bytes(T, K)) // (4 * T * M)),
+                                             "split_partials_MB": round((nws - xf_bytes(T, K)) / 1e6, 1),
                                              "TFLOP/s": round(tf, 1),
                                              "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
     g = out["shapes"]["T2048_gate_proj"]

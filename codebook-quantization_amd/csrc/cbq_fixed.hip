@@ -941,13 +941,12 @@ int embedding_impl(const int32_t *ids, const uint8_t *packed, const float *cb, f
 }  // namespace
 
 // bf16 MFMA prefill path (cbq_prefill.hip); -1 = shape not handled there.
-// S > 1 splits K, with S * T * M floats of workspace; xf: room for x in
-// fragment order (cbq_prefill_xf_bytes) or nullptr.
+// ws (256-byte aligned, >= cbq_prefill_ws_bytes) holds x in fragment order
+// and the split-K partials; without it x is read row-major and K not split.
 int cbq_prefill_bf16(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
-                     int T, int M, int K, int C, int bits, hipStream_t st, int S, float *ws,
-                     uint16_t *xf);
-int cbq_prefill_splits(int T, int M, int K);
-size_t cbq_prefill_xf_bytes(int T, int K);
+                     int T, int M, int K, int C, int bits, hipStream_t st, void *ws,
+                     size_t ws_bytes);
+size_t cbq_prefill_ws_bytes(int T, int M, int K);
 // fp32 MFMA prefill path (cbq_prefill_f32.hip); -1 = shape not handled there.
 int cbq_prefill_f32(const float *x, const uint8_t *packed, const float *cb, float *out, int T,
                     int M, int K, int C, int bits, hipStream_t st, int S, float *ws);
@@ -1141,8 +1140,8 @@ int ck_linear_bf16(const void *x_bf16, const uint8_t *packed, const float *codeb
     if (x_bf16 && packed && codebook && out_bf16 && T >= 64 && M > 0 && K > 0 && C > 0 &&
         bits >= 1 && bits <= 16) {
         const int rc = cbq_prefill_bf16((const uint16_t *)x_bf16, packed, codebook,
-                                        (uint16_t *)out_bf16, T, M, K, C, bits, stream, 1,
-                                        nullptr, nullptr);
+                                        (uint16_t *)out_bf16, T, M, K, C, bits, stream, nullptr,
+                                        0);
         if (rc >= 0) return rc;
     }
     return linear_any_t<uint16_t, uint16_t>((const uint16_t *)x_bf16, packed, codebook,
@@ -1152,10 +1151,7 @@ int ck_linear_bf16(const void *x_bf16, const uint8_t *packed, const float *codeb
 size_t cbq_linear_bf16_workspace(int T, int M, int K)
 {
     if (T <= 0 || M <= 0 || K <= 0) return 0;
-    const size_t xf = cbq_prefill_xf_bytes(T, K);
-    if (xf == 0) return 0;
-    const int S = cbq_prefill_splits(T, M, K);
-    return xf + (S > 1 ? (size_t)S * T * M * sizeof(float) : 0);
+    return cbq_prefill_ws_bytes(T, M, K);
 }
 
 int cbq_linear_bf16_ws(const void *x_bf16, const uint8_t *packed, const float *codebook,
@@ -1164,17 +1160,12 @@ int cbq_linear_bf16_ws(const void *x_bf16, const uint8_t *packed, const float *c
 {
     if (x_bf16 && packed && codebook && out_bf16 && T >= 64 && M > 0 && K > 0 && C > 0 &&
         bits >= 1 && bits <= 16) {
-        // workspace = [x in fragment order][fp32 split partials]
-        const size_t need = cbq_linear_bf16_workspace(T, M, K);
-        if (need > 0 && workspace && ws_bytes >= need && ((uintptr_t)workspace & 255) == 0) {
-            const size_t xf = cbq_prefill_xf_bytes(T, K);
-            const int S = cbq_prefill_splits(T, M, K);
-            const int rc = cbq_prefill_bf16((const uint16_t *)x_bf16, packed, codebook,
-                                            (uint16_t *)out_bf16, T, M, K, C, bits, stream, S,
-                                            S > 1 ? (float *)((char *)workspace + xf) : nullptr,
-                                            (uint16_t *)workspace);
-            if (rc >= 0) return rc;
-        }
+        // workspace = [x in fragment order][fp32 split partials]; a smaller one
+        // runs as ck_linear_bf16
+        const int rc = cbq_prefill_bf16((const uint16_t *)x_bf16, packed, codebook,
+                                        (uint16_t *)out_bf16, T, M, K, C, bits, stream, workspace,
+                                        ws_bytes);
+        if (rc >= 0) return rc;
     }
     return ck_linear_bf16(x_bf16, packed, codebook, out_bf16, T, M, K, C, bits, stream);
 }

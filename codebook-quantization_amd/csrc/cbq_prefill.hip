@@ -252,14 +252,15 @@ __device__ __forceinline__ void prefill_loop(
     }
 }
 
-// SPLIT: block z sums only K groups [z * gs, z * gs + gs) and writes its fp32
-// partial tile to ws + z * T * M; prefill_reduce_kernel adds the partials.
-// Block b takes token tile b % nT of feature tile b / nT.
+// Block b takes tile tix = tile0 + b: token tile tix % nT of feature tile
+// tix / nT.  SPLIT: block (b, z) sums only K groups [z * gs, z * gs + gs) and
+// writes its fp32 partial tile, row-major [512][128], to partial tile
+// z * gridDim.x + b of ws; prefill_reduce_tiles_kernel adds the partials.
 template <int BITS, bool SPLIT, bool XF>
 __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     const uint16_t *__restrict__ x, const uint32_t *__restrict__ words,
     const float *__restrict__ cb, uint16_t *__restrict__ out, int T, int M, int K, int C,
-    float *__restrict__ ws, int gs, int nT)
+    float *__restrict__ ws, int gs, int nT, int tile0)
 {
     __shared__ uint16_t s_cb[1 << BITS];                       // bf16 codebook (hi), padded
     __shared__ uint16_t s_cblo[1 << BITS];                     // bf16(cb - hi)
@@ -271,21 +272,35 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     const int tid = threadIdx.x;
     const int lane = tid & (CBQ_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / CBQ_WAVE);
-    const int t0 = (int)(blockIdx.x % (unsigned)nT) * kPT;
-    const int m0 = (int)(blockIdx.x / (unsigned)nT) * kPM;
+    const int tix = tile0 + (int)blockIdx.x;
+    const int t0 = (tix % nT) * kPT;
+    const int m0 = (tix / nT) * kPM;
     const int G_all = K / kPK;
     const int g_lo = SPLIT ? (int)blockIdx.z * gs : 0;
     const int G = SPLIT ? min(G_all, g_lo + gs) - g_lo : G_all;
 
-    // bf16 codebook, padded to 2^BITS (clamp semantics), split hi + lo
+    // bf16 codebook, padded to 2^BITS (clamp semantics), split hi + lo; every
+    // load of a thread is issued before the first is used (one latency, not
+    // one per entry)
     int inexact = 0;
-    for (int i = tid; i < (1 << BITS); i += kPBlock) {
-        const float v = cb[i < C ? i : C - 1];
-        const uint16_t hi = f32_to_bf16_rne(v);
-        const uint16_t lo = f32_to_bf16_rne(v - __uint_as_float((uint32_t)hi << 16));
-        s_cb[i] = hi;
-        s_cblo[i] = lo;
-        inexact |= (lo & 0x7fffu) != 0;
+    {
+        constexpr int NE = ((1 << BITS) + kPBlock - 1) / kPBlock;
+        float v[NE];
+#pragma unroll
+        for (int e = 0; e < NE; e++) {
+            const int i = e * kPBlock + tid;
+            v[e] = cb[i < C ? i : C - 1];
+        }
+#pragma unroll
+        for (int e = 0; e < NE; e++) {
+            const int i = e * kPBlock + tid;
+            if (i >= (1 << BITS)) break;
+            const uint16_t hi = f32_to_bf16_rne(v[e]);
+            const uint16_t lo = f32_to_bf16_rne(v[e] - __uint_as_float((uint32_t)hi << 16));
+            s_cb[i] = hi;
+            s_cblo[i] = lo;
+            inexact |= (lo & 0x7fffu) != 0;
+        }
     }
     const bool two = __syncthreads_or(inexact);        // also publishes the codebook
 
@@ -374,7 +389,8 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
             const int t = t0 + wave * kWT + p * kEpiRows + row;
             const int m = m0 + c * (16 / ES);
             if (t >= T || m >= M) continue;
-            uint8_t *dst = SPLIT ? (uint8_t *)(ws + ((size_t)blockIdx.z * T + t) * M + m)
+            uint8_t *dst = SPLIT ? (uint8_t *)(ws + (((size_t)blockIdx.z * gridDim.x + blockIdx.x) *
+                                                         kPT + (t - t0)) * kPM + (m - m0))
                                  : (uint8_t *)(out + (size_t)t * M + m);
             if (m + 16 / ES <= M && ((uintptr_t)dst & 15) == 0) {
                 *(u32x4 *)dst = v;
@@ -419,102 +435,175 @@ __global__ __launch_bounds__(256) void prefill_x_frag_kernel(const uint16_t *__r
     }
 }
 
-// out = bf16(sum over s of ws[s]), s in order.
-__global__ void prefill_reduce_kernel(const float *__restrict__ ws, int S, int64_t n,
-                                      uint16_t *__restrict__ out)
+// Output tiles tile0 .. tile0 + ntile - 1 = bf16 of the sum of their S
+// partial tiles (ws partial tile z * ntile + i, row-major [512][128]), added
+// in split order; entries past T or M are skipped.  Four columns a thread.
+__global__ void prefill_reduce_tiles_kernel(const float *__restrict__ ws, int S, int ntile,
+                                            int tile0, int nT, int T, int M,
+                                            uint16_t *__restrict__ out)
 {
+    constexpr int64_t kTile = (int64_t)kPT * kPM;
+    const int64_t n4 = (int64_t)ntile * kTile / 4;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-        float t = ws[i];
-        for (int s = 1; s < S; s++) t += ws[s * n + i];
-        out[i] = f32_to_bf16_rne(t);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        const int64_t e = i * 4;
+        const int tl = (int)(e / kTile);
+        const int r = (int)(e % kTile) / kPM, c = (int)(e % kPM);
+        const int tix = tile0 + tl;
+        const int t = (tix % nT) * kPT + r, m = (tix / nT) * kPM + c;
+        if (t >= T || m >= M) continue;
+        const float *p = ws + (int64_t)tl * kTile + r * kPM + c;
+        f32x4 a = *(const f32x4 *)p;
+        for (int z = 1; z < S; z++) {
+            const f32x4 v = *(const f32x4 *)(p + (int64_t)z * ntile * kTile);
+            a[0] += v[0];
+            a[1] += v[1];
+            a[2] += v[2];
+            a[3] += v[3];
+        }
+        uint16_t *o = out + (size_t)t * M + m;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (m + k < M) o[k] = f32_to_bf16_rne(a[k]);
     }
+}
+
+// How a T x M x K prefill is launched: tiles [0, full) run whole, tiles
+// [full, tiles) split K S ways (S = 1: none).  One 512-thread block per CU.
+// A grid of at most half the CUs splits every tile floor(CUs / tiles) ways;
+// tiles that leave at most half of a last round of the CUs split
+// floor(CUs / leftover) ways, so that round is as short as the others' share
+// of K.  At most 16 splits, each of at least 8 K groups.
+struct PrefillPlan {
+    int nT, tiles, full, S;
+};
+
+PrefillPlan prefill_plan(int T, int M, int K)
+{
+    PrefillPlan p;
+    p.nT = (T + kPT - 1) / kPT;
+    p.tiles = p.nT * ((M + kPM - 1) / kPM);
+    p.full = p.tiles;
+    p.S = 1;
+    const int cus = cbq_num_cus();
+    const int max_s = std::min(16, (K / kPK) / 8);
+    const int r = p.tiles % cus;
+    int left = 0;
+    if (2 * p.tiles <= cus) left = p.tiles;
+    else if (p.tiles > cus && r > 0 && 2 * r <= cus) left = r;
+    if (left > 0) {
+        const int S = std::min(cus / left, max_s);
+        if (S >= 2) {
+            p.full = p.tiles - left;
+            p.S = S;
+        }
+    }
+    return p;
+}
+
+size_t prefill_partial_bytes(const PrefillPlan &p)
+{
+    return p.S > 1 ? (size_t)(p.tiles - p.full) * p.S * kPT * kPM * sizeof(float) : 0;
 }
 
 template <int BITS, bool XF>
 int launch_prefill_x(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
-                     int T, int M, int K, int C, int S, float *ws, hipStream_t st)
+                     int T, int M, int K, int C, const PrefillPlan &p, float *ws, hipStream_t st)
 {
     const int G = K / kPK;
-    const int nT = (T + kPT - 1) / kPT;
-    const unsigned tiles = (unsigned)nT * (unsigned)((M + kPM - 1) / kPM);
-    if (S <= 1) {
-        hipLaunchKernelGGL((fixed_prefill_kernel<BITS, false, XF>), dim3(tiles), dim3(kPBlock), 0,
-                           st, x, (const uint32_t *)packed, cb, out, T, M, K, C, (float *)nullptr,
-                           G, nT);
-        return cbq_launch_status("fixed_prefill_kernel");
+    if (p.full > 0) {
+        hipLaunchKernelGGL((fixed_prefill_kernel<BITS, false, XF>), dim3((unsigned)p.full),
+                           dim3(kPBlock), 0, st, x, (const uint32_t *)packed, cb, out, T, M, K, C,
+                           (float *)nullptr, G, p.nT, 0);
+        const int rc = cbq_launch_status("fixed_prefill_kernel");
+        if (rc) return rc;
     }
-    const int gs = (G + S - 1) / S;
-    S = (G + gs - 1) / gs;                                   // no empty split
-    hipLaunchKernelGGL((fixed_prefill_kernel<BITS, true, XF>), dim3(tiles, 1, (unsigned)S),
+    if (p.full == p.tiles) return CK_SUCCESS;
+    const int n = p.tiles - p.full;
+    const int gs = (G + p.S - 1) / p.S;
+    const int S = (G + gs - 1) / gs;                         // no empty split (<= p.S)
+    hipLaunchKernelGGL((fixed_prefill_kernel<BITS, true, XF>), dim3((unsigned)n, 1, (unsigned)S),
                        dim3(kPBlock), 0, st, x, (const uint32_t *)packed, cb, out, T, M, K, C, ws,
-                       gs, nT);
+                       gs, p.nT, p.full);
     int rc = cbq_launch_status("fixed_prefill_kernel");
     if (rc) return rc;
-    const int64_t n = (int64_t)T * M;
-    const int blocks = (int)std::min<int64_t>((n + 255) / 256, 4096);
-    hipLaunchKernelGGL(prefill_reduce_kernel, dim3(blocks), dim3(256), 0, st, ws, S, n, out);
-    return cbq_launch_status("prefill_reduce_kernel");
+    const int64_t n4 = (int64_t)n * kPT * kPM / 4;
+    const int blocks = (int)std::min<int64_t>((n4 + 255) / 256, 4096);
+    hipLaunchKernelGGL(prefill_reduce_tiles_kernel, dim3(blocks), dim3(256), 0, st, ws, S, n,
+                       p.full, p.nT, T, M, out);
+    return cbq_launch_status("prefill_reduce_tiles_kernel");
 }
 
 // xf != nullptr: x is first copied to fragment order there (prefill_x_frag_kernel)
 template <int BITS>
 int launch_prefill(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
-                   int T, int M, int K, int C, int S, float *ws, uint16_t *xf, hipStream_t st)
+                   int T, int M, int K, int C, const PrefillPlan &p, float *ws, uint16_t *xf,
+                   hipStream_t st)
 {
-    if (!xf) return launch_prefill_x<BITS, false>(x, packed, cb, out, T, M, K, C, S, ws, st);
+    if (!xf) return launch_prefill_x<BITS, false>(x, packed, cb, out, T, M, K, C, p, ws, st);
     const dim3 grid((unsigned)((T + 15) >> 4), (unsigned)((K / kPK + kXfSteps - 1) / kXfSteps));
     hipLaunchKernelGGL(prefill_x_frag_kernel, grid, dim3(256), 0, st, x, xf, T, K);
     const int rc = cbq_launch_status("prefill_x_frag_kernel");
     if (rc) return rc;
-    return launch_prefill_x<BITS, true>(xf, packed, cb, out, T, M, K, C, S, ws, st);
+    return launch_prefill_x<BITS, true>(xf, packed, cb, out, T, M, K, C, p, ws, st);
 }
 
 }  // namespace
 
-// K splits for a T x M x K prefill.  A grid of fewer tiles than CUs (one
-// 512-thread block per CU) splits K so the blocks cover the CUs at most once:
-// floor(CUs / tiles) splits, at most 16, with at least 8 K groups (256
-// inputs) per split.
-int cbq_prefill_splits(int T, int M, int K)
+// Bytes of the fragment-order copy of x a T x K prefill uses.
+static size_t xf_bytes(int T, int K)
 {
-    if (T < 64 || K % kPK != 0) return 1;
-    const int64_t tiles = (int64_t)((T + kPT - 1) / kPT) * ((M + kPM - 1) / kPM);
-    const int64_t cus = cbq_num_cus();
-    if (tiles * 2 > cus) return 1;
-    int S = (int)std::min<int64_t>(cus / tiles, 16);
-    S = std::min(S, (K / kPK) / 8);
-    return S < 2 ? 1 : S;
+    return ((size_t)((T + 15) & ~15) * K * sizeof(uint16_t) + 255) & ~(size_t)255;
 }
 
-// Bytes of the fragment-order copy of x a T x K prefill can use (xf below).
-size_t cbq_prefill_xf_bytes(int T, int K)
+static bool prefill_shape(int T, int M, int K)
 {
-    if (T < 64 || K % kPK != 0) return 0;
-    return ((size_t)((T + 15) & ~15) * K * sizeof(uint16_t) + 255) & ~(size_t)255;
+    return T >= 64 && M > 0 && K > 0 && K % kPK == 0 &&
+           (uint64_t)((T + 15) & ~15) * K < (1ull << 32);    // 32-bit element offsets
+}
+
+static bool prefill_takes(int T, int M, int K, int bits)
+{
+    return prefill_shape(T, M, K) && (bits == 8 || (bits >= 10 && bits <= 14)) &&
+           (uint64_t)M * (K / kPK) * bits < (1ull << 32);   // 32-bit word offsets
+}
+
+// Workspace bytes of the MFMA prefill with a caller workspace: x in fragment
+// order, then the split partials (0: the shape does not take this path).
+size_t cbq_prefill_ws_bytes(int T, int M, int K)
+{
+    if (!prefill_shape(T, M, K)) return 0;
+    return xf_bytes(T, K) + prefill_partial_bytes(prefill_plan(T, M, K));
 }
 
 // Prefill dispatch used by ck_linear_bf16 / cbq_linear_bf16_ws (cbq_fixed.hip).
 // Returns -1 when the shape is not handled here (the caller keeps its
-// token-tile path).  S > 1 needs ws of S * T * M floats; xf (16-byte aligned,
-// cbq_prefill_xf_bytes) holds x in fragment order, or nullptr: x is then read
-// row-major, more slowly (a lane per row).
+// token-tile path).  With a workspace of cbq_prefill_ws_bytes (256-byte
+// aligned) x is copied to fragment order there and K may be split; without
+// one, x is read row-major (a lane per row, more slowly) and K is never split.
 int cbq_prefill_bf16(const uint16_t *x, const uint8_t *packed, const float *cb, uint16_t *out,
-                     int T, int M, int K, int C, int bits, hipStream_t st, int S, float *ws,
-                     uint16_t *xf)
+                     int T, int M, int K, int C, int bits, hipStream_t st, void *ws,
+                     size_t ws_bytes)
 {
-    if (T < 64 || K % kPK != 0 || (((uintptr_t)packed | (uintptr_t)x) & 15) != 0 ||
-        (K * 2) % 16 != 0 || (uint64_t)((T + 15) & ~15) * K >= (1ull << 32) ||
-        (uint64_t)M * (K / kPK) * bits >= (1ull << 32))
-        return -1;                                       // 32-bit element and word offsets
-    if ((S > 1 && !ws) || (((uintptr_t)xf) & 15) != 0) return -1;
+    if (!prefill_takes(T, M, K, bits) || (((uintptr_t)packed | (uintptr_t)x) & 15) != 0)
+        return -1;
+    PrefillPlan p = prefill_plan(T, M, K);
+    uint16_t *xf = nullptr;
+    float *part = nullptr;
+    if (ws && ((uintptr_t)ws & 255) == 0 && ws_bytes >= cbq_prefill_ws_bytes(T, M, K)) {
+        xf = (uint16_t *)ws;
+        part = (float *)((char *)ws + xf_bytes(T, K));
+    } else {
+        p.full = p.tiles;
+        p.S = 1;
+    }
     switch (bits) {
-    case 8: return launch_prefill<8>(x, packed, cb, out, T, M, K, C, S, ws, xf, st);
-    case 10: return launch_prefill<10>(x, packed, cb, out, T, M, K, C, S, ws, xf, st);
-    case 11: return launch_prefill<11>(x, packed, cb, out, T, M, K, C, S, ws, xf, st);
-    case 12: return launch_prefill<12>(x, packed, cb, out, T, M, K, C, S, ws, xf, st);
-    case 13: return launch_prefill<13>(x, packed, cb, out, T, M, K, C, S, ws, xf, st);
-    case 14: return launch_prefill<14>(x, packed, cb, out, T, M, K, C, S, ws, xf, st);
+    case 8: return launch_prefill<8>(x, packed, cb, out, T, M, K, C, p, part, xf, st);
+    case 10: return launch_prefill<10>(x, packed, cb, out, T, M, K, C, p, part, xf, st);
+    case 11: return launch_prefill<11>(x, packed, cb, out, T, M, K, C, p, part, xf, st);
+    case 12: return launch_prefill<12>(x, packed, cb, out, T, M, K, C, p, part, xf, st);
+    case 13: return launch_prefill<13>(x, packed, cb, out, T, M, K, C, p, part, xf, st);
+    case 14: return launch_prefill<14>(x, packed, cb, out, T, M, K, C, p, part, xf, st);
     default: return -1;
     }
 }

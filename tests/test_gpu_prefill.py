@@ -123,13 +123,26 @@ def test_split_k_matches_oracle(cuda, oracle, T, M, K):
     assert rel_l2(ys, y1) <= TOL
 
 
-@pytest.mark.parametrize("T,M,K", [(1030, 8200, 512), (2048, 12288, 128)])
-def test_workspace_path_unsplit_ragged(cuda, oracle, T, M, K):
-    """Grids large enough not to split, through cbq_linear_bf16_ws (x in
-    fragment order): T and M off every tile multiple, the padded last token
-    block and feature tile included."""
+def _tiles(T, M):
+    return -(-T // 512) * -(-M // 128)
+
+
+@pytest.mark.parametrize("T,M,K", [(1030, 8200, 512), (2048, 12288, 128), (1100, 12288, 512)])
+def test_workspace_path_ragged(cuda, oracle, T, M, K):
+    """Large grids through cbq_linear_bf16_ws (x in fragment order): T and M
+    off every tile multiple, the padded last token block and feature tile
+    included.  195 tiles run whole; 384 tiles at K = 128 too (too few K
+    groups to split); 288 tiles (32 past a full round of the CUs) split the
+    last 32 tiles' K in two, with partials in the workspace after x."""
     import cbq_native as nat
-    assert nat.load().cbq_linear_bf16_workspace(T, M, K) == ((T + 15) // 16 * 16 * K * 2 + 255) // 256 * 256
+    xf = ((T + 15) // 16 * 16 * K * 2 + 255) // 256 * 256
+    nws = nat.load().cbq_linear_bf16_workspace(T, M, K)
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    left = _tiles(T, M) % cus
+    if K // 32 >= 16 and _tiles(T, M) > cus and 0 < 2 * left <= cus:
+        assert nws == xf + left * min(cus // left, 16, K // 256) * 512 * 128 * 4
+    else:
+        assert nws == xf
     w = cbb.bf16_round(np.random.default_rng(T + K).standard_normal((M, K)) * 0.02)
     d = cbb.compress_fixed(w)
     xb = torch.randn(T, K, generator=torch.Generator().manual_seed(K)).bfloat16()
