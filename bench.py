@@ -276,7 +276,7 @@ def prefill_section(torch, nat, lib, dev, fixed, kinds, args):
     out["roofline"] = {"bound": "mfma", "achieved": g["TFLOP/s"], "peak": MFMA_BF16_PEAK_TFLOPS,
                        "unit": "TFLOP/s", "frac": g["frac"],
                        "kernel": "fixed_prefill_kernel<13> gate/up 4096->12288, T=2048",
-                       "mfma_busy_rocprof": read_profile_value(
+                       "mfma_busy_rocprof_full_round_launch": read_profile_value(
                            PREFILL_PROFILE, r"\*\*MFMA busy ([0-9.]+) %\*\*", 0.01),
                        "profile": "profiles/" + PREFILL_PROFILE}
     return out
