@@ -62,6 +62,10 @@ constexpr int kEpiRows = 16;
 constexpr int kLdsEpi = kPWaves * kEpiRows * kEpiRow<true>;
 constexpr int kWtChunks = (6 * kWBuf * 16 > kLdsEpi ? 6 * kWBuf * 16 : kLdsEpi) / 16;
 
+// Word 3 of a raw buffer resource on gfx9 (32-bit data format; no swizzle,
+// no stride): loads past num_records bytes return 0.
+constexpr int kBufRsrcWord3 = 0x00020000;
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -71,6 +75,16 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // share a chunk take 16 consecutive rows and so 16 distinct bank groups; so
 // do 16 consecutive decode threads writing one chunk.
 __device__ __forceinline__ int wslot(int r, int c) { return (r << 2) + (c ^ ((r >> 2) & 3)); }
+
+// fp32 -> bf16 bits by the hardware conversion (v_cvt_pk_bf16_f32: round to
+// nearest even), for outputs.
+__device__ __forceinline__ uint16_t bf16_out(float f)
+{
+    const __bf16 h = (__bf16)f;
+    uint16_t u;
+    __builtin_memcpy(&u, &h, 2);
+    return u;
+}
 
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f)
 {
@@ -98,7 +112,7 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f)
 // gathers and stores run while the matrix core works.
 template <int BITS, bool TWO, int HP, bool XF>
 __device__ __forceinline__ void prefill_loop(
-    const uint16_t *__restrict__ xb, const uint32_t (&xoff)[kTB], const uint32_t *__restrict__ wb,
+    __amdgpu_buffer_rsrc_t xb, const uint32_t (&xoff)[kTB], __amdgpu_buffer_rsrc_t wb,
     const uint32_t (&doff)[kRawLoads<BITS>], int G, const uint16_t *s_cb, const uint16_t *s_cblo,
     u32x4 *s_w, u32x4 *s_wlo, uint32_t *s_raw, int wave, int lane, bool active,
     f32x4 (&acc)[kTB][kNB])
@@ -118,7 +132,8 @@ __device__ __forceinline__ void prefill_loop(
     auto load_raw = [&](int g, uint32_t (&rr)[ND]) {     // step g's index words
         const int gc = g < G ? g : G - 1;
 #pragma unroll
-        for (int j = 0; j < ND; j++) rr[j] = wb[(uint32_t)(doff[j] + (uint32_t)gc * BITS)];
+        for (int j = 0; j < ND; j++)
+            rr[j] = __builtin_amdgcn_raw_buffer_load_b32(wb, (int)(doff[j] * 4u), gc * BITS * 4, 0);
     };
     auto store_raw = [&](int slot_i, const uint32_t (&rr)[ND]) {
         uint32_t *slot = s_raw + slot_i * kSlot + tid;
@@ -129,7 +144,8 @@ __device__ __forceinline__ void prefill_loop(
         const int gc = g < G ? g : G - 1;
 #pragma unroll
         for (int tb = 0; tb < kTB; tb++)
-            xr[tb] = *(const bf16x8 *)(xb + (uint32_t)(xoff[tb] + (uint32_t)gc * (XF ? 512 : kPK)));
+            xr[tb] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    xb, (int)(xoff[tb] * 2u), gc * (XF ? 1024 : 2 * kPK), 0));
     };
     auto read_words = [&](int slot_i, uint32_t (&wv)[NW]) {
         const uint32_t *rw = s_raw + slot_i * kSlot + wr * BITS;
@@ -329,6 +345,14 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
         doff[j] = (uint32_t)min(m0 + row, M - 1) * RW + (uint32_t)(g_lo * BITS + w);
     }
 
+    // global operands as buffer resources: a load's per-step advance is a
+    // scalar offset, so the K loop spends no VALU on addresses
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)x, (short)0, (int)(XF ? (uint32_t)((T + 15) & ~15) * (uint32_t)K * 2u
+                                       : (uint32_t)T * (uint32_t)K * 2u), kBufRsrcWord3);
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)words, (short)0, (int)((uint32_t)M * RW * 4u), kBufRsrcWord3);
+
     f32x4 acc[kTB][kNB];
 #pragma unroll
     for (int a = 0; a < kTB; a++)
@@ -337,7 +361,7 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     // waves whose 64 tokens all lie past T decode their share but skip the MFMAs
     const bool active = t0 + wave * kWT < T;
 #define CBQ_PREFILL_LOOP(TW, H)                                                                 \
-    prefill_loop<BITS, TW, H, XF>(x, xoff, words, doff, G, s_cb, s_cblo, s_w, s_wlo, s_raw, wave, \
+    prefill_loop<BITS, TW, H, XF>(xrs, xoff, wrs, doff, G, s_cb, s_cblo, s_w, s_wlo, s_raw, wave, \
                                   lane, active, acc)
     static_assert(kPWaves == 8, "the part switch below has kPWaves / 2 cases");
     if (two) {
@@ -379,8 +403,7 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
                     if (SPLIT)
                         *(float *)(tile + row * RS + col * 4) = acc[HB * p + h][nb][r];
                     else
-                        *(uint16_t *)(tile + row * RS + col * 2) =
-                            f32_to_bf16_rne(acc[HB * p + h][nb][r]);
+                        *(uint16_t *)(tile + row * RS + col * 2) = bf16_out(acc[HB * p + h][nb][r]);
                 }
 #pragma unroll
         for (int i = 0; i < kEpiRows * LPR / CBQ_WAVE; i++) {
@@ -464,7 +487,7 @@ __global__ void prefill_reduce_tiles_kernel(const float *__restrict__ ws, int S,
         uint16_t *o = out + (size_t)t * M + m;
 #pragma unroll
         for (int k = 0; k < 4; k++)
-            if (m + k < M) o[k] = f32_to_bf16_rne(a[k]);
+            if (m + k < M) o[k] = bf16_out(a[k]);
     }
 }
 
@@ -559,13 +582,13 @@ static size_t xf_bytes(int T, int K)
 static bool prefill_shape(int T, int M, int K)
 {
     return T >= 64 && M > 0 && K > 0 && K % kPK == 0 &&
-           (uint64_t)((T + 15) & ~15) * K < (1ull << 32);    // 32-bit element offsets
+           (uint64_t)((T + 15) & ~15) * K < (1ull << 31);    // x within one 4 GiB buffer
 }
 
 static bool prefill_takes(int T, int M, int K, int bits)
 {
     return prefill_shape(T, M, K) && (bits == 8 || (bits >= 10 && bits <= 14)) &&
-           (uint64_t)M * (K / kPK) * bits < (1ull << 32);   // 32-bit word offsets
+           (uint64_t)M * (K / kPK) * bits < (1ull << 30);   // index words within one 4 GiB buffer
 }
 
 // Workspace bytes of the MFMA prefill with a caller workspace: x in fragment
