@@ -464,14 +464,20 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         n = len(sps)
         mats = (ctypes.POINTER(nat.SplitMatrix) * n)(*[ctypes.pointer(sp[1]) for sp in sps])
         m_arr = (ctypes.c_int * n)(*Ms)
+        # output pointers: one array, refilled per call (the entry point reads
+        # it on the host before it returns)
+        o_arr = (ctypes.c_void_p * n)()
+        o_off = [4 * sum(Ms[:i]) for i in range(n)]
 
         def xform(x0, x1, h_out, mode, keep=(sps, mats, m_arr)):
             out = torch.empty(1, sum(Ms), device=dev)
-            offs = [out.data_ptr() + 4 * sum(Ms[:i]) for i in range(n)]
+            base = out.data_ptr()
+            for i in range(n):
+                o_arr[i] = base + o_off[i]
             nat.check(lib.cbq_split_linear_f32(
                 x0.data_ptr(), None if x1 is None else x1.data_ptr(),
                 None if h_out is None else h_out.data_ptr(), mode, cfg.eps, n, mats,
-                (ctypes.c_void_p * n)(*offs), m_arr, K, nat.stream_ptr(dev)),
+                o_arr, m_arr, K, nat.stream_ptr(dev)),
                 "cbq_split_linear_f32")
             return out
 
@@ -527,11 +533,22 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                               canon_pay=tb["pay"].data_ptr(), value_cb=None,
                               C=tb["codebook"].numel(), stage_words=tb["stage_words"])
 
+    inv_tables: Dict[bytes, torch.Tensor] = {}
+
+    def inv_of(cbt):
+        """bf16 value -> index table of a codebook (128 KiB), one per
+        distinct codebook: the tensors of a category share it."""
+        cb_np = cbt.cpu().numpy()
+        key = cb_np.tobytes()
+        if key not in inv_tables:
+            inv_tables[key] = split_inverse(cb_np, dev)
+        return inv_tables[key]
+
     def split_linear(sp, M, K, cbt):
         """A split-format matrix: one token on the split GEMV, batched tokens
         through its transient fixed-width stream.  Captures only the split
         format, so the tensor's stream can be freed."""
-        inv = split_inverse(cbt.cpu().numpy(), dev)
+        inv = inv_of(cbt)
         one, sxform = split_fns([sp], [M], K)
 
         def f(x):

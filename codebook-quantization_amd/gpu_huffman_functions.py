@@ -494,6 +494,17 @@ class HuffmanCodebookLinear:
         return SymbolDecoder(self.dev.words, self.dev.chunk_off, self.dev.sub_len,
                              self._lengths, self.device)
 
+    def _split_args(self):
+        """ctypes argument arrays of the one-token split call, built once;
+        the output slot is refilled per call (the entry point reads the
+        arrays on the host before it returns)."""
+        a = getattr(self, "_sargs", None)
+        if a is None:
+            a = ((ctypes.POINTER(nat.SplitMatrix) * 1)(ctypes.pointer(self.split[1])),
+                 (ctypes.c_void_p * 1)(), (ctypes.c_int * 1)(self.M))
+            self._sargs = a
+        return a
+
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         in_dtype = x.dtype
         x = x.to(self.device)
@@ -507,10 +518,10 @@ class HuffmanCodebookLinear:
             out = torch.empty(0, self.M, dtype=torch.float32, device=self.device)
         elif self.split is not None and T == 1:
             out = torch.empty(1, self.M, dtype=torch.float32, device=self.device)
+            mats, outs, ms = self._split_args()
+            outs[0] = out.data_ptr()
             nat.check(self._lib.cbq_split_linear_f32(
-                xc.data_ptr(), None, None, 0, 0.0, 1,
-                (ctypes.POINTER(nat.SplitMatrix) * 1)(ctypes.pointer(self.split[1])),
-                (ctypes.c_void_p * 1)(out.data_ptr()), (ctypes.c_int * 1)(self.M), self.K, st),
+                xc.data_ptr(), None, None, 0, 0.0, 1, mats, outs, ms, self.K, st),
                 "cbq_split_linear_f32")
         elif self.split is not None:
             out = split_prefill(self.split, self._inv, xc, self.M, self.K, self._cb_dev)
