@@ -93,6 +93,17 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f)
     return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
+// lo | hi << 16 of two 16-bit values (one v_perm; built as a two-element
+// vector, so no mask of the loaded halves is emitted first).
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(uint32_t lo, uint32_t hi)
+{
+    u16x2 p;
+    p.x = (unsigned short)lo;
+    p.y = (unsigned short)hi;
+    return __builtin_bit_cast(uint32_t, p);
+}
+
 // Main K loop of one wave; HP = which part (of kPWaves / 2) of each
 // 32-index group this thread decodes (wave-uniform).  Steps past G clamp their loads to the last
 // group and skip their MFMAs.
@@ -152,16 +163,21 @@ __device__ __forceinline__ void prefill_loop(
 #pragma unroll
         for (int i = 0; i < NW; i++) wv[i] = rw[q0 + i < BITS ? q0 + i : BITS - 1];
     };
+    // Each index is extracted already doubled (the byte offset of its bf16
+    // entry): shift by one bit less, mask with mask << 1.  The tables sit at
+    // the bottom of LDS, so the offset goes to ds_read_u16 as it is.
     auto gather = [&](const uint32_t (&wv)[NW], uint32_t (&v)[NF], uint32_t (&vl)[NF]) {
+        constexpr uint32_t mask2 = mask << 1;
 #pragma unroll
         for (int j = 0; j < NF; j++) {
             const int o = sh0 + j * BITS;
             const int q = o >> 5, sh = o & 31;
-            uint32_t f;
-            if (sh + BITS <= 32) f = (wv[q] >> sh) & mask;
-            else f = __builtin_amdgcn_alignbit(wv[q + 1], wv[q], (uint32_t)sh) & mask;
-            v[j] = s_cb[f];
-            if (TWO) vl[j] = s_cblo[f];
+            uint32_t f2;
+            if (sh == 0) f2 = (wv[q] << 1) & mask2;
+            else if (sh + BITS <= 32) f2 = (wv[q] >> (sh - 1)) & mask2;
+            else f2 = __builtin_amdgcn_alignbit(wv[q + 1], wv[q], (uint32_t)(sh - 1)) & mask2;
+            v[j] = *(const uint16_t *)((const char *)s_cb + f2);
+            if (TWO) vl[j] = *(const uint16_t *)((const char *)s_cblo + f2);
         }
     };
     auto store_w = [&](int buf, const uint32_t (&v)[NF], const uint32_t (&vl)[NF]) {
@@ -169,11 +185,11 @@ __device__ __forceinline__ void prefill_loop(
         for (int h = 0; h < NF / 8; h++) {
             const int o = buf * kWBuf + wslot(wr, (NF / 8) * HP + h);
             const int e = 8 * h;
-            s_w[o] = u32x4{v[e] | (v[e + 1] << 16), v[e + 2] | (v[e + 3] << 16),
-                           v[e + 4] | (v[e + 5] << 16), v[e + 6] | (v[e + 7] << 16)};
+            s_w[o] = u32x4{pack_bf16x2(v[e], v[e + 1]), pack_bf16x2(v[e + 2], v[e + 3]),
+                           pack_bf16x2(v[e + 4], v[e + 5]), pack_bf16x2(v[e + 6], v[e + 7])};
             if (TWO)
-                s_wlo[o] = u32x4{vl[e] | (vl[e + 1] << 16), vl[e + 2] | (vl[e + 3] << 16),
-                                 vl[e + 4] | (vl[e + 5] << 16), vl[e + 6] | (vl[e + 7] << 16)};
+                s_wlo[o] = u32x4{pack_bf16x2(vl[e], vl[e + 1]), pack_bf16x2(vl[e + 2], vl[e + 3]),
+                                 pack_bf16x2(vl[e + 4], vl[e + 5]), pack_bf16x2(vl[e + 6], vl[e + 7])};
         }
     };
     auto read_frag = [&](int buf, int nb, bf16x8 &b, bf16x8 &bl) {
@@ -278,8 +294,11 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     const float *__restrict__ cb, uint16_t *__restrict__ out, int T, int M, int K, int C,
     float *__restrict__ ws, int gs, int nT, int tile0)
 {
-    __shared__ uint16_t s_cb[1 << BITS];                       // bf16 codebook (hi), padded
-    __shared__ uint16_t s_cblo[1 << BITS];                     // bf16(cb - hi)
+    // bf16 codebook (hi), padded, and bf16(cb - hi).  The 64-byte alignment
+    // places them first in LDS (the allocator orders by alignment), below
+    // the 64 KiB that a ds_read offset field reaches.
+    __shared__ __attribute__((aligned(64))) uint16_t s_cb[1 << BITS];
+    __shared__ __attribute__((aligned(64))) uint16_t s_cblo[1 << BITS];
     __shared__ __attribute__((aligned(16))) u32x4 s_wt[kWtChunks];   // W tiles, then the epilogue's
     __shared__ uint32_t s_raw[2 * kRawSlot<BITS>];
     u32x4 *s_w = s_wt;                                         // 3 x [128][32] bf16
