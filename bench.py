@@ -292,6 +292,29 @@ def cpu_model():
     return "unknown"
 
 
+def cpu_ids():
+    """Family / model / stepping numbers of the host CPU (a virtualised host
+    may report only a generic model name; the numbers still give the core
+    generation) and the threads this process may run on."""
+    out = {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k = k.strip()
+            if k in ("cpu family", "model", "stepping", "cache size") and k not in out:
+                out[k] = v.strip()
+            if not line.strip() and out:
+                break
+    except OSError:
+        pass
+    out["logical_cpus"] = os.cpu_count()
+    try:
+        out["usable_threads"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        pass
+    return out
+
+
 def cpu_baseline(np, seconds):
     """BASELINE config 1 on the host cores with the reference's own C kernels
     (oracle/_ref; the restatement when that is not built): W [6144, 2048]
@@ -376,7 +399,7 @@ def cpu_baseline(np, seconds):
                        f"{os.environ.get('OMP_PROC_BIND')}), median of {head['runs']} runs = "
                        f"{head['ms']} ms on {cpu_model()}; every mode, encoding and T in "
                        f"cpu_baseline_detail")}, \
-        {"cpu": cpu_model(), "threads": threads, "omp_proc_bind": os.environ.get("OMP_PROC_BIND"),
+        {"cpu": cpu_model(), "cpu_ids": cpu_ids(), "threads": threads, "omp_proc_bind": os.environ.get("OMP_PROC_BIND"),
          "kind": kind, "codebook": C, "bits": bits,
          "huffman_bits_per_weight": round(8.0 * stream_b / (M * K), 3), "cells": res}
 

@@ -154,6 +154,57 @@ def test_workspace_path_ragged(cuda, oracle, T, M, K):
     assert rel_l2(y, y1) <= TOL
 
 
+def test_split_workspace_reused_and_replayed(cuda, oracle):
+    """One workspace (x in fragment order, split partials) reused by eager
+    calls and by graph replays with new x in between: every result against
+    the oracle (a stale x copy or partial would not match)."""
+    import bitpack
+    import cbq_native as nat
+    lib = nat.load()
+    T, M, K = 512, 1024, 4096                     # 8 tiles, K in 16
+    w = cbb.bf16_round(np.random.default_rng(77).standard_normal((M, K)) * 0.02)
+    d = cbb.compress_fixed(w)
+    pd = torch.from_numpy(bitpack.device_padded(d["indices"])).to(cuda)
+    cd = torch.from_numpy(np.ascontiguousarray(d["codebook"], np.float32)).to(cuda)
+    nws = int(lib.cbq_linear_bf16_workspace(T, M, K))
+    ws = torch.full((nws // 4,), float("nan"), dtype=torch.float32, device=cuda)
+    xd = torch.empty(T, K, dtype=torch.bfloat16, device=cuda)
+    out = torch.empty(T, M, dtype=torch.bfloat16, device=cuda)
+
+    def call():
+        nat.check(lib.cbq_linear_bf16_ws(xd.data_ptr(), pd.data_ptr(), cd.data_ptr(),
+                                         out.data_ptr(), T, M, K, len(d["codebook"]),
+                                         d["bits"], ws.data_ptr(), nws,
+                                         nat.stream_ptr(cuda)), "cbq_linear_bf16_ws")
+
+    def check():
+        xb = xd.float().cpu().numpy()
+        ref = oracle.fixed_gemv(xb, d["indices"], d["codebook"], M, K, d["bits"],
+                                chunk_rows=None)
+        _check(out.float().cpu().numpy(), ref)
+
+    for seed in (1, 2):                           # eager, same workspace
+        xd.copy_(torch.randn(T, K, generator=torch.Generator().manual_seed(seed)).bfloat16())
+        out.fill_(float("nan"))
+        call()
+        torch.cuda.synchronize()
+        check()
+    s = torch.cuda.Stream(cuda)
+    s.wait_stream(torch.cuda.current_stream(cuda))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call()
+    torch.cuda.current_stream(cuda).wait_stream(s)
+    for seed in (3, 4, 5):                        # replays, new x each time
+        xd.copy_(torch.randn(T, K, generator=torch.Generator().manual_seed(seed)).bfloat16())
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        check()
+
+
 def test_split_k_inexact_codebook_and_clamp(cuda, oracle):
     T, M, K, bits, C = 128, 200, 8192, 12, 3000
     rng = np.random.default_rng(9)
