@@ -144,18 +144,27 @@ __device__ __forceinline__ float silu_mul_value(float g, float u)
 // round, so fused and unfused paths give identical x.
 enum { XF_NONE = 0, XF_SILU = CBQ_XF_SILU, XF_ADD_RMS = CBQ_XF_ADD_RMS, XF_RMS = CBQ_XF_RMS };
 
+// The same transform of element i from values already loaded (v0 = x0[i],
+// v1 = x1[i] where the mode reads x1).
+__device__ __forceinline__ float xform_of(int mode, float v0, float v1, float *h_out,
+                                          bool store_h, int i, float r)
+{
+#pragma clang fp contract(off)
+    if (mode == XF_SILU) return silu_mul_value(v0, v1);
+    float v = v0;
+    if (mode == XF_ADD_RMS) {
+        v = v + v1;
+        if (store_h) h_out[i] = v;
+    }
+    return v * r;
+}
+
 __device__ __forceinline__ float xform_value(int mode, const float *__restrict__ x0,
                                              const float *__restrict__ x1, float *h_out,
                                              bool store_h, int i, float r)
 {
-#pragma clang fp contract(off)
-    if (mode == XF_SILU) return silu_mul_value(x0[i], x1[i]);
-    float v = x0[i];
-    if (mode == XF_ADD_RMS) {
-        v = v + x1[i];
-        if (store_h) h_out[i] = v;
-    }
-    return v * r;
+    const bool two = mode == XF_SILU || mode == XF_ADD_RMS;
+    return xform_of(mode, x0[i], two ? x1[i] : 0.f, h_out, store_h, i, r);
 }
 
 // Workgroup barrier for LDS hand-off only: waits for this wave's LDS

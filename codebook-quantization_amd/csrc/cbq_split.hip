@@ -212,10 +212,57 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
         __builtin_amdgcn_global_load_lds(S.lut + i * 4 * CBQ_WAVE + 4 * lane,
                                          (__attribute__((address_space(3))) void *)(s_lds + i * 4 * CBQ_WAVE),
                                          16, 0, 0);
+    // Plain x: the first x tile (seg 0, phase 0) goes to LDS together with
+    // the table, so the first barrier waits for one round trip of both
+    // instead of the tile's loads following it.
+    constexpr bool kXDma = XMODE == XF_NONE;
+    if (kXDma && rows_max > 0) {                   // (the block then reaches the barrier)
+        for (int r = wave; r < 64; r += NW) {
+            int t = (r << 6) + (lane ^ ((r & 15) << 2));
+            if constexpr (GR > 1) t %= K;
+            __builtin_amdgcn_global_load_lds(x + t,
+                                             (__attribute__((address_space(3))) void *)(s_x + (r << 6)),
+                                             4, 0, 0);
+        }
+    }
+    // SiLU product: the first tile's inputs are read into registers now
+    // (their loads overlap the table's) and multiplied after the barrier.
+    // The norms with whole-chunk rows write the first tile from the glue
+    // registers (the normalised x, already in this thread) before it.
+    constexpr bool kXRegs = XMODE == XF_SILU;
+    constexpr bool kXTile = (XMODE == XF_ADD_RMS || XMODE == XF_RMS) && GR == 1;
+    constexpr int kXR = kXRegs ? 64 / NW : 1;      // tile rows per wave
+    float x0r[kXR], x1r[kXR];
+    if (kXRegs && rows_max > 0) {
+#pragma unroll
+        for (int i = 0; i < kXR; i++) {
+            const int r = wave + i * NW;
+            int t = (r << 6) + (lane ^ ((r & 15) << 2));
+            if constexpr (GR > 1) t %= K;
+            x0r[i] = x[t];
+            x1r[i] = x1[t];
+        }
+    }
     float xr_scale = 1.f;
-    if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS)
-        xr_scale = tile.finish(K, eps, s_x);      // s_x is staged after the next barrier
     const bool store_h = XMODE == XF_ADD_RMS && blockIdx.x == 0 && h_out != nullptr;
+    if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS) {
+        // the norm's 16 wave sums go to wave 0's code slot (first written
+        // two barriers later), so the first x tile can be written at once
+        xr_scale = tile.finish(K, eps, kXTile ? (float *)(s_lds + kSLut + kSChunk) : s_x);
+        if constexpr (kXTile) {
+            // element i = tid + k NW*64 + 1024 j (< 4096) goes to the slot
+            // the staging loop below gives it
+#pragma unroll
+            for (int k = 0; k < tile.VPT; k++)
+#pragma unroll
+                for (int j = 0; j < kSChunk / 1024; j++) {
+                    const int i = (int)threadIdx.x + k * NW * CBQ_WAVE + j * 1024;
+                    const int r = i >> 6;
+                    s_x[(r << 6) + ((i & 63) ^ ((r & 15) << 2))] = tile.value(k, j, xr_scale);
+                }
+            if (store_h) tile.store_sum(h_out, K);
+        }
+    }
     float a_best = -INFINITY;                      // greedy-pick candidate of this lane
     int a_idx = kArgNone;
 
@@ -226,11 +273,27 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
         const int seg_rows = min(64, rows - seg * 64);
         for (int p = 0; p < R; p++) {
             __syncthreads();
-            for (int r = wave; r < 64; r += NW) {
-                int t = p * kSChunk + (r << 6) + (lane ^ ((r & 15) << 2));
-                if constexpr (GR > 1) t %= K;
-                if constexpr (XMODE == XF_NONE) s_x[(r << 6) + lane] = x[t];
-                else s_x[(r << 6) + lane] = xform_value(XMODE, x, x1, h_out, store_h, t, xr_scale);
+            if (seg == 0 && p == 0 && (kXDma || kXRegs || kXTile)) {
+                // first tile: DMA'd with the table, written already, or from registers
+                if constexpr (kXRegs) {
+#pragma unroll
+                    for (int i = 0; i < kXR; i++) {
+                        const int r = wave + i * NW;
+                        int t = (r << 6) + (lane ^ ((r & 15) << 2));
+                        if constexpr (GR > 1) t %= K;
+                        s_x[(r << 6) + lane] =
+                            xform_of(XMODE, x0r[i], x1r[i], h_out, store_h, t, xr_scale);
+                    }
+                }
+            } else {
+                for (int r = wave; r < 64; r += NW) {
+                    int t = p * kSChunk + (r << 6) + (lane ^ ((r & 15) << 2));
+                    if constexpr (GR > 1) t %= K;
+                    if constexpr (XMODE == XF_NONE) s_x[(r << 6) + lane] = x[t];
+                    else
+                        s_x[(r << 6) + lane] =
+                            xform_value(XMODE, x, x1, h_out, store_h, t, xr_scale);
+                }
             }
             __syncthreads();
             // rows of the group that chunk p touches, and this lane's row
