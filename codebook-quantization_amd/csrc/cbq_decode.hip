@@ -223,7 +223,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rope_decode_kernel(
 {
     extern __shared__ float s_att[];                              // [max_len + 1]
     __shared__ float s_raw[2][HD];
-    __shared__ float s_q[HD], s_k[HD], s_v[HD], s_cs[2][HD];
+    __shared__ __attribute__((aligned(16))) float s_q[HD];       // read as float4
+    __shared__ __attribute__((aligned(16))) float s_k[HD];
+    __shared__ float s_v[HD], s_cs[2][HD];
     __shared__ __attribute__((aligned(16))) float s_part[4 * kAttnThreads];
     __shared__ float s_red[kAttnThreads / CBQ_WAVE];
     const int h = blockIdx.x, g = h / group, tid = threadIdx.x;
@@ -290,24 +292,36 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rope_decode_kernel(
     const float *V = vc + (size_t)g * max_len * HD;
     typedef float f4 __attribute__((ext_vector_type(4)));
     float mx = -INFINITY;
-    for (int j = tid; j <= n_old; j += kAttnThreads) {
+    // q . k_j: 8 lanes per row, lane s of a row taking float4 s, s + 8, ...,
+    // so the 8 lanes of a row read 128 contiguous bytes per load (a lane per
+    // row reads one line per lane and is bound by the address path); the 8
+    // partial sums add by shuffles.  Row n_old is the new key, from LDS.
+    static_assert(HD % 32 == 0, "whole float4 per lane of a row");
+    constexpr int NQ = HD / 32;                                   // float4 per lane
+    const int sub = lane & 7;
+    f4 qv[NQ];
+#pragma unroll
+    for (int m = 0; m < NQ; m++) qv[m] = ((const f4 *)s_q)[sub + 8 * m];
+    for (int j0 = 0; j0 <= n_old; j0 += kAttnThreads / 8) {
+        const int j = j0 + tid / 8;
         float acc = 0.f;
-        if (j < n_old) {
-            const f4 *kr = (const f4 *)(K + (size_t)j * HD);
-#pragma unroll 8
-            for (int d4 = 0; d4 < HD / 4; d4++) {
-                const f4 kv = kr[d4];
-                acc = fmaf(s_q[4 * d4 + 0], kv.x, acc);
-                acc = fmaf(s_q[4 * d4 + 1], kv.y, acc);
-                acc = fmaf(s_q[4 * d4 + 2], kv.z, acc);
-                acc = fmaf(s_q[4 * d4 + 3], kv.w, acc);
+        if (j <= n_old) {
+            const f4 *kr = j < n_old ? (const f4 *)(K + (size_t)j * HD) : (const f4 *)s_k;
+#pragma unroll
+            for (int m = 0; m < NQ; m++) {
+                const f4 kv = kr[sub + 8 * m];
+                acc = fmaf(qv[m].x, kv.x, acc);
+                acc = fmaf(qv[m].y, kv.y, acc);
+                acc = fmaf(qv[m].z, kv.z, acc);
+                acc = fmaf(qv[m].w, kv.w, acc);
             }
-        } else {
-            for (int d = 0; d < HD; d++) acc = fmaf(s_q[d], s_k[d], acc);
         }
-        const float sc = __fmul_rn(acc, scale);
-        s_att[j] = sc;
-        mx = fmaxf(mx, sc);
+        acc = group_sum(acc, 8);
+        if (j <= n_old) {
+            const float sc = __fmul_rn(acc, scale);
+            if (sub == 0) s_att[j] = sc;
+            mx = fmaxf(mx, sc);
+        }
     }
     mx = block_max(mx, s_red);
     float sum = 0.f;
