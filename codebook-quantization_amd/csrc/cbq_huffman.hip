@@ -198,11 +198,20 @@ __device__ __forceinline__ bool stage_words(uint32_t *__restrict__ stg, int stg_
                                             int lane)
 {
     const int64_t w0 = (int64_t)(b0 >> 5);
-    const int64_t nw = (int64_t)((b1 + 31) >> 5) - w0 + 2;
-    if (nw > stg_words) return false;
-    for (int64_t i = lane; i < nw; i += CBQ_WAVE) {
-        const int64_t src = w0 + i;
-        stg[i] = src < n_words ? words[src] : 0u;
+    const int nw = (int)((int64_t)((b1 + 31) >> 5) - w0 + 2);
+    if (nw > stg_words || n_words <= 0) return false;
+    // 8 loads of a lane in flight before its stores; slots past nw copy the
+    // last word again (same value, same place), so nothing is conditional
+    for (int b = 0; b < nw; b += 8 * CBQ_WAVE) {
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int64_t src = w0 + min(b + u * CBQ_WAVE + lane, nw - 1);
+            v[u] = words[src < n_words ? src : n_words - 1];
+            v[u] = src < n_words ? v[u] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) stg[min(b + u * CBQ_WAVE + lane, nw - 1)] = v[u];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -235,16 +244,50 @@ __device__ __forceinline__ uint32_t window_global(const uint32_t *__restrict__ w
 }
 
 // Load the block-shared decode tables into LDS.
+// n words global -> LDS, with a thread's loads of up to 8 pieces in flight
+// before its first store (one round trip per 8 pieces, not one per element);
+// 16-byte pieces when both ends are 16-byte aligned.  Indices past the end
+// copy the last piece again (the same value to the same place), so loads and
+// stores are unconditional and no wait is needed before the next batch.
+__device__ __forceinline__ void copy_to_lds(uint32_t *dst, const uint32_t *__restrict__ src,
+                                            int n)
+{
+    const int nt = (int)blockDim.x, t = (int)threadIdx.x;
+    int done = 0;
+    if ((((uintptr_t)src | (uintptr_t)dst) & 15) == 0 && n >= 4) {
+        typedef uint32_t w4 __attribute__((ext_vector_type(4)));
+        const int n4 = n >> 2;
+        const w4 *s4 = (const w4 *)src;
+        w4 *d4 = (w4 *)dst;
+        for (int b = 0; b < n4; b += 8 * nt) {
+            w4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = s4[min(b + u * nt + t, n4 - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++) d4[min(b + u * nt + t, n4 - 1)] = v[u];
+        }
+        done = n4 << 2;
+    }
+    if (done < n) {
+        for (int b = done; b < n; b += 8 * nt) {
+            uint32_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = src[min(b + u * nt + t, n - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++) dst[min(b + u * nt + t, n - 1)] = v[u];
+        }
+    }
+}
+
 __device__ __forceinline__ void load_tables(uint32_t *s_lut1, uint32_t *s_lut2,
                                             const uint32_t *__restrict__ lut1,
                                             const uint32_t *__restrict__ lut2, int n_lut2,
                                             bool lut2_lds, float *s_cb,
                                             const float *__restrict__ cb, int n_cb)
 {
-    for (int i = threadIdx.x; i < kLutSize; i += blockDim.x) s_lut1[i] = lut1[i];
-    if (lut2_lds)
-        for (int i = threadIdx.x; i < n_lut2; i += blockDim.x) s_lut2[i] = lut2[i];
-    for (int i = threadIdx.x; i < n_cb; i += blockDim.x) s_cb[i] = cb[i];
+    copy_to_lds(s_lut1, lut1, kLutSize);
+    if (lut2_lds) copy_to_lds(s_lut2, lut2, n_lut2);
+    if (n_cb > 0) copy_to_lds((uint32_t *)s_cb, (const uint32_t *)cb, n_cb);
 }
 
 // Payload -> weight.  VALUE_MODE: bf16 bits in the payload; else symbol
