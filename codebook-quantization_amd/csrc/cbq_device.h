@@ -96,6 +96,40 @@ template <typename OT> __device__ __forceinline__ OT from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <> __device__ __forceinline__ uint16_t from_f32<uint16_t>(float v) { return f32_to_bf16(v); }
 
+// dst[i] = src[min(i, n_src - 1)] for i < n_dst (0 < n_src <= n_dst), global
+// to LDS by the whole block, with a thread's loads (up to 8 pieces) in flight
+// before its first store: one round trip per 8 pieces rather than one per
+// element.  16-byte pieces over the aligned whole pieces of src; indices past
+// the end repeat the last one (the same value to the same place), so nothing
+// is conditional and no wait is needed between batches.
+__device__ __forceinline__ void stage_clamped(float *dst, const float *__restrict__ src,
+                                              int n_src, int n_dst)
+{
+    typedef float v4 __attribute__((ext_vector_type(4)));
+    const int nt = (int)blockDim.x, t = (int)threadIdx.x;
+    int done = 0;
+    const int n4 = n_src >> 2;
+    if ((((uintptr_t)src | (uintptr_t)dst) & 15) == 0 && n4 > 0) {
+        const v4 *s4 = (const v4 *)src;
+        v4 *d4 = (v4 *)dst;
+        for (int b = 0; b < n4; b += 8 * nt) {
+            v4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = s4[min(b + u * nt + t, n4 - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++) d4[min(b + u * nt + t, n4 - 1)] = v[u];
+        }
+        done = n4 << 2;
+    }
+    for (int b = done; b < n_dst; b += 8 * nt) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = src[min(min(b + u * nt + t, n_dst - 1), n_src - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) dst[min(b + u * nt + t, n_dst - 1)] = v[u];
+    }
+}
+
 // Butterfly sum over aligned groups of `width` lanes (power of two <= 64);
 // every lane of a group ends with the group total.
 __device__ __forceinline__ float group_sum(float v, int width)

@@ -161,7 +161,7 @@ __global__ __launch_bounds__(kFBlock) void fixed_prefill_f32_kernel(
     const float *__restrict__ cb, float *__restrict__ out, int T, int M, int K, int C,
     float *__restrict__ ws, int gs)
 {
-    __shared__ float s_cb[1 << BITS];                                   // padded codebook
+    __shared__ __attribute__((aligned(16))) float s_cb[1 << BITS];       // padded codebook
     __shared__ __attribute__((aligned(16))) float s_x[kFT * kFK];      // [256][32]
     __shared__ __attribute__((aligned(16))) float s_w[kFM * kFK];      // [128][32]
 
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kFBlock) void fixed_prefill_f32_kernel(
     const int g_lo = SPLIT ? (int)blockIdx.z * gs : 0;
     const int G = SPLIT ? min(G_all, g_lo + gs) - g_lo : G_all;
 
-    for (int i = tid; i < (1 << BITS); i += kFBlock) s_cb[i] = cb[i < C ? i : C - 1];
+    stage_clamped(s_cb, cb, C < (1 << BITS) ? C : (1 << BITS), 1 << BITS);
     // (the loop's first barrier publishes the codebook)
 
     // x staging: thread -> tile row tid/2, k half tid%2 (clamped row)

@@ -67,7 +67,7 @@ __global__ __launch_bounds__(kTinyThreads) void fixed_tiny_mfma_kernel(
     uint32_t *s_w = (uint32_t *)(s_dyn + cs + kTinyWaves * CBQ_WAVE * 4) +
                     wave * (kTinyRing * 16 * 16);
 
-    for (int i = threadIdx.x; i < cs; i += kTinyThreads) s_dyn[i] = cb[i < C ? i : C - 1];
+    stage_clamped(s_dyn, cb, C, cs);
 
     // this lane's 8 indices of a group: bits [8 j BITS, 8 j BITS + 8 BITS)
     constexpr uint32_t mask = (1u << BITS) - 1u;
