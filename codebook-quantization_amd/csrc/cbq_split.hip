@@ -286,13 +286,28 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
                     }
                 }
             } else {
-                for (int r = wave; r < 64; r += NW) {
+                // a wave's 64 / NW rows of the tile: every load first, then
+                // the transforms and stores (one round trip, not one per row)
+                constexpr int kRows = 64 / NW;
+                constexpr bool kTwoIn = XMODE == XF_SILU || XMODE == XF_ADD_RMS;
+                float a0[kRows], a1[kRows];
+#pragma unroll
+                for (int i = 0; i < kRows; i++) {
+                    const int r = wave + i * NW;
                     int t = p * kSChunk + (r << 6) + (lane ^ ((r & 15) << 2));
                     if constexpr (GR > 1) t %= K;
-                    if constexpr (XMODE == XF_NONE) s_x[(r << 6) + lane] = x[t];
-                    else
-                        s_x[(r << 6) + lane] =
-                            xform_value(XMODE, x, x1, h_out, store_h, t, xr_scale);
+                    a0[i] = x[t];
+                    a1[i] = kTwoIn ? x1[t] : 0.f;
+                }
+#pragma unroll
+                for (int i = 0; i < kRows; i++) {
+                    const int r = wave + i * NW;
+                    int t = p * kSChunk + (r << 6) + (lane ^ ((r & 15) << 2));
+                    if constexpr (GR > 1) t %= K;
+                    s_x[(r << 6) + lane] = XMODE == XF_NONE
+                                               ? a0[i]
+                                               : xform_of(XMODE, a0[i], a1[i], h_out, store_h, t,
+                                                          xr_scale);
                 }
             }
             __syncthreads();
