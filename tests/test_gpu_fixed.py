@@ -111,6 +111,35 @@ def test_matrix_core_token_tiles(cuda, oracle, bits, T):
     assert rel_l2(y, ref) <= TOL, (bits, T)
 
 
+@pytest.mark.parametrize("T", [8, 64])
+def test_codebook_staging_unaligned(cuda, oracle, T):
+    """The few-token (T = 8) and fp32-prefill (T = 64) kernels stage the
+    codebook in 16-byte pieces when it is 16-byte aligned; a codebook 4 bytes
+    off alignment, with C not a multiple of 4 and indices past C, takes the
+    element-wise copy and must give the same result."""
+    nat, lib = _nat()
+    rng = np.random.default_rng(41 + T)
+    M, K, bits, C = 200, 1024, 12, 3001
+    raw = rng.integers(0, 1 << bits, size=M * K)
+    cb = (rng.standard_normal(C) * 0.02).astype(np.float32)
+    pk = oracle.pack_lsb(raw, bits)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    ref = oracle.fixed_gemv(x, pk, cb, M, K, bits, C=C, chunk_rows=None)
+    buf = torch.zeros(C + 8, device=cuda)
+    cd = buf[1:1 + C]                                 # 4 bytes past a 16-byte boundary
+    cd.copy_(torch.from_numpy(cb))
+    assert cd.data_ptr() % 16 == 4
+    xd = torch.from_numpy(x).to(cuda)
+    pd = _dev_packed(pk, cuda)
+    out = torch.full((T, M), float("nan"), device=cuda)
+    nat.check(lib.ck_linear_f32(xd.data_ptr(), pd.data_ptr(), cd.data_ptr(), out.data_ptr(), T,
+                                M, K, C, bits, nat.stream_ptr(cuda)), "ck_linear_f32")
+    torch.cuda.synchronize()
+    assert rel_l2(out.cpu().numpy(), ref) <= TOL
+    y = _run_linear(cuda, x, pk, cb, M, K, C, bits)   # aligned codebook, same kernel
+    assert rel_l2(out.cpu().numpy(), y) <= TOL
+
+
 @pytest.mark.parametrize("K,Ts", [(2048, (1, 5)), (4096, (16, 3, 9))])
 def test_bf16_io(cuda, oracle, K, Ts):
     """ck_linear_bf16: streaming kernel (T <= 4) and matrix cores (5..16
