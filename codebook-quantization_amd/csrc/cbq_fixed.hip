@@ -290,6 +290,18 @@ constexpr int kStreamLds = 152 * 1024;      // codebook + staged x, per block
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 
+// Pieces [n16, n_pieces) of a padded LDS codebook, written from registers:
+// piece n16 = mix (the last entries of cb, then cb[C - 1]), later pieces all
+// cb[C - 1].  The 16-byte loads of the staging wrote pieces [0, n16) only.
+__device__ __forceinline__ void pad_codebook(float *s_cb, int n16, int n_pieces,
+                                             const float (&mix)[4], float last)
+{
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    for (int q = n16 + (int)threadIdx.x; q < n_pieces; q += (int)blockDim.x)
+        ((f4v *)s_cb)[q] = q == n16 ? f4v{mix[0], mix[1], mix[2], mix[3]}
+                                    : f4v{last, last, last, last};
+}
+
 // Byte offsets into the LDS codebook of the 32 indices of one group: each
 // field is extracted already shifted left by 2 (alignbit/shift + and).  A
 // PADDED codebook has 2^BITS entries (entries >= C repeat cb[C-1]), so the
@@ -408,7 +420,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     CBQ_TS(ts_entry);
     unsigned long long ts_first = 0;
 #endif
-    __shared__ float s_cbp[PADDED ? (1 << BITS) : 1];
+    __shared__ __attribute__((aligned(16))) float s_cbp[PADDED ? (1 << BITS) : 1];
     __shared__ float s_red16[XMODE >= XF_ADD_RMS ? 16 : 1];
     extern __shared__ float s_dyn[];
     const int C_eff = C < (1 << BITS) ? C : (1 << BITS);
@@ -428,17 +440,48 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     const int n_items = rows * NGW;
     const uint32_t cmax4 = (uint32_t)(C_eff - 1) << 2;
 
-    // Staging: direct global->LDS dword loads, every wave a share.
-    for (int i = wave; i < (cb_slots >> 6); i += kStreamWaves) {
-        const int e = (i << 6) + lane;
-        __builtin_amdgcn_global_load_lds((const void *)(cb + (e < C ? e : C - 1)),
-                                         (lds_ptr_t)(s_cb + (i << 6)), 4, 0, 0);
+    // Staging: direct global->LDS loads, every wave a share.  Padded
+    // codebook: whole 16-byte pieces of cb by 16-byte loads (lanes past them
+    // idle); the piece holding entry C and the padding up to 2^BITS (all
+    // cb[C - 1]) are written from registers once the loads have landed.
+    int n16 = 0;                                   // 16-byte pieces loaded
+    float pad_mix[4], pad_last = 0.f;
+    if constexpr (PADDED) {
+        n16 = C_eff >> 2;
+        for (int i = wave; i < ((n16 + 63) >> 6); i += kStreamWaves) {
+            const int q = (i << 6) + lane;
+            if (q < n16)
+                __builtin_amdgcn_global_load_lds((const void *)(cb + 4 * q),
+                                                 (lds_ptr_t)(s_cb + (i << 8)), 16, 0, 0);
+        }
+        pad_last = cb[C_eff - 1];
+#pragma unroll
+        for (int j = 0; j < 4; j++) pad_mix[j] = cb[min(4 * n16 + j, C_eff - 1)];
+    } else {
+        for (int i = wave; i < (cb_slots >> 6); i += kStreamWaves) {
+            const int e = (i << 6) + lane;
+            __builtin_amdgcn_global_load_lds((const void *)(cb + (e < C ? e : C - 1)),
+                                             (lds_ptr_t)(s_cb + (i << 6)), 4, 0, 0);
+        }
     }
     constexpr int GD = XStage<XT>::kGroupDw;
     const int xdw = G * GD;                        // dwords of one token's x
     const int n_xdw = T * xdw;
     const uint32_t *xw = (const uint32_t *)x;
-    if constexpr (XMODE == XF_NONE) {
+    // x by 16-byte loads (each a swizzled chunk) when it is 16-byte aligned
+    // and a whole number of 64-lane loads; else by dword loads.
+    const bool x16 = ((uintptr_t)x & 15) == 0 && (n_xdw & 255) == 0;
+    if (XMODE == XF_NONE && x16) {
+        const int cpt = xdw >> 2, cpg = GD >> 2;   // chunks per token, per group
+        for (int i = wave; i < (n_xdw >> 8); i += kStreamWaves) {
+            const int qs = (i << 6) + lane;        // LDS chunk slot (this lane's)
+            const int t = qs / cpt, dq = qs - t * cpt;
+            const int g = dq / cpg, c = dq - g * cpg;
+            const int src = t * (Gf * GD) + (g0 + g) * GD + (XStage<XT>::chunk(c, g) << 2);
+            __builtin_amdgcn_global_load_lds((const void *)(xw + src),
+                                             (lds_ptr_t)(s_x + (i << 8)), 16, 0, 0);
+        }
+    } else if constexpr (XMODE == XF_NONE) {
         for (int i = wave; i < ((n_xdw + 63) >> 6); i += kStreamWaves) {
             int sl = (i << 6) + lane;              // LDS dword slot (this lane's)
             sl = sl < n_xdw ? sl : n_xdw - 1;      // tail lanes re-copy the last dword
@@ -475,6 +518,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
         // D ring loads can take (dwordx4), so every older staging load has landed.
         constexpr int kAfter = D * ((BITS + 3) / 4);
         __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | (15 << 8) | ((kAfter >> 4) << 14));
+        if constexpr (PADDED) pad_codebook(s_cb, n16, (1 << BITS) >> 2, pad_mix, pad_last);
         lds_barrier();
     } else {
         // the transformed x from registers, while the first weight loads fly;
@@ -490,6 +534,8 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
                 const int sl = (g << 5) + ((((i >> 2) & 7) ^ (g & 7)) << 2) + (i & 3);
                 if (i < K) s_x[sl] = __float_as_uint(tile.value(k, j, r));
             }
+        // (the codebook loads landed before the glue loads finish() waited for)
+        if constexpr (PADDED) pad_codebook(s_cb, n16, (1 << BITS) >> 2, pad_mix, pad_last);
         lds_barrier();
     }
 
