@@ -217,12 +217,23 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
     // instead of the tile's loads following it.
     constexpr bool kXDma = XMODE == XF_NONE;
     if (kXDma && rows_max > 0) {                   // (the block then reaches the barrier)
-        for (int r = wave; r < 64; r += NW) {
-            int t = (r << 6) + (lane ^ ((r & 15) << 2));
-            if constexpr (GR > 1) t %= K;
-            __builtin_amdgcn_global_load_lds(x + t,
-                                             (__attribute__((address_space(3))) void *)(s_x + (r << 6)),
-                                             4, 0, 0);
+        if (((uintptr_t)x & 15) == 0) {
+            // 16-byte pieces: chunk c of row r holds x chunk c ^ (r & 15) of
+            // that row; one load covers 4 rows
+            for (int i = wave; i < 16; i += NW) {
+                const int r = (i << 2) + (lane >> 4), c = lane & 15;
+                int t = (r << 6) + ((c ^ (r & 15)) << 2);
+                if constexpr (GR > 1) t %= K;
+                __builtin_amdgcn_global_load_lds(
+                    x + t, (__attribute__((address_space(3))) void *)(s_x + (i << 8)), 16, 0, 0);
+            }
+        } else {
+            for (int r = wave; r < 64; r += NW) {
+                int t = (r << 6) + (lane ^ ((r & 15) << 2));
+                if constexpr (GR > 1) t %= K;
+                __builtin_amdgcn_global_load_lds(
+                    x + t, (__attribute__((address_space(3))) void *)(s_x + (r << 6)), 4, 0, 0);
+            }
         }
     }
     // SiLU product: the first tile's inputs are read into registers now
