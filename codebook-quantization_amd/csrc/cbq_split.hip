@@ -89,6 +89,28 @@ __device__ __forceinline__ void split_load(SplitItem &it, const SplitSeg &S, int
         if (4 * k < (int)H) it.ew[k] = wp[k * kSSub];
 }
 
+// split_load with every load issued (4 + (kSRows + 3) / 4 of them): code
+// pieces past the item's last one re-load that piece (an address split_load
+// reads too), so the count does not depend on H and a wait can leave these
+// loads in flight while everything issued before them has landed.
+__device__ __forceinline__ void split_load_all(SplitItem &it, const SplitSeg &S, int64_t c,
+                                               uint32_t r0, uint32_t H, int lane)
+{
+    const u4 *rp = (const u4 *)(S.raw + (size_t)c * kSChunk + lane * kSSub);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const u4 v = rp[k];
+        it.raw[4 * k] = v.x;
+        it.raw[4 * k + 1] = v.y;
+        it.raw[4 * k + 2] = v.z;
+        it.raw[4 * k + 3] = v.w;
+    }
+    const u4 *wp = (const u4 *)(S.cwords + (size_t)r0 * kSSub) + lane;
+    const int klast = H > 0 ? (int)((H - 1) >> 2) : 0;
+#pragma unroll
+    for (int k = 0; k < (kSRows + 3) / 4; k++) it.ew[k] = wp[(k < klast ? k : klast) * kSSub];
+}
+
 // Writes an item's code rows into the wave's slot (same row-major layout).
 __device__ __forceinline__ void split_stage(const SplitItem &it, uint32_t H, uint32_t *s_slot,
                                             int lane)
@@ -204,10 +226,12 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
     // decoded.  The wave's first item is requested before the table staging.
     SplitItem A, B;
     uint32_t rA = 0, hA = 0, rB = 0, hB = 0;
-    if (rows > 0) {
-        const int64_t c = chunk_of(0, 0, 0, rA, hA);
-        split_load(A, S, c, rA, hA, lane);
-    }
+    // The first chunk's row offsets are requested first, its data last:
+    // lanes 0 and 1 read row_off[c0] and row_off[c0 + 1] (a wave without
+    // rows reads chunk 0's, unused); the table and x loads go out while they
+    // return, and the first barrier waits for those alone.
+    const int64_t c0 = rows > 0 ? (int64_t)__builtin_amdgcn_readfirstlane(wid * R) : 0;
+    const uint32_t v_off0 = S.row_off[c0 + (lane & 1)];
     for (int i = wave; i < kSLut / (4 * CBQ_WAVE); i += NW)
         __builtin_amdgcn_global_load_lds(S.lut + i * 4 * CBQ_WAVE + 4 * lane,
                                          (__attribute__((address_space(3))) void *)(s_lds + i * 4 * CBQ_WAVE),
@@ -254,6 +278,15 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
             x1r[i] = x1[t];
         }
     }
+    // the first chunk: exactly kFirstLoads loads, issued after every other
+    // load of the prologue
+    constexpr int kFirstLoads = 4 + (kSRows + 3) / 4;
+    __builtin_amdgcn_sched_barrier(0);
+    rA = __builtin_amdgcn_readfirstlane(v_off0);
+    hA = __builtin_amdgcn_readlane(v_off0, 1) - rA;
+    hA = hA < (uint32_t)kSRows ? hA : (uint32_t)kSRows;
+    split_load_all(A, S, c0, rA, hA, lane);
+    __builtin_amdgcn_sched_barrier(0);
     float xr_scale = 1.f;
     const bool store_h = XMODE == XF_ADD_RMS && blockIdx.x == 0 && h_out != nullptr;
     if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS) {
@@ -283,7 +316,15 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
         for (int q = 0; q < GR; q++) res[q] = 0.f;
         const int seg_rows = min(64, rows - seg * 64);
         for (int p = 0; p < R; p++) {
-            __syncthreads();
+            if (seg == 0 && p == 0) {
+                // every prologue load but the first chunk's has landed (they
+                // were issued before it); the first chunk stays in flight
+                __builtin_amdgcn_s_waitcnt((kFirstLoads & 15) | (7 << 4) | (15 << 8) |
+                                           ((kFirstLoads >> 4) << 14));
+                lds_barrier();
+            } else {
+                __syncthreads();
+            }
             if (seg == 0 && p == 0 && (kXDma || kXRegs || kXTile)) {
                 // first tile: DMA'd with the table, written already, or from registers
                 if constexpr (kXRegs) {
