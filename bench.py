@@ -34,6 +34,12 @@ import os
 # The CPU baseline's OpenMP team binds to neighbouring cores; set before any
 # OpenMP runtime is loaded (torch loads one).
 os.environ.setdefault("OMP_PROC_BIND", "close")
+# threads this process may run on, read before any OpenMP runtime binds the
+# main thread to one core (OMP_PROC_BIND=close does, once it starts)
+try:
+    USABLE_THREADS = len(os.sched_getaffinity(0))
+except (AttributeError, OSError):
+    USABLE_THREADS = None
 
 import argparse  # noqa: E402
 import json  # noqa: E402
@@ -308,10 +314,8 @@ def cpu_ids():
     except OSError:
         pass
     out["logical_cpus"] = os.cpu_count()
-    try:
-        out["usable_threads"] = len(os.sched_getaffinity(0))
-    except (AttributeError, OSError):
-        pass
+    if USABLE_THREADS is not None:
+        out["usable_threads_at_start"] = USABLE_THREADS
     return out
 
 
