@@ -90,6 +90,8 @@ SIGNATURES = {
                                            _vp, _i, _vp]),
     "cbq_linear_xform_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _i, _i, _i,
                                   _i, _vp]),
+    "cbq_linear_xform_glu_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _i, _i,
+                                      _i, _i, _vp]),
     "cbq_split_bits": (_i, [_vp, _i64, _vp, _i, _vp, _vp]),
     "cbq_pack_indices": (_i, [_vp, _i64, _i, _vp, _vp]),
     "cbq_split_to_packed": (_i, [_vp, _vp, _i, _vp, _vp]),

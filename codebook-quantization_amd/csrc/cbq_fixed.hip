@@ -400,8 +400,12 @@ __device__ __forceinline__ void put_out_t(OT *o, float v, int accum)
 // (x is [T, Kfull]); accum != 0 adds the partial products to out instead of
 // writing them.  The host splits K this way when x of all T tokens does not
 // fit in LDS, one launch per column range in order.
+// GLU (T = 1): the matrix holds 2M rows, gate rows [0, M) then up rows
+// [M, 2M); a wave takes gate row j and up row j back to back and writes
+// out[j] = silu(gate_j . x) * (up_j . x), rounded as silu_mul_value, so the
+// down projection that consumes it stages plain x.
 template <int BITS, int TMAX, typename XT, typename OT, bool AFFINE = false, int XMODE = XF_NONE,
-          bool KCHUNK = false>
+          bool KCHUNK = false, bool GLU = false>
 __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     const XT *__restrict__ x, const uint32_t *__restrict__ words,
     const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C,
@@ -410,6 +414,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     int *__restrict__ arg_i = nullptr)
 {
     static_assert(!KCHUNK || (XMODE == XF_NONE && !AFFINE), "column ranges: plain x only");
+    static_assert(!GLU || (TMAX == 1 && !KCHUNK && XMODE != XF_SILU), "gate/up pairs: one token");
     // arg_v / arg_i (T = 1): besides writing out (when out is not null), the
     // block reduces its rows to one (max, first index) pair of the greedy
     // pick, written to arg_v / arg_i [blockIdx.x].
@@ -436,7 +441,8 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CBQ_WAVE);
     const int W = gridDim.x * kStreamWaves;
     const int wid = blockIdx.x * kStreamWaves + wave;
-    const int rows = wid < M ? (M - wid + W - 1) / W : 0;
+    // rows of this wave (GLU: two per output, gate then up)
+    const int rows = wid < M ? (GLU ? 2 : 1) * ((M - wid + W - 1) / W) : 0;
     const int n_items = rows * NGW;
     const uint32_t cmax4 = (uint32_t)(C_eff - 1) << 2;
 
@@ -506,7 +512,8 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
         const int ri = it / NGW, ch = it - ri * NGW;
         int g = ch * CBQ_WAVE + lane;
         g = g < G ? g : G - 1;
-        const int row = rows > 0 ? wid + ri * W : 0;
+        const int row = rows <= 0 ? 0 : GLU ? ((ri & 1) ? M : 0) + wid + (ri >> 1) * W
+                                            : wid + ri * W;
         return words + ((size_t)row * Gf + g0 + g) * BITS + zero;
     };
     uint32_t buf[D][BITS];
@@ -547,6 +554,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     for (int t = 0; t < TMAX; t++) acc[t] = res[t] = 0.f;
     float a_best = -INFINITY;                      // greedy-pick candidate of this lane
     int a_idx = kArgNone;
+    float g_row = 0.f;                             // GLU: the pair's gate product
     int ri = 0, ch = 0, base = 0;
     do {
 #pragma unroll
@@ -588,7 +596,21 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
                 }
             }
             __builtin_memcpy(buf[d], item_ptr(item + D), sizeof(buf[d]));
-            if (++ch == NGW) {                       // row done (wave-uniform)
+            if (GLU && ++ch == NGW) {                // gate or up row done (wave-uniform)
+                ch = 0;
+                const float s = wave_sum(acc[0]);
+                acc[0] = 0.f;
+                if (ri & 1) {
+                    const int pi = ri >> 1;
+                    const float v = silu_mul_value(g_row, s);
+                    res[0] = (lane == (pi & 63) && ri < rows) ? v : res[0];
+                } else {
+                    g_row = s;
+                }
+                ri++;
+                if ((ri & 127) == 0 && ri <= rows)
+                    out[wid + ((ri >> 1) - 64 + lane) * W] = from_f32<OT>(res[0]);
+            } else if (!GLU && ++ch == NGW) {       // row done (wave-uniform)
                 ch = 0;
 #pragma unroll
                 for (int t = 0; t < TMAX; t++) {
@@ -621,8 +643,9 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
 #ifdef CBQ_TIMELINE
     CBQ_TS(ts_loop);
 #endif
-    const int rb = rows & ~63;
-    if (lane < rows - rb) {
+    const int n_res = GLU ? rows >> 1 : rows;       // outputs of this wave
+    const int rb = n_res & ~63;
+    if (lane < n_res - rb) {
         const int row = wid + (rb + lane) * W;
         if (out) {
 #pragma unroll
@@ -1102,6 +1125,46 @@ int cbq_linear_xform_f32(const float *x0, const float *x1, float *h_out, int mod
 #undef CBQ_XF_MODES
 #undef CBQ_XF
     return cbq_launch_status("fixed_stream_kernel<xform>");
+}
+
+int cbq_linear_xform_glu_f32(const float *x0, const float *x1, float *h_out, int mode,
+                             float eps, const uint8_t *packed, const float *codebook, float *out,
+                             int M, int K, int C, int bits, hipStream_t stream)
+{
+    if (!x0 || !packed || !codebook || !out || M <= 0 || M > (1 << 29) || K <= 0 ||
+        K % 32 != 0 || C <= 0 || C > kMaxLdsCodebook)
+        return CK_ERR_ARG;
+    if (mode != XF_NONE && mode != XF_ADD_RMS && mode != XF_RMS) return CK_ERR_ARG;
+    if ((mode == XF_ADD_RMS && !x1) || (mode != XF_NONE && K > 16384)) return CK_ERR_ARG;
+    if (((uintptr_t)packed & 3) != 0 || ((uintptr_t)x0 & 3) != 0) return CK_ERR_ARG;
+    const int blocks =
+        std::max(1, std::min(cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
+    size_t dyn = 0;
+#define CBQ_XG(B, MODE)                                                                        \
+    hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE, false, true>),     \
+                       dim3(blocks), dim3(kStreamBlock), dyn, stream, x0,                       \
+                       (const uint32_t *)packed, codebook, out, 1, M, K, C, 0u, 0u, x1, h_out,  \
+                       eps, K, 0, 0)
+#define CBQ_XG_MODES(B)                                                                        \
+    do {                                                                                       \
+        dyn = stream_dyn_lds<B, float>(1, K, C);                                               \
+        if (!dyn) return CK_ERR_ARG;                                                           \
+        if (mode == XF_ADD_RMS) CBQ_XG(B, XF_ADD_RMS);                                         \
+        else if (mode == XF_RMS) CBQ_XG(B, XF_RMS);                                            \
+        else CBQ_XG(B, XF_NONE);                                                               \
+    } while (0)
+    switch (bits) {
+    case 8: CBQ_XG_MODES(8); break;
+    case 10: CBQ_XG_MODES(10); break;
+    case 11: CBQ_XG_MODES(11); break;
+    case 12: CBQ_XG_MODES(12); break;
+    case 13: CBQ_XG_MODES(13); break;
+    case 14: CBQ_XG_MODES(14); break;
+    default: return CK_ERR_ARG;
+    }
+#undef CBQ_XG_MODES
+#undef CBQ_XG
+    return cbq_launch_status("fixed_stream_kernel<glu>");
 }
 
 int cbq_linear_xform_argmax_f32(const float *x0, const float *x1, float *h_out, int mode,

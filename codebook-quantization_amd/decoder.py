@@ -290,6 +290,12 @@ class Qwen3Decoder:
                                          self.sin, pos_dev, self.cache[i, 0], self.cache[i, 1])
             o = L[p + "self_attn.o_proj"](att)
             h2 = torch.empty_like(h)
+            glu = getattr(L[p + "mlp.gate_up_proj"], "xform_glu", None)
+            if glu is not None:                     # SiLU product in the gate/up epilogue
+                a = glu(h, o, h2, nat.XF_ADD_RMS)
+                h = h2
+                delta = L[p + "mlp.down_proj"](a)
+                continue
             gu = L[p + "mlp.gate_up_proj"].xform(h, o, h2, nat.XF_ADD_RMS)
             h = h2
             delta = L[p + "mlp.down_proj"].xform(gu[:, :c.inter], gu[:, c.inter:], None,
@@ -520,8 +526,20 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
                 t.codebook.numel(), t.bits, argmax_ws.data_ptr(), argmax_ws.numel(),
                 ids32.data_ptr(), toks.data_ptr(), pos.data_ptr(), first, toks.numel(),
                 nat.stream_ptr(dev)), "cbq_linear_xform_argmax_f32")
+        def xform_glu(x0, x1, h_out, mode):
+            """One token over a row-stacked [gate; up] matrix: silu(gate . x) *
+            (up . x), x = transform(x0, x1), in one launch."""
+            out = torch.empty(1, M // 2, device=dev)
+            nat.check(lib.cbq_linear_xform_glu_f32(
+                x0.data_ptr(), None if x1 is None else x1.data_ptr(),
+                None if h_out is None else h_out.data_ptr(), mode, cfg.eps, t.packed.data_ptr(),
+                t.codebook.data_ptr(), out.data_ptr(), M // 2, K, t.codebook.numel(), t.bits,
+                nat.stream_ptr(dev)), "cbq_linear_xform_glu_f32")
+            return out
         f.xform = xform
         f.xform_argmax = xform_argmax
+        if M % 2 == 0:
+            f.xform_glu = xform_glu
         return f
 
     def huff_desc(t):

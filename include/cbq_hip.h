@@ -285,6 +285,20 @@ int cbq_linear_xform_f32(const float *x0, const float *x1, float *h_out, int mod
                          const uint8_t *packed, const float *codebook, float *out, int M, int K,
                          int C, int bits, hipStream_t stream);
 
+/* The gated MLP's gate and up projections in one launch, with the SiLU
+ * product in the epilogue: packed holds 2M rows, gate_proj's M rows then
+ * up_proj's (the row-stacked [gate; up] matrix ck_linear_f32 takes), and
+ * out[j] = silu(gate_j . x) * (up_j . x) for j < M, with x =
+ * transform(x0, x1) (mode 0, CBQ_XF_ADD_RMS or CBQ_XF_RMS).  Each product
+ * sums as in cbq_linear_xform_f32 and the SiLU product rounds as
+ * cbq_silu_mul_f32, so out equals those two calls bit for bit.  Same widths
+ * and limits as cbq_linear_xform_f32.  Replaces the reference's separate
+ * gate_proj / up_proj module calls and HF's act_fn(gate) * up
+ * (src/compressed_modules.py:77-490 modules inside HF's Qwen3MLP). */
+int cbq_linear_xform_glu_f32(const float *x0, const float *x1, float *h_out, int mode,
+                             float eps, const uint8_t *packed, const float *codebook, float *out,
+                             int M, int K, int C, int bits, hipStream_t stream);
+
 /* cbq_huff_linear_col_multi_f32 with x = transform(x0, x1) (mode above, or
  * 0 for none); modes other than 0 need every matrix's unified tables. */
 int cbq_huff_linear_col_xform_f32(const float *x0, const float *x1, float *h_out, int mode,

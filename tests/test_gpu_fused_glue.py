@@ -105,3 +105,60 @@ def test_long_cache_split_attention_decoder(cuda, model, monkeypatch):
     assert rel <= 1e-5, (kind, rel)
     tc, lc = run(True)
     assert tc == ta and torch.equal(lc, la), kind
+
+
+@pytest.mark.parametrize("M,K,bits,C", [(12288, 4096, 13, 5000),     # 8B gate/up shape
+                                        (137733, 32, 13, 8192),     # > 64 pairs per wave
+                                        (1003, 4096, 11, 2048),     # ragged pair count
+                                        (77, 96, 8, 300)])          # fewer pairs than waves
+def test_glu_epilogue_equals_gemv_then_silu(cuda, M, K, bits, C):
+    """cbq_linear_xform_glu_f32 over a row-stacked [gate; up] matrix equals
+    the stacked GEMV (same x transform) followed by cbq_silu_mul_f32, bit for
+    bit; plain x (mode 0) is checked against ck_linear_f32 + silu within the
+    GEMV tolerance, since ck_linear_f32 may pick another kernel at small K."""
+    lib = nat.load()
+    gen = torch.Generator(device=cuda).manual_seed(M + K)
+    nbytes = 2 * M * K * bits // 8
+    packed = torch.randint(0, 256, (nbytes + 256,), dtype=torch.uint8, device=cuda,
+                           generator=gen)
+    cb = torch.randn(C, device=cuda, generator=gen)
+    st = nat.stream_ptr(cuda)
+
+    def silu_mul(y):
+        out = torch.empty(1, M, device=cuda)
+        nat.check(lib.cbq_silu_mul_f32(y[:, :M].contiguous().data_ptr(),
+                                       y[:, M:].contiguous().data_ptr(), out.data_ptr(), M, st),
+                  "cbq_silu_mul_f32")
+        return out
+
+    def glu(h, d, h_out, mode):
+        out = torch.full((1, M), float("nan"), device=cuda)
+        nat.check(lib.cbq_linear_xform_glu_f32(
+            h.data_ptr(), None if d is None else d.data_ptr(),
+            None if h_out is None else h_out.data_ptr(), mode, 1e-6, packed.data_ptr(),
+            cb.data_ptr(), out.data_ptr(), M, K, C, bits, st), "cbq_linear_xform_glu_f32")
+        return out
+
+    for rep in range(2):
+        h = torch.randn(1, K, device=cuda, generator=gen) * 2
+        d = torch.randn(1, K, device=cuda, generator=gen)
+        for mode in (nat.XF_RMS, nat.XF_ADD_RMS):
+            y = torch.empty(1, 2 * M, device=cuda)
+            h_ref = torch.full_like(h, float("nan"))
+            nat.check(lib.cbq_linear_xform_f32(
+                h.data_ptr(), d.data_ptr() if mode == nat.XF_ADD_RMS else None,
+                h_ref.data_ptr(), mode, 1e-6, packed.data_ptr(), cb.data_ptr(), y.data_ptr(),
+                2 * M, K, C, bits, st), "cbq_linear_xform_f32")
+            want = silu_mul(y)
+            h_out = torch.full_like(h, float("nan"))
+            got = glu(h, d if mode == nat.XF_ADD_RMS else None, h_out, mode)
+            assert torch.equal(got, want), (M, K, rep, mode)
+            if mode == nat.XF_ADD_RMS:
+                assert torch.equal(h_out, h_ref), (M, K, rep)
+        y = torch.empty(1, 2 * M, device=cuda)
+        nat.check(lib.ck_linear_f32(h.data_ptr(), packed.data_ptr(), cb.data_ptr(), y.data_ptr(),
+                                    1, 2 * M, K, C, bits, st), "ck_linear_f32")
+        want = silu_mul(y).double()
+        got = glu(h, None, None, 0).double()
+        rel = float((got - want).norm() / want.norm())
+        assert rel <= 1e-5, (M, K, rep, rel)

@@ -82,7 +82,13 @@ def test_argument_validation_before_launch(lib):
     assert xf(p, None, None, 1, 1e-6, p, p, p, 64, 4096, 16, 13, None) == 2     # silu needs x1
     assert xf(p, None, None, 2, 1e-6, p, p, p, 64, 4096, 16, 13, None) == 2     # add needs x1
     assert xf(p, None, None, 3, 1e-6, p, p, p, 64, 32768, 16, 13, None) == 2    # norm K > 16384
-    one = (ctypes.c_void_p * 1)(p)
+    glu = lib.cbq_linear_xform_glu_f32
+    assert glu(p, p, None, 1, 1e-6, p, p, p, 64, 4096, 16, 13, None) == 2       # input is not silu
+    assert glu(p, None, None, 2, 1e-6, p, p, p, 64, 4096, 16, 13, None) == 2    # add needs x1
+    assert glu(p, None, None, 3, 1e-6, p, p, p, 64, 32768, 16, 13, None) == 2   # norm K > 16384
+    assert glu(p, None, None, 0, 1e-6, p, p, p, 64, 4096, 16, 9, None) == 2     # width 9
+    assert glu(p, None, None, 0, 1e-6, p, p, p, 0, 4096, 16, 13, None) == 2     # no rows
+    one =(ctypes.c_void_p * 1)(p)
     m1 = (ctypes.c_int * 1)(64)
     hxf = lib.cbq_huff_linear_col_xform_f32
     assert hxf(p, None, None, 1, 1e-6, 1, one, one, one, m1, 4096, None) == 2   # silu needs x1
