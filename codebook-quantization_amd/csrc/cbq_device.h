@@ -217,14 +217,17 @@ __device__ __forceinline__ void lds_barrier()
 // exactly the order of a 1024-thread block whose thread vt adds the
 // squares of v[vt + 1024 j] for j = 0..15 (terms past K are +0), whose
 // waves reduce by wave_sum and whose 16 wave sums add in wave order: the
-// decoder's standalone RMSNorm kernel.
-template <int NTHR, int XMODE>
+// decoder's standalone RMSNorm kernel.  NJ < 16 holds only j < NJ, for
+// K <= 1024 NJ (the terms it drops are +0 and leave the sums unchanged).
+template <int NTHR, int XMODE, int NJ = 16>
 struct GlueTile {
     static_assert(1024 % NTHR == 0 && NTHR >= CBQ_WAVE, "block size divides 1024");
+    static_assert(NJ >= 1 && NJ <= 16, "16 terms per virtual thread at most");
     static constexpr int VPT = 1024 / NTHR;
+    static constexpr int kJ = NJ;
     static constexpr bool TWO = XMODE == XF_SILU || XMODE == XF_ADD_RMS;
-    float a[VPT][16];
-    float b[TWO ? VPT : 1][16];
+    float a[VPT][NJ];
+    float b[TWO ? VPT : 1][NJ];
 
     __device__ __forceinline__ void load(const float *__restrict__ x0,
                                          const float *__restrict__ x1, int K)
@@ -232,7 +235,7 @@ struct GlueTile {
 #pragma unroll
         for (int k = 0; k < VPT; k++)
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
+            for (int j = 0; j < NJ; j++) {
                 const int i = (int)threadIdx.x + k * NTHR + j * 1024;
                 a[k][j] = i < K ? x0[i] : 0.f;
                 if constexpr (TWO) b[k][j] = i < K ? x1[i] : 0.f;
@@ -249,7 +252,7 @@ struct GlueTile {
 #pragma unroll
         for (int k = 0; k < VPT; k++)
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
+            for (int j = 0; j < NJ; j++) {
                 if constexpr (XMODE == XF_SILU) a[k][j] = silu_mul_value(a[k][j], b[k][j]);
                 if constexpr (XMODE == XF_ADD_RMS) a[k][j] = a[k][j] + b[k][j];
             }
@@ -258,7 +261,7 @@ struct GlueTile {
         for (int k = 0; k < VPT; k++) {
             float ss = 0.f;
 #pragma unroll
-            for (int j = 0; j < 16; j++) ss = add_square(ss, a[k][j]);
+            for (int j = 0; j < NJ; j++) ss = add_square(ss, a[k][j]);
             ss = wave_sum(ss);
             if ((threadIdx.x & (CBQ_WAVE - 1)) == 0)
                 s_red16[((int)threadIdx.x + k * NTHR) / CBQ_WAVE] = ss;
@@ -284,7 +287,7 @@ struct GlueTile {
 #pragma unroll
             for (int k = 0; k < VPT; k++)
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
+                for (int j = 0; j < NJ; j++) {
                     const int i = (int)threadIdx.x + k * NTHR + j * 1024;
                     if (i < K) h_out[i] = a[k][j];
                 }

@@ -286,6 +286,10 @@ __device__ unsigned long long cbq_timeline_wave[kTimelineWaves * kTimelineFields
 #define CBQ_TS(var) const unsigned long long var = __builtin_amdgcn_s_memrealtime()
 #endif
 constexpr int kStreamD = 2;
+// Folded norms with K <= kGlueSmallK (the hidden size of the 8B shapes) hold
+// 4 of GlueTile's 16 terms per virtual thread: the 12 others are past K.
+constexpr int kGlueSmallK = 4096;
+static_assert(kGlueSmallK <= 1024 * 4, "4 terms per virtual thread cover kGlueSmallK");
 constexpr int kStreamLds = 152 * 1024;      // codebook + staged x, per block
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
@@ -405,7 +409,7 @@ __device__ __forceinline__ void put_out_t(OT *o, float v, int accum)
 // out[j] = silu(gate_j . x) * (up_j . x), rounded as silu_mul_value, so the
 // down projection that consumes it stages plain x.
 template <int BITS, int TMAX, typename XT, typename OT, bool AFFINE = false, int XMODE = XF_NONE,
-          bool KCHUNK = false, bool GLU = false>
+          bool KCHUNK = false, bool GLU = false, int NJ = 16>
 __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     const XT *__restrict__ x, const uint32_t *__restrict__ words,
     const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C,
@@ -499,7 +503,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
         }
     }
     // Folded glue: x0 (and x1) into registers ahead of the weight stream.
-    GlueTile<kStreamBlock, XMODE> tile;
+    GlueTile<kStreamBlock, XMODE, NJ> tile;       // NJ < 16: K <= 1024 NJ
     if constexpr (XMODE != XF_NONE) tile.load((const float *)x, x1, K);
     // The weight addresses depend on `zero`, produced by a volatile asm with a
     // memory clobber, so no weight load is issued before the staging loads.
@@ -535,7 +539,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
 #pragma unroll
         for (int k = 0; k < tile.VPT; k++)
 #pragma unroll
-            for (int j = 0; j < 16; j++) {
+            for (int j = 0; j < tile.kJ; j++) {
                 const int i = (int)threadIdx.x + k * kStreamBlock + j * 1024;
                 const int g = i >> 5;
                 const int sl = (g << 5) + ((((i >> 2) & 7) ^ (g & 7)) << 2) + (i & 3);
@@ -1101,17 +1105,20 @@ int cbq_linear_xform_f32(const float *x0, const float *x1, float *h_out, int mod
     const int blocks =
         std::max(1, std::min(cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
     size_t dyn = 0;
-#define CBQ_XF(B, MODE)                                                                        \
-    hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE>), dim3(blocks),    \
-                       dim3(kStreamBlock), dyn, stream, x0, (const uint32_t *)packed, codebook, \
-                       out, 1, M, K, C, 0u, 0u, x1, h_out, eps, K, 0, 0)
+#define CBQ_XF(B, MODE, NJ)                                                                    \
+    hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE, false, false, NJ>), \
+                       dim3(blocks), dim3(kStreamBlock), dyn, stream, x0,                       \
+                       (const uint32_t *)packed, codebook, out, 1, M, K, C, 0u, 0u, x1, h_out,  \
+                       eps, K, 0, 0)
 #define CBQ_XF_MODES(B)                                                                        \
     do {                                                                                       \
         dyn = stream_dyn_lds<B, float>(1, K, C);                                               \
         if (!dyn) return CK_ERR_ARG;                                                           \
-        if (mode == XF_SILU) CBQ_XF(B, XF_SILU);                                               \
-        else if (mode == XF_ADD_RMS) CBQ_XF(B, XF_ADD_RMS);                                    \
-        else CBQ_XF(B, XF_RMS);                                                                \
+        if (mode == XF_SILU) CBQ_XF(B, XF_SILU, 16);                                           \
+        else if (mode == XF_ADD_RMS && K <= kGlueSmallK) CBQ_XF(B, XF_ADD_RMS, 4);             \
+        else if (mode == XF_ADD_RMS) CBQ_XF(B, XF_ADD_RMS, 16);                                \
+        else if (K <= kGlueSmallK) CBQ_XF(B, XF_RMS, 4);                                       \
+        else CBQ_XF(B, XF_RMS, 16);                                                            \
     } while (0)
     switch (bits) {
     case 8: CBQ_XF_MODES(8); break;
@@ -1140,8 +1147,8 @@ int cbq_linear_xform_glu_f32(const float *x0, const float *x1, float *h_out, int
     const int blocks =
         std::max(1, std::min(cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
     size_t dyn = 0;
-#define CBQ_XG(B, MODE)                                                                        \
-    hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE, false, true>),     \
+#define CBQ_XG(B, MODE, NJ)                                                                    \
+    hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE, false, true, NJ>), \
                        dim3(blocks), dim3(kStreamBlock), dyn, stream, x0,                       \
                        (const uint32_t *)packed, codebook, out, 1, M, K, C, 0u, 0u, x1, h_out,  \
                        eps, K, 0, 0)
@@ -1149,9 +1156,11 @@ int cbq_linear_xform_glu_f32(const float *x0, const float *x1, float *h_out, int
     do {                                                                                       \
         dyn = stream_dyn_lds<B, float>(1, K, C);                                               \
         if (!dyn) return CK_ERR_ARG;                                                           \
-        if (mode == XF_ADD_RMS) CBQ_XG(B, XF_ADD_RMS);                                         \
-        else if (mode == XF_RMS) CBQ_XG(B, XF_RMS);                                            \
-        else CBQ_XG(B, XF_NONE);                                                               \
+        if (mode == XF_ADD_RMS && K <= kGlueSmallK) CBQ_XG(B, XF_ADD_RMS, 4);                  \
+        else if (mode == XF_ADD_RMS) CBQ_XG(B, XF_ADD_RMS, 16);                                \
+        else if (mode == XF_RMS && K <= kGlueSmallK) CBQ_XG(B, XF_RMS, 4);                     \
+        else if (mode == XF_RMS) CBQ_XG(B, XF_RMS, 16);                                        \
+        else CBQ_XG(B, XF_NONE, 16);                                                           \
     } while (0)
     switch (bits) {
     case 8: CBQ_XG_MODES(8); break;
@@ -1188,18 +1197,21 @@ int cbq_linear_xform_argmax_f32(const float *x0, const float *x1, float *h_out, 
     float *part_v = (float *)workspace;
     int *part_i = (int *)(part_v + kArgMaxParts);
     size_t dyn = 0;
-#define CBQ_XA(B, MODE)                                                                        \
-    hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE>), dim3(blocks),    \
-                       dim3(kStreamBlock), dyn, stream, x0, (const uint32_t *)packed, codebook, \
-                       out, 1, M, K, C, 0u, 0u, x1, h_out, eps, K, 0, 0, part_v, part_i)
+#define CBQ_XA(B, MODE, NJ)                                                                    \
+    hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE, false, false, NJ>), \
+                       dim3(blocks), dim3(kStreamBlock), dyn, stream, x0,                       \
+                       (const uint32_t *)packed, codebook, out, 1, M, K, C, 0u, 0u, x1, h_out,  \
+                       eps, K, 0, 0, part_v, part_i)
 #define CBQ_XA_MODES(B)                                                                        \
     do {                                                                                       \
         dyn = stream_dyn_lds<B, float>(1, K, C);                                               \
         if (!dyn) return CK_ERR_ARG;                                                           \
-        if (mode == XF_SILU) CBQ_XA(B, XF_SILU);                                               \
-        else if (mode == XF_ADD_RMS) CBQ_XA(B, XF_ADD_RMS);                                    \
-        else if (mode == XF_RMS) CBQ_XA(B, XF_RMS);                                            \
-        else CBQ_XA(B, XF_NONE);                                                               \
+        if (mode == XF_SILU) CBQ_XA(B, XF_SILU, 16);                                           \
+        else if (mode == XF_ADD_RMS && K <= kGlueSmallK) CBQ_XA(B, XF_ADD_RMS, 4);             \
+        else if (mode == XF_ADD_RMS) CBQ_XA(B, XF_ADD_RMS, 16);                                \
+        else if (mode == XF_RMS && K <= kGlueSmallK) CBQ_XA(B, XF_RMS, 4);                     \
+        else if (mode == XF_RMS) CBQ_XA(B, XF_RMS, 16);                                        \
+        else CBQ_XA(B, XF_NONE, 16);                                                           \
     } while (0)
     switch (bits) {
     case 8: CBQ_XA_MODES(8); break;

@@ -177,7 +177,7 @@ __device__ __forceinline__ float split_decode(const uint32_t (&raw)[16], const u
 // per phase p as before.  Lane l's sub-block lies in row (p * 4096 + 64 l) / K
 // of the group (K % 64 == 0), and a chunk's dot products are summed per row
 // with masked wave sums.  GR = 1 (K % 4096 == 0) is the plain row walk.
-template <int NW, int XMODE, int GR>
+template <int NW, int XMODE, int GR, int NJ = 16>
 __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *__restrict__ x,
                                                                    SplitSegs segs, int K,
                                                                    const float *__restrict__ x1,
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
         return c;
     };
 
-    GlueTile<NW * CBQ_WAVE, XMODE == XF_SILU ? XF_NONE : XMODE> tile;
+    GlueTile<NW * CBQ_WAVE, XMODE == XF_SILU ? XF_NONE : XMODE, NJ> tile;   // K <= 1024 NJ
     if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS) tile.load(x, x1, K);
     // Two items in flight: the next one's loads go out before this one is
     // decoded.  The wave's first item is requested before the table staging.
@@ -674,6 +674,23 @@ int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits
 
 namespace {
 
+// Norm modes with K <= 4096 hold 4 of GlueTile's 16 terms per virtual thread.
+template <int NW, int XMODE, int GR>
+void launch_split_gemv(int blocks, hipStream_t stream, const float *x, const SplitSegs &segs,
+                       int K, const float *x1, float *h_out, float eps, float *arg_v, int *arg_i)
+{
+    if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS) {
+        if (K <= 4096) {
+            hipLaunchKernelGGL((split_gemv_kernel<NW, XMODE, GR, 4>), dim3(blocks),
+                               dim3(NW * CBQ_WAVE), 0, stream, x, segs, K, x1, h_out, eps, arg_v,
+                               arg_i);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((split_gemv_kernel<NW, XMODE, GR>), dim3(blocks), dim3(NW * CBQ_WAVE), 0,
+                       stream, x, segs, K, x1, h_out, eps, arg_v, arg_i);
+}
+
 // cbq_split_linear_f32, with the greedy-pick pairs of every block written to
 // arg_v / arg_i when those are not null (one matrix; outs[0] may be null).
 int split_linear(const float *x, const float *x1, float *h_out, int mode, float eps, int n,
@@ -726,8 +743,7 @@ int split_linear(const float *x, const float *x1, float *h_out, int mode, float 
         blocks += g.nblocks;
     }
 #define CBQ_SPLIT_GR(NWV, MODE, G)                                                                \
-    hipLaunchKernelGGL((split_gemv_kernel<NWV, MODE, G>), dim3(blocks), dim3(NWV * CBQ_WAVE), 0,  \
-                       stream, x, segs, K, x1, h_out, eps, arg_v, arg_i)
+    launch_split_gemv<NWV, MODE, G>(blocks, stream, x, segs, K, x1, h_out, eps, arg_v, arg_i)
 #define CBQ_SPLIT(NWV, MODE)                                                                      \
     do {                                                                                          \
         if (GR == 1) CBQ_SPLIT_GR(NWV, MODE, 1);                                                  \
