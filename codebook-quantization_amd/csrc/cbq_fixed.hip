@@ -558,7 +558,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     for (int t = 0; t < TMAX; t++) acc[t] = res[t] = 0.f;
     float a_best = -INFINITY;                      // greedy-pick candidate of this lane
     int a_idx = kArgNone;
-    float g_row = 0.f;                             // GLU: the pair's gate product
+    float g_res = 0.f;                             // GLU: gate sums, lane = pair % 64
     int ri = 0, ch = 0, base = 0;
     do {
 #pragma unroll
@@ -602,18 +602,17 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
             __builtin_memcpy(buf[d], item_ptr(item + D), sizeof(buf[d]));
             if (GLU && ++ch == NGW) {                // gate or up row done (wave-uniform)
                 ch = 0;
+                // gate and up sums wait in lane pair % 64; each lane forms its
+                // pair's SiLU product when the 64 pairs are written
                 const float s = wave_sum(acc[0]);
                 acc[0] = 0.f;
-                if (ri & 1) {
-                    const int pi = ri >> 1;
-                    const float v = silu_mul_value(g_row, s);
-                    res[0] = (lane == (pi & 63) && ri < rows) ? v : res[0];
-                } else {
-                    g_row = s;
-                }
+                const bool mine = lane == ((ri >> 1) & 63) && ri < rows;
+                if (ri & 1) res[0] = mine ? s : res[0];
+                else g_res = mine ? s : g_res;
                 ri++;
                 if ((ri & 127) == 0 && ri <= rows)
-                    out[wid + ((ri >> 1) - 64 + lane) * W] = from_f32<OT>(res[0]);
+                    out[wid + ((ri >> 1) - 64 + lane) * W] =
+                        from_f32<OT>(silu_mul_value(g_res, res[0]));
             } else if (!GLU && ++ch == NGW) {       // row done (wave-uniform)
                 ch = 0;
 #pragma unroll
@@ -649,6 +648,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
 #endif
     const int n_res = GLU ? rows >> 1 : rows;       // outputs of this wave
     const int rb = n_res & ~63;
+    if (GLU) res[0] = silu_mul_value(g_res, res[0]);
     if (lane < n_res - rb) {
         const int row = wid + (rb + lane) * W;
         if (out) {
