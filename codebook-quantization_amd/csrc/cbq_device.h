@@ -165,11 +165,17 @@ __device__ __forceinline__ float add_square(float ss, float v)
     return ss + v * v;
 }
 
-// silu(g) * u = g / (1 + exp(-g)) * u, each step rounded.
+// silu(g) * u = g / (1 + exp(-g)) * u on the hardware exp2 and reciprocal
+// (v_exp_f32 of -g log2(e), v_rcp_f32; each about 1 ulp): 6 instructions
+// where expf and an IEEE divide take ~22, which matters for a GEMV that
+// stages silu(gate) * up for all 12 288 columns in every block.  Relative
+// error below 1e-6 for |g| < 16, and the limits hold: g -> -inf gives -0
+// (exp overflows, rcp(inf) = 0), g -> +inf gives g * u.
 __device__ __forceinline__ float silu_mul_value(float g, float u)
 {
 #pragma clang fp contract(off)
-    return __fdiv_rn(g, 1.0f + expf(-g)) * u;
+    const float e = __builtin_amdgcn_exp2f(-g * 1.44269504f);
+    return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
 // The activation transforms a GEMV can apply while it stages x (T = 1):
