@@ -238,13 +238,16 @@ struct GlueTile {
     __device__ __forceinline__ void load(const float *__restrict__ x0,
                                          const float *__restrict__ x1, int K)
     {
+        // unconditional loads (past K: element K - 1 again, zeroed in
+        // finish), so the wait for them leaves later weight loads in flight
 #pragma unroll
         for (int k = 0; k < VPT; k++)
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
                 const int i = (int)threadIdx.x + k * NTHR + j * 1024;
-                a[k][j] = i < K ? x0[i] : 0.f;
-                if constexpr (TWO) b[k][j] = i < K ? x1[i] : 0.f;
+                const int ic = i < K ? i : K - 1;
+                a[k][j] = x0[ic];
+                if constexpr (TWO) b[k][j] = x1[ic];
             }
     }
 
@@ -259,6 +262,10 @@ struct GlueTile {
         for (int k = 0; k < VPT; k++)
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
+                if ((int)threadIdx.x + k * NTHR + j * 1024 >= K) {   // terms past K are +0
+                    a[k][j] = 0.f;
+                    if constexpr (TWO) b[k][j] = 0.f;
+                }
                 if constexpr (XMODE == XF_SILU) a[k][j] = silu_mul_value(a[k][j], b[k][j]);
                 if constexpr (XMODE == XF_ADD_RMS) a[k][j] = a[k][j] + b[k][j];
             }

@@ -290,6 +290,8 @@ constexpr int kStreamD = 2;
 // 4 of GlueTile's 16 terms per virtual thread: the 12 others are past K.
 constexpr int kGlueSmallK = 4096;
 static_assert(kGlueSmallK <= 1024 * 4, "4 terms per virtual thread cover kGlueSmallK");
+// LDS for those launches' x0 and x1 (4 terms x 1024 virtual threads each).
+constexpr size_t kGlueScratchBytes = 2 * 4 * 1024 * sizeof(float);
 constexpr int kStreamLds = 152 * 1024;      // codebook + staged x, per block
 
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
@@ -400,6 +402,33 @@ __device__ __forceinline__ void put_out_t(OT *o, float v, int accum)
 }
 
 //
+// GlueTile::load through LDS (K <= 1024 NJ): element i = tid + k NTHR +
+// 1024 j of x0 goes to s_glue[(k NJ + j) NTHR + tid] (x1 after all of
+// x0's), one direct global->LDS dword load per element; indices past K load
+// element K - 1 again (finish() zeroes those terms).  A lane reads back only
+// what its own loads wrote, so a wait for them is enough (no barrier).
+template <int NTHR, int NJ, bool TWO>
+__device__ __forceinline__ void glue_dma(const float *__restrict__ x0,
+                                         const float *__restrict__ x1, int K, float *s_glue)
+{
+    constexpr int V = 1024 / NTHR;
+    const int wbase = (int)(threadIdx.x & ~(CBQ_WAVE - 1));
+#pragma unroll
+    for (int k = 0; k < V; k++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int i = (int)threadIdx.x + k * NTHR + j * 1024;
+            const int ic = i < K ? i : K - 1;
+            const int slot = k * NJ + j;
+            __builtin_amdgcn_global_load_lds((const void *)(x0 + ic),
+                                             (lds_ptr_t)(s_glue + slot * NTHR + wbase), 4, 0, 0);
+            if constexpr (TWO)
+                __builtin_amdgcn_global_load_lds(
+                    (const void *)(x1 + ic), (lds_ptr_t)(s_glue + (V * NJ + slot) * NTHR + wbase),
+                    4, 0, 0);
+        }
+}
+
 // KCHUNK: the launch covers index columns [k0, k0 + K) of rows Kfull long
 // (x is [T, Kfull]); accum != 0 adds the partial products to out instead of
 // writing them.  The host splits K this way when x of all T tokens does not
@@ -449,6 +478,18 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     const int rows = wid < M ? (GLU ? 2 : 1) * ((M - wid + W - 1) / W) : 0;
     const int n_items = rows * NGW;
     const uint32_t cmax4 = (uint32_t)(C_eff - 1) << 2;
+
+    // Folded glue: x0 (and x1) requested first, ahead of the codebook and
+    // the weight stream.  At K <= kGlueSmallK the loads go straight to LDS
+    // past the staged x (kGlueScratchBytes of dynamic LDS), so no register
+    // waits on them and the explicit wait below leaves the ring in flight.
+    GlueTile<kStreamBlock, XMODE, NJ> tile;       // NJ < 16: K <= 1024 NJ
+    constexpr bool kGlueDma = XMODE != XF_NONE && NJ == 4;
+    float *const s_glue =
+        (float *)s_x + ((T * G * XStage<XT>::kGroupDw + 63) & ~63);
+    if constexpr (kGlueDma) glue_dma<kStreamBlock, NJ, decltype(tile)::TWO>(
+        (const float *)x, x1, K, s_glue);
+    else if constexpr (XMODE != XF_NONE) tile.load((const float *)x, x1, K);
 
     // Staging: direct global->LDS loads, every wave a share.  Padded
     // codebook: whole 16-byte pieces of cb by 16-byte loads (lanes past them
@@ -502,9 +543,6 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
                                              (lds_ptr_t)(s_x + (i << 6)), 4, 0, 0);
         }
     }
-    // Folded glue: x0 (and x1) into registers ahead of the weight stream.
-    GlueTile<kStreamBlock, XMODE, NJ> tile;       // NJ < 16: K <= 1024 NJ
-    if constexpr (XMODE != XF_NONE) tile.load((const float *)x, x1, K);
     // The weight addresses depend on `zero`, produced by a volatile asm with a
     // memory clobber, so no weight load is issued before the staging loads.
     uint32_t zero;
@@ -524,16 +562,32 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
 #pragma unroll
     for (int d = 0; d < D; d++) __builtin_memcpy(buf[d], item_ptr(d), sizeof(buf[d]));
     __builtin_amdgcn_sched_barrier(0);
+    // vmcnt(N): at most N loads outstanding.  N = the fewest instructions the
+    // D ring loads can take (dwordx4), so every older staging (and glue) load
+    // has landed while the ring stays in flight.  Explicit, since the
+    // compiler's own wait before the first use of a glue value drains the
+    // ring as well (it cannot count past the codebook DMA loop).
+    constexpr int kAfter = D * ((BITS + 3) / 4);
+    __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | (15 << 8) | ((kAfter >> 4) << 14));
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (XMODE == XF_NONE) {
-        // vmcnt(N): at most N loads outstanding.  N = the fewest instructions the
-        // D ring loads can take (dwordx4), so every older staging load has landed.
-        constexpr int kAfter = D * ((BITS + 3) / 4);
-        __builtin_amdgcn_s_waitcnt((kAfter & 15) | (7 << 4) | (15 << 8) | ((kAfter >> 4) << 14));
         if constexpr (PADDED) pad_codebook(s_cb, n16, (1 << BITS) >> 2, pad_mix, pad_last);
         lds_barrier();
     } else {
         // the transformed x from registers, while the first weight loads fly;
         // element i goes where the swizzled staging above would put it
+        if constexpr (kGlueDma) {                  // this lane's own direct loads
+            constexpr int V = decltype(tile)::VPT;
+#pragma unroll
+            for (int k = 0; k < V; k++)
+#pragma unroll
+                for (int j = 0; j < NJ; j++) {
+                    const int slot = k * NJ + j;
+                    tile.a[k][j] = s_glue[slot * kStreamBlock + threadIdx.x];
+                    if constexpr (decltype(tile)::TWO)
+                        tile.b[k][j] = s_glue[(V * NJ + slot) * kStreamBlock + threadIdx.x];
+                }
+        }
         const float r = tile.finish(K, eps, s_red16);
         if (XMODE == XF_ADD_RMS && blockIdx.x == 0 && h_out != nullptr) tile.store_sum(h_out, K);
 #pragma unroll
@@ -1107,7 +1161,8 @@ int cbq_linear_xform_f32(const float *x0, const float *x1, float *h_out, int mod
     size_t dyn = 0;
 #define CBQ_XF(B, MODE, NJ)                                                                    \
     hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE, false, false, NJ>), \
-                       dim3(blocks), dim3(kStreamBlock), dyn, stream, x0,                       \
+                       dim3(blocks), dim3(kStreamBlock),                                        \
+                       dyn + (NJ == 4 ? kGlueScratchBytes : 0), stream, x0,                     \
                        (const uint32_t *)packed, codebook, out, 1, M, K, C, 0u, 0u, x1, h_out,  \
                        eps, K, 0, 0)
 #define CBQ_XF_MODES(B)                                                                        \
@@ -1149,7 +1204,8 @@ int cbq_linear_xform_glu_f32(const float *x0, const float *x1, float *h_out, int
     size_t dyn = 0;
 #define CBQ_XG(B, MODE, NJ)                                                                    \
     hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE, false, true, NJ>), \
-                       dim3(blocks), dim3(kStreamBlock), dyn, stream, x0,                       \
+                       dim3(blocks), dim3(kStreamBlock),                                        \
+                       dyn + (NJ == 4 ? kGlueScratchBytes : 0), stream, x0,                     \
                        (const uint32_t *)packed, codebook, out, 1, M, K, C, 0u, 0u, x1, h_out,  \
                        eps, K, 0, 0)
 #define CBQ_XG_MODES(B)                                                                        \
@@ -1199,7 +1255,8 @@ int cbq_linear_xform_argmax_f32(const float *x0, const float *x1, float *h_out, 
     size_t dyn = 0;
 #define CBQ_XA(B, MODE, NJ)                                                                    \
     hipLaunchKernelGGL((fixed_stream_kernel<B, 1, float, float, false, MODE, false, false, NJ>), \
-                       dim3(blocks), dim3(kStreamBlock), dyn, stream, x0,                       \
+                       dim3(blocks), dim3(kStreamBlock),                                        \
+                       dyn + (NJ == 4 ? kGlueScratchBytes : 0), stream, x0,                     \
                        (const uint32_t *)packed, codebook, out, 1, M, K, C, 0u, 0u, x1, h_out,  \
                        eps, K, 0, 0, part_v, part_i)
 #define CBQ_XA_MODES(B)                                                                        \
