@@ -110,7 +110,8 @@ def test_long_cache_split_attention_decoder(cuda, model, monkeypatch):
 @pytest.mark.parametrize("M,K,bits,C", [(12288, 4096, 13, 5000),     # 8B gate/up shape
                                         (137733, 32, 13, 8192),     # > 64 pairs per wave
                                         (1003, 4096, 11, 2048),     # ragged pair count
-                                        (77, 96, 8, 300)])          # fewer pairs than waves
+                                        (77, 96, 8, 300),           # fewer pairs than waves
+                                        (300, 6144, 13, 4000)])     # K > 4096: 16 glue terms
 def test_glu_epilogue_equals_gemv_then_silu(cuda, M, K, bits, C):
     """cbq_linear_xform_glu_f32 over a row-stacked [gate; up] matrix equals
     the stacked GEMV (same x transform) followed by cbq_silu_mul_f32, bit for
