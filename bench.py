@@ -319,6 +319,20 @@ def cpu_ids():
     return out
 
 
+def config5_cpu_record():
+    """Config 5 on the CPU: the golden run's own timing (the 36-layer model
+    decoded by oracle/cpu_decoder.py with every GEMV on the reference's
+    compiled C kernel, tests/golden/gen_e2e_full_golden.py), recorded beside
+    the fixture.  Measured on the host that generated the fixture, not on the
+    GPU box (the run takes ~35 minutes)."""
+    path = os.path.join(ROOT, "tests", "golden", "e2e_qwen3_8b_cpu_timing.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
 def cpu_baseline(np, seconds):
     """BASELINE config 1 on the host cores with the reference's own C kernels
     (oracle/_ref; the restatement when that is not built): W [6144, 2048]
@@ -336,7 +350,7 @@ def cpu_baseline(np, seconds):
     import huffman_codebook as hc
     import synthetic
     kind = "reference" if O.ref_available() else "port"
-    lk = "ref" if kind == "reference" else "oracle"
+    lk = "ref_native" if kind == "reference" else "oracle"
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
     threads = min(threads, os.cpu_count() or threads)
     M, K = 6144, 2048
@@ -348,6 +362,7 @@ def cpu_baseline(np, seconds):
     enc = hc.huffman_encode_indices(idx, shape=(M, K))
     C = len(cb)
     L = O.lib(lk)
+    march = "x86-64-v4 (AVX-512)" if L.path.endswith("_avx512.so") else "x86-64-v3 (AVX2+FMA)"
     pk_pad = np.concatenate([packed, np.zeros(4, np.uint8)])
     tabs = O.huff_cpu_tables(enc)
     stream_b = len(enc["huff_stream"])
@@ -395,16 +410,70 @@ def cpu_baseline(np, seconds):
             med, n = timed(fn)
             res[f"T{T}_{name}"] = {"ms": round(med * 1e3, 3), "GB/s": round(nb / med / 1e9, 3),
                                    "runs": n}
+    # configs 2 / 3: every distinct linear shape of the 28-layer 1.7B decoder
+    # at T = 1, 4, 16, one call over all rows, fixed width and Huffman; the
+    # per-step figure sums a layer's seven linears x 28
+    shapes = {"q_o": (2048, 2048), "k_v": (1024, 2048), "gate_up": (6144, 2048),
+              "down": (2048, 6144)}
+    per_layer = {"q_o": 2, "k_v": 2, "gate_up": 2, "down": 1}
+    budget = max(0.2, seconds / 60.0)
+    small = {}
+    for sname, (Ms, Ks) in shapes.items():
+        ws = w if (Ms, Ks) == (M, K) else \
+            synthetic.make_bf16((Ms, Ks), f"config2.{sname}", device="cpu").float().numpy()
+        cbs, idxs = cbb.frequency_sorted_codebook(ws)
+        bs = cbb.bits_for(len(cbs))
+        pks = np.concatenate([bitpack.pack_any_bits(idxs, bs), np.zeros(4, np.uint8)])
+        encs = hc.huffman_encode_indices(idxs, shape=(Ms, Ks))
+        tbs = O.huff_cpu_tables(encs)
+        Cs = len(cbs)
+        for T in (1, 4, 16):
+            x = rng.standard_normal((T, Ks)).astype(np.float32)
+            out = np.zeros((T, Ms), np.float32)
+
+            def fx():
+                out[:] = 0
+                with O._omp_threads(threads):
+                    L.fixed_rows(O._p(x, O._f32p), O._p(pks, O._u8p), O._p(cbs, O._f32p),
+                                 O._p(out, O._f32p), T, Ms, Ks, Cs, bs, 0, Ms)
+
+            def hf():
+                out[:] = 0
+                with O._omp_threads(threads):
+                    L.huff_rows(O._p(x, O._f32p), *O._tab_args(tbs), O._p(cbs, O._f32p),
+                                O._p(out, O._f32p), T, Ms, Ks, Cs, 0, Ms, tbs["max_len"])
+            for enc_name, fn in (("fixed", fx), ("huffman", hf)):
+                fn()
+                ts = []
+                t_end = time.perf_counter() + budget
+                while len(ts) < 3 or (time.perf_counter() < t_end and len(ts) < 50):
+                    t0 = time.perf_counter()
+                    fn()
+                    ts.append(time.perf_counter() - t0)
+                small[f"{sname}_T{T}_{enc_name}"] = round(float(np.median(ts)) * 1e3, 3)
+    steps = {}
+    for enc_name in ("fixed", "huffman"):
+        for T in (1, 4, 16):
+            ms = 28 * sum(n * small[f"{k}_T{T}_{enc_name}"] for k, n in per_layer.items())
+            steps[f"{enc_name}_T{T}"] = {"ms_per_step": round(ms, 1),
+                                         "tok_per_s": round(1000.0 * T / ms, 2)}
+    res["qwen3_1_7b_linears_ms"] = small
+    res["qwen3_1_7b_steps"] = steps
     head = res["T1_fixed_single"]
     return {"value": head["GB/s"], "unit": "GB/s", "cores": threads, "kind": kind,
             "sample": (f"config 1 (K={K} -> M={M}, 13-bit fixed width, T=1): one call over all "
                        f"rows of src/compressed_matmul.c compressed_matmul_f32_chunk "
-                       f"(gcc -O3 -fopenmp, {threads} threads, OMP_PROC_BIND="
+                       f"(gcc -O3 -march={march.split()[0]} -fopenmp, {threads} threads, OMP_PROC_BIND="
                        f"{os.environ.get('OMP_PROC_BIND')}), median of {head['runs']} runs = "
                        f"{head['ms']} ms on {cpu_model()}; every mode, encoding and T in "
                        f"cpu_baseline_detail")}, \
         {"cpu": cpu_model(), "cpu_ids": cpu_ids(), "threads": threads, "omp_proc_bind": os.environ.get("OMP_PROC_BIND"),
-         "kind": kind, "codebook": C, "bits": bits,
+         "kind": kind, "march": march,
+         "march_note": "the reference wrapper builds with -march=native "
+                       "(src/compressed_matmul_cpu.py:88-91); gcc 11 here has no znver5 target, "
+                       "so AVX-512 hosts run the x86-64-v4 build and others the x86-64-v3 one",
+         "codebook": C, "bits": bits,
+         "config5_cpu_decode": config5_cpu_record(),
          "huffman_bits_per_weight": round(8.0 * stream_b / (M * K), 3), "cells": res}
 
 

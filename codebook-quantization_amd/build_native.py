@@ -41,6 +41,34 @@ def command(out: str = SO):
 
 
 TIMELINE_SO = os.path.join(HERE, "libcbq_hip_timeline.so")
+TORCH_SO = os.path.join(HERE, "libcbq_torch.so")
+TORCH_SRC = os.path.join(CSRC, "cbq_torch_ops.cpp")
+
+
+def torch_ops_command(out: str = TORCH_SO):
+    """g++ line of libcbq_torch.so: the torch.ops.cbq binding (host C++ only,
+    no device code) over libcbq_hip.so, found next to it through $ORIGIN."""
+    import torch
+    tdir = os.path.dirname(torch.__file__)
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    return (["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__=1",
+             "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+             "-I/opt/rocm/include", f"-I{tdir}/include",
+             f"-I{tdir}/include/torch/csrc/api/include", TORCH_SRC, "-o", out,
+             f"-L{tdir}/lib", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip",
+             f"-L{HERE}", "-lcbq_hip", "-Wl,-rpath,$ORIGIN"])
+
+
+def build_torch_ops(verbose: bool = False, out: str = TORCH_SO) -> str:
+    """Compile the torch operator library (after libcbq_hip.so, which it links)."""
+    cmd = torch_ops_command(out + ".tmp")
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("g++ failed on cbq_torch_ops.cpp:\n" + res.stderr[-4000:])
+    os.replace(out + ".tmp", out)
+    return out
 
 
 def build(verbose: bool = False, jobs: int = 0, out: str = SO, defines=()) -> str:
@@ -82,5 +110,8 @@ if __name__ == "__main__":
     if "--timeline" in sys.argv:
         # the diagnostic library (per-wave timeline of the streaming GEMV)
         print(build(verbose="-v" in sys.argv, out=TIMELINE_SO, defines=("CBQ_TIMELINE",)))
+    elif "--torch-ops" in sys.argv:
+        print(build_torch_ops(verbose="-v" in sys.argv))
     else:
         print(build(verbose="-v" in sys.argv))
+        print(build_torch_ops(verbose="-v" in sys.argv))

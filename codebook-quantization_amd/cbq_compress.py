@@ -18,7 +18,18 @@ benchmark configurations), ordered by descending count (--order
 frequency) or ascending bit pattern (--order pattern, the reference's
 lossless order); indices are ceil(log2 C) bits wide, fixed-width packed or,
 with --entropy-code, canonical-Huffman coded (24-bit limited, 4096-symbol
-chunk index written beside the stream).  Other tensors are stored 'exact'.
+chunk index written beside the stream).  Other tensors are stored 'exact'
+as uint16 bf16 bit patterns, the payload the reference decodes with
+(raw.astype(uint32) << 16) (src/adaptive_compressor.py:599-602).
+
+Two defaults differ from the reference's lossless pass, on purpose:
+  * the reference codebook-encodes every bf16 tensor of >= 1000 weights
+    whatever its rank (src/adaptive_compressor.py:85); this tool encodes
+    2-D matrices only, the tensors the compressed kernels consume, and keeps
+    1-D norm vectors 'exact' (bit-identical weights either way);
+  * the default codebook order is descending frequency, the order the
+    benchmark configurations name; --order pattern gives the reference's
+    ascending-bit-pattern order (src/adaptive_compressor.py:91).
 
 Outputs, under MODEL_DIR/codebook-lossless[-huffman]/ (the reference's
 directory name, compress.py:87-94) or --out:
@@ -76,6 +87,19 @@ def checkpoint_tensors(model_dir) -> Iterator[Tuple[str, torch.Tensor]]:
 
 def compressible(t: torch.Tensor) -> bool:
     return t.dtype == torch.bfloat16 and t.dim() == 2 and t.numel() >= MIN_PARAMS
+
+
+def exact_bits(t: torch.Tensor) -> np.ndarray:
+    """'exact' payload as the reference stores it: bf16 bit patterns in a
+    uint16 array (src/adaptive_compressor.py:174-176), read back as
+    (raw.astype(uint32) << 16).view(float32) (src/adaptive_compressor.py:599-602,
+    src/compressor.py:464-466).  bf16 tensors keep their bits; wider floats
+    are truncated to their top 16 bits as float32_to_bfloat16 does
+    (src/compressor.py:28-34)."""
+    if t.dtype == torch.bfloat16:
+        return t.contiguous().view(torch.int16).numpy().view(np.uint16).copy()
+    u = t.detach().to(torch.float32).contiguous().numpy().view(np.uint32)
+    return (u >> 16).astype(np.uint16)
 
 
 def codebook_for(counts: torch.Tensor, order: str):
@@ -165,7 +189,7 @@ def compress_checkpoint(model_dir, out_dir=None, entropy_code: bool = False,
             if write_npz:
                 cache_io.save_cached_tensor(tdir / f"{cache_io.safe_name(name)}.npz", name,
                                             {"mode": "exact", "shape": tuple(w.shape),
-                                             "data": w.float().numpy()})
+                                             "data": exact_bits(w)})
             dense[name] = w
             continue
         cat = cbb.classify_tensor(name)

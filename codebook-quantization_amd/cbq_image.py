@@ -179,7 +179,7 @@ def validate_header(h: dict, file_size: int) -> None:
     (row offsets, chunk offsets) are checked after upload by load_image."""
     import huffman_codebook as hc
     D, P = int(h.get("data_offset", -1)), int(h.get("payload_bytes", -1))
-    if D < 16 or D % ALIGN or P < 0 or D + P != file_size:
+    if D < 16 or D % ALIGN or P < 0 or P % ALIGN or D + P != file_size:
         raise ValueError(f"image payload [{D}, {D + P}) does not match the file size {file_size}")
 
     def sec(where, s, dtype=None, at_least=0, exact=None):
@@ -217,7 +217,10 @@ def validate_header(h: dict, file_size: int) -> None:
             bits = int(e.get("bits", 0))
             if not 1 <= bits <= 16:
                 raise ValueError(f"{name}: bits {bits}")
-            sec(f"{name}.packed", s.get("packed"), "uint8", at_least=(n * bits + 7) // 8 + 4)
+            # the writer pads the stream to 16-byte pieces plus 16 bytes: the
+            # streaming kernels load whole 16-byte pieces past the last word
+            sec(f"{name}.packed", s.get("packed"), "uint8",
+                at_least=((n * bits + 7) // 8 + 15) // 16 * 16 + 16)
         elif kind == "split":
             nch = int(e.get("n_chunks", -1))
             if n % hc.CHUNK_SYMBOLS or nch != n // hc.CHUNK_SYMBOLS:

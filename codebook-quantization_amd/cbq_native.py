@@ -104,6 +104,8 @@ SIGNATURES = {
     "cbq_split_linear_argmax_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float,
                                          ctypes.POINTER(SplitMatrix), _vp, _i, _i, _vp,
                                          ctypes.c_size_t, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "ck_upload_packed": (_vp, [_vp, ctypes.c_size_t]),
+    "ck_upload_codebook": (_vp, [_vp, _i]),
     "cbq_file_upload": (_i, [ctypes.c_char_p, ctypes.POINTER(UploadPart), _i, ctypes.c_size_t,
                              _i]),
     # include/cbq_decode.h

@@ -499,11 +499,23 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
     float pad_mix[4], pad_last = 0.f;
     if constexpr (PADDED) {
         n16 = C_eff >> 2;
-        for (int i = wave; i < ((n16 + 63) >> 6); i += kStreamWaves) {
-            const int q = (i << 6) + lane;
-            if (q < n16)
-                __builtin_amdgcn_global_load_lds((const void *)(cb + 4 * q),
-                                                 (lds_ptr_t)(s_cb + (i << 8)), 16, 0, 0);
+        if (((uintptr_t)cb & 15) == 0) {
+            for (int i = wave; i < ((n16 + 63) >> 6); i += kStreamWaves) {
+                const int q = (i << 6) + lane;
+                if (q < n16)
+                    __builtin_amdgcn_global_load_lds((const void *)(cb + 4 * q),
+                                                     (lds_ptr_t)(s_cb + (i << 8)), 16, 0, 0);
+            }
+        } else {
+            // codebook off 16-byte alignment: the same 4 n16 entries by dword
+            // loads (none past them: pad_codebook writes those slots)
+            const int n4 = n16 << 2;
+            for (int i = wave; i < ((n4 + 63) >> 6); i += kStreamWaves) {
+                const int e = (i << 6) + lane;
+                if (e < n4)
+                    __builtin_amdgcn_global_load_lds((const void *)(cb + e),
+                                                     (lds_ptr_t)(s_cb + (i << 6)), 4, 0, 0);
+            }
         }
         pad_last = cb[C_eff - 1];
 #pragma unroll
@@ -1154,7 +1166,8 @@ int cbq_linear_xform_f32(const float *x0, const float *x1, float *h_out, int mod
         return CK_ERR_ARG;
     if (mode < XF_SILU || mode > XF_RMS || ((mode == XF_SILU || mode == XF_ADD_RMS) && !x1))
         return CK_ERR_ARG;
-    if (mode != XF_SILU && K > 16384) return CK_ERR_ARG;
+    // x is staged by GlueTile<.., 16>: 16 terms of 1024 virtual threads
+    if (K > 16384) return CK_ERR_ARG;
     if (((uintptr_t)packed & 3) != 0) return CK_ERR_ARG;
     const int blocks =
         std::max(1, std::min(cbq_num_cus(), (M + kStreamWaves - 1) / kStreamWaves));
@@ -1243,7 +1256,7 @@ int cbq_linear_xform_argmax_f32(const float *x0, const float *x1, float *h_out, 
         return CK_ERR_ARG;
     if (mode < XF_NONE || mode > XF_RMS || ((mode == XF_SILU || mode == XF_ADD_RMS) && !x1))
         return CK_ERR_ARG;
-    if (mode >= XF_ADD_RMS && K > 16384) return CK_ERR_ARG;
+    if (mode != XF_NONE && K > 16384) return CK_ERR_ARG;   // GlueTile<.., 16> covers 16384
     if (((uintptr_t)packed & 3) != 0 || ((uintptr_t)x0 & 3) != 0 ||
         ((uintptr_t)workspace & 3) != 0 || workspace_bytes < CBQ_ARGMAX_WORKSPACE)
         return CK_ERR_ARG;

@@ -144,3 +144,34 @@ extern "C" int cbq_file_upload(const char *path, const cbq_upload_part *parts, i
     close(fd);
     return status.load();
 }
+
+// Host buffer -> fresh device allocation (synchronous copy); nullptr on any
+// failure, with nothing left allocated.
+static void *upload_bytes(const void *host, size_t nbytes, const char *what)
+{
+    if (!host || nbytes == 0) return nullptr;
+    void *dev = nullptr;
+    hipError_t e = hipMalloc(&dev, nbytes);
+    if (e != hipSuccess) {
+        fprintf(stderr, "%s: hipMalloc(%zu): %s\n", what, nbytes, hipGetErrorString(e));
+        return nullptr;
+    }
+    e = hipMemcpy(dev, host, nbytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        fprintf(stderr, "%s: hipMemcpy: %s\n", what, hipGetErrorString(e));
+        (void)hipFree(dev);
+        return nullptr;
+    }
+    return dev;
+}
+
+extern "C" uint8_t *ck_upload_packed(const uint8_t *host_packed, size_t nbytes)
+{
+    return (uint8_t *)upload_bytes(host_packed, nbytes, "ck_upload_packed");
+}
+
+extern "C" float *ck_upload_codebook(const float *host_codebook, int C)
+{
+    if (C <= 0) return nullptr;
+    return (float *)upload_bytes(host_codebook, (size_t)C * sizeof(float), "ck_upload_codebook");
+}

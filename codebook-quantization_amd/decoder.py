@@ -182,11 +182,12 @@ class Qwen3Decoder:
         # One-token steps fold RMSNorm / SiLU into the GEMVs' x staging when
         # every linear that consumes them offers `xform` (stacked q/k/v and
         # gate/up, down, lm_head): 5 launches per layer instead of 8, with
-        # values identical to the separate glue kernels.
+        # values identical to the separate glue kernels.  The GEMVs stage a
+        # transformed x of at most 16384 values.
         need = ["lm_head"] + [f"model.layers.{i}.{n}" for i in range(cfg.layers)
                               for n in ("self_attn.qkv_proj", "mlp.gate_up_proj", "mlp.down_proj")]
-        self.fused = fuse_glue and all(callable(getattr(linears.get(n), "xform", None))
-                                       for n in need)
+        self.fused = (fuse_glue and max(cfg.hidden, cfg.inter) <= 16384 and
+                      all(callable(getattr(linears.get(n), "xform", None)) for n in need))
 
     # ---- building blocks (HF Qwen3 semantics, fp32) -------------------------
     def _attend(self, i: int, q: torch.Tensor, L: int, pos: torch.Tensor) -> torch.Tensor:

@@ -7,8 +7,9 @@ Same classes, constructor and call signatures as the reference
     GPUAcceleratedEmbedding(name, indices_np, codebook, shape, bits)(ids)
 
 The packed indices (+ zero padding) and the float32 codebook are copied to
-the device once, at construction.  Each call launches one kernel of
-libcbq_hip.so on torch's current stream, with no synchronisation:
+the device once, at construction.  Each call is one torch.ops.cbq op
+(cbq_ops: libcbq_torch.so over libcbq_hip.so's C ABI) on torch's current
+stream, with no synchronisation:
   * linear: out = x @ W^T with W[m, k] = codebook[min(idx, C-1)], fp32
     accumulate, output in x's dtype (bf16 x runs the bf16-I/O kernel
     directly; other dtypes go through fp32);
@@ -24,6 +25,7 @@ import torch
 
 import bitpack
 import cbq_native as nat
+import cbq_ops
 
 
 def _device_for(codebook: torch.Tensor) -> torch.device:
@@ -99,31 +101,14 @@ class GPUAcceleratedLinear:
         T = int(x.numel() // self.K)
         if T == 0:
             return torch.empty(*lead, self.M, dtype=in_dtype, device=dev)
+        ops = cbq_ops.load()
         if in_dtype == torch.bfloat16:
-            xc = x.reshape(T, self.K).contiguous()
-            out = torch.empty(T, self.M, dtype=torch.bfloat16, device=dev)
-            # batched tokens: x in MFMA fragment order (and fp32 partials when
-            # K is split) in a workspace from torch's caching allocator
-            nws = int(self._lib.cbq_linear_bf16_workspace(T, self.M, self.K)) if T >= 64 else 0
-            ws = torch.empty(max(1, nws // 4), dtype=torch.float32, device=dev) if nws else None
-            rc = self._lib.cbq_linear_bf16_ws(xc.data_ptr(), self.packed.data_ptr(),
-                                              self.codebook.data_ptr(), out.data_ptr(), T, self.M,
-                                              self.K, self.C, self.bits,
-                                              None if ws is None else ws.data_ptr(), nws,
-                                              nat.stream_ptr(dev))
-            nat.check(rc, "cbq_linear_bf16_ws")
+            # bf16 I/O kernel (batched tokens: bf16 MFMA with fp32 accumulation)
+            out = ops.linear(x.reshape(T, self.K).contiguous(), self.packed, self.codebook,
+                             self.M, self.bits)
             return out.reshape(*lead, self.M)
         xc = x.reshape(T, self.K).to(torch.float32).contiguous()
-        out = torch.empty(T, self.M, dtype=torch.float32, device=dev)
-        nws = int(self._lib.cbq_linear_f32_workspace(T, self.M, self.K)) if T >= 64 else 0
-        ws = torch.empty(max(1, nws // 4), dtype=torch.float32, device=dev) if nws else None
-        rc = self._lib.cbq_linear_f32_ws(xc.data_ptr(), self.packed.data_ptr(),
-                                         self.codebook.data_ptr(), out.data_ptr(), T, self.M,
-                                         self.K, self.C, self.bits,
-                                         None if ws is None else ws.data_ptr(), nws,
-                                         nat.stream_ptr(dev))
-        nat.check(rc, "cbq_linear_f32_ws")
-        out = out.reshape(*lead, self.M)
+        out = ops.linear(xc, self.packed, self.codebook, self.M, self.bits).reshape(*lead, self.M)
         return out if in_dtype == torch.float32 else out.to(in_dtype)
 
 
@@ -160,12 +145,6 @@ class GPUAcceleratedEmbedding:
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         dev = self.codebook.device
         ids = x.to(dev).reshape(-1).to(torch.int32).contiguous()
-        T = int(ids.numel())
-        out = torch.empty(T, self.hidden, dtype=torch.float32, device=dev)
-        if T:
-            rc = self._lib.cbq_embedding_f32(ids.data_ptr(), self.packed.data_ptr(),
-                                             self.codebook.data_ptr(), out.data_ptr(), T,
-                                             self.vocab, self.hidden, self.C, self.bits,
-                                             nat.stream_ptr(dev))
-            nat.check(rc, "cbq_embedding_f32")
+        out = cbq_ops.load().embedding(ids, self.packed, self.codebook, self.vocab, self.bits,
+                                       self.hidden)
         return out.reshape(*x.shape, self.hidden)

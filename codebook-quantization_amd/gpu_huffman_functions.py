@@ -32,6 +32,7 @@ import numpy as np
 import torch
 
 import cbq_native as nat
+import cbq_ops
 import huffman_codebook as hc
 
 _BF16_PAYLOAD_MAX_C = 1 << 16
@@ -92,6 +93,11 @@ class _DeviceStream:
             canon=self.canon.data_ptr(), canon_pay=self.canon_pay.data_ptr(),
             value_cb=None if self.value_cb is None else self.value_cb.data_ptr(),
             C=self.C, stage_words=hc.stage_words_for(chunk_offsets))
+
+    def op_args(self):
+        """The stream's tensors and sizes in torch.ops.cbq.huff_* argument order."""
+        return (self.words, self.chunk_off, self.sub_len, self.lut1, self.lut2, self.canon,
+                self.canon_pay, self.value_cb, self.C, int(self.desc.stage_words))
 
 
 def stream_from_device(t) -> _DeviceStream:
@@ -494,17 +500,6 @@ class HuffmanCodebookLinear:
         return SymbolDecoder(self.dev.words, self.dev.chunk_off, self.dev.sub_len,
                              self._lengths, self.device)
 
-    def _split_args(self):
-        """ctypes argument arrays of the one-token split call, built once;
-        the output slot is refilled per call (the entry point reads the
-        arrays on the host before it returns)."""
-        a = getattr(self, "_sargs", None)
-        if a is None:
-            a = ((ctypes.POINTER(nat.SplitMatrix) * 1)(ctypes.pointer(self.split[1])),
-                 (ctypes.c_void_p * 1)(), (ctypes.c_int * 1)(self.M))
-            self._sargs = a
-        return a
-
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         in_dtype = x.dtype
         x = x.to(self.device)
@@ -517,12 +512,8 @@ class HuffmanCodebookLinear:
         if T == 0:
             out = torch.empty(0, self.M, dtype=torch.float32, device=self.device)
         elif self.split is not None and T == 1:
-            out = torch.empty(1, self.M, dtype=torch.float32, device=self.device)
-            mats, outs, ms = self._split_args()
-            outs[0] = out.data_ptr()
-            nat.check(self._lib.cbq_split_linear_f32(
-                xc.data_ptr(), None, None, 0, 0.0, 1, mats, outs, ms, self.K, st),
-                "cbq_split_linear_f32")
+            cw, ro, raw, lut = self.split[0]
+            out = cbq_ops.load().split_linear(xc, cw, ro, raw, lut, self.M)
         elif self.split is not None:
             out = split_prefill(self.split, self._inv, xc, self.M, self.K, self._cb_dev)
         elif T >= 64 or self.K % hc.SUB_SYMBOLS:
@@ -533,13 +524,7 @@ class HuffmanCodebookLinear:
                 xc.data_ptr(), ctypes.byref(self.dev.desc), ctypes.byref(self.cols),
                 out.data_ptr(), self.M, self.K, st), "cbq_huff_linear_col_f32")
         else:
-            out = torch.empty(T, self.M, dtype=torch.float32, device=self.device)
-            for t0 in range(0, T, 16):
-                tt = min(16, T - t0)
-                rc = self._lib.cbq_huff_linear_f32(
-                    xc.data_ptr() + t0 * self.K * 4, ctypes.byref(self.dev.desc),
-                    out.data_ptr() + t0 * self.M * 4, tt, self.M, self.K, st)
-                nat.check(rc, "cbq_huff_linear_f32")
+            out = cbq_ops.load().huff_linear(xc, *self.dev.op_args(), self.M)
         out = out.reshape(*lead, self.M)
         return out if in_dtype == torch.float32 else out.to(in_dtype)
 
@@ -614,8 +599,5 @@ class HuffmanCodebookEmbedding:
             sym = idx.view(self.vocab, self.hidden)[rows].to(torch.int64)
             out = self._cb_dev[sym.clamp(0, self._cb_dev.numel() - 1)]
         elif T:
-            rc = self._lib.cbq_huff_embedding_f32(ids.data_ptr(), ctypes.byref(self.dev.desc),
-                                                  out.data_ptr(), T, self.vocab, self.hidden,
-                                                  nat.stream_ptr(self.device))
-            nat.check(rc, "cbq_huff_embedding_f32")
+            out = cbq_ops.load().huff_embedding(ids, *self.dev.op_args(), self.vocab, self.hidden)
         return out.reshape(*x.shape, self.hidden)

@@ -6,7 +6,7 @@
  * (LSB-first bitstream, index i at bits [i*b, (i+1)*b)) or canonical-Huffman
  * codes.  Every entry point takes plain device pointers and sizes, runs
  * asynchronously on `stream` (NULL = default stream), never synchronises and
- * never allocates device memory.  Return codes follow the reference
+ * never allocates device memory (the two upload helpers aside).  Return codes follow the reference
  * (rocm/compressed_kernel.h:37-41, rocm/huffman_kernel.h:26-28):
  *   0 success, 1 HIP runtime error (message on stderr), 2 invalid argument.
  * Kernel faults surface asynchronously, as with any HIP launch.
@@ -272,7 +272,7 @@ int cbq_huff_linear_col_multi_f32(const float *x, int n, const cbq_huff_stream *
  *   CBQ_XF_RMS      x = rmsnorm(x0)
  * RMSNorm has unit weight and the reduction order of cbq_add_rmsnorm_f32,
  * and every step rounds as the separate kernels do, so fused and unfused
- * decoders produce identical values.  K <= 16384 for the norms.  No
+ * decoders produce identical values.  K <= 16384 in every mode.  No
  * counterpart in the reference (its glue is HF PyTorch code). */
 #define CBQ_XF_SILU    1
 #define CBQ_XF_ADD_RMS 2
@@ -377,6 +377,19 @@ int cbq_pack_indices(const int32_t *indices, int64_t n, int bits, uint8_t *packe
  * src/compressed_matmul.c:296-322) when the codebook's values are distinct. */
 int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits,
                         uint8_t *packed, hipStream_t stream);
+
+/* ==== upload helpers ===================================================== */
+
+/* Allocate device memory (hipMalloc) and copy `nbytes` host bytes into it
+ * synchronously; NULL on failure (message on stderr) or when the source is
+ * NULL / empty.  The caller hipFree()s the pointer.  These two are the only
+ * entry points that allocate.  ck_upload_packed takes the packed stream as
+ * the caller has it: ceil(M*K*bits/8) bytes plus the >= 4 pad bytes
+ * ck_linear_f32 requires.
+ * Replace ck_upload_packed / ck_upload_codebook
+ * (rocm/compressed_kernel.h:153-161); same arguments and ownership. */
+uint8_t *ck_upload_packed(const uint8_t *host_packed, size_t nbytes);
+float *ck_upload_codebook(const float *host_codebook, int C);
 
 /* ==== library introspection ============================================== */
 

@@ -45,6 +45,21 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "libcbq_oracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libref_compressed_matmul.so")
+# the same source built with -march=x86-64-v4 (oracle/Makefile), for hosts with AVX-512
+REF_SO_AVX512 = os.path.join(HERE, "_ref", "libref_compressed_matmul_avx512.so")
+_AVX512 = ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl")
+
+
+def host_has_avx512() -> bool:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    return all(x in flags for x in _AVX512)
+    except OSError:
+        pass
+    return False
 CHUNK_ROWS = 256          # src/compressed_matmul_cpu.py:276
 LUT_BITS = 12             # src/huffman_codebook.py:349
 LUT_SIZE = 1 << LUT_BITS
@@ -119,6 +134,14 @@ def lib(kind: str = "oracle") -> _Lib:
             if not os.path.exists(REF_SO):
                 raise FileNotFoundError(f"{REF_SO} not built (reference tree absent?)")
             _cache[kind] = _Lib(REF_SO, _REF_NAMES)
+        elif kind == "ref_native":
+            # the wrapper's -march=native as nearly as this gcc builds it:
+            # the AVX-512 build on hosts that run it, else the x86-64-v3 one
+            path = REF_SO_AVX512 if (host_has_avx512() and os.path.exists(REF_SO_AVX512)) \
+                else REF_SO
+            if not os.path.exists(path):
+                raise FileNotFoundError(f"{path} not built (reference tree absent?)")
+            _cache[kind] = _Lib(path, _REF_NAMES)
         else:
             raise ValueError(kind)
     return _cache[kind]

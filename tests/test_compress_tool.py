@@ -78,7 +78,11 @@ def test_fixed_cache_roundtrip(ckpt, tmp_path, order):
         data = cache[n]
         if w.dim() != 2 or w.numel() < 1000:
             assert data["mode"] == "exact"
-            assert np.array_equal(np.asarray(data["data"], np.float32), w.float().numpy())
+            raw = np.asarray(data["data"])
+            assert raw.dtype == np.uint16
+            # the reference's decode of 'exact' (src/adaptive_compressor.py:599-602)
+            ref = (raw.astype(np.uint32) << 16).view(np.float32).reshape(tuple(data["shape"]))
+            assert np.array_equal(ref, w.float().numpy())
             continue
         assert data["mode"] == "direct_codebook"
         assert data["codebook_type"] == cbb.classify_tensor(n)
@@ -210,6 +214,17 @@ def test_image_validation_rejects_corrupt_headers(ckpt, tmp_path):
         e = h["tensors"][name]
         short = (M * K * e.get("bits", 0) + 7) // 8 if not enc else nb - 8   # no pad / one fewer
         bad["tensors"][name]["sections"][key] = [off, short, dt]
+        with pytest.raises(ValueError):
+            cbq_image.validate_header(bad, size)
+        if not enc:
+            # the reference's 4-byte pad is short of the 16-byte pieces the
+            # streaming kernels read past the last word
+            bad["tensors"][name]["sections"][key] = [off, short + 4, dt]
+            with pytest.raises(ValueError):
+                cbq_image.validate_header(bad, size)
+        bad = copy.deepcopy(h)
+        bad["payload_bytes"] = h["payload_bytes"] - 16            # payload not whole pages
+        bad["data_offset"] = h["data_offset"] + 16
         with pytest.raises(ValueError):
             cbq_image.validate_header(bad, size)
         bad = copy.deepcopy(h)

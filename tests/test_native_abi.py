@@ -121,3 +121,40 @@ def test_build_luts_sizes(lib):
     lut1, lut2, canon, pay = hc.device_luts(lengths, None, 0, value_payload=False, clamp=False)
     assert lut1.size == 4096 and lut2.size == 4     # one 14-bit prefix -> 2^2 subtable
     assert canon[33 + 14] == 2 and list(pay[:5]) == [0, 1, 2, 3, 4]
+
+
+def test_upload_helpers_refuse_empty_sources(lib):
+    # NULL / empty sources return NULL before any HIP call
+    assert lib.ck_upload_packed(None, 16) is None
+    buf = ctypes.create_string_buffer(16)
+    assert lib.ck_upload_packed(ctypes.addressof(buf), 0) is None
+    assert lib.ck_upload_codebook(ctypes.addressof(buf), 0) is None
+    assert lib.ck_upload_codebook(None, 4) is None
+
+
+def test_torch_ops_registered():
+    """libcbq_torch.so loads without a GPU and registers torch.ops.cbq with the
+    documented schemas; the meta kernels give the output shapes."""
+    import torch
+    import cbq_ops
+    ops = cbq_ops.load()
+    want = {"linear": "linear(Tensor x, Tensor packed, Tensor codebook, int M, int bits) -> Tensor",
+            "embedding": "embedding(Tensor ids, Tensor packed, Tensor codebook, int vocab, "
+                         "int bits, int H) -> Tensor",
+            "split_linear": "split_linear(Tensor x, Tensor cwords, Tensor row_off, Tensor raw, "
+                            "Tensor lut, int M) -> Tensor"}
+    for name, schema in want.items():
+        assert str(getattr(ops, name).default._schema) == "cbq::" + schema
+    for name in ("huff_linear", "huff_embedding"):
+        assert "Tensor? value_cb" in str(getattr(ops, name).default._schema)
+    m = torch.device("meta")
+    x = torch.empty(3, 64, device=m)
+    pk = torch.empty(100, dtype=torch.uint8, device=m)
+    cb = torch.empty(10, device=m)
+    assert ops.linear(x, pk, cb, 7, 4).shape == (3, 7)
+    assert ops.linear(x.bfloat16(), pk, cb, 7, 4).dtype == torch.bfloat16
+    ids = torch.empty(5, dtype=torch.int32, device=m)
+    assert ops.embedding(ids, pk, cb, 10, 4, 64).shape == (5, 64)
+    # the CPU has no kernel behind the ops: they refuse host tensors
+    with pytest.raises(NotImplementedError):
+        ops.linear(torch.zeros(1, 64), torch.zeros(100, dtype=torch.uint8), torch.zeros(10), 7, 4)
