@@ -111,12 +111,12 @@ def test_matrix_core_token_tiles(cuda, oracle, bits, T):
     assert rel_l2(y, ref) <= TOL, (bits, T)
 
 
-@pytest.mark.parametrize("T", [8, 64])
+@pytest.mark.parametrize("T", [1, 8, 64])
 def test_codebook_staging_unaligned(cuda, oracle, T):
-    """The few-token (T = 8) and fp32-prefill (T = 64) kernels stage the
-    codebook in 16-byte pieces when it is 16-byte aligned; a codebook 4 bytes
-    off alignment, with C not a multiple of 4 and indices past C, takes the
-    element-wise copy and must give the same result."""
+    """The streaming (T = 1), few-token (T = 8) and fp32-prefill (T = 64)
+    kernels stage the codebook in 16-byte pieces when it is 16-byte aligned;
+    a codebook 4 bytes off alignment, with C not a multiple of 4 and indices
+    past C, takes the element-wise copy and must give the same result."""
     nat, lib = _nat()
     rng = np.random.default_rng(41 + T)
     M, K, bits, C = 200, 1024, 12, 3001
@@ -138,6 +138,27 @@ def test_codebook_staging_unaligned(cuda, oracle, T):
     assert rel_l2(out.cpu().numpy(), ref) <= TOL
     y = _run_linear(cuda, x, pk, cb, M, K, C, bits)   # aligned codebook, same kernel
     assert rel_l2(out.cpu().numpy(), y) <= TOL
+    if T == 1:
+        # the one-token GEMVs that stage x through a transform, and the
+        # gate/up pair launch: bit-equal with an aligned copy of the codebook
+        ca = torch.from_numpy(cb).to(cuda)
+        assert ca.data_ptr() % 16 == 0
+        st = nat.stream_ptr(cuda)
+        for cbd in (cd, ca):
+            o1 = torch.full((1, M), float("nan"), device=cuda)
+            o2 = torch.full((1, M // 2), float("nan"), device=cuda)
+            nat.check(lib.cbq_linear_xform_f32(xd.data_ptr(), None, None, nat.XF_RMS, 1e-6,
+                                               pd.data_ptr(), cbd.data_ptr(), o1.data_ptr(), M,
+                                               K, C, bits, st), "cbq_linear_xform_f32")
+            nat.check(lib.cbq_linear_xform_glu_f32(xd.data_ptr(), None, None, 0, 1e-6,
+                                                   pd.data_ptr(), cbd.data_ptr(), o2.data_ptr(),
+                                                   M // 2, K, C, bits, st),
+                      "cbq_linear_xform_glu_f32")
+            torch.cuda.synchronize()
+            if cbd is cd:
+                u1, u2 = o1.clone(), o2.clone()
+        assert torch.equal(u1, o1) and torch.equal(u2, o2)
+        assert not torch.isnan(o1).any() and not torch.isnan(o2).any()
 
 
 @pytest.mark.parametrize("K,Ts", [(2048, (1, 5)), (4096, (16, 3, 9))])

@@ -82,6 +82,12 @@ def test_argument_validation_before_launch(lib):
     assert xf(p, None, None, 1, 1e-6, p, p, p, 64, 4096, 16, 13, None) == 2     # silu needs x1
     assert xf(p, None, None, 2, 1e-6, p, p, p, 64, 4096, 16, 13, None) == 2     # add needs x1
     assert xf(p, None, None, 3, 1e-6, p, p, p, 64, 32768, 16, 13, None) == 2    # norm K > 16384
+    assert xf(p, p, None, 1, 1e-6, p, p, p, 64, 17408, 16, 13, None) == 2       # silu K > 16384
+    ws = ctypes.create_string_buffer(8192)
+    w = ctypes.addressof(ws)
+    xa = lib.cbq_linear_xform_argmax_f32
+    assert xa(p, p, None, 1, 1e-6, p, p, p, 64, 17408, 16, 13, w, 8192, p, p, p, 0, 1,
+              None) == 2                                                        # silu K > 16384
     glu = lib.cbq_linear_xform_glu_f32
     assert glu(p, p, None, 1, 1e-6, p, p, p, 64, 4096, 16, 13, None) == 2       # input is not silu
     assert glu(p, None, None, 2, 1e-6, p, p, p, 64, 4096, 16, 13, None) == 2    # add needs x1
