@@ -2,8 +2,8 @@
 
     python codebook-quantization_amd/build_native.py
 
-Compiles each csrc/*.hip with hipcc (in parallel) and links them into a
-shared library next to this file.  Packed-fp32 VALU ops are disabled (-packed-fp32-ops): the kernels are
+Compiles each csrc/*.hip with hipcc and the host-only csrc/*.cpp with g++
+(in parallel) and links them into a shared library next to this file.  Packed-fp32 VALU ops are disabled (-packed-fp32-ops): the kernels are
 written for scalar fp32 FMAs.
 """
 import os
@@ -16,7 +16,11 @@ CSRC = os.path.join(HERE, "csrc")
 SO = os.path.join(HERE, "libcbq_hip.so")
 ARCH = "gfx950"
 SOURCES = ["cbq_fixed.hip", "cbq_huffman.hip", "cbq_prefill.hip", "cbq_prefill_f32.hip",
-           "cbq_decode.hip", "cbq_split.hip", "cbq_tiny.hip", "cbq_io.hip"]
+           "cbq_decode.hip", "cbq_split.hip", "cbq_tiny.hip"]
+# host-only C++ (no device code): compiled by the host compiler
+HOST_SOURCES = ["cbq_huff_host.cpp", "cbq_io.cpp"]
+HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-pthread", "-D__HIP_PLATFORM_AMD__=1",
+              "-I/opt/rocm/include", "-Wall"]
 
 
 def hipcc() -> str:
@@ -35,9 +39,8 @@ def sources():
     return [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
 
 
-def command(out: str = SO):
-    """One hipcc line that compiles every source and links the library."""
-    return [hipcc()] + FLAGS + ["-shared", "-pthread", "-o", out] + sources()
+def host_sources():
+    return [os.path.join(CSRC, s) for s in HOST_SOURCES]
 
 
 TIMELINE_SO = os.path.join(HERE, "libcbq_hip_timeline.so")
@@ -78,14 +81,17 @@ def build(verbose: bool = False, jobs: int = 0, out: str = SO, defines=()) -> st
     diagnostic variant)."""
     import tempfile
     from concurrent.futures import ThreadPoolExecutor
-    srcs = sources()
+    srcs = sources() + host_sources()
     jobs = jobs or min(len(srcs), max(1, os.cpu_count() or 1))
     with tempfile.TemporaryDirectory(prefix="cbq_build_") as tmpd:
         objs = [os.path.join(tmpd, os.path.basename(s) + ".o") for s in srcs]
 
         def compile_one(so):
             src, obj = so
-            cmd = [hipcc()] + FLAGS + [f"-D{d}" for d in defines] + ["-c", "-o", obj, src]
+            if src.endswith(".cpp"):
+                cmd = ["g++"] + HOST_FLAGS + [f"-D{d}" for d in defines] + ["-c", "-o", obj, src]
+            else:
+                cmd = [hipcc()] + FLAGS + [f"-D{d}" for d in defines] + ["-c", "-o", obj, src]
             if verbose:
                 print(" ".join(cmd), flush=True)
             return subprocess.run(cmd, capture_output=True, text=True)

@@ -144,7 +144,7 @@ __global__ __launch_bounds__(kGlueBlock) void attn_decode_kernel(
     const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc,
     const int64_t *__restrict__ pos, float *__restrict__ out, int group, int max_len, float scale)
 {
-    extern __shared__ float s_att[];                              // [max_len]
+    extern __shared__ __attribute__((aligned(16))) float s_att[];                              // [max_len]
     __shared__ float s_q[HD];
     __shared__ float s_part[kGlueBlock];
     __shared__ float s_red[kGlueBlock / CBQ_WAVE];
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_rope_decode_kernel(
     float *__restrict__ vc, float *__restrict__ out, int group, int max_len, float scale,
     float eps)
 {
-    extern __shared__ float s_att[];                              // [max_len + 1]
+    extern __shared__ __attribute__((aligned(16))) float s_att[];                              // [max_len + 1]
     __shared__ float s_raw[2][HD];
     __shared__ __attribute__((aligned(16))) float s_q[HD];       // read as float4
     __shared__ __attribute__((aligned(16))) float s_k[HD];

@@ -106,7 +106,7 @@ __global__ __launch_bounds__(kBlock) void fixed_gemv_kernel(
     // lane-private 128-byte global read per lane would cost 64 cache-line
     // lookups per instruction); XREG then copies a lane's 32 values to VGPRs.
     constexpr bool XLDS = XMODE == 1 || XREG;
-    extern __shared__ float lds[];
+    extern __shared__ __attribute__((aligned(16))) float lds[];
     const int G = K >> 5;                          // 32-index groups per row
     float *s_cb = lds;
     float *s_red = lds + ((C + 3) & ~3);           // [kWavesPerBlock][TMAX]
@@ -460,7 +460,7 @@ __global__ __launch_bounds__(kStreamBlock) void fixed_stream_kernel(
 #endif
     __shared__ __attribute__((aligned(16))) float s_cbp[PADDED ? (1 << BITS) : 1];
     __shared__ float s_red16[XMODE >= XF_ADD_RMS ? 16 : 1];
-    extern __shared__ float s_dyn[];
+    extern __shared__ __attribute__((aligned(16))) float s_dyn[];
     const int C_eff = C < (1 << BITS) ? C : (1 << BITS);
     const int cb_slots = AFFINE ? 0 : PADDED ? (1 << BITS) : ((C_eff + 63) & ~63);
     float *s_cb = PADDED ? s_cbp : s_dyn;

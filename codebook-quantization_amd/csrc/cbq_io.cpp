@@ -8,6 +8,7 @@
 
 #include <errno.h>
 #include <fcntl.h>
+#include <sys/stat.h>
 #include <stdio.h>
 #include <string.h>
 #include <unistd.h>
@@ -69,6 +70,22 @@ extern "C" int cbq_file_upload(const char *path, const cbq_upload_part *parts, i
         fprintf(stderr, "cbq_file_upload: cannot open %s: %s\n", path, strerror(errno));
         return CK_ERR_ARG;
     }
+    // every range inside the file, checked before any HIP call
+    struct stat st;
+    if (fstat(fd, &st) != 0) {
+        fprintf(stderr, "cbq_file_upload: cannot stat %s: %s\n", path, strerror(errno));
+        close(fd);
+        return CK_ERR_ARG;
+    }
+    for (int i = 0; i < n_parts; i++)
+        if (parts[i].file_offset > (int64_t)st.st_size ||
+            parts[i].nbytes > (int64_t)st.st_size - parts[i].file_offset) {
+            fprintf(stderr, "cbq_file_upload: range [%lld, +%lld) past the end of %s (%lld bytes)\n",
+                    (long long)parts[i].file_offset, (long long)parts[i].nbytes, path,
+                    (long long)st.st_size);
+            close(fd);
+            return CK_ERR_ARG;
+        }
     const int nw = n_threads < (int)pieces.size() ? n_threads : (int)pieces.size();
     std::vector<Worker> w(nw);
     hipError_t herr = hipSuccess;

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(kTinyThreads) void fixed_tiny_mfma_kernel(
     static_assert(BITS >= 8 && BITS <= 16, "widths with a 4-dword 8-index window");
     // codebook [cs], partials [8][64][4], then per wave kTinyRing slots of
     // 16 rows x 16 words of packed groups
-    extern __shared__ float s_dyn[];
+    extern __shared__ __attribute__((aligned(16))) float s_dyn[];
     const int G = K >> 5;
     const int lane = threadIdx.x & (CBQ_WAVE - 1);
     const int wave = threadIdx.x / CBQ_WAVE;

@@ -52,6 +52,7 @@ def main(argv=None):
           "µs per item after it (p0/p10/p50/p90/p100) | loop end µs (p0/p10/p50/p90/p100) | "
           "waves 0-3 / 4-7 loop end µs | MB | span GB/s |")
     print("|---|---|---|---|---|---|---|---|---|---|")
+    xcd_rows = []
     for name, M, K in SHAPES:
         w = synthetic.make_bf16((M, K), f"timeline.{name}", device=dev)
         cb, lut = cbb.codebook_from_counts_torch(cbb.counts_torch(w))
@@ -96,8 +97,25 @@ def main(argv=None):
               f"{np.median(r[:, 2] - r[:, 1]):.2f} | {pct(per_item)} | {pct(r[:, 3])} | "
               f"{r[half, 3].mean():.2f} / {r[~half, 3].mean():.2f} | {mb:.1f} | "
               f"{mb / span * 1e3:.0f} |", flush=True)
+        # per XCD (block b runs on XCD b % 8): when its blocks start and end
+        blk = np.arange(W) // 8
+        nbk = W // 8
+        b_entry = np.array([r[blk == b, 0].min() for b in range(nbk)])
+        b_end = np.array([r[blk == b, 3].max() for b in range(nbk)])
+        xe = [b_entry[np.arange(nbk) % 8 == k].mean() for k in range(8)]
+        xd = [b_end[np.arange(nbk) % 8 == k].mean() for k in range(8)]
+        corr = float(np.corrcoef(b_entry, b_end)[0, 1]) if nbk > 2 else float("nan")
+        xcd_rows.append(f"| {name} | {' / '.join(f'{v:.2f}' for v in xe)} | "
+                        f"{' / '.join(f'{v:.2f}' for v in xd)} | "
+                        f"{b_end.min():.2f} - {b_end.max():.2f} | {corr:.2f} |")
         del mats
         torch.cuda.empty_cache()
+    print()
+    print("| shape | XCD 0..7 block entry mean µs | XCD 0..7 block loop end mean µs | "
+          "block loop end min - max µs | corr(block entry, block end) |")
+    print("|---|---|---|---|---|")
+    for row in xcd_rows:
+        print(row)
 
 
 if __name__ == "__main__":
