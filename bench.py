@@ -196,6 +196,71 @@ def build_split_formats(torch, dev, huff, names):
     return splits, stream_bytes
 
 
+def stack_gate_up(torch, dev, huff, splits, plan):
+    """Every layer's gate/up pair re-coded as one stacked split matrix under
+    a shared table (the decoder's format for the gate/up launch with the SiLU
+    epilogue); the pair's entries in `splits` become descriptors into it and
+    the stacked pair is stored under ("glu", gate name)."""
+    import numpy as np
+    from gpu_huffman_functions import stack_split
+    for e in plan:
+        if not (isinstance(e, tuple) and e[0].endswith("mlp.gate_proj")):
+            continue
+        g, u = e
+        M, K = huff[g].shape
+        cb = huff[g].tables["codebook"].cpu().numpy()
+        if K % 4096 or huff[u].shape != (M, K) or g not in splits or u not in splits or \
+                not np.array_equal(cb, huff[u].tables["codebook"].cpu().numpy()):
+            continue
+        st = stack_split([splits[g], splits[u]], cb, [M, M], K, dev)
+        if st is None:
+            continue
+        keep, sdesc, parts = st
+        splits[g], splits[u] = (keep, parts[0]), (keep, parts[1])
+        splits[("glu", g)] = (keep, sdesc)
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def stream_gate_up(torch, nat, lib, dev, huff, plan, steps, warmup, layers=8):
+    """The config-3 stream format's fused kernel (cbq_huff_linear_f32, T = 1)
+    on the gate and up matrices of the first `layers` layers, before their
+    streams are freed: mean us per matrix launch and GB/s on the stream's
+    bytes (stream + chunk offsets + sub-block lengths + x + y)."""
+    import ctypes
+    pairs = [e for e in plan if isinstance(e, tuple) and e[0].endswith("mlp.gate_proj")][:layers]
+    mats = [n for e in pairs for n in e]
+    descs, outs = {}, {}
+    for n in mats:
+        t = huff[n]
+        tb = t.tables
+        descs[n] = nat.HuffStream(words=t.words.data_ptr(), n_words=t.words.numel(),
+                                  chunk_off=t.chunk_off.data_ptr(), sub_len=t.sub_len.data_ptr(),
+                                  lut1=tb["lut1"].data_ptr(), lut2=tb["lut2"].data_ptr(),
+                                  n_lut2=tb["lut2"].numel(), canon=tb["canon"].data_ptr(),
+                                  canon_pay=tb["pay"].data_ptr(), value_cb=None,
+                                  C=tb["codebook"].numel(), stage_words=tb["stage_words"])
+        outs[n] = torch.empty(1, t.shape[0], device=dev)
+    K = huff[mats[0]].shape[1]
+    x = torch.randn(1, K, device=dev)
+
+    def run():
+        for n in mats:
+            M = huff[n].shape[0]
+            rc = lib.cbq_huff_linear_f32(x.data_ptr(), ctypes.byref(descs[n]), outs[n].data_ptr(),
+                                         1, M, K, nat.stream_ptr(dev))
+            if rc:
+                raise RuntimeError(f"cbq_huff_linear_f32 rc={rc}")
+    ms, _ = timed_graph(torch, run, steps, warmup)
+    nb = sum(huff[n].nbytes + 4 * K + 4 * huff[n].shape[0] for n in mats)
+    us = ms * 1e3 / len(mats)
+    return {"kernel": "cbq_huff_linear_f32 (stream format, huff_tile_fast_kernel), gate or up "
+                      f"{K}->{huff[mats[0]].shape[0]}",
+            "us_per_launch": round(us, 2), "bytes_per_launch": nb // len(mats),
+            "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+            "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "matrices": len(mats)}
+
+
 def split_launch_args(nat, splits, huff, ns, outs):
     import ctypes
     k = len(ns)
@@ -207,32 +272,46 @@ def split_launch_args(nat, splits, huff, ns, outs):
 def huffman_sweep(torch, nat, lib, dev, huff, splits, plan, steps, warmup):
     """Graph-replayed split-format step (grouped q/k/v and gate/up) ->
     (ms, bytes the kernels stream, per-launch args)."""
+    import ctypes
     from gpu_huffman_functions import split_bytes
     outs, xs, launches = {}, {}, []
+    nbytes = 0
     for e in plan:
         ns = list(e) if isinstance(e, tuple) else [e]
         missing = [n for n in ns if n not in splits]
         if missing:
             raise RuntimeError(f"no split format for {missing}")
+        M, K = huff[ns[0]].shape
+        if K not in xs:
+            xs[K] = torch.randn(1, K, device=dev)
+        glu = splits.get(("glu", ns[0])) if len(ns) == 2 else None
+        if glu is not None:                       # gate/up: one launch, SiLU in the epilogue
+            out = torch.empty(1, M, device=dev)
+            outs[ns[0]] = out
+            launches.append(("glu", glu, out, M, K))
+            nbytes += split_bytes(glu[0]) + 4 * M + 4 * K
+            continue
         for n in ns:
-            M, K = huff[n].shape
-            outs[n] = torch.empty(1, M, device=dev)
-            if K not in xs:
-                xs[K] = torch.randn(1, K, device=dev)
-        launches.append(split_launch_args(nat, splits, huff, ns, outs))
+            outs[n] = torch.empty(1, huff[n].shape[0], device=dev)
+        launches.append(("split",) + split_launch_args(nat, splits, huff, ns, outs))
+        keeps = {id(splits[n][0]): splits[n][0] for n in ns}
+        nbytes += sum(split_bytes(k) for k in keeps.values())
+        nbytes += sum(4 * huff[n].shape[0] for n in ns) + 4 * K
 
     def run():
-        for k, mats, out_a, m_a, K in launches:
-            rc = lib.cbq_split_linear_f32(xs[K].data_ptr(), None, None, 0, 0.0, k, mats, out_a,
-                                          m_a, K, nat.stream_ptr(dev))
+        for a in launches:
+            if a[0] == "glu":
+                _, glu, out, M, K = a
+                rc = lib.cbq_split_linear_glu_f32(xs[K].data_ptr(), None, None, 0, 0.0,
+                                                  ctypes.byref(glu[1]), out.data_ptr(), M, K,
+                                                  nat.stream_ptr(dev))
+            else:
+                _, k, mats, out_a, m_a, K = a
+                rc = lib.cbq_split_linear_f32(xs[K].data_ptr(), None, None, 0, 0.0, k, mats,
+                                              out_a, m_a, K, nat.stream_ptr(dev))
             if rc:
                 raise RuntimeError(f"split GEMV rc={rc}")
     ms, _ = timed_graph(torch, run, steps, warmup)
-    nbytes = 0
-    for e in plan:
-        ns = list(e) if isinstance(e, tuple) else [e]
-        nbytes += sum(split_bytes(splits[n][0]) + 4 * huff[n].shape[0] for n in ns)
-        nbytes += 4 * huff[ns[0]].shape[1]
     return ms, nbytes
 
 
@@ -515,7 +594,7 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
     splits, stream_bytes = build_split_formats(torch, dev, huff, names)
     ms1, nb1 = huffman_sweep(torch, nat, lib, dev, huff, splits, plan, args.steps, args.warmup)
     n_w = sum(huff[n].shape[0] * huff[n].shape[1] for n in names)
-    res_b = sum(split_bytes(splits[n][0]) for n in names)
+    res_b = sum(split_bytes(k) for k in {id(splits[n][0]): splits[n][0] for n in names}.values())
     hu = {"T1": {"ms_per_step": round(ms1, 4), "GB/s": round(nb1 / (ms1 * 1e-3) / 1e9, 1),
                  "pct_of_hbm_peak": round(100 * nb1 / (ms1 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1),
                  "stream_equivalent_GB/s": round(sum(stream_bytes.values()) / (ms1 * 1e-3) / 1e9,
@@ -855,28 +934,35 @@ def main():
         from gpu_huffman_functions import split_bytes
         t0 = time.time()
         huff = dec.build_huffman(tensors)
+        stream_k = stream_gate_up(torch, nat, lib, dev, huff, plan, args.steps, args.warmup)
+        log(f"stream-format gate/up: {stream_k['us_per_launch']} us per matrix, "
+            f"{stream_k['GB/s']} GB/s")
         splits, stream_bytes = build_split_formats(torch, dev, huff, names)
+        stack_gate_up(torch, dev, huff, splits, plan)
         log(f"built {len(huff)} Huffman tensors, {len(splits)} split formats, in "
             f"{time.time() - t0:.1f}s")
         ms_h, sbytes = huffman_sweep(torch, nat, lib, dev, huff, splits, plan, args.steps,
                                      args.warmup)
         hbytes = sum(stream_bytes.values())
         n_w = sum(h.shape[0] * h.shape[1] for h in huff.values())
-        res_b = sum(split_bytes(splits[n][0]) for n in names)
+        res_b = sum(split_bytes(k) for k in {id(splits[n][0]): splits[n][0]
+                                            for n in names}.values())
         gate_up = [e for e in plan if isinstance(e, tuple) and e[0].endswith("mlp.gate_proj")]
         ms_gg, b_gg = huffman_sweep(torch, nat, lib, dev, huff, splits, gate_up, args.steps,
                                     args.warmup)
         us_gg = ms_gg * 1e3 / len(gate_up)
         b_gg //= len(gate_up)
         s_gg = sum(stream_bytes[n] for n in gate_up[0]) + 4 * (
-            sum(huff[n].shape[0] for n in gate_up[0]) + huff[gate_up[0][0]].shape[1])
+            huff[gate_up[0][0]].shape[0] + huff[gate_up[0][0]].shape[1])
         ach = b_gg / (us_gg * 1e-6) / 1e9
         result["huffman"] = {
             "value": round(sbytes / (ms_h * 1e-3) / 1e9, 1), "unit": "GB/s",
             "ms_per_step": round(ms_h, 4), "bytes_per_step": sbytes,
             "format": "split (raw low byte of bf16, <=7-bit Huffman code of the high byte), "
                       "built on the GPU from each matrix's canonical-Huffman index stream, "
-                      "which is then freed: the only resident format",
+                      "which is then freed: the only resident format; each layer's gate/up "
+                      "pair stacked under one shared table",
+            "stream_format_kernel": stream_k,
             "stream_bytes_per_step": hbytes,
             "stream_equivalent_GB/s": round(hbytes / (ms_h * 1e-3) / 1e9, 1),
             "launches_per_step": len(plan),
@@ -889,10 +975,11 @@ def main():
                 "stream_equivalent_achieved": round(s_gg / (us_gg * 1e-6) / 1e9, 1),
                 "stream_equivalent_frac": round(s_gg / (us_gg * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
                 "traffic": read_traffic("split_gemv_kernel_gate_up_qwen3-8b_pmc.md"),
-                "kernel": "split_gemv_kernel<16> grouped gate+up, 2 x 4096->12288 in one launch",
+                "kernel": "split_gemv_kernel<16,glu> stacked gate+up under one table, "
+                          "4096->2x12288, silu(gate)*up in the epilogue",
                 "bytes_per_launch": b_gg, "us_per_launch": round(us_gg, 2)}}
         log(f"huffman sweep (split format): {ms_h:.3f} ms/step, {sbytes / 1e9:.2f} GB/step; "
-            f"grouped gate+up {us_gg:.2f} us; {8.0 * res_b / n_w:.3f} bits/weight resident")
+            f"stacked gate+up {us_gg:.2f} us; {8.0 * res_b / n_w:.3f} bits/weight resident")
         del huff, splits
         torch.cuda.empty_cache()
 

@@ -98,6 +98,8 @@ SIGNATURES = {
     "cbq_split_pack": (_i, [_vp, _i64, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
     "cbq_split_linear_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _i, _vp, _vp, _vp, _i,
                                   _vp]),
+    "cbq_split_linear_glu_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float,
+                                      ctypes.POINTER(SplitMatrix), _vp, _i, _i, _vp]),
     "cbq_linear_xform_argmax_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _vp, _vp, _vp, _i,
                                          _i, _i, _i, _vp, ctypes.c_size_t, _vp, _vp, _vp, _i64,
                                          _i64, _vp]),

@@ -177,7 +177,13 @@ __device__ __forceinline__ float split_decode(const uint32_t (&raw)[16], const u
 // per phase p as before.  Lane l's sub-block lies in row (p * 4096 + 64 l) / K
 // of the group (K % 64 == 0), and a chunk's dot products are summed per row
 // with masked wave sums.  GR = 1 (K % 4096 == 0) is the plain row walk.
-template <int NW, int XMODE, int GR, int NJ = 16>
+//
+// GLU (GR = 1, one segment): the segment's matrix holds 2M rows, gate rows
+// [0, M) then up rows [M, 2M), under one code table; a wave takes gate row j
+// and up row j as consecutive items and writes out[j] = silu(gate_j . x) *
+// (up_j . x), rounded as silu_mul_value, so the down projection stages
+// plain x.  Each product sums exactly as the plain launch does.
+template <int NW, int XMODE, int GR, int NJ = 16, bool GLU = false>
 __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *__restrict__ x,
                                                                    SplitSegs segs, int K,
                                                                    const float *__restrict__ x1,
@@ -186,6 +192,8 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
                                                                    float *__restrict__ arg_v,
                                                                    int *__restrict__ arg_i)
 {
+    static_assert(!GLU || (GR == 1 && XMODE != XF_SILU), "gate/up pairs: whole-chunk rows");
+    constexpr int NI = GLU ? 2 : 1;                    // items per output row
     int sidx = 0;
 #pragma unroll
     for (int i = 1; i < kSMaxSeg; i++)
@@ -212,7 +220,8 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
     const float *const xr = s_x + lane * 64;
     const int xsw = (lane & 15) << 2;
     auto chunk_of = [&](int seg, int p, int b, uint32_t &r0, uint32_t &H) {
-        const int64_t row = wid + (int64_t)(seg * 64 + b) * W;
+        // item b: output row seg * 64 + b / NI of this wave (GLU: odd b the up row)
+        const int64_t row = wid + (int64_t)(seg * 64 + b / NI) * W + (GLU && (b & 1) ? M : 0);
         const int64_t c = __builtin_amdgcn_readfirstlane((int)(row * R + p));
         r0 = S.row_off[c];
         H = S.row_off[c + 1] - r0;
@@ -314,7 +323,9 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
         float res[GR];
 #pragma unroll
         for (int q = 0; q < GR; q++) res[q] = 0.f;
+        float res_u = 0.f;                         // GLU: up sums, lane = row % 64
         const int seg_rows = min(64, rows - seg * 64);
+        const int seg_items = seg_rows * NI;
         for (int p = 0; p < R; p++) {
             if (seg == 0 && p == 0) {
                 // every prologue load but the first chunk's has landed (they
@@ -367,7 +378,13 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
             const int q_lo = p * kSChunk / K, q_hi = (p * kSChunk + kSChunk - 1) / K;
             const int q_me = (p * kSChunk + lane * kSSub) / K;
             auto add_rows = [&](float acc, int b) {
-                if constexpr (GR == 1) {
+                if constexpr (GLU) {
+                    const float s = wave_sum(acc);
+                    if (lane == (b >> 1)) {
+                        if (b & 1) res_u += s;
+                        else res[0] += s;
+                    }
+                } else if constexpr (GR == 1) {
                     const float s = wave_sum(acc);
                     if (lane == b) res[0] += s;
                 } else {
@@ -381,19 +398,19 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
             };
             // The slot is rewritten only after the previous item's reads (LDS
             // operations of a wave complete in order).
-            if (seg_rows > 0 && (seg > 0 || p > 0)) {
+            if (seg_items > 0 && (seg > 0 || p > 0)) {
                 const int64_t c = chunk_of(seg, p, 0, rA, hA);
                 split_load(A, S, c, rA, hA, lane);
             }
-            for (int b = 0; b < seg_rows; b += 2) {
-                if (b + 1 < seg_rows) {
+            for (int b = 0; b < seg_items; b += 2) {
+                if (b + 1 < seg_items) {
                     const int64_t c = chunk_of(seg, p, b + 1, rB, hB);
                     split_load(B, S, c, rB, hB, lane);
                 }
                 split_stage(A, hA, s_slot, lane);
                 add_rows(split_decode(A.raw, s_lds, lane_addr, xr, xsw), b);
-                if (b + 1 >= seg_rows) break;
-                if (b + 2 < seg_rows) {
+                if (b + 1 >= seg_items) break;
+                if (b + 2 < seg_items) {
                     const int64_t c = chunk_of(seg, p, b + 2, rA, hA);
                     split_load(A, S, c, rA, hA, lane);
                 }
@@ -401,7 +418,10 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
                 add_rows(split_decode(B.raw, s_lds, lane_addr, xr, xsw), b + 1);
             }
         }
-        if (lane < seg_rows) {
+        if (GLU && lane < seg_rows) {
+            const int64_t g = wid + (int64_t)(seg * 64 + lane) * W;
+            S.out[g] = silu_mul_value(res[0], res_u);
+        } else if (!GLU && lane < seg_rows) {
             const int64_t g = wid + (int64_t)(seg * 64 + lane) * W;
 #pragma unroll
             for (int q = 0; q < GR; q++) {
@@ -675,20 +695,66 @@ int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits
 namespace {
 
 // Norm modes with K <= 4096 hold 4 of GlueTile's 16 terms per virtual thread.
-template <int NW, int XMODE, int GR>
+template <int NW, int XMODE, int GR, bool GLU = false>
 void launch_split_gemv(int blocks, hipStream_t stream, const float *x, const SplitSegs &segs,
                        int K, const float *x1, float *h_out, float eps, float *arg_v, int *arg_i)
 {
     if constexpr (XMODE == XF_ADD_RMS || XMODE == XF_RMS) {
         if (K <= 4096) {
-            hipLaunchKernelGGL((split_gemv_kernel<NW, XMODE, GR, 4>), dim3(blocks),
+            hipLaunchKernelGGL((split_gemv_kernel<NW, XMODE, GR, 4, GLU>), dim3(blocks),
                                dim3(NW * CBQ_WAVE), 0, stream, x, segs, K, x1, h_out, eps, arg_v,
                                arg_i);
             return;
         }
     }
-    hipLaunchKernelGGL((split_gemv_kernel<NW, XMODE, GR>), dim3(blocks), dim3(NW * CBQ_WAVE), 0,
-                       stream, x, segs, K, x1, h_out, eps, arg_v, arg_i);
+    hipLaunchKernelGGL((split_gemv_kernel<NW, XMODE, GR, 16, GLU>), dim3(blocks),
+                       dim3(NW * CBQ_WAVE), 0, stream, x, segs, K, x1, h_out, eps, arg_v, arg_i);
+}
+
+// One stacked [gate; up] matrix (2M rows, one code table), out[j] =
+// silu(gate_j . x) * (up_j . x); K % 4096 == 0.
+int split_linear_glu(const float *x, const float *x1, float *h_out, int mode, float eps,
+                     const cbq_split_matrix *m, float *out, int M, int K, hipStream_t stream)
+{
+    if (!x || !m || !out || M <= 0 || M > (1 << 29) || K <= 0 || K % kSChunk != 0)
+        return CK_ERR_ARG;
+    if (mode != XF_NONE && mode != XF_ADD_RMS && mode != XF_RMS) return CK_ERR_ARG;
+    if ((mode == XF_ADD_RMS && !x1) || (mode != XF_NONE && K > 16384)) return CK_ERR_ARG;
+    if (!m->cwords || !m->row_off || !m->raw || !m->lut ||
+        m->n_chunks * kSChunk != 2 * (int64_t)M * K)
+        return CK_ERR_ARG;
+    if (((uintptr_t)m->raw & 15) != 0 || ((uintptr_t)m->lut & 15) != 0 ||
+        ((uintptr_t)m->cwords & 15) != 0)
+        return CK_ERR_ARG;
+    SplitSegs segs = {};
+    segs.n = 1;
+    SplitSeg &g = segs.s[0];
+    g.cwords = m->cwords;
+    g.row_off = m->row_off;
+    g.raw = m->raw;
+    g.lut = m->lut;
+    g.out = out;
+    g.M = M;                                       // outputs: pairs of rows
+    const int cus = cbq_num_cus();
+    const int per = M / cus;                       // pairs per CU (two items each)
+    const int nw = per >= 8 ? 16 : per >= 4 ? 8 : 4;
+    g.block0 = 0;
+    g.nblocks = std::max(1, std::min(cus, (M + nw - 1) / nw));
+#define CBQ_GLU(NWV, MODE)                                                                        \
+    launch_split_gemv<NWV, MODE, 1, true>(g.nblocks, stream, x, segs, K, x1, h_out, eps, nullptr, \
+                                          nullptr)
+#define CBQ_GLU_MODES(NWV)                                                                        \
+    do {                                                                                          \
+        if (mode == XF_ADD_RMS) CBQ_GLU(NWV, XF_ADD_RMS);                                         \
+        else if (mode == XF_RMS) CBQ_GLU(NWV, XF_RMS);                                            \
+        else CBQ_GLU(NWV, XF_NONE);                                                               \
+    } while (0)
+    if (nw == 4) CBQ_GLU_MODES(4);
+    else if (nw == 8) CBQ_GLU_MODES(8);
+    else CBQ_GLU_MODES(16);
+#undef CBQ_GLU_MODES
+#undef CBQ_GLU
+    return cbq_launch_status("split_gemv_kernel<glu>");
 }
 
 // cbq_split_linear_f32, with the greedy-pick pairs of every block written to
@@ -777,6 +843,13 @@ int cbq_split_linear_f32(const float *x, const float *x1, float *h_out, int mode
 {
     return split_linear(x, x1, h_out, mode, eps, n, mats, outs, Ms, K, nullptr, nullptr, nullptr,
                         stream);
+}
+
+int cbq_split_linear_glu_f32(const float *x0, const float *x1, float *h_out, int mode, float eps,
+                             const cbq_split_matrix *m, float *out, int M, int K,
+                             hipStream_t stream)
+{
+    return split_linear_glu(x0, x1, h_out, mode, eps, m, out, M, K, stream);
 }
 
 int cbq_split_linear_argmax_f32(const float *x0, const float *x1, float *h_out, int mode,

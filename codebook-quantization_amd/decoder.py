@@ -433,7 +433,7 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
     import synthetic
     from gpu_huffman_functions import (SymbolDecoder, build_split, huffman_prefill,
                                        split_bytes, split_eligible, split_inverse,
-                                       split_prefill)
+                                       split_prefill, stack_split)
     lib = nat.load()
     dev = torch.device(device)
     resident: Dict[str, int] = {}               # device bytes of each matrix's format
@@ -619,7 +619,11 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
     def huff_group(ts, name):
         """One grouped split-GEMV launch for matrices sharing x (q/k/v,
         gate/up), each with its own code; None when a part has no split
-        format (the parts then run one by one)."""
+        format (the parts then run one by one).  gate/up of one codebook with
+        K % 4096 == 0 are re-coded as one stacked matrix under a shared table
+        (the only resident copy; the parts point into it), which adds the
+        one-launch gate/up with the SiLU product in its epilogue
+        (`xform_glu`)."""
         K = ts[0].shape[1]
         presplit = all(isinstance(t, synthetic.SplitTensor) for t in ts)
         if any(t.shape[1] != K for t in ts) or not (split or presplit):
@@ -628,6 +632,28 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
         if not all(sp is not None for sp in sps):
             return None
         Ms = [t.shape[0] for t in ts]
+        glu = None
+        cbs = [cb_of(t).cpu().numpy() for t in ts]
+        if (name.endswith("gate_up_proj") and len(ts) == 2 and Ms[0] == Ms[1]
+                and K % 4096 == 0 and np.array_equal(cbs[0], cbs[1])):
+            st = stack_split(sps, cbs[0], Ms, K, dev)
+            if st is not None:
+                keep, sdesc, parts = st
+                sps = [(keep, parts[0]), (keep, parts[1])]
+                for t in ts:
+                    resident.pop(t.name, None)
+                resident[name] = split_bytes(keep)
+                M = Ms[0]
+
+                def glu(x0, x1, h_out, mode, keep=(keep, sdesc)):
+                    """silu(gate . x) * (up . x), x = transform(x0, x1), one launch."""
+                    out = torch.empty(1, M, device=dev)
+                    nat.check(lib.cbq_split_linear_glu_f32(
+                        x0.data_ptr(), None if x1 is None else x1.data_ptr(),
+                        None if h_out is None else h_out.data_ptr(), mode, cfg.eps,
+                        ctypes.byref(sdesc), out.data_ptr(), M, K, nat.stream_ptr(dev)),
+                        "cbq_split_linear_glu_f32")
+                    return out
         one, sxform = split_fns(sps, Ms, K)
         singles = [split_linear(sp, t.shape[0], K, cb_of(t))   # batched tokens
                    for t, sp in zip(ts, sps)]
@@ -639,6 +665,8 @@ def from_synthetic(cfg: DecoderConfig, tensors: Dict[str, object], device="cuda"
             return one(x)
         g.xform = sxform
         g.name = name
+        if glu is not None:
+            g.xform_glu = glu
         return g
 
     def embed_fn(t):

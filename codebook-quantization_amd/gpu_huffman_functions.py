@@ -366,6 +366,34 @@ def split_indices(split, inv: torch.Tensor, n: int, device) -> torch.Tensor:
     return out
 
 
+def stack_split(splits, codebook: np.ndarray, Ms, K: int, device):
+    """One split-format matrix of the row-stacked matrices `splits` (same
+    codebook, same K), coded with one table built from their combined
+    high-byte counts, so a single launch (cbq_split_linear_glu_f32) serves
+    them all.  Returns (keep, stacked descriptor, part descriptors) -- the
+    part descriptors point into the stacked arrays (row offsets and raw
+    bytes offset by the parts before them), so the stacked matrix is the
+    only resident copy -- or None when the shared code would need codes
+    longer than 7 bits."""
+    inv = split_inverse(codebook, device)
+    idx = torch.cat([split_indices(sp, inv, M * K, device) for sp, M in zip(splits, Ms)])
+    st = build_split(idx, codebook, device)
+    del idx
+    if st is None:
+        return None
+    keep, desc = st
+    cwords, row_off, raw, lut = keep
+    parts = []
+    c0 = 0
+    for M in Ms:
+        n_ch = M * K // hc.CHUNK_SYMBOLS
+        parts.append(nat.SplitMatrix(cwords=cwords.data_ptr(), row_off=row_off.data_ptr() + 4 * c0,
+                                     raw=raw.data_ptr() + c0 * hc.CHUNK_SYMBOLS,
+                                     lut=lut.data_ptr(), n_chunks=n_ch))
+        c0 += n_ch
+    return keep, desc, parts
+
+
 def columns_eligible(desc: "nat.HuffStream", K: int) -> bool:
     """The column GEMV serves T = 1 rows of whole 4096-symbol chunks with
     bf16-value payloads and a second table level that fits its LDS."""

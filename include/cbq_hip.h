@@ -348,6 +348,20 @@ int cbq_split_linear_f32(const float *x0, const float *x1, float *h_out, int mod
                          const cbq_split_matrix *const *mats, float *const *outs, const int *Ms,
                          int K, hipStream_t stream);
 
+/* The gated MLP's gate and up projections in one launch over the split
+ * format, with the SiLU product in the epilogue: m holds 2M rows, gate_proj's
+ * M rows then up_proj's, coded with one shared table (the two matrices share
+ * their category codebook), and out[j] = silu(gate_j . x) * (up_j . x) for
+ * j < M, x = transform(x0, x1) (mode 0, CBQ_XF_ADD_RMS or CBQ_XF_RMS).  Each
+ * product sums as cbq_split_linear_f32 does and the SiLU product rounds as
+ * cbq_silu_mul_f32, so out equals those calls bit for bit.  K % 4096 == 0;
+ * K <= 16384 for the norms.  Replaces the reference's separate gate_proj /
+ * up_proj Huffman module calls and HF's act_fn(gate) * up
+ * (src/gpu_huffman_functions.py:834-855 inside HF's Qwen3MLP). */
+int cbq_split_linear_glu_f32(const float *x0, const float *x1, float *h_out, int mode, float eps,
+                             const cbq_split_matrix *m, float *out, int M, int K,
+                             hipStream_t stream);
+
 /* Decode flat symbols [0, n_symbols) to int32 with the chunked kernel (lut
  * payloads must be raw symbols).  The bit-exact check of the fused decoder;
  * the equivalent of huffman_decode_to_weights_f32 with an identity codebook

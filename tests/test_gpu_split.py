@@ -256,3 +256,76 @@ def test_split_decode_indices_exact(cuda, oracle):
         x = rng.standard_normal((T, K)).astype(np.float32)
         y = lin(torch.from_numpy(x).to(cuda)).cpu().numpy()
         assert rel_l2(y, oracle.huff_gemv(x, enc, cb, M, K, chunk_rows=None)) <= 1e-5, T
+
+
+@pytest.mark.parametrize("M,K", [(12288, 4096),      # 8B gate/up shape (reduced to 1 layer's)
+                                 (1003, 4096),       # ragged pair count
+                                 (40, 8192)])        # fewer pairs than waves, two chunks a row
+def test_stacked_glu_equals_split_then_silu(cuda, oracle, M, K):
+    """cbq_split_linear_glu_f32 over a [gate; up] pair re-coded under one
+    shared table (stack_split) equals the two matrices' own split GEMVs
+    followed by cbq_silu_mul_f32, bit for bit, for plain x and both folded
+    norms; the part descriptors into the stacked arrays give each matrix's
+    own outputs bit for bit; plain x agrees with the oracle's C GEMVs."""
+    from gpu_huffman_functions import stack_split, split_indices, split_inverse
+    lib = nat.load()
+    st = nat.stream_ptr(cuda)
+    import bitpack
+    import codebook_builder as cbb
+    # one codebook for both matrices, as the MLP category's
+    ws = [synthetic.make_bf16((M, K), f"glu.{nm}.{M}x{K}", device=cuda) for nm in ("gate", "up")]
+    cbt, lut = cbb.codebook_from_counts_torch(cbb.counts_torch(ws[0]) + cbb.counts_torch(ws[1]))
+    cb = cbt.cpu().numpy()
+    bits = cbb.bits_for(cb.size)
+    sps, idxs = [], []
+    for wb in ws:
+        idx = lut[cbb.patterns_torch(wb).reshape(-1).to(torch.int64)].to(torch.int32)
+        sp = build_split(idx, cb, cuda)
+        assert sp is not None
+        sps.append(sp)
+        idxs.append(idx.cpu().numpy())
+    del ws
+    keep, sdesc, parts = stack_split(sps, cb, [M, M], K, cuda)
+    inv = split_inverse(cb, cuda)
+    for i in range(2):                            # parts decode to each matrix's indices
+        got = split_indices((keep, parts[i]), inv, M * K, cuda).cpu().numpy()
+        assert np.array_equal(got, idxs[i])
+    gen = torch.Generator(device=cuda).manual_seed(M + K)
+
+    def silu_mul(g, u):
+        out = torch.empty(1, M, device=cuda)
+        nat.check(lib.cbq_silu_mul_f32(g.data_ptr(), u.data_ptr(), out.data_ptr(), M, st),
+                  "cbq_silu_mul_f32")
+        return out
+
+    def glu(x, d, h_out, mode):
+        out = torch.full((1, M), float("nan"), device=cuda)
+        nat.check(lib.cbq_split_linear_glu_f32(
+            x.data_ptr(), None if d is None else d.data_ptr(),
+            None if h_out is None else h_out.data_ptr(), mode, 1e-6, ctypes.byref(sdesc),
+            out.data_ptr(), M, K, st), "cbq_split_linear_glu_f32")
+        return out
+
+    for mode in (0, nat.XF_RMS, nat.XF_ADD_RMS):
+        h = torch.randn(1, K, device=cuda, generator=gen) * 2
+        d = torch.randn(1, K, device=cuda, generator=gen) if mode == nat.XF_ADD_RMS else None
+        h1 = torch.full_like(h, float("nan"))
+        yg = _split(lib, h, [sps[0]], [M], K, mode, d, h1 if d is not None else None)
+        yu = _split(lib, h, [sps[1]], [M], K, mode, d, None)
+        # the part descriptors (shared table) give the same outputs
+        both = _split(lib, h, [(keep, parts[0]), (keep, parts[1])], [M, M], K, mode, d, None)
+        assert torch.equal(both[:, :M], yg) and torch.equal(both[:, M:], yu), mode
+        want = silu_mul(yg, yu)
+        h2 = torch.full_like(h, float("nan"))
+        got = glu(h, d, h2 if d is not None else None, mode)
+        assert torch.equal(got, want), mode
+        if d is not None:
+            assert torch.equal(h1, h2)
+        if mode == 0:
+            xs = h.cpu().numpy()
+            gref = oracle.fixed_gemv(xs, bitpack.pack_any_bits(idxs[0], bits), cb, M, K, bits)
+            uref = oracle.fixed_gemv(xs, bitpack.pack_any_bits(idxs[1], bits), cb, M, K, bits)
+            g64, u64 = gref.astype(np.float64), uref.astype(np.float64)
+            ref = g64 / (1.0 + np.exp(-g64)) * u64
+            rel = float(np.linalg.norm(got.cpu().numpy() - ref) / np.linalg.norm(ref))
+            assert rel <= 1e-5, rel
