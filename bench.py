@@ -60,6 +60,25 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
+class mark:
+    """A named range around a bench section (roctx through torch.cuda.nvtx),
+    so a `rocprofv3 --kernel-trace --marker-trace` run attributes every
+    kernel dispatch to the section that launched it."""
+
+    def __init__(self, name):
+        self.name = name
+
+    def __enter__(self):
+        import torch
+        torch.cuda.nvtx.range_push("bench:" + self.name)
+        return self
+
+    def __exit__(self, *exc):
+        import torch
+        torch.cuda.nvtx.range_pop()
+        return False
+
+
 def fixed_bytes(M, K, bits, C, T=1):
     return (M * K * bits + 7) // 8 + 4 * C + T * K * 4 + T * M * 4
 
@@ -573,7 +592,8 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
     mats = fixed_launches(torch, nat, lib, dev, synthetic, fixed, plan)
     fx = {}
     for T in (1, 4, 16):
-        ms, nb = fixed_sweep(torch, nat, lib, dev, mats, T, args.steps, args.warmup)
+        with mark(f"1p7b:fixed:sweep:T{T}"):
+            ms, nb = fixed_sweep(torch, nat, lib, dev, mats, T, args.steps, args.warmup)
         fx[f"T{T}"] = {"ms_per_step": round(ms, 4), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
                        "pct_of_hbm_peak": round(100 * nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1)}
     per = {}
@@ -581,18 +601,32 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
                       ("o_proj", "self_attn.o_proj"), ("gate_proj", "mlp.gate_proj"),
                       ("down_proj", "mlp.down_proj")):
         ms_k = [fixed[n] for n in names if n.endswith(sel)]
-        ms, nb = fixed_sweep(torch, nat, lib, dev, ms_k, 1, max(3, args.steps // 2), 1)
+        with mark(f"1p7b:fixed:{kind}"):
+            ms, nb = fixed_sweep(torch, nat, lib, dev, ms_k, 1, max(3, args.steps // 2), 1)
         t = ms_k[0]
         per[kind] = {"shape": f"{t.shape[1]}->{t.shape[0]}",
                      "us_per_launch": round(ms * 1e3 / len(ms_k), 2),
                      "GB/s": round(nb / (ms * 1e-3) / 1e9, 1)}
-    out["fixed"] = {"sweep": fx, "per_shape_T1": per}
+    # the config's dominant launch: stacked gate+up (2 x 2048->6144), one token
+    gu = [m for m in mats if m.shape[0] == 2 * dec.cfg["inter"] and "+stacked" in m.name]
+    with mark("1p7b:fixed:gate_up_stacked"):
+        ms, nb = fixed_sweep(torch, nat, lib, dev, gu, 1, args.steps, args.warmup)
+    us = ms * 1e3 / len(gu)
+    ach = nb / len(gu) / (us * 1e-6) / 1e9
+    roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBPS, 4),
+            "kernel": f"fixed_stream_kernel<{gu[0].bits},1,f32> stacked gate+up "
+                      f"{gu[0].shape[1]}->{gu[0].shape[0]}",
+            "bytes_per_launch": nb // len(gu), "us_per_launch": round(us, 2)}
+    out["fixed"] = {"sweep": fx, "per_shape_T1": per, "roofline": roof}
     del fixed, mats
     torch.cuda.empty_cache()
 
     huff = dec.build_huffman(tensors)
     splits, stream_bytes = build_split_formats(torch, dev, huff, names)
-    ms1, nb1 = huffman_sweep(torch, nat, lib, dev, huff, splits, plan, args.steps, args.warmup)
+    with mark("1p7b:huffman:sweep:T1"):
+        ms1, nb1 = huffman_sweep(torch, nat, lib, dev, huff, splits, plan, args.steps,
+                                 args.warmup)
     n_w = sum(huff[n].shape[0] * huff[n].shape[1] for n in names)
     res_b = sum(split_bytes(k) for k in {id(splits[n][0]): splits[n][0] for n in names}.values())
     hu = {"T1": {"ms_per_step": round(ms1, 4), "GB/s": round(nb1 / (ms1 * 1e-3) / 1e9, 1),
@@ -603,14 +637,23 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
     for kind, sel in (("qkv_grouped", "self_attn.q_proj"), ("o_proj", "self_attn.o_proj"),
                       ("gate_up_grouped", "mlp.gate_proj"), ("down_proj", "mlp.down_proj")):
         sub = [e for e in plan if (e[0] if isinstance(e, tuple) else e).endswith(sel)]
-        ms_k, nb_k = huffman_sweep(torch, nat, lib, dev, huff, splits, sub,
-                                   max(3, args.steps // 2), 1)
+        with mark(f"1p7b:huffman:{kind}"):
+            ms_k, nb_k = huffman_sweep(torch, nat, lib, dev, huff, splits, sub,
+                                       max(3, args.steps // 2), 1)
         e0 = sub[0]
         ns0 = list(e0) if isinstance(e0, tuple) else [e0]
         per_h[kind] = {"shape": " + ".join(f"{huff[n].shape[1]}->{huff[n].shape[0]}"
                                            for n in ns0),
                        "us_per_launch": round(ms_k * 1e3 / len(sub), 2),
                        "GB/s": round(nb_k / (ms_k * 1e-3) / 1e9, 1)}
+        if kind == "gate_up_grouped":
+            ach = nb_k / len(sub) / (ms_k * 1e3 / len(sub) * 1e-6) / 1e9
+            hu["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
+                              "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
+                              "kernel": "split_gemv_kernel grouped gate+up (2 x 2048->6144, "
+                                        "row groups of 2)",
+                              "bytes_per_launch": nb_k // len(sub),
+                              "us_per_launch": round(ms_k * 1e3 / len(sub), 2)}
     hu["per_shape_T1"] = per_h
     invs = {}
     for T in (4, 16):
@@ -629,17 +672,14 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
                 M, K = t.shape
                 split_prefill(splits[n], invs[id(t.tables["codebook"])], xs[K], M, K,
                               t.tables["codebook"])
-        run()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        reps = max(2, args.steps // 4)
-        for _ in range(reps):
-            run()
-        torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / reps
+        with mark(f"1p7b:huffman:sweep:T{T}"):
+            ms, _ = timed_graph(torch, run, max(3, args.steps // 2), 1)
         hu[f"T{T}"] = {"ms_per_step": round(ms, 3),
-                       "note": "transient fixed-width decode + ck_linear_f32 per matrix, "
-                               "eager launches with allocations (not graph-captured)"}
+                       "vs_T1": round(ms / ms1, 3),
+                       "note": "per matrix: the split format decoded to a transient "
+                               "fixed-width stream (cbq_split_to_packed) and ck_linear_f32's "
+                               "kernels over it; graph-replayed (transients from the graph's "
+                               "pool)"}
     out["huffman"] = {"sweep": hu, "bits_per_weight_resident": round(8.0 * res_b / n_w, 3),
                       "bits_per_weight_stream_incl_index":
                           round(8.0 * sum(stream_bytes.values()) / n_w, 3)}
@@ -794,6 +834,30 @@ def e2e_section(torch, dec, args):
     return out
 
 
+def roofline_only(torch, nat, lib, dev, dec, tensors, names, plan, mats, args):
+    """The two roofline launches alone, for counter runs: the fixed-width
+    stacked gate+up graph (36 launches) and the Huffman stacked gate+up graph
+    with the SiLU epilogue (36 launches); prints their mean times."""
+    gus = [m for m in mats if m.shape[0] == 2 * dec.cfg["inter"] and "+stacked" in m.name]
+    with mark("fixed:gate_up_stacked:T1"):
+        ms_gu, nb = fixed_sweep(torch, nat, lib, dev, gus, 1, args.steps, args.warmup)
+    out = {"fixed_gate_up_us": round(ms_gu * 1e3 / len(gus), 2),
+           "fixed_gate_up_bytes": nb // len(gus), "fixed_launches": len(gus)}
+    del mats, gus
+    torch.cuda.empty_cache()
+    huff = dec.build_huffman(tensors)
+    splits, _ = build_split_formats(torch, dev, huff, names)
+    stack_gate_up(torch, dev, huff, splits, plan)
+    gate_up = [e for e in plan if isinstance(e, tuple) and e[0].endswith("mlp.gate_proj")]
+    with mark("huffman:gate_up_glu"):
+        ms_gg, b_gg = huffman_sweep(torch, nat, lib, dev, huff, splits, gate_up, args.steps,
+                                    args.warmup)
+    out.update({"huffman_gate_up_glu_us": round(ms_gg * 1e3 / len(gate_up), 2),
+                "huffman_gate_up_glu_bytes": b_gg // len(gate_up),
+                "huffman_launches": len(gate_up)})
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -815,6 +879,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--copy-probe", type=int, default=0,
                     help="only run a plain device copy of this many MiB (PMC calibration)")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the two roofline launches (fixed-width stacked gate+up, Huffman "
+                         "stacked gate+up with the SiLU epilogue) and their JSON (PMC runs)")
+    ap.add_argument("--only-1p7b", action="store_true",
+                    help="only the configs 2/3 (1.7B) sweeps and their JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the compressed GEMV "
@@ -838,6 +907,11 @@ def main():
         print(json.dumps({"copy_probe_bytes": a.numel()}))
         return
 
+    if args.only_1p7b:
+        print(json.dumps({"qwen3_1_7b": sweep_1p7b(torch, nat, lib, dev, synthetic, args)}),
+              flush=True)
+        return
+
     dec = synthetic.SyntheticDecoder(args.config, layers=args.layers, log=log)
     tensors = dec.all_linears()
     names = [n for n, _, _ in tensors]
@@ -856,7 +930,12 @@ def main():
 
     plan = step_plan(dec)
     mats = fixed_launches(torch, nat, lib, dev, synthetic, fixed, plan)
-    ms_step, step_bytes = fixed_sweep(torch, nat, lib, dev, mats, 1, args.steps, args.warmup)
+    if args.roofline_only:
+        roofline_only(torch, nat, lib, dev, dec, tensors, names, plan, mats, args)
+        return
+    with mark("fixed:sweep:T1"):
+        ms_step, step_bytes = fixed_sweep(torch, nat, lib, dev, mats, 1, args.steps,
+                                          args.warmup)
     log(f"fixed sweep: {ms_step:.3f} ms/step, {step_bytes / 1e9:.2f} GB/step, "
         f"{len(mats)} launches")
 
@@ -872,13 +951,15 @@ def main():
     groups = {k: [fixed[n] for n in ns] for k, ns in kinds.items()}
     groups.update({k: v for k, v in stacked.items() if v})
     for kind, ts in groups.items():
-        ms, nb = fixed_sweep(torch, nat, lib, dev, ts, 1, max(3, args.steps // 2), 1)
+        with mark(f"fixed:{kind}"):
+            ms, nb = fixed_sweep(torch, nat, lib, dev, ts, 1, max(3, args.steps // 2), 1)
         t = ts[0]
         breakdown[kind] = {"shape": f"{t.shape[1]}->{t.shape[0]}", "bits": t.bits,
                            "us_per_launch": round(ms * 1e3 / len(ts), 2),
                            "GB/s": round(nb / (ms * 1e-3) / 1e9, 1)}
     gus = stacked["gate_up_proj"] or groups["gate_proj"] + groups["up_proj"]
-    ms_gu, _ = fixed_sweep(torch, nat, lib, dev, gus, 1, args.steps, args.warmup)
+    with mark("fixed:gate_up_stacked:T1"):
+        ms_gu, _ = fixed_sweep(torch, nat, lib, dev, gus, 1, args.steps, args.warmup)
     t = gus[0]
     b_gu = fixed_bytes(t.shape[0], t.shape[1], t.bits, t.codebook.numel())
     us_gu = ms_gu * 1e3 / len(gus)
@@ -894,7 +975,8 @@ def main():
     # weight is read once for all T rows of x
     batch = {}
     for T in (2, 4, 8, 16):
-        ms_T, nb = fixed_sweep(torch, nat, lib, dev, gus, T, args.steps, args.warmup)
+        with mark(f"fixed:gate_up_stacked:T{T}"):
+            ms_T, nb = fixed_sweep(torch, nat, lib, dev, gus, T, args.steps, args.warmup)
         us_T = ms_T * 1e3 / len(gus)
         batch[f"T{T}"] = {"us_per_launch": round(us_T, 2),
                           "GB/s": round(nb / len(gus) / (us_T * 1e-6) / 1e9, 1),
@@ -922,7 +1004,8 @@ def main():
     }
 
     if not args.no_prefill:
-        result["prefill"] = prefill_section(torch, nat, lib, dev, fixed, kinds, args)
+        with mark("prefill"):
+            result["prefill"] = prefill_section(torch, nat, lib, dev, fixed, kinds, args)
     del fixed, mats, gus, groups, stacked
     torch.cuda.empty_cache()
 
@@ -934,22 +1017,25 @@ def main():
         from gpu_huffman_functions import split_bytes
         t0 = time.time()
         huff = dec.build_huffman(tensors)
-        stream_k = stream_gate_up(torch, nat, lib, dev, huff, plan, args.steps, args.warmup)
+        with mark("huffman:stream_format:gate_up"):
+            stream_k = stream_gate_up(torch, nat, lib, dev, huff, plan, args.steps, args.warmup)
         log(f"stream-format gate/up: {stream_k['us_per_launch']} us per matrix, "
             f"{stream_k['GB/s']} GB/s")
         splits, stream_bytes = build_split_formats(torch, dev, huff, names)
         stack_gate_up(torch, dev, huff, splits, plan)
         log(f"built {len(huff)} Huffman tensors, {len(splits)} split formats, in "
             f"{time.time() - t0:.1f}s")
-        ms_h, sbytes = huffman_sweep(torch, nat, lib, dev, huff, splits, plan, args.steps,
-                                     args.warmup)
+        with mark("huffman:sweep:T1"):
+            ms_h, sbytes = huffman_sweep(torch, nat, lib, dev, huff, splits, plan, args.steps,
+                                         args.warmup)
         hbytes = sum(stream_bytes.values())
         n_w = sum(h.shape[0] * h.shape[1] for h in huff.values())
         res_b = sum(split_bytes(k) for k in {id(splits[n][0]): splits[n][0]
                                             for n in names}.values())
         gate_up = [e for e in plan if isinstance(e, tuple) and e[0].endswith("mlp.gate_proj")]
-        ms_gg, b_gg = huffman_sweep(torch, nat, lib, dev, huff, splits, gate_up, args.steps,
-                                    args.warmup)
+        with mark("huffman:gate_up_glu"):
+            ms_gg, b_gg = huffman_sweep(torch, nat, lib, dev, huff, splits, gate_up, args.steps,
+                                        args.warmup)
         us_gg = ms_gg * 1e3 / len(gate_up)
         b_gg //= len(gate_up)
         s_gg = sum(stream_bytes[n] for n in gate_up[0]) + 4 * (
@@ -984,11 +1070,13 @@ def main():
         torch.cuda.empty_cache()
 
     if not args.no_1p7b and args.config == "qwen3-8b" and args.layers is None:
-        result["qwen3_1_7b"] = sweep_1p7b(torch, nat, lib, dev, synthetic, args)
+        with mark("1p7b"):
+            result["qwen3_1_7b"] = sweep_1p7b(torch, nat, lib, dev, synthetic, args)
         log(f"1.7B sweeps: {result['qwen3_1_7b']['fixed']['sweep']}")
 
     if not args.no_e2e:
-        result["e2e"] = e2e_section(torch, dec, args)
+        with mark("e2e"):
+            result["e2e"] = e2e_section(torch, dec, args)
 
     print(json.dumps(result), flush=True)
 

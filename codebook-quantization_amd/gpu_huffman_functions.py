@@ -300,7 +300,8 @@ def _packed_for_gemm(idx_or_split, n: int, C: int, dev, inv: Optional[torch.Tens
     st = nat.stream_ptr(dev)
     bits = prefill_bits(C) or 16
     nb = (n * bits + 7) // 8
-    packed = torch.zeros(((nb + 15) // 16) * 16 + 16, dtype=torch.uint8, device=dev)
+    packed = torch.empty(((nb + 15) // 16) * 16 + 16, dtype=torch.uint8, device=dev)
+    packed[nb:].zero_()                            # the padding; the stream is written below
     if inv is not None:
         nat.check(lib.cbq_split_to_packed(ctypes.byref(idx_or_split[1]), inv.data_ptr(), bits,
                                           packed.data_ptr(), st), "cbq_split_to_packed")
