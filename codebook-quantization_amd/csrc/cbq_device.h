@@ -312,3 +312,27 @@ __device__ __forceinline__ uint32_t funnel(uint32_t hi, uint32_t lo, uint32_t s)
 {
     return __builtin_amdgcn_alignbit(hi, lo, s);
 }
+
+// Byte offsets into the LDS codebook of the 32 indices of one group: each
+// field is extracted already shifted left by 2 (alignbit/shift + and).  A
+// PADDED codebook has 2^BITS entries (entries >= C repeat cb[C-1]), so the
+// index clamp of the reference (idx >= C -> C-1) costs nothing; otherwise the
+// offset is clamped to 4*(C-1).
+template <int BITS, bool PADDED>
+__device__ __forceinline__ void group_offsets(const uint32_t (&w)[BITS], uint32_t cmax4,
+                                              uint32_t off[32])
+{
+    constexpr uint32_t m4 = ((1u << BITS) - 1u) << 2;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        const int o = j * BITS, q = o >> 5, s = o & 31;
+        uint32_t a;
+        if (s >= 2)
+            a = (s + BITS <= 32) ? ((w[q] >> (s - 2)) & m4)
+                                 : (funnel(w[q + 1], w[q], (uint32_t)(s - 2)) & m4);
+        else
+            a = (w[q] << (2 - s)) & m4;
+        if (!PADDED) a = a < cmax4 ? a : cmax4;
+        off[j] = a;
+    }
+}

@@ -18,8 +18,12 @@
 #include <algorithm>
 #include <type_traits>
 
-// Matrix-core path for 2..16 fp32 tokens (cbq_tiny.hip); -1 = shape not
-// handled there.
+// Matrix-core paths for 2..16 tokens (cbq_tiny.hip); -1 = shape not handled
+// there.  fewtok: bf16 matrix cores, K % 128 == 0; tiny: fp32 matrix cores.
+int cbq_fixed_fewtok_t(const float *x, const uint8_t *packed, const float *cb, float *out, int T,
+                       int M, int K, int C, int bits, hipStream_t st);
+int cbq_fixed_fewtok_t_bf16(const uint16_t *x, const uint8_t *packed, const float *cb,
+                            uint16_t *out, int T, int M, int K, int C, int bits, hipStream_t st);
 int cbq_fixed_tiny_t(const float *x, const uint8_t *packed, const float *cb, float *out, int T,
                      int M, int K, int C, int bits, hipStream_t st);
 int cbq_fixed_tiny_t_bf16(const uint16_t *x, const uint8_t *packed, const float *cb,
@@ -31,7 +35,7 @@ constexpr int kBlock = 1024;                // 16 waves share one LDS codebook
 constexpr int kWavesPerBlock = kBlock / CBQ_WAVE;
 constexpr int kMaxLdsBytes = 64 * 1024;     // per-workgroup budget we allow
 constexpr int kMaxLdsCodebook = 16384;      // entries of fp32 codebook in LDS
-constexpr int kTinyMinT = 5;                // fp32 token tiles of 5..16 go to the matrix cores
+constexpr int kTinyMinT = 5;                // K % 128 != 0: tiles of 5..16 to the fp32 matrix cores
 // The x-in-registers path runs one block per CU, so it may use most of the
 // CU's 160 KB of LDS (codebook + padded x + row partials).
 constexpr int kMaxLdsBytesXReg = 152 * 1024;
@@ -306,30 +310,6 @@ __device__ __forceinline__ void pad_codebook(float *s_cb, int n16, int n_pieces,
     for (int q = n16 + (int)threadIdx.x; q < n_pieces; q += (int)blockDim.x)
         ((f4v *)s_cb)[q] = q == n16 ? f4v{mix[0], mix[1], mix[2], mix[3]}
                                     : f4v{last, last, last, last};
-}
-
-// Byte offsets into the LDS codebook of the 32 indices of one group: each
-// field is extracted already shifted left by 2 (alignbit/shift + and).  A
-// PADDED codebook has 2^BITS entries (entries >= C repeat cb[C-1]), so the
-// index clamp of the reference (idx >= C -> C-1) costs nothing; otherwise the
-// offset is clamped to 4*(C-1).
-template <int BITS, bool PADDED>
-__device__ __forceinline__ void group_offsets(const uint32_t (&w)[BITS], uint32_t cmax4,
-                                              uint32_t off[32])
-{
-    constexpr uint32_t m4 = ((1u << BITS) - 1u) << 2;
-#pragma unroll
-    for (int j = 0; j < 32; j++) {
-        const int o = j * BITS, q = o >> 5, s = o & 31;
-        uint32_t a;
-        if (s >= 2)
-            a = (s + BITS <= 32) ? ((w[q] >> (s - 2)) & m4)
-                                 : (funnel(w[q + 1], w[q], (uint32_t)(s - 2)) & m4);
-        else
-            a = (w[q] << (2 - s)) & m4;
-        if (!PADDED) a = a < cmax4 ? a : cmax4;
-        off[j] = a;
-    }
 }
 
 // The 32 raw BITS-wide indices of a lane's group.
@@ -1005,12 +985,17 @@ int linear_tile(const XT *x, const uint8_t *packed, const float *cb, OT *out, in
 {
     const bool fast = (K % 32 == 0) && C <= kMaxLdsCodebook &&
                       ((uintptr_t)packed & 3) == 0;
-    if (fast && T >= kTinyMinT) {
+    if (fast && T >= 2) {
         int rc = -1;
-        if constexpr (std::is_same<XT, float>::value && std::is_same<OT, float>::value)
-            rc = cbq_fixed_tiny_t(x, packed, cb, out, T, M, K, C, bits, st);
-        if constexpr (std::is_same<XT, uint16_t>::value && std::is_same<OT, uint16_t>::value)
-            rc = cbq_fixed_tiny_t_bf16(x, packed, cb, out, T, M, K, C, bits, st);
+        if constexpr (std::is_same<XT, float>::value && std::is_same<OT, float>::value) {
+            rc = cbq_fixed_fewtok_t(x, packed, cb, out, T, M, K, C, bits, st);
+            if (rc < 0 && T >= kTinyMinT) rc = cbq_fixed_tiny_t(x, packed, cb, out, T, M, K, C, bits, st);
+        }
+        if constexpr (std::is_same<XT, uint16_t>::value && std::is_same<OT, uint16_t>::value) {
+            rc = cbq_fixed_fewtok_t_bf16(x, packed, cb, out, T, M, K, C, bits, st);
+            if (rc < 0 && T >= kTinyMinT)
+                rc = cbq_fixed_tiny_t_bf16(x, packed, cb, out, T, M, K, C, bits, st);
+        }
         if (rc >= 0) return rc;
     }
     if (fast) {

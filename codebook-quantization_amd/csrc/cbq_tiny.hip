@@ -1,25 +1,48 @@
 // Fixed-width GEMM for a few tokens (2 <= T <= 16; ck_linear_f32 and
-// ck_linear_bf16 send it tiles of 5..16) on the fp32 matrix cores of gfx950
-// (v_mfma_f32_16x16x4_f32)
+// ck_linear_bf16 send it tiles of 2..16) on the matrix cores of gfx950
 // (rocm/compressed_kernel.hip:607-627 is the reference entry point; its
 // kernel runs one block per output scalar).
 //
 // Same arithmetic as the reference's loop (src/compressed_matmul.c:416-450):
-// out[t, r] = sum_k x[t, k] * cb[min(idx[r, k], C - 1)], fp32 products
-// (exact in the fp32 MFMA) and fp32 sums in a different order.
+// out[t, r] = sum_k x[t, k] * cb[min(idx[r, k], C - 1)], exact products and
+// fp32 sums in a different order.
 //
-// A wave owns a tile of 16 rows and a quarter of the 32-index groups of K.
-// Per group, lane l decodes indices 8j .. 8j+7 (j = l / 16) of row l % 16:
-// one 4-dword window of the packed row holds them for every width here (the
-// 16 rows' groups arrive with one 16-byte load per lane and are rearranged
-// through LDS).  The
-// group then takes 8 MFMAs; in step s the k slot j stands for column
-// 32 g + 8 j + s, for the weights (A: row l % 16, slot l / 16) and for x
-// (B: slot l / 16, token l % 16) alike, so the 16 x 16 product is exact for
-// any T <= 16.  x rows are read straight from memory (two float4 per lane and
-// group, shared by the 16 rows).  The four quarters of a row tile are summed
-// through LDS in order.  Tokens past T compute on token 0's x and are not
-// written.
+// fixed_fewtok_kernel (K % 128 == 0): bf16 matrix cores
+// (v_mfma_f32_16x16x32_bf16).  The codebook values are bf16 numbers (the
+// lossless codebooks are bf16 weights), and an fp32 x is split exactly into
+// three bf16 parts, x = h + m + l (truncations: h keeps the top 8 significand
+// bits, m the next 8 of x - h, l = x - h - m the rest, at most 8 bits), so
+// every product w * part is exact and the three MFMAs sum them in fp32.  A
+// codebook with any entry that is not a bf16 number (found while staging
+// it) is split the same way and six MFMAs of the nine part products run
+// (the three left out are below 2^-24 of the product).  bf16 x is one part.
+//   - Block: 8 waves over R tiles of 16 rows; wave w takes the 128-column
+//     steps w, w + 8, w + 16, ... (the block's waves read neighbouring spans
+//     of each row at the same time).
+//   - A tile-step (16 rows x 4 groups of 32 indices) is loaded with 16-byte
+//     chunks, consecutive lanes on consecutive bytes of a row, Q tile-steps
+//     ahead into registers; a wave-private LDS buffer re-lays it so that
+//     lane l holds group l / 16 of row l % 16 (BITS words).
+//   - MFMA c of a tile-step takes chunk c (indices 8c .. 8c+7) of each of the
+//     step's four groups, for the weights (A: row l % 16) and for x (B: token
+//     l % 16) alike.  x of a step is split once and serves the R tiles.
+//   - The 8 waves' partial tiles are summed through LDS in wave order.
+// Measured against the per-lane loads of one 52-byte group each (16 rows x
+// 4 groups per instruction): 44.6 us for the 163.6 MB stacked gate+up read
+// alone against 30.9 us for these chunk loads.
+//
+// fixed_tiny_mfma_kernel (K % 32 == 0 otherwise): fp32 matrix cores
+// (v_mfma_f32_16x16x4_f32).  A wave owns a tile of 16 rows and a quarter of
+// the 32-index groups of K.  Per group, lane l decodes indices 8j .. 8j+7
+// (j = l / 16) of row l % 16: one 4-dword window of the packed row holds
+// them for every width here (the 16 rows' groups arrive with one 16-byte
+// load per lane and are rearranged through LDS).  The group then takes 8
+// MFMAs; in step s the k slot j stands for column 32 g + 8 j + s, for the
+// weights (A: row l % 16, slot l / 16) and for x (B: slot l / 16, token
+// l % 16) alike, so the 16 x 16 product is exact for any T <= 16.  x rows are
+// read straight from memory (two float4 per lane and group, shared by the 16
+// rows).  The four quarters of a row tile are summed through LDS in order.
+// Tokens past T compute on token 0's x and are not written.
 #include "cbq_device.h"
 
 #include <algorithm>
@@ -41,6 +64,261 @@ __device__ __forceinline__ void wave_sync_lds()
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---- fixed_fewtok_kernel ------------------------------------------------------
+
+constexpr int kFtWaves = 8;
+constexpr int kFtThreads = kFtWaves * CBQ_WAVE;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// bf16 bits of a (low half) and of b (high half), both truncated: v_perm
+// picks the upper two bytes of each
+__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b)
+{
+    return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// v = h + m + l exactly, each a bf16 number: r = v - h and l = r - m are
+// exact fp32 differences, and l has at most 8 significant bits
+__device__ __forceinline__ void split3(const float (&v)[8], u32x4 &h, u32x4 &m, u32x4 &l)
+{
+    uint32_t hp[4], mp[4], lp[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        const uint32_t a = __float_as_uint(v[e]), b = __float_as_uint(v[e + 1]);
+        const float ra = v[e] - __uint_as_float(a & 0xffff0000u);
+        const float rb = v[e + 1] - __uint_as_float(b & 0xffff0000u);
+        const uint32_t ua = __float_as_uint(ra), ub = __float_as_uint(rb);
+        const float la = ra - __uint_as_float(ua & 0xffff0000u);
+        const float lb = rb - __uint_as_float(ub & 0xffff0000u);
+        hp[e >> 1] = hi_pair(a, b);
+        mp[e >> 1] = hi_pair(ua, ub);
+        lp[e >> 1] = hi_pair(__float_as_uint(la), __float_as_uint(lb));
+    }
+    h = u32x4{hp[0], hp[1], hp[2], hp[3]};
+    m = u32x4{mp[0], mp[1], mp[2], mp[3]};
+    l = u32x4{lp[0], lp[1], lp[2], lp[3]};
+}
+
+__device__ __forceinline__ f4 mfma_bf16(u32x4 a, u32x4 b, f4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// x of one lane and step: 32 values of token l % 16, group l / 16 of the step
+template <typename XT> struct FtX;
+template <> struct FtX<float> {
+    static constexpr int kWords = 32;
+    static constexpr int kParts = 3;
+    __device__ static void parts(const uint32_t (&xw)[kWords], u32x4 (&b)[4][3])
+    {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float q[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) q[e] = __uint_as_float(xw[8 * c + e]);
+            split3(q, b[c][0], b[c][1], b[c][2]);
+        }
+    }
+};
+template <> struct FtX<uint16_t> {
+    static constexpr int kWords = 16;
+    static constexpr int kParts = 1;
+    __device__ static void parts(const uint32_t (&xw)[kWords], u32x4 (&b)[4][3])
+    {
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            b[c][0] = u32x4{xw[4 * c], xw[4 * c + 1], xw[4 * c + 2], xw[4 * c + 3]};
+    }
+};
+
+// R row tiles per block, Q tile-steps of weights in flight per wave (Q
+// divides R, so every ring slot is a compile-time register array).
+template <int BITS, int R, int Q, typename XT, typename OT>
+__global__ __launch_bounds__(kFtThreads) void fixed_fewtok_kernel(
+    const XT *__restrict__ x, const uint32_t *__restrict__ words,
+    const float *__restrict__ cb, OT *__restrict__ out, int T, int M, int K, int C)
+{
+    static_assert(R % Q == 0, "ring slots are static: Q divides R");
+    static_assert(BITS >= 4 && BITS <= 16, "a group's words per lane");
+    constexpr bool PADDED = BITS <= 14;           // 2^BITS-entry table: the clamp is free
+    constexpr int NI = (BITS + 3) / 4;            // 16-byte loads per lane and tile-step
+    constexpr int CH = 16 * BITS;                 // 16-byte chunks of a tile-step
+    constexpr int XW = FtX<XT>::kWords;
+    __shared__ __attribute__((aligned(16))) float s_cb[PADDED ? (1 << BITS) : kTinyMaxCodebook];
+    __shared__ __attribute__((aligned(16))) uint32_t s_tr[kFtWaves][64 * BITS];
+    __shared__ int s_flag[kFtWaves];
+    extern __shared__ __attribute__((aligned(16))) f4 s_part[];     // [8][R][64]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (CBQ_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / CBQ_WAVE);
+    const int rsub = lane & 15, j = lane >> 4;
+    const int G = K >> 5;
+    const int NS = G >> 2;                        // 128-column steps of a row
+    const int Sw = NS > wave ? (NS - wave + kFtWaves - 1) / kFtWaves : 0;
+    const int tile0 = blockIdx.x * R;
+    const size_t rowstride = (size_t)G * BITS;    // words of a packed row
+    const int C_eff = C < (1 << BITS) ? C : (1 << BITS);
+    const int NT = PADDED ? (1 << BITS) : ((C_eff + 63) & ~63);
+
+    // codebook loads first, so that waiting for them leaves the weight and
+    // x loads below in flight
+    constexpr int kMaxNE = ((PADDED ? (1 << BITS) : kTinyMaxCodebook) + kFtThreads - 1) / kFtThreads;
+    const int NE = (NT + kFtThreads - 1) / kFtThreads;
+    float cv[kMaxNE];
+#pragma unroll
+    for (int e = 0; e < kMaxNE; e++) {
+        const int i = e * kFtThreads + tid;
+        if (e < NE) cv[e] = cb[i < C_eff ? i : C_eff - 1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // this lane's chunks of a tile-step: c = 64 k + lane -> row c / BITS,
+    // 16-byte piece c % BITS of the row's 4 BITS words (lanes past CH re-read
+    // the last chunk and store nothing)
+    int crow[NI], cpiece[NI];
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+        int c = 64 * k + lane;
+        c = c < CH ? c : CH - 1;
+        crow[k] = c / BITS;
+        cpiece[k] = c % BITS;
+    }
+    // global step of local step s; steps past the wave's last re-read it (an L2 hit)
+    auto gstep = [&](int s) {
+        const int sl = s < Sw ? s : (Sw > 0 ? Sw - 1 : 0);
+        const int g = kFtWaves * sl + wave;
+        return g < NS ? g : NS - 1;
+    };
+    auto load_item = [&](int s, int t, u32x4 (&dst)[NI]) {
+        const size_t col = (size_t)gstep(s) * 4 * BITS;
+#pragma unroll
+        for (int k = 0; k < NI; k++) {
+            int row = (tile0 + t) * 16 + crow[k];
+            row = row < M ? row : M - 1;
+            __builtin_memcpy(&dst[k], words + (size_t)row * rowstride + col + 4 * cpiece[k], 16);
+        }
+    };
+    auto load_x = [&](int s, uint32_t (&xw)[XW]) {
+        if (rsub < T) {
+            __builtin_memcpy(xw, x + (size_t)rsub * K + (size_t)(4 * gstep(s) + j) * 32,
+                             sizeof(xw));
+        } else {
+#pragma unroll
+            for (int i = 0; i < XW; i++) xw[i] = 0u;
+        }
+    };
+    u32x4 wr[Q][NI];
+#pragma unroll
+    for (int q = 0; q < Q; q++) load_item(0, q, wr[q]);
+    uint32_t xn[XW];
+    load_x(0, xn);
+    __builtin_amdgcn_sched_barrier(0);
+
+    int inexact = 0;
+#pragma unroll
+    for (int e = 0; e < kMaxNE; e++) {
+        const int i = e * kFtThreads + tid;
+        if (e < NE && i < NT) {
+            s_cb[i] = cv[e];
+            inexact |= (__float_as_uint(cv[e]) & 0xffffu) != 0;
+        }
+    }
+    {
+        const bool any = __ballot(inexact) != 0;
+        if (lane == 0) s_flag[wave] = any;
+    }
+    __syncthreads();                               // codebook and flags staged
+    bool wsplit = false;
+#pragma unroll
+    for (int w = 0; w < kFtWaves; w++) wsplit |= s_flag[w] != 0;
+    const uint32_t cmax4 = (uint32_t)(C_eff - 1) << 2;
+
+    f4 acc[R];
+#pragma unroll
+    for (int t = 0; t < R; t++) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    uint32_t *tr = s_tr[wave];
+
+    for (int s = 0; s < Sw; s++) {
+        u32x4 xb[4][3];
+        FtX<XT>::parts(xn, xb);
+        load_x(s + 1, xn);                         // next step's x, one step ahead
+#pragma unroll
+        for (int t = 0; t < R; t++) {
+            u32x4 (&slot)[NI] = wr[t % Q];
+#pragma unroll
+            for (int k = 0; k < NI; k++)
+                if (64 * k + lane < CH) *(u32x4 *)(tr + 4 * (64 * k + lane)) = slot[k];
+            wave_sync_lds();
+            uint32_t w[BITS];
+#pragma unroll
+            for (int q = 0; q < BITS; q++) w[q] = tr[(rsub * 4 + j) * BITS + q];
+            wave_sync_lds();
+            // this slot's next tile-step, Q ahead in (step, tile) order
+            if (t + Q < R) load_item(s, t + Q, slot);
+            else load_item(s + 1, t + Q - R, slot);
+
+            uint32_t off[32];
+            group_offsets<BITS, PADDED>(w, cmax4, off);
+            float wv[32];
+#pragma unroll
+            for (int q = 0; q < 32; q++) wv[q] = *(const float *)((const char *)s_cb + off[q]);
+            u32x4 a[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                a[c] = u32x4{hi_pair(__float_as_uint(wv[8 * c]), __float_as_uint(wv[8 * c + 1])),
+                             hi_pair(__float_as_uint(wv[8 * c + 2]), __float_as_uint(wv[8 * c + 3])),
+                             hi_pair(__float_as_uint(wv[8 * c + 4]), __float_as_uint(wv[8 * c + 5])),
+                             hi_pair(__float_as_uint(wv[8 * c + 6]), __float_as_uint(wv[8 * c + 7]))};
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+#pragma unroll
+                for (int p = 0; p < FtX<XT>::kParts; p++) acc[t] = mfma_bf16(a[c], xb[c][p], acc[t]);
+            if (wsplit) {                          // codebook not bf16: w = wh + wm + wl
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    float q8[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) q8[e] = wv[8 * c + e];
+                    u32x4 wh, wm, wl;
+                    split3(q8, wh, wm, wl);
+                    acc[t] = mfma_bf16(wm, xb[c][0], acc[t]);
+                    acc[t] = mfma_bf16(wl, xb[c][0], acc[t]);
+                    if (FtX<XT>::kParts > 1) acc[t] = mfma_bf16(wm, xb[c][1], acc[t]);
+                }
+            }
+        }
+    }
+
+    // the 8 waves' partial tiles, summed in wave order
+#pragma unroll
+    for (int t = 0; t < R; t++) s_part[(wave * R + t) * CBQ_WAVE + lane] = acc[t];
+    __syncthreads();
+    if (wave < R) {
+        const int t = wave;
+        f4 sum = s_part[t * CBQ_WAVE + lane];
+#pragma unroll
+        for (int w = 1; w < kFtWaves; w++) {
+            const f4 v = s_part[(w * R + t) * CBQ_WAVE + lane];
+            sum.x += v.x;
+            sum.y += v.y;
+            sum.z += v.z;
+            sum.w += v.w;
+        }
+        // D[m][n]: lane l, element v holds row m = 4 (l / 16) + v, token n = l % 16
+        const int n = lane & 15;
+        const float vals[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int row = (tile0 + t) * 16 + 4 * j + v;
+            if (row < M && n < T) out[(size_t)n * M + row] = from_f32<OT>(vals[v]);
+        }
+    }
 }
 
 // x in XT (fp32, or bf16 widened exactly); out in OT (one rounding for bf16).
@@ -205,6 +483,51 @@ int tiny_launch(const XT *x, const uint8_t *packed, const float *cb, OT *out, in
     return cbq_launch_status("fixed_tiny_mfma_kernel");
 }
 
+template <int R, int Q, typename XT, typename OT>
+int fewtok_launch_r(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T, int M,
+                    int K, int C, int bits, int blocks, hipStream_t st)
+{
+    const size_t lds = (size_t)kFtWaves * R * CBQ_WAVE * sizeof(f4);
+#define CBQ_FT(B)                                                                              \
+    hipLaunchKernelGGL((fixed_fewtok_kernel<B, R, Q, XT, OT>), dim3(blocks), dim3(kFtThreads),  \
+                       lds, st, x, (const uint32_t *)packed, cb, out, T, M, K, C)
+    switch (bits) {
+    case 8: CBQ_FT(8); break;
+    case 10: CBQ_FT(10); break;
+    case 11: CBQ_FT(11); break;
+    case 12: CBQ_FT(12); break;
+    case 13: CBQ_FT(13); break;
+    case 14: CBQ_FT(14); break;
+    case 16: CBQ_FT(16); break;
+    default: return -1;
+    }
+#undef CBQ_FT
+    return cbq_launch_status("fixed_fewtok_kernel");
+}
+
+// Row tiles per block: the most of 6 / 3 / 2 / 1 that still gives every CU
+// a block (a block holds one CU: 8 waves, up to 141 KiB of LDS).
+template <typename XT, typename OT>
+int fewtok_launch(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T, int M,
+                  int K, int C, int bits, hipStream_t st)
+{
+    if (T < 2 || T > 16 || M <= 0 || K <= 0 || K % 128 || C <= 0 || C > kTinyMaxCodebook)
+        return -1;
+    if (((uintptr_t)x & 15) != 0 || ((uintptr_t)packed & 15) != 0) return -1;
+    if (bits != 8 && (bits < 10 || bits > 14) && bits != 16) return -1;
+    const long tiles = (M + 15) / 16;
+    const long ncu = cbq_num_cus();
+    const int R = tiles >= 6 * ncu ? 6 : tiles >= 3 * ncu ? 3 : tiles >= 2 * ncu ? 2 : 1;
+    const long blocks = (tiles + R - 1) / R;
+    if (blocks > 0x7fffffffL) return -1;
+    switch (R) {
+    case 6: return fewtok_launch_r<6, 2>(x, packed, cb, out, T, M, K, C, bits, (int)blocks, st);
+    case 3: return fewtok_launch_r<3, 3>(x, packed, cb, out, T, M, K, C, bits, (int)blocks, st);
+    case 2: return fewtok_launch_r<2, 2>(x, packed, cb, out, T, M, K, C, bits, (int)blocks, st);
+    default: return fewtok_launch_r<1, 1>(x, packed, cb, out, T, M, K, C, bits, (int)blocks, st);
+    }
+}
+
 }  // namespace
 
 // 2 <= T <= 16 tokens (fp32, or bf16 x and out), K % 32 == 0, widths 8,
@@ -220,4 +543,19 @@ int cbq_fixed_tiny_t_bf16(const uint16_t *x, const uint8_t *packed, const float 
                           uint16_t *out, int T, int M, int K, int C, int bits, hipStream_t st)
 {
     return tiny_launch<uint16_t, uint16_t>(x, packed, cb, out, T, M, K, C, bits, st);
+}
+
+// 2 <= T <= 16 tokens (fp32, or bf16 x and out), K % 128 == 0, 16-byte
+// aligned x and stream, widths 8, 10-14 and 16, C <= 16384: the bf16
+// matrix-core kernel above; returns -1 for shapes it does not take.
+int cbq_fixed_fewtok_t(const float *x, const uint8_t *packed, const float *cb, float *out, int T,
+                       int M, int K, int C, int bits, hipStream_t st)
+{
+    return fewtok_launch<float, float>(x, packed, cb, out, T, M, K, C, bits, st);
+}
+
+int cbq_fixed_fewtok_t_bf16(const uint16_t *x, const uint8_t *packed, const float *cb,
+                            uint16_t *out, int T, int M, int K, int C, int bits, hipStream_t st)
+{
+    return fewtok_launch<uint16_t, uint16_t>(x, packed, cb, out, T, M, K, C, bits, st);
 }

@@ -97,10 +97,12 @@ def test_column_ranges_large_x(cuda, oracle, M, K, T):
 @pytest.mark.parametrize("bits", [8, 10, 11, 12, 13, 14, 16])
 @pytest.mark.parametrize("T", [5, 16])
 def test_matrix_core_token_tiles(cuda, oracle, bits, T):
-    """5..16 fp32 tokens run on the fp32 matrix cores (cbq_tiny.hip): every
-    width it takes, indices past C clamped, rows not a multiple of 32."""
+    """5..16 fp32 tokens with K % 128 != 0 run on the fp32 matrix cores
+    (fixed_tiny_mfma_kernel, cbq_tiny.hip): every width it takes, indices past
+    C clamped, rows not a multiple of 32.  (K % 128 == 0 takes the bf16
+    matrix-core kernel, tests/test_gpu_fewtok.py.)"""
     rng = np.random.default_rng(bits * 31 + T)
-    M, K = 200, 1024
+    M, K = 200, 1056
     C = min(1 << bits, 3000)
     raw = rng.integers(0, 1 << bits, size=M * K)
     cb = (rng.standard_normal(C) * 0.02).astype(np.float32)
@@ -113,7 +115,7 @@ def test_matrix_core_token_tiles(cuda, oracle, bits, T):
 
 @pytest.mark.parametrize("T", [1, 8, 64])
 def test_codebook_staging_unaligned(cuda, oracle, T):
-    """The streaming (T = 1), few-token (T = 8) and fp32-prefill (T = 64)
+    """The streaming (T = 1), bf16 few-token (T = 8) and fp32-prefill (T = 64)
     kernels stage the codebook in 16-byte pieces when it is 16-byte aligned;
     a codebook 4 bytes off alignment, with C not a multiple of 4 and indices
     past C, takes the element-wise copy and must give the same result."""
@@ -261,8 +263,8 @@ def test_affine_implicit_codebook_bit_exact(cuda, oracle, T):
     """cbq_linear_affine_f32 over re-indexed weights equals ck_linear_f32 over
     the frequency-sorted codebook bit for bit at T = 1 (same values, same
     streaming kernel and order of accumulation), zeros of either sign
-    included; at T = 20 the table path's 16-token tile runs on the matrix
-    cores (another order of accumulation), so there the two agree to
+    included; with 2..16-token tiles (T = 3, 20) the table path runs on the
+    matrix cores (another order of accumulation), so there the two agree to
     rounding; both match the oracle."""
     import bitpack
     import cbq_native as nat
@@ -290,7 +292,7 @@ def test_affine_implicit_codebook_bit_exact(cuda, oracle, T):
                                 len(cb), bits, st), "table")
     nat.check(lib.cbq_linear_affine_f32(x.data_ptr(), pka.data_ptr(), lo, wid, ya.data_ptr(), T, M,
                                         K, bits, st), "affine")
-    if T < 5:
+    if T == 1:
         assert torch.equal(y, ya)
     else:
         assert rel_l2(y.cpu().numpy(), ya.cpu().numpy()) <= 2e-6
