@@ -581,7 +581,8 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
     fixed-width 13-bit indices, and the same weights Huffman-coded in the
     split format (one token on the split GEMV; 4 and 16 tokens through the
     transient fixed-width stream and ck_linear_f32)."""
-    from gpu_huffman_functions import split_bytes, split_inverse, split_prefill
+    from gpu_huffman_functions import (split_bytes, split_fewtok, split_fewtok_eligible,
+                                       split_inverse, split_prefill)
     dec = synthetic.SyntheticDecoder("qwen3-1.7b", log=log)
     tensors = dec.all_linears(with_head=False)
     names = [n for n, _, _ in tensors]
@@ -667,19 +668,28 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
                 invs[id(cbt)] = split_inverse(cbt.cpu().numpy(), dev)
 
         def run(T=T, xs=xs):
-            for n in names:
-                t = huff[n]
-                M, K = t.shape
-                split_prefill(splits[n], invs[id(t.tables["codebook"])], xs[K], M, K,
-                              t.tables["codebook"])
+            # the decoder's launches: q/k/v and gate/up grouped (one fused
+            # launch each, matrices sharing x); shapes the fused kernel does
+            # not take (down, K = 6144) through split_prefill's transient stream
+            for e in plan:
+                ns = list(e) if isinstance(e, tuple) else [e]
+                M0, K = huff[ns[0]].shape
+                if split_fewtok_eligible(K):
+                    split_fewtok([splits[n] for n in ns], xs[K], [huff[n].shape[0] for n in ns], K)
+                    continue
+                for n in ns:
+                    t = huff[n]
+                    split_prefill(splits[n], invs[id(t.tables["codebook"])], xs[K], t.shape[0],
+                                  K, t.tables["codebook"])
         with mark(f"1p7b:huffman:sweep:T{T}"):
             ms, _ = timed_graph(torch, run, max(3, args.steps // 2), 1)
         hu[f"T{T}"] = {"ms_per_step": round(ms, 3),
                        "vs_T1": round(ms / ms1, 3),
-                       "note": "per matrix: the split format decoded to a transient "
-                               "fixed-width stream (cbq_split_to_packed) and ck_linear_f32's "
-                               "kernels over it; graph-replayed (transients from the graph's "
-                               "pool)"}
+                       "note": "the decoder's launch list: q/k/v, o and gate/up straight from "
+                               "the split format on the matrix cores (cbq_split_linear_fewtok_f32,"
+                               " q/k/v and gate/up one launch each); down (K = 6144) decoded to a "
+                               "transient fixed-width stream and ck_linear_f32's kernels; "
+                               "graph-replayed"}
     out["huffman"] = {"sweep": hu, "bits_per_weight_resident": round(8.0 * res_b / n_w, 3),
                       "bits_per_weight_stream_incl_index":
                           round(8.0 * sum(stream_bytes.values()) / n_w, 3)}

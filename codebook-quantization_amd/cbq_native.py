@@ -95,6 +95,7 @@ SIGNATURES = {
     "cbq_split_bits": (_i, [_vp, _i64, _vp, _i, _vp, _vp]),
     "cbq_pack_indices": (_i, [_vp, _i64, _i, _vp, _vp]),
     "cbq_split_to_packed": (_i, [_vp, _vp, _i, _vp, _vp]),
+    "cbq_split_linear_fewtok_f32": (_i, [_vp, _i, _i, _vp, _vp, _vp, _i, _vp]),
     "cbq_split_pack": (_i, [_vp, _i64, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
     "cbq_split_linear_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _i, _vp, _vp, _vp, _i,
                                   _vp]),

@@ -96,6 +96,52 @@ template <typename OT> __device__ __forceinline__ OT from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <> __device__ __forceinline__ uint16_t from_f32<uint16_t>(float v) { return f32_to_bf16(v); }
 
+// ---- exact products on the bf16 matrix cores --------------------------------
+typedef __bf16 cbq_bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t cbq_u32x4 __attribute__((ext_vector_type(4)));
+typedef float cbq_f32x4 __attribute__((ext_vector_type(4)));
+
+// bf16 bits of a (low half) and of b (high half), both truncated: v_perm
+// picks the upper two bytes of each
+__device__ __forceinline__ uint32_t cbq_hi_pair(uint32_t a, uint32_t b)
+{
+    return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// v = h + m + l exactly, each a bf16 number (8 values, packed two to a
+// dword): h keeps the top 8 significand bits of v (its low 16 bits
+// cleared), m the same of r = v - h, l = r - m; both differences are exact
+// in fp32 and l has at most 8 significant bits
+__device__ __forceinline__ void cbq_split3(const float (&v)[8], cbq_u32x4 &h, cbq_u32x4 &m,
+                                           cbq_u32x4 &l)
+{
+    uint32_t hp[4], mp[4], lp[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+        const uint32_t a = __float_as_uint(v[e]), b = __float_as_uint(v[e + 1]);
+        const float ra = v[e] - __uint_as_float(a & 0xffff0000u);
+        const float rb = v[e + 1] - __uint_as_float(b & 0xffff0000u);
+        const uint32_t ua = __float_as_uint(ra), ub = __float_as_uint(rb);
+        const float la = ra - __uint_as_float(ua & 0xffff0000u);
+        const float lb = rb - __uint_as_float(ub & 0xffff0000u);
+        hp[e >> 1] = cbq_hi_pair(a, b);
+        mp[e >> 1] = cbq_hi_pair(ua, ub);
+        lp[e >> 1] = cbq_hi_pair(__float_as_uint(la), __float_as_uint(lb));
+    }
+    h = cbq_u32x4{hp[0], hp[1], hp[2], hp[3]};
+    m = cbq_u32x4{mp[0], mp[1], mp[2], mp[3]};
+    l = cbq_u32x4{lp[0], lp[1], lp[2], lp[3]};
+}
+
+// c + A * B on v_mfma_f32_16x16x32_bf16: lane l holds A row l % 16 and B
+// column l % 16, k = 8 (l / 16) .. +7 of both; D lane l: rows 4 (l / 16) + v,
+// column l % 16
+__device__ __forceinline__ cbq_f32x4 cbq_mfma_bf16(cbq_u32x4 a, cbq_u32x4 b, cbq_f32x4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(cbq_bf16x8, a),
+                                                   __builtin_bit_cast(cbq_bf16x8, b), c, 0, 0, 0);
+}
+
 // dst[i] = src[min(i, n_src - 1)] for i < n_dst (0 < n_src <= n_dst), global
 // to LDS by the whole block, with a thread's loads (up to 8 pieces) in flight
 // before its first store: one round trip per 8 pieces rather than one per

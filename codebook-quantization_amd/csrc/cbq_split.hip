@@ -523,6 +523,202 @@ __global__ __launch_bounds__(kPackWaves * CBQ_WAVE) void split_to_packed_kernel(
     }
 }
 
+// ---- a few tokens straight from the split format -------------------------------
+//
+// y[t, r] = W[r, :] . x[t, :] for 2 <= T <= 16 tokens on the bf16 matrix cores,
+// every weight decoded once for all tokens and never written out.  The split
+// weights are bf16 numbers; x is split exactly into three bf16 parts
+// (cbq_split3), so each product is exact and only the fp32 summation order
+// differs from the reference loop (src/compressed_matmul.c:208-239).
+//
+// Block: 16 waves (one per CU, persistent over tiles).  A tile is 16 "units":
+// K % 4096 == 0: 16 rows, each of K / 4096 chunks (CPR), a wave per row;
+// K = 1024 or 2048: 16 chunks of 4096 / K rows each (RPC), a wave per chunk.
+// A wave decodes its chunk in eight phases of 8 weights per lane (lane l
+// holds sub-block l: 64 consecutive weights of a row, as the one-token
+// GEMV's decode) and writes them as bf16 to a 16 KiB phase tile in LDS,
+// [16 RPC rows][64 / RPC sub-blocks][8 values], sub-block slot m ^ (row & 15).
+// After a barrier the 16 waves run the phase's MFMAs: wave w takes row tile
+// w / (16 / RPC) and k-block w % (16 / RPC) (4 sub-blocks x 8 columns), so
+// its x columns are 4096 cc + 64 (4 kb + j) + 8 p + e for lane group j.
+// The phase tiles are double-buffered: one barrier per phase.  At the end of
+// a tile the waves' 16 x 16 partials are summed through LDS in k-block order.
+//
+// LDS: the two-code table at address 0 (64 KiB), 16 code slots (64 KiB),
+// two phase tiles (32 KiB): 160 KiB.
+constexpr int kSfWaves = 16;
+constexpr int kSfPhaseWords = 4096;               // 16 KiB: 16 RPC rows x 64 / RPC x 4 words
+
+__device__ __forceinline__ int sf_slot(int row, int m, int per_row)
+{
+    return (row * per_row + (m ^ (row & 15))) * 4;   // word offset of (row, sub-block m)
+}
+
+template <typename OT>
+__global__ __launch_bounds__(kSfWaves * CBQ_WAVE) void split_fewtok_kernel(
+    const float *__restrict__ x, SplitSegs segs, int T, int K, int RPC, int CPR)
+{
+    // the block's matrix: blocks [block0, block0 + nblocks) of the grid
+    int sidx = 0;
+#pragma unroll
+    for (int i = 1; i < kSMaxSeg; i++)
+        if (i < segs.n && (int)blockIdx.x >= segs.s[i].block0) sidx = i;
+    const SplitSeg &S = segs.s[sidx];
+    const int M = S.M;
+    OT *__restrict__ const out = (OT *)S.out;
+    const int bid = (int)blockIdx.x - S.block0, nbl = S.nblocks;
+    const int n_units = RPC == 1 ? M : M / RPC;    // rows, or chunks of RPC rows
+    const int n_tiles = (n_units + kSfWaves - 1) / kSfWaves;
+    __shared__ __attribute__((aligned(16))) uint32_t
+        s_lds[kSLut + kSfWaves * kSSlotWords + 2 * kSfPhaseWords];
+    uint32_t *const s_ph = s_lds + kSLut + kSfWaves * kSSlotWords;
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CBQ_WAVE);
+    uint32_t *const s_slot = s_lds + kSLut + wave * kSSlotWords;
+    const int lane_addr =
+        __builtin_amdgcn_readfirstlane(4 * (kSLut + wave * kSSlotWords)) + 4 * lane;
+    const int rsub = lane & 15, j = lane >> 4;
+    const int per_row = 64 / RPC;                  // sub-blocks of a row in one chunk
+    const int KB = 16 / RPC;                       // k-blocks per row tile
+    const int rt = wave / KB, kb = wave - rt * KB;
+    // this lane's place in the phase tile when it decodes
+    const int my_row = wave * RPC + lane / per_row;
+    const int my_m = lane % per_row;
+
+    for (int i = wave; i < kSLut / (4 * CBQ_WAVE); i += kSfWaves)
+        __builtin_amdgcn_global_load_lds(S.lut + i * 4 * CBQ_WAVE + 4 * lane,
+                                         (__attribute__((address_space(3))) void *)(s_lds + i * 4 * CBQ_WAVE),
+                                         16, 0, 0);
+
+    // items of this wave: (tile, chunk of the unit); all waves of the block
+    // walk the same count, so every barrier is reached by all of them
+    const int my_tiles = bid < n_tiles ? (n_tiles - bid + nbl - 1) / nbl : 0;
+    const int n_items = my_tiles * CPR;
+    auto item_chunk = [&](int k, bool &valid) {
+        const int tile = bid + (k / CPR) * nbl;
+        const int unit = tile * kSfWaves + wave;
+        valid = unit < n_units;
+        return valid ? (int64_t)unit * CPR + (k % CPR) : (int64_t)0;
+    };
+    // row offsets by scalar loads (a uniform address in the constant space),
+    // so waiting for them does not wait for the vector loads before them;
+    // every chunk load is issued (split_load_all), so the wait counts are static
+    const __attribute__((address_space(4))) uint32_t *const ro =
+        (const __attribute__((address_space(4))) uint32_t *)S.row_off;
+    auto load_item = [&](int k, SplitItem &it, uint32_t &H) {
+        bool v;
+        const int64_t c = __builtin_amdgcn_readfirstlane((int)item_chunk(k < n_items ? k : 0, v));
+        const uint32_t r0 = ro[c];
+        H = ro[c + 1] - r0;
+        H = H < (uint32_t)kSRows ? H : (uint32_t)kSRows;
+        split_load_all(it, S, c, r0, H, lane);
+    };
+    // x of one phase for lane (token rsub, k-block lane group j): 8 values.
+    // Every load is issued (tokens past T read token T - 1 and are zeroed,
+    // items past the last read the last), so the compiler's wait counts stay
+    // exact and a wait for x never drains the chunk loads issued after it.
+    const bool tok_on = rsub < T;
+    const float *const xrow = x + (size_t)(tok_on ? rsub : T - 1) * K;
+    auto load_x = [&](int k, int p, float (&xv)[8]) {
+        const int cc = (k < n_items ? k : (n_items > 0 ? n_items - 1 : 0)) % CPR;
+        __builtin_memcpy(xv, xrow + (size_t)cc * kSChunk + 64 * (4 * kb + j) + 8 * p, sizeof(xv));
+    };
+
+    // x two phases ahead (xq[p & 1] holds phase p); the next chunk's loads go
+    // out after the x loads of phase 2, so waiting for the x of phases 1
+    // and 2 leaves them in flight (loads complete in issue order)
+    SplitItem A, B;
+    uint32_t hA = 0, hB = 0;
+    load_item(0, A, hA);
+    float xq[2][8];
+    load_x(0, 0, xq[0]);
+    load_x(0, 1, xq[1]);
+    __syncthreads();                               // table staged: the barrier waits for the DMA
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+
+    for (int k = 0; k < n_items; k++) {
+        bool valid;
+        (void)item_chunk(k, valid);
+        split_stage(A, hA, s_slot, lane);
+        uint32_t pos = 30;                          // as split_decode
+        uint32_t d1 = 0;
+        const char *base = (const char *)s_lds + lane_addr;
+        uint32_t w0 = *(const uint32_t *)(base - 4 * kSSub);
+        uint32_t w1 = *(const uint32_t *)base;
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            uint32_t pr[4];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int g = 2 * p + h;
+                const uint32_t w2 = *(const uint32_t *)(base + (d1 + 1) * (4 * kSSub));
+                uint32_t w = __builtin_amdgcn_alignbit(w1, w0, pos);
+#pragma unroll
+                for (int u = 0; u < 4; u += 2) {
+                    const uint32_t e =
+                        *(const uint32_t *)((const char *)s_lds + (w & (4u * kSLut - 4u)));
+                    // bf16 of weights 4g+u and 4g+u+1: raw low byte, table high byte
+                    pr[2 * h + (u >> 1)] = __builtin_amdgcn_perm(
+                        e, A.raw[g], 0x06000700u | (uint32_t)u | ((uint32_t)(u + 1) << 16));
+                    w >>= (e & 31u);
+                    pos += e;
+                }
+                const uint32_t dn = __builtin_amdgcn_ubfe(pos, 5, 11);
+                w0 = dn != d1 ? w1 : w0;
+                w1 = dn != d1 ? w2 : w1;
+                d1 = dn;
+            }
+            uint32_t *ph = s_ph + (p & 1) * kSfPhaseWords;
+            *(u4 *)(ph + sf_slot(my_row, my_m, per_row)) =
+                valid ? u4{pr[0], pr[1], pr[2], pr[3]} : u4{0u, 0u, 0u, 0u};
+            // this phase's x parts, then x of phase p + 2 requested
+            cbq_u32x4 xb[3];
+            float xv[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) xv[e] = tok_on ? xq[p & 1][e] : 0.f;
+            cbq_split3(xv, xb[0], xb[1], xb[2]);
+            if (p < 6) load_x(k, p + 2, xq[p & 1]);
+            else load_x(k + 1, p - 6, xq[p & 1]);
+            if (p == 0) {
+                __builtin_amdgcn_sched_barrier(0);
+                load_item(k + 1, B, hB);           // past the last item: item 0 again
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __syncthreads();                       // the phase tile is complete
+            const u4 a = *(const u4 *)(ph + sf_slot(16 * rt + rsub, 4 * kb + j, per_row));
+#pragma unroll
+            for (int q = 0; q < 3; q++) acc = cbq_mfma_bf16(a, xb[q], acc);
+        }
+        if (k % CPR == CPR - 1) {
+            // tile done: the 16 partial tiles summed per row tile in k-block order
+            __syncthreads();                       // every wave's phase-7 reads are done
+            *(f4 *)(s_ph + 4 * (wave * CBQ_WAVE + lane)) = acc;
+            __syncthreads();
+            if (kb == 0) {
+                f4 sum = *(const f4 *)(s_ph + 4 * (wave * CBQ_WAVE + lane));
+                for (int q = 1; q < KB; q++) {
+                    const f4 v = *(const f4 *)(s_ph + 4 * ((wave + q) * CBQ_WAVE + lane));
+                    sum.x += v.x;
+                    sum.y += v.y;
+                    sum.z += v.z;
+                    sum.w += v.w;
+                }
+                const int tile = bid + (k / CPR) * nbl;
+                const int64_t row0 = (int64_t)tile * kSfWaves * RPC + 16 * rt + 4 * j;
+                const float vals[4] = {sum.x, sum.y, sum.z, sum.w};
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    if (row0 + v < M && rsub < T)
+                        out[(size_t)rsub * M + row0 + v] = from_f32<OT>(vals[v]);
+            }
+            __syncthreads();                       // partials read before phase 0 rewrites them
+            acc = f4{0.f, 0.f, 0.f, 0.f};
+        }
+        A = B;
+        hA = hB;
+    }
+}
+
 // ---- build ------------------------------------------------------------------
 
 // sym_code[i]: bit-reversed high-byte code | len << 24 of symbol i.
@@ -688,6 +884,65 @@ int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits
     }
 #undef CBQ_S2P
     return cbq_launch_status("split_to_packed_kernel");
+}
+
+int cbq_split_linear_fewtok_f32(const float *x, int T, int n, const cbq_split_matrix *const *mats,
+                                float *const *outs, const int *Ms, int K, hipStream_t stream)
+{
+    if (!x || T < 1 || n < 1 || n > kSMaxSeg || !mats || !outs || !Ms || K <= 0)
+        return CK_ERR_ARG;
+    const int RPC = K % kSChunk == 0 ? 1 : (K == 1024 || K == 2048) ? kSChunk / K : 0;
+    if (!RPC || ((uintptr_t)x & 15) != 0) return CK_ERR_ARG;
+    const int CPR = RPC == 1 ? K / kSChunk : 1;
+    SplitSegs segs = {};
+    segs.n = n;
+    int64_t tiles_sum = 0;
+    int tiles[kSMaxSeg];
+    for (int i = 0; i < n; i++) {
+        const cbq_split_matrix *m = mats[i];
+        if (!m || !m->cwords || !m->row_off || !m->raw || !m->lut || !outs[i] || Ms[i] <= 0)
+            return CK_ERR_ARG;
+        if ((int64_t)Ms[i] * K % kSChunk != 0 || m->n_chunks != (int64_t)Ms[i] * K / kSChunk)
+            return CK_ERR_ARG;
+        if (((uintptr_t)m->raw & 15) != 0 || ((uintptr_t)m->lut & 15) != 0 ||
+            ((uintptr_t)m->cwords & 15) != 0)
+            return CK_ERR_ARG;
+        SplitSeg &g = segs.s[i];
+        g.cwords = m->cwords;
+        g.row_off = m->row_off;
+        g.raw = m->raw;
+        g.lut = m->lut;
+        g.out = outs[i];
+        g.M = Ms[i];
+        const int units = RPC == 1 ? Ms[i] : Ms[i] / RPC;
+        tiles[i] = (units + kSfWaves - 1) / kSfWaves;
+        tiles_sum += tiles[i];
+    }
+    // one block per CU in all: a matrix gets one block per tile when the
+    // tiles fit, else blocks in proportion to its tiles (each block then
+    // walks several tiles, staging the table once)
+    const int cus = cbq_num_cus();
+    int blocks = 0;
+    for (int i = 0; i < n; i++) {
+        SplitSeg &g = segs.s[i];
+        g.block0 = blocks;
+        const int share =
+            tiles_sum <= cus ? tiles[i]
+                             : (int)std::max<int64_t>(1, (cus * (int64_t)tiles[i] + tiles_sum / 2) /
+                                                             tiles_sum);
+        g.nblocks = std::max(1, std::min(share, tiles[i]));
+        blocks += g.nblocks;
+    }
+    for (int t0 = 0; t0 < T; t0 += 16) {
+        const int tt = std::min(16, T - t0);
+        SplitSegs sg = segs;
+        for (int i = 0; i < n; i++) sg.s[i].out = outs[i] + (size_t)t0 * Ms[i];
+        hipLaunchKernelGGL(split_fewtok_kernel<float>, dim3(blocks), dim3(kSfWaves * CBQ_WAVE), 0,
+                           stream, x + (size_t)t0 * K, sg, tt, K, RPC, CPR);
+        const int rc = cbq_launch_status("split_fewtok_kernel");
+        if (rc) return rc;
+    }
+    return CK_SUCCESS;
 }
 
 }  // extern "C"

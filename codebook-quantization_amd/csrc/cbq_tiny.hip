@@ -71,43 +71,7 @@ __device__ __forceinline__ void wave_sync_lds()
 constexpr int kFtWaves = 8;
 constexpr int kFtThreads = kFtWaves * CBQ_WAVE;
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// bf16 bits of a (low half) and of b (high half), both truncated: v_perm
-// picks the upper two bytes of each
-__device__ __forceinline__ uint32_t hi_pair(uint32_t a, uint32_t b)
-{
-    return __builtin_amdgcn_perm(b, a, 0x07060302u);
-}
-
-// v = h + m + l exactly, each a bf16 number: r = v - h and l = r - m are
-// exact fp32 differences, and l has at most 8 significant bits
-__device__ __forceinline__ void split3(const float (&v)[8], u32x4 &h, u32x4 &m, u32x4 &l)
-{
-    uint32_t hp[4], mp[4], lp[4];
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-        const uint32_t a = __float_as_uint(v[e]), b = __float_as_uint(v[e + 1]);
-        const float ra = v[e] - __uint_as_float(a & 0xffff0000u);
-        const float rb = v[e + 1] - __uint_as_float(b & 0xffff0000u);
-        const uint32_t ua = __float_as_uint(ra), ub = __float_as_uint(rb);
-        const float la = ra - __uint_as_float(ua & 0xffff0000u);
-        const float lb = rb - __uint_as_float(ub & 0xffff0000u);
-        hp[e >> 1] = hi_pair(a, b);
-        mp[e >> 1] = hi_pair(ua, ub);
-        lp[e >> 1] = hi_pair(__float_as_uint(la), __float_as_uint(lb));
-    }
-    h = u32x4{hp[0], hp[1], hp[2], hp[3]};
-    m = u32x4{mp[0], mp[1], mp[2], mp[3]};
-    l = u32x4{lp[0], lp[1], lp[2], lp[3]};
-}
-
-__device__ __forceinline__ f4 mfma_bf16(u32x4 a, u32x4 b, f4 c)
-{
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
+typedef cbq_u32x4 u32x4;
 
 // x of one lane and step: 32 values of token l % 16, group l / 16 of the step
 template <typename XT> struct FtX;
@@ -121,7 +85,7 @@ template <> struct FtX<float> {
             float q[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) q[e] = __uint_as_float(xw[8 * c + e]);
-            split3(q, b[c][0], b[c][1], b[c][2]);
+            cbq_split3(q, b[c][0], b[c][1], b[c][2]);
         }
     }
 };
@@ -271,14 +235,14 @@ __global__ __launch_bounds__(kFtThreads) void fixed_fewtok_kernel(
             u32x4 a[4];
 #pragma unroll
             for (int c = 0; c < 4; c++)
-                a[c] = u32x4{hi_pair(__float_as_uint(wv[8 * c]), __float_as_uint(wv[8 * c + 1])),
-                             hi_pair(__float_as_uint(wv[8 * c + 2]), __float_as_uint(wv[8 * c + 3])),
-                             hi_pair(__float_as_uint(wv[8 * c + 4]), __float_as_uint(wv[8 * c + 5])),
-                             hi_pair(__float_as_uint(wv[8 * c + 6]), __float_as_uint(wv[8 * c + 7]))};
+                a[c] = u32x4{cbq_hi_pair(__float_as_uint(wv[8 * c]), __float_as_uint(wv[8 * c + 1])),
+                             cbq_hi_pair(__float_as_uint(wv[8 * c + 2]), __float_as_uint(wv[8 * c + 3])),
+                             cbq_hi_pair(__float_as_uint(wv[8 * c + 4]), __float_as_uint(wv[8 * c + 5])),
+                             cbq_hi_pair(__float_as_uint(wv[8 * c + 6]), __float_as_uint(wv[8 * c + 7]))};
 #pragma unroll
             for (int c = 0; c < 4; c++)
 #pragma unroll
-                for (int p = 0; p < FtX<XT>::kParts; p++) acc[t] = mfma_bf16(a[c], xb[c][p], acc[t]);
+                for (int p = 0; p < FtX<XT>::kParts; p++) acc[t] = cbq_mfma_bf16(a[c], xb[c][p], acc[t]);
             if (wsplit) {                          // codebook not bf16: w = wh + wm + wl
 #pragma unroll
                 for (int c = 0; c < 4; c++) {
@@ -286,10 +250,10 @@ __global__ __launch_bounds__(kFtThreads) void fixed_fewtok_kernel(
 #pragma unroll
                     for (int e = 0; e < 8; e++) q8[e] = wv[8 * c + e];
                     u32x4 wh, wm, wl;
-                    split3(q8, wh, wm, wl);
-                    acc[t] = mfma_bf16(wm, xb[c][0], acc[t]);
-                    acc[t] = mfma_bf16(wl, xb[c][0], acc[t]);
-                    if (FtX<XT>::kParts > 1) acc[t] = mfma_bf16(wm, xb[c][1], acc[t]);
+                    cbq_split3(q8, wh, wm, wl);
+                    acc[t] = cbq_mfma_bf16(wm, xb[c][0], acc[t]);
+                    acc[t] = cbq_mfma_bf16(wl, xb[c][0], acc[t]);
+                    if (FtX<XT>::kParts > 1) acc[t] = cbq_mfma_bf16(wm, xb[c][1], acc[t]);
                 }
             }
         }

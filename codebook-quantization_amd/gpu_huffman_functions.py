@@ -348,13 +348,45 @@ def huffman_prefill(sym: "SymbolDecoder", x: torch.Tensor, M: int, K: int,
     return linear_from_packed(x, packed, bits, M, K, codebook)
 
 
+FEWTOK_MAX_T = 32       # up to two 16-token launches of the fused kernel
+
+
+def split_fewtok_eligible(K: int) -> bool:
+    """Shapes cbq_split_linear_fewtok_f32 takes: whole 4096-symbol chunks per
+    row piece (K % 4096 == 0) or whole rows per chunk (K = 1024, 2048)."""
+    return K % hc.CHUNK_SYMBOLS == 0 or K in (1024, 2048)
+
+
 def split_prefill(split, inv: torch.Tensor, x: torch.Tensor, M: int, K: int,
                   codebook: torch.Tensor) -> torch.Tensor:
-    """y [T, M] for batched fp32 tokens from the split format: decoded
-    straight to a transient fixed-width stream (cbq_split_to_packed, one
-    table read per two weights) and multiplied by ck_linear_f32's kernels."""
+    """y [T, M] for batched fp32 tokens from the split format.  Up to 32
+    tokens (and a shape it takes): one fused launch per 16 tokens
+    (cbq_split_linear_fewtok_f32), every weight decoded once into LDS and
+    multiplied on the matrix cores, no transient buffer.  Otherwise the
+    format is decoded to a transient fixed-width stream (cbq_split_to_packed,
+    one table read per two weights) and multiplied by ck_linear_f32's
+    kernels."""
+    T = int(x.shape[0])
+    if 1 <= T <= FEWTOK_MAX_T and split_fewtok_eligible(K) and x.data_ptr() % 16 == 0:
+        return split_fewtok([split], x, [M], K)[0]
     packed, bits = _packed_for_gemm(split, M * K, int(codebook.numel()), x.device, inv)
     return linear_from_packed(x, packed, bits, M, K, codebook)
+
+
+def split_fewtok(splits, x: torch.Tensor, Ms, K: int):
+    """[y_i [T, M_i]] for up to four split-format matrices sharing x [T, K]
+    (fp32, 16-byte aligned), one fused launch per 16 tokens
+    (cbq_split_linear_fewtok_f32; split_fewtok_eligible(K) must hold)."""
+    n = len(splits)
+    T = int(x.shape[0])
+    outs = [torch.empty(T, int(M), dtype=torch.float32, device=x.device) for M in Ms]
+    mats = (ctypes.POINTER(nat.SplitMatrix) * n)(*[ctypes.pointer(sp[1]) for sp in splits])
+    optr = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    mptr = (ctypes.c_int * n)(*[int(M) for M in Ms])
+    nat.check(nat.load().cbq_split_linear_fewtok_f32(x.data_ptr(), T, n, mats, optr, mptr, K,
+                                                     nat.stream_ptr(x.device)),
+              "cbq_split_linear_fewtok_f32")
+    return outs
 
 
 def split_indices(split, inv: torch.Tensor, n: int, device) -> torch.Tensor:

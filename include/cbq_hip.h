@@ -392,6 +392,20 @@ int cbq_pack_indices(const int32_t *indices, int64_t n, int bits, uint8_t *packe
 int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits,
                         uint8_t *packed, hipStream_t stream);
 
+/* y_i[T, M_i] = x[T, K] @ W_i^T for up to four split-format matrices sharing
+ * x (one launch), any T >= 1 (fp32 x and outputs, 16-byte aligned x), in
+ * launches of up to 16 tokens: every weight is decoded once per launch into
+ * LDS and multiplied on the bf16 matrix cores (x split exactly into three
+ * bf16 parts), never written out.  K % 4096 == 0, or K = 1024 or 2048
+ * (whole rows per chunk); M_i * K a whole number of 4096-weight chunks;
+ * other shapes return CK_ERR_ARG.  Never allocates.  Replaces, for Huffman
+ * modules whose split format exists, the batched-token path of
+ * huffman_matmul (src/compressed_matmul.c:208-239 over several rows of x,
+ * src/gpu_huffman_functions.py:834-855), which decodes to a transient index
+ * buffer first (rocm/huffman_kernel.hip:61-156). */
+int cbq_split_linear_fewtok_f32(const float *x, int T, int n, const cbq_split_matrix *const *mats,
+                                float *const *outs, const int *Ms, int K, hipStream_t stream);
+
 /* ==== upload helpers ===================================================== */
 
 /* Allocate device memory (hipMalloc) and copy `nbytes` host bytes into it
