@@ -669,8 +669,8 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
 
         def run(T=T, xs=xs):
             # the decoder's launches: q/k/v and gate/up grouped (one fused
-            # launch each, matrices sharing x); shapes the fused kernel does
-            # not take (down, K = 6144) through split_prefill's transient stream
+            # launch each, matrices sharing x); a shape the fused kernel does
+            # not take would go through split_prefill's transient stream
             for e in plan:
                 ns = list(e) if isinstance(e, tuple) else [e]
                 M0, K = huff[ns[0]].shape
@@ -685,11 +685,9 @@ def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
             ms, _ = timed_graph(torch, run, max(3, args.steps // 2), 1)
         hu[f"T{T}"] = {"ms_per_step": round(ms, 3),
                        "vs_T1": round(ms / ms1, 3),
-                       "note": "the decoder's launch list: q/k/v, o and gate/up straight from "
-                               "the split format on the matrix cores (cbq_split_linear_fewtok_f32,"
-                               " q/k/v and gate/up one launch each); down (K = 6144) decoded to a "
-                               "transient fixed-width stream and ck_linear_f32's kernels; "
-                               "graph-replayed"}
+                       "note": "the decoder's launch list straight from the split format on "
+                               "the matrix cores (cbq_split_linear_fewtok_f32; q/k/v and gate/up "
+                               "one launch each, down in row groups of 2); graph-replayed"}
     out["huffman"] = {"sweep": hu, "bits_per_weight_resident": round(8.0 * res_b / n_w, 3),
                       "bits_per_weight_stream_incl_index":
                           round(8.0 * sum(stream_bytes.values()) / n_w, 3)}

@@ -95,7 +95,9 @@ SIGNATURES = {
     "cbq_split_bits": (_i, [_vp, _i64, _vp, _i, _vp, _vp]),
     "cbq_pack_indices": (_i, [_vp, _i64, _i, _vp, _vp]),
     "cbq_split_to_packed": (_i, [_vp, _vp, _i, _vp, _vp]),
-    "cbq_split_linear_fewtok_f32": (_i, [_vp, _i, _i, _vp, _vp, _vp, _i, _vp]),
+    "cbq_split_linear_fewtok_f32": (_i, [_vp, _i, _i, _vp, _vp, _vp, _i, _vp, ctypes.c_size_t,
+                                         _vp]),
+    "cbq_split_fewtok_ws_bytes": (ctypes.c_size_t, [_i]),
     "cbq_split_pack": (_i, [_vp, _i64, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
     "cbq_split_linear_f32": (_i, [_vp, _vp, _vp, _i, ctypes.c_float, _i, _vp, _vp, _vp, _i,
                                   _vp]),

@@ -525,38 +525,87 @@ __global__ __launch_bounds__(kPackWaves * CBQ_WAVE) void split_to_packed_kernel(
 
 // ---- a few tokens straight from the split format -------------------------------
 //
-// y[t, r] = W[r, :] . x[t, :] for 2 <= T <= 16 tokens on the bf16 matrix cores,
+// y[t, r] = W[r, :] . x[t, :] for up to 16 tokens on the bf16 matrix cores,
 // every weight decoded once for all tokens and never written out.  The split
 // weights are bf16 numbers; x is split exactly into three bf16 parts
 // (cbq_split3), so each product is exact and only the fp32 summation order
 // differs from the reference loop (src/compressed_matmul.c:208-239).
 //
-// Block: 16 waves (one per CU, persistent over tiles).  A tile is 16 "units":
-// K % 4096 == 0: 16 rows, each of K / 4096 chunks (CPR), a wave per row;
-// K = 1024 or 2048: 16 chunks of 4096 / K rows each (RPC), a wave per chunk.
-// A wave decodes its chunk in eight phases of 8 weights per lane (lane l
-// holds sub-block l: 64 consecutive weights of a row, as the one-token
-// GEMV's decode) and writes them as bf16 to a 16 KiB phase tile in LDS,
-// [16 RPC rows][64 / RPC sub-blocks][8 values], sub-block slot m ^ (row & 15).
-// After a barrier the 16 waves run the phase's MFMAs: wave w takes row tile
-// w / (16 / RPC) and k-block w % (16 / RPC) (4 sub-blocks x 8 columns), so
-// its x columns are 4096 cc + 64 (4 kb + j) + 8 p + e for lane group j.
-// The phase tiles are double-buffered: one barrier per phase.  At the end of
-// a tile the waves' 16 x 16 partials are summed through LDS in k-block order.
+// Block: 16 waves (one per CU, persistent over tiles).  A tile is TR whole
+// rows (SfGeo): with K % 4096 == 0, 16 rows, wave w decoding row w chunk by
+// chunk (CPR chunks); otherwise GPT groups of GR rows (GR = 4096 / gcd(K,
+// 4096), RCH chunks each), wave w decoding chunk w of the tile.  A wave
+// decodes its chunk in eight phases of 8 weights per lane (lane l holds
+// sub-block l: 64 consecutive weights of a row, as the one-token GEMV's
+// decode) and writes them as bf16 to a phase tile in LDS, [TR rows][per_row
+// sub-blocks][8 values], sub-block slot m ^ (row & 15).  After one barrier
+// the block runs the phase's MFMAs: pair q (row tile q / KBt, k-block
+// q % KBt: 4 sub-blocks x 8 columns) goes to wave q % 16, in pass q / 16
+// (at most two passes, npairs <= 32); the x columns of lane group j are
+// 4096 cc + 64 (4 kb + j) + 8 p + e.  The phase tiles are double-buffered.
+// At the end of a tile the pairs' 16 x 16 partials are summed through LDS,
+// per row tile in k-block order.
 //
 // LDS: the two-code table at address 0 (64 KiB), 16 code slots (64 KiB),
-// two phase tiles (32 KiB): 160 KiB.
+// two phase tiles (32 KiB; the partials reuse them): 160 KiB.
 constexpr int kSfWaves = 16;
-constexpr int kSfPhaseWords = 4096;               // 16 KiB: 16 RPC rows x 64 / RPC x 4 words
+constexpr int kSfPhaseWords = 4096;               // 16 KiB
+
+struct SfGeo {
+    int GR;       // rows per group
+    int RCH;      // chunks per group
+    int GPT;      // groups per tile
+    int CPR;      // chunks per row, walked in turn by one wave (K % 4096 == 0), else 1
+    int TR;       // rows per tile (GPT * GR)
+    int per_row;  // sub-blocks of a row in a phase tile
+    int KBt;      // k-blocks per row tile (per_row / 4)
+    int npairs;   // (row tile, k-block) pairs: ceil(TR / 16) * KBt, <= 32
+};
 
 __device__ __forceinline__ int sf_slot(int row, int m, int per_row)
 {
     return (row * per_row + (m ^ (row & 15))) * 4;   // word offset of (row, sub-block m)
 }
 
-template <typename OT>
+// x operands of one MFMA step for this lane: 8 fp32 values split in the
+// kernel, or (PRE) the three bf16 parts read from the fragment-order
+// workspace that split_x_parts_kernel wrote: part q of columns 8 piece .. +7
+// of token n is the 16-byte word (piece * 3 + q) * 16 + n, so for one piece
+// and part the 16 tokens are 256 contiguous bytes.
+template <bool PRE> struct SfX;
+template <> struct SfX<false> {
+    float v[8];
+};
+template <> struct SfX<true> {
+    cbq_u32x4 q[3];
+};
+
+__global__ __launch_bounds__(256) void split_x_parts_kernel(const float *__restrict__ x, int T,
+                                                            int K, cbq_u32x4 *__restrict__ ws)
+{
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t piece = i >> 4;
+    const int n = (int)(i & 15);
+    if (piece >= K / 8) return;
+    float v[8];
+    if (n < T) {
+        __builtin_memcpy(v, x + (size_t)n * K + 8 * piece, sizeof(v));
+    } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = 0.f;
+    }
+    cbq_u32x4 h, m, l;
+    cbq_split3(v, h, m, l);
+    ws[(piece * 3 + 0) * 16 + n] = h;
+    ws[(piece * 3 + 1) * 16 + n] = m;
+    ws[(piece * 3 + 2) * 16 + n] = l;
+}
+
+// NSUB: MFMA passes per phase (1 when npairs <= 16, else 2).
+template <typename OT, bool PRE, int NSUB>
 __global__ __launch_bounds__(kSfWaves * CBQ_WAVE) void split_fewtok_kernel(
-    const float *__restrict__ x, SplitSegs segs, int T, int K, int RPC, int CPR)
+    const float *__restrict__ x, const cbq_u32x4 *__restrict__ xws, SplitSegs segs, int T, int K,
+    SfGeo G)
 {
     // the block's matrix: blocks [block0, block0 + nblocks) of the grid
     int sidx = 0;
@@ -567,8 +616,8 @@ __global__ __launch_bounds__(kSfWaves * CBQ_WAVE) void split_fewtok_kernel(
     const int M = S.M;
     OT *__restrict__ const out = (OT *)S.out;
     const int bid = (int)blockIdx.x - S.block0, nbl = S.nblocks;
-    const int n_units = RPC == 1 ? M : M / RPC;    // rows, or chunks of RPC rows
-    const int n_tiles = (n_units + kSfWaves - 1) / kSfWaves;
+    const int groups = M / G.GR;
+    const int n_tiles = (groups + G.GPT - 1) / G.GPT;
     __shared__ __attribute__((aligned(16))) uint32_t
         s_lds[kSLut + kSfWaves * kSSlotWords + 2 * kSfPhaseWords];
     uint32_t *const s_ph = s_lds + kSLut + kSfWaves * kSSlotWords;
@@ -578,27 +627,40 @@ __global__ __launch_bounds__(kSfWaves * CBQ_WAVE) void split_fewtok_kernel(
     const int lane_addr =
         __builtin_amdgcn_readfirstlane(4 * (kSLut + wave * kSSlotWords)) + 4 * lane;
     const int rsub = lane & 15, j = lane >> 4;
-    const int per_row = 64 / RPC;                  // sub-blocks of a row in one chunk
-    const int KB = 16 / RPC;                       // k-blocks per row tile
-    const int rt = wave / KB, kb = wave - rt * KB;
-    // this lane's place in the phase tile when it decodes
-    const int my_row = wave * RPC + lane / per_row;
-    const int my_m = lane % per_row;
+    const int per_row = G.per_row;
+    // this lane's place in the phase tile when it decodes: chunk wave % RCH
+    // of group wave / RCH (a chunk's sub-block l starts 64 l into it)
+    const bool decodes = wave < G.GPT * G.RCH;
+    const int cw = G.CPR > 1 ? kSChunk : K;        // columns a phase tile row covers
+    const int f = kSChunk * (wave % G.RCH) + 64 * lane;
+    const int my_row = (wave / G.RCH) * G.GR + f / cw;
+    const int my_m = (f % cw) >> 6;
+    // MFMA pairs of this wave: q = wave + 16 s
+    int rt[NSUB], kb[NSUB];
+    bool on[NSUB];
+#pragma unroll
+    for (int sp = 0; sp < NSUB; sp++) {
+        const int q = wave + kSfWaves * sp;
+        on[sp] = q < G.npairs;
+        const int qq = on[sp] ? q : 0;
+        rt[sp] = qq / G.KBt;
+        kb[sp] = qq - rt[sp] * G.KBt;
+    }
 
     for (int i = wave; i < kSLut / (4 * CBQ_WAVE); i += kSfWaves)
         __builtin_amdgcn_global_load_lds(S.lut + i * 4 * CBQ_WAVE + 4 * lane,
                                          (__attribute__((address_space(3))) void *)(s_lds + i * 4 * CBQ_WAVE),
                                          16, 0, 0);
 
-    // items of this wave: (tile, chunk of the unit); all waves of the block
+    // items of this wave: (tile, chunk cc of its row); all waves of the block
     // walk the same count, so every barrier is reached by all of them
     const int my_tiles = bid < n_tiles ? (n_tiles - bid + nbl - 1) / nbl : 0;
-    const int n_items = my_tiles * CPR;
+    const int n_items = my_tiles * G.CPR;
     auto item_chunk = [&](int k, bool &valid) {
-        const int tile = bid + (k / CPR) * nbl;
-        const int unit = tile * kSfWaves + wave;
-        valid = unit < n_units;
-        return valid ? (int64_t)unit * CPR + (k % CPR) : (int64_t)0;
+        const int tile = bid + (k / G.CPR) * nbl;
+        valid = decodes && tile * G.GPT + wave / G.RCH < groups;
+        const int64_t unit = (int64_t)tile * G.GPT * G.RCH + wave;
+        return valid ? unit * G.CPR + (k % G.CPR) : (int64_t)0;
     };
     // row offsets by scalar loads (a uniform address in the constant space),
     // so waiting for them does not wait for the vector loads before them;
@@ -613,28 +675,41 @@ __global__ __launch_bounds__(kSfWaves * CBQ_WAVE) void split_fewtok_kernel(
         H = H < (uint32_t)kSRows ? H : (uint32_t)kSRows;
         split_load_all(it, S, c, r0, H, lane);
     };
-    // x of one phase for lane (token rsub, k-block lane group j): 8 values.
-    // Every load is issued (tokens past T read token T - 1 and are zeroed,
-    // items past the last read the last), so the compiler's wait counts stay
-    // exact and a wait for x never drains the chunk loads issued after it.
+    // x of one MFMA step (phase p, pass sp) for lane (token rsub, k-block
+    // lane group j).  Every load is issued (tokens past T read token T - 1
+    // and are zeroed, items past the last read the last), so the compiler's
+    // wait counts stay exact and a wait for x never drains the chunk loads
+    // issued after it.
     const bool tok_on = rsub < T;
     const float *const xrow = x + (size_t)(tok_on ? rsub : T - 1) * K;
-    auto load_x = [&](int k, int p, float (&xv)[8]) {
-        const int cc = (k < n_items ? k : (n_items > 0 ? n_items - 1 : 0)) % CPR;
-        __builtin_memcpy(xv, xrow + (size_t)cc * kSChunk + 64 * (4 * kb + j) + 8 * p, sizeof(xv));
+    auto load_x = [&](int k, int p, int sp, SfX<PRE> &xv) {
+        const int cc = (k < n_items ? k : (n_items > 0 ? n_items - 1 : 0)) % G.CPR;
+        const size_t col = (size_t)cc * kSChunk + 64 * (4 * kb[sp] + j) + 8 * p;
+        if constexpr (PRE) {
+            const cbq_u32x4 *w = xws + (col / 8) * 48 + rsub;
+#pragma unroll
+            for (int q = 0; q < 3; q++) xv.q[q] = w[16 * q];
+        } else {
+            __builtin_memcpy(xv.v, xrow + col, sizeof(xv.v));
+        }
     };
 
-    // x two phases ahead (xq[p & 1] holds phase p); the next chunk's loads go
-    // out after the x loads of phase 2, so waiting for the x of phases 1
-    // and 2 leaves them in flight (loads complete in issue order)
+    // x PD steps ahead (step u = NSUB p + sp in slot u % PD); the next
+    // chunk's loads go out after the x loads issued in phase 0, so waiting
+    // for the x of the next steps leaves them in flight (loads complete in
+    // issue order).  PRE: the parts take 12 registers a step, one step ahead.
+    constexpr int PD = PRE ? 1 : 2;
+    constexpr int NSTEP = 8 * NSUB;
     SplitItem A, B;
     uint32_t hA = 0, hB = 0;
     load_item(0, A, hA);
-    float xq[2][8];
-    load_x(0, 0, xq[0]);
-    load_x(0, 1, xq[1]);
+    SfX<PRE> xq[PD];
+#pragma unroll
+    for (int d = 0; d < PD; d++) load_x(0, d / NSUB, d % NSUB, xq[d]);
     __syncthreads();                               // table staged: the barrier waits for the DMA
-    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+    f4 acc[NSUB];
+#pragma unroll
+    for (int sp = 0; sp < NSUB; sp++) acc[sp] = f4{0.f, 0.f, 0.f, 0.f};
 
     for (int k = 0; k < n_items; k++) {
         bool valid;
@@ -669,50 +744,76 @@ __global__ __launch_bounds__(kSfWaves * CBQ_WAVE) void split_fewtok_kernel(
                 d1 = dn;
             }
             uint32_t *ph = s_ph + (p & 1) * kSfPhaseWords;
-            *(u4 *)(ph + sf_slot(my_row, my_m, per_row)) =
-                valid ? u4{pr[0], pr[1], pr[2], pr[3]} : u4{0u, 0u, 0u, 0u};
-            // this phase's x parts, then x of phase p + 2 requested
-            cbq_u32x4 xb[3];
-            float xv[8];
+            if (decodes)
+                *(u4 *)(ph + sf_slot(my_row, my_m, per_row)) =
+                    valid ? u4{pr[0], pr[1], pr[2], pr[3]} : u4{0u, 0u, 0u, 0u};
+            // this phase's x parts; the x of the step PD ahead requested
+            cbq_u32x4 xb[NSUB][3];
 #pragma unroll
-            for (int e = 0; e < 8; e++) xv[e] = tok_on ? xq[p & 1][e] : 0.f;
-            cbq_split3(xv, xb[0], xb[1], xb[2]);
-            if (p < 6) load_x(k, p + 2, xq[p & 1]);
-            else load_x(k + 1, p - 6, xq[p & 1]);
+            for (int sp = 0; sp < NSUB; sp++) {
+                const int u = NSUB * p + sp;
+                if constexpr (PRE) {
+#pragma unroll
+                    for (int q = 0; q < 3; q++) xb[sp][q] = xq[u % PD].q[q];
+                } else {
+                    float xv[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) xv[e] = tok_on ? xq[u % PD].v[e] : 0.f;
+                    cbq_split3(xv, xb[sp][0], xb[sp][1], xb[sp][2]);
+                }
+                const int un = u + PD;
+                if (un < NSTEP) load_x(k, un / NSUB, un % NSUB, xq[u % PD]);
+                else load_x(k + 1, (un - NSTEP) / NSUB, (un - NSTEP) % NSUB, xq[u % PD]);
+            }
             if (p == 0) {
                 __builtin_amdgcn_sched_barrier(0);
                 load_item(k + 1, B, hB);           // past the last item: item 0 again
                 __builtin_amdgcn_sched_barrier(0);
             }
             __syncthreads();                       // the phase tile is complete
-            const u4 a = *(const u4 *)(ph + sf_slot(16 * rt + rsub, 4 * kb + j, per_row));
 #pragma unroll
-            for (int q = 0; q < 3; q++) acc = cbq_mfma_bf16(a, xb[q], acc);
+            for (int sp = 0; sp < NSUB; sp++) {
+                if (on[sp]) {                      // wave-uniform
+                    int r = 16 * rt[sp] + rsub;
+                    r = r < G.TR ? r : G.TR - 1;   // rows past the tile: not written
+                    const u4 a = *(const u4 *)(ph + sf_slot(r, 4 * kb[sp] + j, per_row));
+#pragma unroll
+                    for (int q = 0; q < 3; q++) acc[sp] = cbq_mfma_bf16(a, xb[sp][q], acc[sp]);
+                }
+            }
         }
-        if (k % CPR == CPR - 1) {
-            // tile done: the 16 partial tiles summed per row tile in k-block order
+        if (k % G.CPR == G.CPR - 1) {
+            // tile done: the pairs' partial tiles summed per row tile in
+            // k-block order (partial q at s_ph + 256 q words, both phase tiles)
             __syncthreads();                       // every wave's phase-7 reads are done
-            *(f4 *)(s_ph + 4 * (wave * CBQ_WAVE + lane)) = acc;
+#pragma unroll
+            for (int sp = 0; sp < NSUB; sp++)
+                if (on[sp])
+                    *(f4 *)(s_ph + 256 * (wave + kSfWaves * sp) + 4 * lane) = acc[sp];
             __syncthreads();
-            if (kb == 0) {
-                f4 sum = *(const f4 *)(s_ph + 4 * (wave * CBQ_WAVE + lane));
-                for (int q = 1; q < KB; q++) {
-                    const f4 v = *(const f4 *)(s_ph + 4 * ((wave + q) * CBQ_WAVE + lane));
+            const int NRT = (G.TR + 15) / 16;
+            if (wave < NRT) {
+                const int r0 = wave;
+                f4 sum = *(const f4 *)(s_ph + 256 * (r0 * G.KBt) + 4 * lane);
+                for (int q = 1; q < G.KBt; q++) {
+                    const f4 v = *(const f4 *)(s_ph + 256 * (r0 * G.KBt + q) + 4 * lane);
                     sum.x += v.x;
                     sum.y += v.y;
                     sum.z += v.z;
                     sum.w += v.w;
                 }
-                const int tile = bid + (k / CPR) * nbl;
-                const int64_t row0 = (int64_t)tile * kSfWaves * RPC + 16 * rt + 4 * j;
+                const int tile = bid + (k / G.CPR) * nbl;
+                const int rloc = 16 * r0 + 4 * j;          // first of this lane's 4 rows
+                const int64_t row0 = (int64_t)tile * G.TR + rloc;
                 const float vals[4] = {sum.x, sum.y, sum.z, sum.w};
 #pragma unroll
                 for (int v = 0; v < 4; v++)
-                    if (row0 + v < M && rsub < T)
+                    if (rloc + v < G.TR && row0 + v < M && rsub < T)
                         out[(size_t)rsub * M + row0 + v] = from_f32<OT>(vals[v]);
             }
             __syncthreads();                       // partials read before phase 0 rewrites them
-            acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int sp = 0; sp < NSUB; sp++) acc[sp] = f4{0.f, 0.f, 0.f, 0.f};
         }
         A = B;
         hA = hB;
@@ -886,14 +987,49 @@ int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits
     return cbq_launch_status("split_to_packed_kernel");
 }
 
+size_t cbq_split_fewtok_ws_bytes(int K) { return K > 0 ? (size_t)K * 96 : 0; }
+
+// The tile geometry of split_fewtok_kernel at this K; false when it does not
+// take the shape.
+static bool sf_geometry(int K, SfGeo &g)
+{
+    if (K <= 0 || K % 1024 != 0) return false;
+    if (K % kSChunk == 0) {                        // a wave per row, K / 4096 chunks in turn
+        g.GR = 1;
+        g.RCH = 1;
+        g.GPT = kSfWaves;
+        g.CPR = K / kSChunk;
+        g.per_row = kSSub;
+    } else {
+        int a = K, b = kSChunk;                    // gcd(K, 4096)
+        while (b) {
+            const int t = a % b;
+            a = b;
+            b = t;
+        }
+        g.GR = kSChunk / a;
+        g.RCH = K / a;
+        g.GPT = kSfWaves / g.RCH;
+        g.CPR = 1;
+        g.per_row = K / kSSub;
+        if (g.GPT < 1) return false;
+    }
+    g.TR = g.GPT * g.GR;
+    g.KBt = g.per_row / 4;
+    g.npairs = (g.TR + 15) / 16 * g.KBt;
+    // the phase tile (TR x per_row x 16 bytes) fits 16 KiB; at most two passes
+    return g.per_row % 16 == 0 && g.TR * g.per_row * 4 <= kSfPhaseWords && g.npairs <= 32 &&
+           g.npairs >= 1;
+}
+
 int cbq_split_linear_fewtok_f32(const float *x, int T, int n, const cbq_split_matrix *const *mats,
-                                float *const *outs, const int *Ms, int K, hipStream_t stream)
+                                float *const *outs, const int *Ms, int K, void *ws,
+                                size_t ws_bytes, hipStream_t stream)
 {
     if (!x || T < 1 || n < 1 || n > kSMaxSeg || !mats || !outs || !Ms || K <= 0)
         return CK_ERR_ARG;
-    const int RPC = K % kSChunk == 0 ? 1 : (K == 1024 || K == 2048) ? kSChunk / K : 0;
-    if (!RPC || ((uintptr_t)x & 15) != 0) return CK_ERR_ARG;
-    const int CPR = RPC == 1 ? K / kSChunk : 1;
+    SfGeo geo;
+    if (!sf_geometry(K, geo) || ((uintptr_t)x & 15) != 0) return CK_ERR_ARG;
     SplitSegs segs = {};
     segs.n = n;
     int64_t tiles_sum = 0;
@@ -902,7 +1038,8 @@ int cbq_split_linear_fewtok_f32(const float *x, int T, int n, const cbq_split_ma
         const cbq_split_matrix *m = mats[i];
         if (!m || !m->cwords || !m->row_off || !m->raw || !m->lut || !outs[i] || Ms[i] <= 0)
             return CK_ERR_ARG;
-        if ((int64_t)Ms[i] * K % kSChunk != 0 || m->n_chunks != (int64_t)Ms[i] * K / kSChunk)
+        if (Ms[i] % geo.GR != 0 || (int64_t)Ms[i] * K % kSChunk != 0 ||
+            m->n_chunks != (int64_t)Ms[i] * K / kSChunk)
             return CK_ERR_ARG;
         if (((uintptr_t)m->raw & 15) != 0 || ((uintptr_t)m->lut & 15) != 0 ||
             ((uintptr_t)m->cwords & 15) != 0)
@@ -914,8 +1051,8 @@ int cbq_split_linear_fewtok_f32(const float *x, int T, int n, const cbq_split_ma
         g.lut = m->lut;
         g.out = outs[i];
         g.M = Ms[i];
-        const int units = RPC == 1 ? Ms[i] : Ms[i] / RPC;
-        tiles[i] = (units + kSfWaves - 1) / kSfWaves;
+        const int groups = Ms[i] / geo.GR;
+        tiles[i] = (groups + geo.GPT - 1) / geo.GPT;
         tiles_sum += tiles[i];
     }
     // one block per CU in all: a matrix gets one block per tile when the
@@ -933,12 +1070,29 @@ int cbq_split_linear_fewtok_f32(const float *x, int T, int n, const cbq_split_ma
         g.nblocks = std::max(1, std::min(share, tiles[i]));
         blocks += g.nblocks;
     }
+    // with a workspace, x's three bf16 parts are written once per 16 tokens
+    // in fragment order and the GEMM loads them ready-made
+    const bool pre = ws && ws_bytes >= cbq_split_fewtok_ws_bytes(K) && ((uintptr_t)ws & 15) == 0;
+    const bool two = geo.npairs > kSfWaves;
+    if (two && !pre) return CK_ERR_ARG;            // two passes need the staged x parts
     for (int t0 = 0; t0 < T; t0 += 16) {
         const int tt = std::min(16, T - t0);
         SplitSegs sg = segs;
         for (int i = 0; i < n; i++) sg.s[i].out = outs[i] + (size_t)t0 * Ms[i];
-        hipLaunchKernelGGL(split_fewtok_kernel<float>, dim3(blocks), dim3(kSfWaves * CBQ_WAVE), 0,
-                           stream, x + (size_t)t0 * K, sg, tt, K, RPC, CPR);
+        const float *xt = x + (size_t)t0 * K;
+        const cbq_u32x4 *xw = pre ? (const cbq_u32x4 *)ws : nullptr;
+        if (pre) {
+            const int64_t threads = (int64_t)(K / 8) * 16;
+            hipLaunchKernelGGL(split_x_parts_kernel, dim3((unsigned)((threads + 255) / 256)),
+                               dim3(256), 0, stream, xt, tt, K, (cbq_u32x4 *)ws);
+        }
+#define CBQ_SF(PRE, NS)                                                                          \
+    hipLaunchKernelGGL((split_fewtok_kernel<float, PRE, NS>), dim3(blocks),                       \
+                       dim3(kSfWaves * CBQ_WAVE), 0, stream, xt, xw, sg, tt, K, geo)
+        if (pre && two) CBQ_SF(true, 2);
+        else if (pre) CBQ_SF(true, 1);
+        else CBQ_SF(false, 1);
+#undef CBQ_SF
         const int rc = cbq_launch_status("split_fewtok_kernel");
         if (rc) return rc;
     }

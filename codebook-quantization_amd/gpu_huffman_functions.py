@@ -26,6 +26,7 @@ format and the stream is freed (HuffmanCodebookLinear's `layout`).
 from __future__ import annotations
 
 import ctypes
+import math
 from typing import Optional, Tuple
 
 import numpy as np
@@ -352,9 +353,21 @@ FEWTOK_MAX_T = 32       # up to two 16-token launches of the fused kernel
 
 
 def split_fewtok_eligible(K: int) -> bool:
-    """Shapes cbq_split_linear_fewtok_f32 takes: whole 4096-symbol chunks per
-    row piece (K % 4096 == 0) or whole rows per chunk (K = 1024, 2048)."""
-    return K % hc.CHUNK_SYMBOLS == 0 or K in (1024, 2048)
+    """Shapes cbq_split_linear_fewtok_f32 takes (its tile geometry): K % 4096
+    == 0, or K % 1024 == 0 with the rows of a chunk group tiling 16 waves in
+    at most two MFMA passes (K = 1024, 2048, 3072, 5120, 6144, 7168)."""
+    ch = hc.CHUNK_SYMBOLS
+    if K <= 0 or K % 1024:
+        return False
+    if K % ch == 0:
+        return True
+    g = math.gcd(K, ch)
+    gr, rch = ch // g, K // g
+    gpt = 16 // rch
+    per_row = K // 64
+    tr = gpt * gr
+    npairs = (tr + 15) // 16 * (per_row // 4)
+    return gpt >= 1 and per_row % 16 == 0 and tr * per_row * 4 <= 4096 and 1 <= npairs <= 32
 
 
 def split_prefill(split, inv: torch.Tensor, x: torch.Tensor, M: int, K: int,
@@ -376,15 +389,23 @@ def split_prefill(split, inv: torch.Tensor, x: torch.Tensor, M: int, K: int,
 def split_fewtok(splits, x: torch.Tensor, Ms, K: int):
     """[y_i [T, M_i]] for up to four split-format matrices sharing x [T, K]
     (fp32, 16-byte aligned), one fused launch per 16 tokens
-    (cbq_split_linear_fewtok_f32; split_fewtok_eligible(K) must hold)."""
+    (cbq_split_linear_fewtok_f32; split_fewtok_eligible(K) must hold), x's
+    bf16 parts staged in a transient workspace (96 K bytes) when it pays."""
     n = len(splits)
     T = int(x.shape[0])
     outs = [torch.empty(T, int(M), dtype=torch.float32, device=x.device) for M in Ms]
     mats = (ctypes.POINTER(nat.SplitMatrix) * n)(*[ctypes.pointer(sp[1]) for sp in splits])
     optr = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
     mptr = (ctypes.c_int * n)(*[int(M) for M in Ms])
-    nat.check(nat.load().cbq_split_linear_fewtok_f32(x.data_ptr(), T, n, mats, optr, mptr, K,
-                                                     nat.stream_ptr(x.device)),
+    lib = nat.load()
+    # x's bf16 parts staged once: from 5 tokens on (the in-GEMM split then
+    # costs more than the extra launch) and for the two-pass tile shapes
+    two_pass = K % hc.CHUNK_SYMBOLS != 0 and K not in (1024, 2048)
+    wsb = int(lib.cbq_split_fewtok_ws_bytes(K)) if (T > 4 or two_pass) else 0
+    ws = torch.empty(wsb, dtype=torch.uint8, device=x.device) if wsb else None
+    nat.check(lib.cbq_split_linear_fewtok_f32(x.data_ptr(), T, n, mats, optr, mptr, K,
+                                              ws.data_ptr() if ws is not None else None, wsb,
+                                              nat.stream_ptr(x.device)),
               "cbq_split_linear_fewtok_f32")
     return outs
 

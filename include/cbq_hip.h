@@ -396,15 +396,27 @@ int cbq_split_to_packed(const cbq_split_matrix *m, const uint16_t *inv, int bits
  * x (one launch), any T >= 1 (fp32 x and outputs, 16-byte aligned x), in
  * launches of up to 16 tokens: every weight is decoded once per launch into
  * LDS and multiplied on the bf16 matrix cores (x split exactly into three
- * bf16 parts), never written out.  K % 4096 == 0, or K = 1024 or 2048
- * (whole rows per chunk); M_i * K a whole number of 4096-weight chunks;
- * other shapes return CK_ERR_ARG.  Never allocates.  Replaces, for Huffman
+ * bf16 parts), never written out.  K % 4096 == 0, or K % 1024 == 0 with
+ * the rows of a 4096-weight chunk group tiling 16 waves (K = 1024, 2048,
+ * 3072, 5120, 6144, 7168; M_i a multiple of 4096 / gcd(K, 4096)); M_i * K a
+ * whole number of chunks; other shapes return CK_ERR_ARG.  ws (16-byte
+ * aligned, at least cbq_split_fewtok_ws_bytes(K) bytes, or NULL): x's three
+ * bf16 parts are written there once per 16 tokens in fragment order and
+ * read ready-made, instead of every lane splitting its x in the GEMM; the
+ * shapes whose row tiles need two MFMA passes per phase (K = 3072, 5120,
+ * 6144, 7168) require it.  Never allocates.
+ * Replaces, for Huffman
  * modules whose split format exists, the batched-token path of
  * huffman_matmul (src/compressed_matmul.c:208-239 over several rows of x,
  * src/gpu_huffman_functions.py:834-855), which decodes to a transient index
  * buffer first (rocm/huffman_kernel.hip:61-156). */
 int cbq_split_linear_fewtok_f32(const float *x, int T, int n, const cbq_split_matrix *const *mats,
-                                float *const *outs, const int *Ms, int K, hipStream_t stream);
+                                float *const *outs, const int *Ms, int K, void *ws,
+                                size_t ws_bytes, hipStream_t stream);
+
+/* Workspace bytes cbq_split_linear_fewtok_f32 uses at this K (96 K); no
+ * counterpart in the reference. */
+size_t cbq_split_fewtok_ws_bytes(int K);
 
 /* ==== upload helpers ===================================================== */
 

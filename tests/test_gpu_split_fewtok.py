@@ -41,13 +41,19 @@ def _ref(oracle, x, cb, idx, M, K):
     return oracle.fixed_gemv(x, packed, cb, M, K, bits, chunk_rows=None)
 
 
-def _call(sps, xd, outs, Ms, K, cuda):
+def _call(sps, xd, outs, Ms, K, cuda, ws=True):
+    """ws: stage x's bf16 parts in a workspace (the path the modules take);
+    False: every lane splits its x in the GEMM."""
     n = len(sps)
     mats = (ctypes.POINTER(nat.SplitMatrix) * n)(*[ctypes.pointer(sp[1]) for sp in sps])
     optr = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
     mptr = (ctypes.c_int * n)(*Ms)
-    return nat.load().cbq_split_linear_fewtok_f32(xd.data_ptr(), xd.shape[0], n, mats, optr,
-                                                  mptr, K, nat.stream_ptr(cuda))
+    lib = nat.load()
+    wsb = int(lib.cbq_split_fewtok_ws_bytes(K)) if ws else 0
+    _call.keep = torch.empty(max(wsb, 16), dtype=torch.uint8, device=cuda)
+    return lib.cbq_split_linear_fewtok_f32(xd.data_ptr(), xd.shape[0], n, mats, optr, mptr, K,
+                                           _call.keep.data_ptr() if ws else None, wsb,
+                                           nat.stream_ptr(cuda))
 
 
 def _fewtok(cuda, sp, x, M, K, extra_rows=0):
@@ -60,7 +66,8 @@ def _fewtok(cuda, sp, x, M, K, extra_rows=0):
 
 
 @pytest.mark.parametrize("M,K", [(300, 4096), (70, 12288), (640, 2048), (96, 1024),
-                                 (5000, 4096)])
+                                 (5000, 4096), (256, 6144), (2048, 6144), (96, 3072),
+                                 (120, 5120), (64, 7168)])
 def test_against_oracle(cuda, oracle, M, K):
     rng, cb, idx, sp = _case(cuda, M, K, M + K)
     for T in (1, 2, 5, 16, 17, 32):
@@ -72,9 +79,12 @@ def test_against_oracle(cuda, oracle, M, K):
 
 
 def test_refused_shape_uses_transient_stream(cuda, oracle):
-    """K = 6144 (a chunk straddles rows): the kernel refuses it, and
-    split_prefill takes the transient fixed-width stream with the same result."""
-    M, K = 256, 6144
+    """K = 9216 (a chunk group's 4 rows need 9 chunks: more than the 16-wave
+    tile's passes take): the kernel refuses it, and split_prefill takes the
+    transient fixed-width stream with the same result."""
+    from gpu_huffman_functions import split_fewtok_eligible
+    M, K = 64, 9216
+    assert not split_fewtok_eligible(K) and split_fewtok_eligible(6144)
     rng, cb, idx, sp = _case(cuda, M, K, 9)
     x = rng.standard_normal((4, K)).astype(np.float32)
     rc, _ = _fewtok(cuda, sp, x, M, K)
@@ -152,3 +162,26 @@ def test_grouped_matrices(cuda, oracle, Ms, K):
         torch.cuda.synchronize()
         assert torch.equal(o, single)
         assert rel_l2(o.cpu().numpy(), _ref(oracle, x, cb, idx, M, K)) <= TOL
+
+
+def test_two_pass_shapes_need_the_workspace(cuda):
+    M, K = 256, 6144
+    rng, cb, idx, sp = _case(cuda, M, K, 31)
+    xd = torch.from_numpy(rng.standard_normal((4, K)).astype(np.float32)).to(cuda)
+    out = torch.empty(4, M, device=cuda)
+    assert _call([sp], xd, [out], [M], K, cuda, ws=False) == nat.CK_ERR_ARG
+
+
+@pytest.mark.parametrize("M,K", [(300, 4096), (640, 2048)])
+def test_workspace_and_in_kernel_split_agree(cuda, M, K):
+    """x's parts staged in the workspace or split by every lane in the GEMM:
+    the same bf16 operands, so the outputs are equal bit for bit."""
+    rng, cb, idx, sp = _case(cuda, M, K, 77)
+    for T in (3, 16, 20):
+        xd = torch.from_numpy(rng.standard_normal((T, K)).astype(np.float32)).to(cuda)
+        a = torch.full((T, M), float("nan"), device=cuda)
+        b = torch.full((T, M), float("nan"), device=cuda)
+        assert _call([sp], xd, [a], [M], K, cuda, ws=True) == 0
+        assert _call([sp], xd, [b], [M], K, cuda, ws=False) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), T
