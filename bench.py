@@ -1049,6 +1049,27 @@ def main():
         s_gg = sum(stream_bytes[n] for n in gate_up[0]) + 4 * (
             huff[gate_up[0][0]].shape[0] + huff[gate_up[0][0]].shape[1])
         ach = b_gg / (us_gg * 1e-6) / 1e9
+        # config 3's batches on the 9B stacked gate+up (both matrices under
+        # one table, 2 x 12288 rows): one fused launch per step, every weight
+        # decoded once for all T tokens
+        from gpu_huffman_functions import split_fewtok
+        glus = [splits[("glu", e[0])] for e in gate_up if ("glu", e[0]) in splits]
+        hbatch = {}
+        if glus:
+            Mg = 2 * huff[gate_up[0][0]].shape[0]
+            Kg = huff[gate_up[0][0]].shape[1]
+            gbytes = split_bytes(glus[0][0])
+            for T in (2, 4, 8, 16):
+                xg = torch.randn(T, Kg, device=dev)
+                with mark(f"huffman:gate_up_stacked:T{T}"):
+                    ms_T, _ = timed_graph(
+                        torch, lambda xg=xg: [split_fewtok([g], xg, [Mg], Kg) for g in glus],
+                        args.steps, args.warmup)
+                us_T = ms_T * 1e3 / len(glus)
+                hbatch[f"T{T}"] = {"us_per_launch": round(us_T, 2),
+                                   "GB/s": round(gbytes / (us_T * 1e-6) / 1e9, 1),
+                                   "vs_T1": round(us_T / us_gg, 3)}
+            log(f"huffman stacked gate+up at T=2/4/8/16: {hbatch}")
         result["huffman"] = {
             "value": round(sbytes / (ms_h * 1e-3) / 1e9, 1), "unit": "GB/s",
             "ms_per_step": round(ms_h, 4), "bytes_per_step": sbytes,
@@ -1057,6 +1078,12 @@ def main():
                       "which is then freed: the only resident format; each layer's gate/up "
                       "pair stacked under one shared table",
             "stream_format_kernel": stream_k,
+            "batch_stacked_gate_up": {
+                "kernel": "cbq_split_linear_fewtok_f32 (split_fewtok_kernel: decode into LDS, "
+                          "bf16 MFMA, x split into three exact bf16 parts), stacked gate+up "
+                          "4096->24576 under one table",
+                "vs_T1_is": "against the one-token GLU launch of the same stacked matrix",
+                **hbatch},
             "stream_bytes_per_step": hbytes,
             "stream_equivalent_GB/s": round(hbytes / (ms_h * 1e-3) / 1e9, 1),
             "launches_per_step": len(plan),
