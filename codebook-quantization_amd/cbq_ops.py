@@ -4,7 +4,9 @@ ABI of libcbq_hip.so).
 
     linear(x, packed, codebook, M, bits)              fixed-width GEMV / GEMM
     embedding(ids, packed, codebook, vocab, bits, H)  fixed-width row gather
-    split_linear(x, cwords, row_off, raw, lut, M)     Huffman (split format), T = 1
+    split_linear(x, cwords, row_off, raw, lut, M)     Huffman (split format): T = 1 the
+                                                      GEMV, T >= 2 the fused few-token
+                                                      kernel (K % 1024 == 0 shapes)
     huff_linear(x, words, chunk_off, sub_len, lut1, lut2, canon, canon_pay,
                 value_cb, C, stage_words, M)           Huffman (stream format)
     huff_embedding(ids, <stream tensors>, C, stage_words, vocab, H)

@@ -113,11 +113,19 @@ at::Tensor embedding(const at::Tensor &ids, const at::Tensor &packed, const at::
     return out;
 }
 
+// T = 1: the one-token GEMV (cbq_split_linear_f32).  T >= 2: the fused
+// few-token kernel (cbq_split_linear_fewtok_f32, 16 tokens a launch), which
+// takes K % 1024 == 0 shapes whose row-group tile fits (it refuses the rest
+// with an error here); x's bf16 parts go to a workspace from torch's
+// allocator from 5 tokens on and for the shapes with two MFMA passes per
+// phase (K % 4096 != 0 other than 1024 and 2048), as the Python wrapper
+// split_fewtok does.
 at::Tensor split_linear(const at::Tensor &x, const at::Tensor &cwords, const at::Tensor &row_off,
                         const at::Tensor &raw, const at::Tensor &lut, int64_t M)
 {
-    TORCH_CHECK(x.is_cuda() && x.scalar_type() == at::kFloat && x.dim() == 2 && x.size(0) == 1,
-                "cbq::split_linear: x must be a [1, K] float32 device tensor");
+    TORCH_CHECK(x.is_cuda() && x.scalar_type() == at::kFloat && x.dim() == 2 && x.size(0) >= 1 &&
+                    x.is_contiguous(),
+                "cbq::split_linear: x must be a contiguous [T, K] float32 device tensor");
     for (const auto &p : {std::make_pair(&cwords, "cwords"), std::make_pair(&row_off, "row_off"),
                           std::make_pair(&raw, "raw"), std::make_pair(&lut, "lut")})
         check_dev(*p.first, x, p.second);
@@ -126,7 +134,8 @@ at::Tensor split_linear(const at::Tensor &x, const at::Tensor &cwords, const at:
                     raw.numel() == M * K && lut.numel() == 16384,
                 "cbq::split_linear: tensors do not describe a ", M, "x", K, " split matrix");
     c10::DeviceGuard guard(x.device());
-    at::Tensor out = at::empty({1, M}, x.options());
+    const int64_t T = x.size(0);
+    at::Tensor out = at::empty({T, M}, x.options());
     cbq_split_matrix m;
     m.cwords = cptr<uint32_t>(cwords);
     m.row_off = cptr<uint32_t>(row_off);
@@ -136,9 +145,26 @@ at::Tensor split_linear(const at::Tensor &x, const at::Tensor &cwords, const at:
     const cbq_split_matrix *mats[1] = {&m};
     float *outs[1] = {(float *)out.data_ptr()};
     const int Ms[1] = {(int)M};
-    check_rc(cbq_split_linear_f32(cptr<float>(x), nullptr, nullptr, 0, 0.f, 1, mats, outs, Ms,
-                                  (int)K, current_stream(x)),
-             "cbq_split_linear_f32");
+    if (T == 1) {
+        check_rc(cbq_split_linear_f32(cptr<float>(x), nullptr, nullptr, 0, 0.f, 1, mats, outs,
+                                      Ms, (int)K, current_stream(x)),
+                 "cbq_split_linear_f32");
+        return out;
+    }
+    TORCH_CHECK(T <= (int64_t)1 << 24, "cbq::split_linear: too many tokens");
+    const bool two_pass = K % 4096 != 0 && K != 1024 && K != 2048;
+    at::Tensor ws;
+    size_t wsb = 0;
+    if (T > 4 || two_pass) {
+        wsb = cbq_split_fewtok_ws_bytes((int)K);
+        ws = at::empty({(int64_t)wsb}, x.options().dtype(at::kByte));
+    }
+    const int rc = cbq_split_linear_fewtok_f32(cptr<float>(x), (int)T, 1, mats, outs, Ms, (int)K,
+                                               wsb ? ws.data_ptr() : nullptr, wsb,
+                                               current_stream(x));
+    TORCH_CHECK(rc != CK_ERR_ARG, "cbq::split_linear: the few-token kernel does not take K = ", K,
+                " (or x is not 16-byte aligned)");
+    check_rc(rc, "cbq_split_linear_fewtok_f32");
     return out;
 }
 

@@ -593,7 +593,9 @@ class HuffmanCodebookLinear:
         st = nat.stream_ptr(self.device)
         if T == 0:
             out = torch.empty(0, self.M, dtype=torch.float32, device=self.device)
-        elif self.split is not None and T == 1:
+        elif self.split is not None and (T == 1 or (
+                T <= FEWTOK_MAX_T and split_fewtok_eligible(self.K) and xc.data_ptr() % 16 == 0)):
+            # one token: the split GEMV; up to 32: the fused few-token kernel
             cw, ro, raw, lut = self.split[0]
             out = cbq_ops.load().split_linear(xc, cw, ro, raw, lut, self.M)
         elif self.split is not None:

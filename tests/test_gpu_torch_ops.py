@@ -101,6 +101,31 @@ def test_huff_linear(cuda, ops, oracle, layout):
     assert e <= 1e-5
 
 
+@pytest.mark.parametrize("K", [2048, 4096, 6144])
+def test_split_linear_tokens(cuda, ops, oracle, K):
+    """split_linear with 2..20 tokens runs the fused few-token kernel (one
+    pass per phase at K = 2048 / 4096, two at 6144, x's parts staged from 5
+    tokens on); the module's batched forward is the same op."""
+    M = 256
+    w, cb, enc, lin = _huff_module(M, K, 20 + K // 1024, "split")
+    rng = np.random.default_rng(K)
+    for T in (2, 4, 5, 16, 20):
+        x = rng.standard_normal((T, K)).astype(np.float32)
+        y = ops.split_linear(_dev(x, cuda), *lin.split[0], M)
+        e = rel_l2(y.cpu().numpy(), oracle.huff_gemv(x, enc, cb, M, K))
+        assert e <= 1e-5, (K, T, e)
+        assert torch.equal(lin(_dev(x, cuda)), y)
+
+
+def test_split_linear_refuses_untaken_k(cuda, ops):
+    """K = 9216: the few-token kernel's row-group tile does not fit, and the
+    op says so instead of computing anything."""
+    M, K = 64, 9216
+    _, cb, enc, lin = _huff_module(M, K, 31, "split")
+    with pytest.raises(RuntimeError, match="does not take K = 9216"):
+        ops.split_linear(torch.zeros(3, K, device=cuda), *lin.split[0], M)
+
+
 def test_huff_embedding(cuda, ops):
     from gpu_huffman_functions import HuffmanCodebookEmbedding
     V, H = 300, 128
@@ -116,8 +141,9 @@ def test_huff_embedding(cuda, ops):
 
 
 def test_graph_capture_replays(cuda, ops, oracle):
-    """fixed T=1 and T=64 (workspace from the graph's pool), split and stream
-    Huffman, embedding: one graph, 3 replays with fresh inputs, each against
+    """fixed T=1 and T=64 (workspace from the graph's pool), split Huffman at
+    T = 1 and 8 (the few-token kernel, its workspace from the graph's pool),
+    stream Huffman, embedding: one graph, 3 replays with fresh inputs, each against
     the oracle; eager launches run between the replays."""
     M, K = 1024, 2048
     _, d = _fixed(M, K, 9)
@@ -126,6 +152,7 @@ def test_graph_capture_replays(cuda, ops, oracle):
     _, tcb, tenc, ht = _huff_module(256, K, 11, "stream")
     xs1 = torch.zeros(1, K, device=cuda)
     xs64 = torch.zeros(64, K, device=cuda)
+    xs8 = torch.zeros(8, K, device=cuda)
     ids = torch.zeros(4, dtype=torch.int32, device=cuda)
     emb_w, emb_d = _fixed(200, 128, 12)
     epk, ecb = _fixed_dev(emb_d, cuda)
@@ -135,6 +162,7 @@ def test_graph_capture_replays(cuda, ops, oracle):
         ops.linear(xs1, pk, cb, M, d["bits"])
         ops.linear(xs64, pk, cb, M, d["bits"])
         ops.split_linear(xs1, *hs.split[0], 512)
+        ops.split_linear(xs8, *hs.split[0], 512)
         ops.huff_linear(xs1, *ht.dev.op_args(), 256)
         ops.embedding(ids, epk, ecb, 200, emb_d["bits"], 128)
     torch.cuda.current_stream().wait_stream(s)
@@ -143,15 +171,18 @@ def test_graph_capture_replays(cuda, ops, oracle):
         y1 = ops.linear(xs1, pk, cb, M, d["bits"])
         y64 = ops.linear(xs64, pk, cb, M, d["bits"])
         ysp = ops.split_linear(xs1, *hs.split[0], 512)
+        ysp8 = ops.split_linear(xs8, *hs.split[0], 512)
         yst = ops.huff_linear(xs1, *ht.dev.op_args(), 256)
         ye = ops.embedding(ids, epk, ecb, 200, emb_d["bits"], 128)
     for r in range(3):
         rng = np.random.default_rng(100 + r)
         x1 = rng.standard_normal((1, K)).astype(np.float32)
         x64 = rng.standard_normal((64, K)).astype(np.float32)
+        x8 = rng.standard_normal((8, K)).astype(np.float32)
         idv = rng.integers(0, 200, 4).astype(np.int32)
         xs1.copy_(torch.from_numpy(x1))
         xs64.copy_(torch.from_numpy(x64))
+        xs8.copy_(torch.from_numpy(x8))
         ids.copy_(torch.from_numpy(idv))
         g.replay()
         eager = ops.linear(xs1, pk, cb, M, d["bits"])          # eager work between replays
@@ -161,6 +192,7 @@ def test_graph_capture_replays(cuda, ops, oracle):
              "T64": rel_l2(y64.cpu().numpy(), oracle.fixed_gemv(x64, d["indices"],
                                                                  d["codebook"], M, K, d["bits"])),
              "split": rel_l2(ysp.cpu().numpy(), oracle.huff_gemv(x1, henc, hcb, 512, K)),
+             "split T8": rel_l2(ysp8.cpu().numpy(), oracle.huff_gemv(x8, henc, hcb, 512, K)),
              "stream": rel_l2(yst.cpu().numpy(), oracle.huff_gemv(x1, tenc, tcb, 256, K))}
         print(f"replay {r}: " + ", ".join(f"{k} {v:.2e}" for k, v in e.items()), flush=True)
         assert max(e.values()) <= 1e-5, (r, e)
