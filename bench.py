@@ -21,7 +21,7 @@ repeats).  Further keys:
 - "huffman": the same sweep with canonical-Huffman weights held in the split
   format alone (the decoder's format; each matrix's stream is decoded on the
   GPU, re-encoded and freed), with its resident bits per weight;
-- "qwen3_1_7b": BASELINE configs 2 and 3, the 28-layer 1.7B shapes at 1, 4
+- "qwen3_1_7b": benchmark configs 2 and 3, the 28-layer 1.7B shapes at 1, 4
   and 16 tokens, fixed-width and Huffman;
 - "prefill": the bf16 MFMA GEMM at T = 512 and 2048 (config 4);
 - "e2e": greedy decode of the whole 36-layer model (config 5), both encodings,
@@ -344,7 +344,7 @@ def xf_bytes(T, K):
 
 
 def prefill_section(torch, nat, lib, dev, fixed, kinds, args):
-    """bf16 MFMA prefill over the same fixed-width weights,
+    """benchmark config 4: bf16 MFMA prefill over the same fixed-width weights,
     T = 512 and 2048 tokens of bf16 N(0, 1) activations; per shape the mean
     time of one cbq_linear_bf16_ws call (the x fragment-order copy, the GEMM
     and, when K is split, the partial sum) over 8 layers' distinct weights
@@ -432,7 +432,7 @@ def config5_cpu_record():
 
 
 def cpu_baseline(np, seconds):
-    """BASELINE config 1 on the host cores with the reference's own C kernels
+    """benchmark config 1 on the host cores with the reference's own C kernels
     (oracle/_ref; the restatement when that is not built): W [6144, 2048]
     N(0, 0.02) bf16 (synthetic.make_bf16, seed "config1"), frequency-sorted
     lossless codebook, 13-bit fixed-width indices and the canonical-Huffman
@@ -576,7 +576,7 @@ def cpu_baseline(np, seconds):
 
 
 def sweep_1p7b(torch, nat, lib, dev, synthetic, args):
-    """BASELINE configs 2 and 3: every layer linear of the 28-layer 1.7B-shape
+    """benchmark configs 2 and 3: every layer linear of the 28-layer 1.7B-shape
     decoder (no lm_head), decoder launch order, at 1, 4 and 16 tokens;
     fixed-width 13-bit indices, and the same weights Huffman-coded in the
     split format (one token on the split GEMV; 4 and 16 tokens through the
@@ -763,7 +763,7 @@ def torch_tensors_of(tensors):
 
 
 def e2e_section(torch, dec, args):
-    """always-compressed greedy decode of the random-init
+    """benchmark config 5: always-compressed greedy decode of the random-init
     36-layer Qwen3-8B-shape decoder at batch 1: all linears, the lm_head and
     the embedding Huffman-coded (24-bit canonical codes, 4096-symbol chunks;
     linears re-encoded to the split format, their streams freed); 128-token

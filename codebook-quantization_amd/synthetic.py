@@ -36,10 +36,10 @@ def layer_shapes(hidden: int, inter: int, n_q: int, n_kv: int, head_dim: int):
 
 
 CONFIGS = {
-    # Qwen3-8B-style, 36 layers
+    # benchmark config 5: Qwen3-8B-style, 36 layers
     "qwen3-8b": dict(layers=36, hidden=4096, inter=12288, n_q=32, n_kv=8, head_dim=128,
                      vocab=151936),
-    # Qwen3-1.7B-style, 28 layers
+    # benchmark config 2: Qwen3-1.7B-style, 28 layers
     "qwen3-1.7b": dict(layers=28, hidden=2048, inter=6144, n_q=16, n_kv=8, head_dim=128,
                        vocab=151936),
 }

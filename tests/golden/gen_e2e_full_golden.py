@@ -1,4 +1,4 @@
-"""Golden greedy tokens of the full BASELINE config-5 decoder, written by the
+"""Golden greedy tokens of the full benchmark config-5 decoder, written by the
 CPU oracle (test fixture generator; run in this container, not on the GPU box).
 
 The model is the random-init 36-layer Qwen3-8B-shape decoder the bench and

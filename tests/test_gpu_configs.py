@@ -1,4 +1,4 @@
-"""BASELINE configs 2 and 4 at their own shapes.
+"""benchmark configs 2 and 4 at their own shapes.
 
 Config 2: every Qwen3-1.7B layer shape (K -> M: 2048 -> 2048, 2048 -> 1024,
 6144 -> 2048, 2048 -> 6144), fixed-width lossless indices, T = 1, 4, 16,

@@ -1,4 +1,4 @@
-"""BASELINE config 5 at full size: the random-init 36-layer Qwen3-8B-shape
+"""benchmark config 5 at full size: the random-init 36-layer Qwen3-8B-shape
 decoder on the GPU against the CPU oracle's golden run
 (tests/golden/gen_e2e_full_golden.py: the reference's own C kernel for every
 GEMV, numpy fp32 glue pinned to transformers' Qwen3).

@@ -1,6 +1,6 @@
 """bf16 MFMA prefill path of ck_linear_bf16 (T >= 64) vs the oracle.
 
-Bar: rel-L2 <= 2e-3 against the fp32 reference GEMV
+Bar for the bf16-MFMA prefill: rel-L2 <= 2e-3 against the fp32 reference GEMV
 on the same bf16 inputs; outputs are bf16, so >= 95% of them must also equal
 the oracle's fp32 result rounded to bf16 within one bf16 ulp.
 """
