@@ -469,8 +469,13 @@ int fewtok_launch_r(const XT *x, const uint8_t *packed, const float *cb, OT *out
     return cbq_launch_status("fixed_fewtok_kernel");
 }
 
-// Row tiles per block: the most of 6 / 3 / 2 / 1 that still gives every CU
-// a block (a block holds one CU: 8 waves, up to 141 KiB of LDS).
+// Row tiles per block R (6, 3, 2 or 1; a block holds one CU: 8 waves, up to
+// 141 KiB of LDS): the R of least rounds x (R + 1), rounds =
+// ceil(ceil(tiles / R) / CUs) and the + 1 a block's fixed cost in tiles
+// (codebook staging, the first loads, the partial-tile sums), larger R on a
+// tie.  E.g. 384 tiles on 256 CUs take R = 2 (one round of 192 blocks, 16
+// us for the 9B stacked q/k/v at 2 tokens) rather than two rounds of R = 1
+// (20 us); 1536 tiles take R = 6.
 template <typename XT, typename OT>
 int fewtok_launch(const XT *x, const uint8_t *packed, const float *cb, OT *out, int T, int M,
                   int K, int C, int bits, hipStream_t st)
@@ -481,7 +486,15 @@ int fewtok_launch(const XT *x, const uint8_t *packed, const float *cb, OT *out, 
     if (bits != 8 && (bits < 10 || bits > 14) && bits != 16) return -1;
     const long tiles = (M + 15) / 16;
     const long ncu = cbq_num_cus();
-    const int R = tiles >= 6 * ncu ? 6 : tiles >= 3 * ncu ? 3 : tiles >= 2 * ncu ? 2 : 1;
+    int R = 1;
+    long best = -1;
+    for (const int r : {1, 2, 3, 6}) {
+        const long cost = ((tiles + r - 1) / r + ncu - 1) / ncu * (r + 1);
+        if (best < 0 || cost <= best) {
+            best = cost;
+            R = r;
+        }
+    }
     const long blocks = (tiles + R - 1) / R;
     if (blocks > 0x7fffffffL) return -1;
     switch (R) {

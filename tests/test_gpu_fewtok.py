@@ -72,8 +72,9 @@ def test_widths_and_codebooks(cuda, oracle, bits, bf16_cb):
 
 
 def _plan_rows(ncu):
-    # tiles of 16 rows: >= 6, 3, 2 CUs' worth pick 6, 3, 2 tiles per block; fewer, 1
-    return {6: 6 * ncu * 16 + 40, 3: 3 * ncu * 16 + 8, 2: 2 * ncu * 16 + 24, 1: ncu * 16 - 72}
+    # tiles of 16 rows, R tiles per block of least rounds x (R + 1):
+    # 6 ncu - 2 tiles -> 6, 2.5 ncu + 1 -> 3, 1.5 ncu + 1 -> 2, ncu - 4 -> 1 (ragged M)
+    return {6: 96 * ncu - 40, 3: 40 * ncu + 8, 2: 24 * ncu + 8, 1: ncu * 16 - 72}
 
 
 @pytest.mark.parametrize("plan", [6, 3, 2, 1])
