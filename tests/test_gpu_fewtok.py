@@ -136,6 +136,28 @@ def test_refused_shapes_fall_back(cuda, oracle):
             assert rel_l2(y, ref) <= TOL, (M, K, off, T)
 
 
+@pytest.mark.parametrize("plan", [6, 2])
+def test_bf16_row_tile_plans(cuda, oracle, plan):
+    """bf16 x and out (ck_linear_bf16) through the 6- and 2-tile plans."""
+    nat, lib = _nat()
+    ncu = torch.cuda.get_device_properties(cuda).multi_processor_count
+    M, K, bits, C = _plan_rows(ncu)[plan], 512, 13, 5000
+    rng = np.random.default_rng(40 + plan)
+    raw, cb = _case(rng, M, K, bits, C, True)
+    pk = oracle.pack_lsb(raw, bits)
+    pd = _dev_packed(pk, cuda)
+    cd = torch.from_numpy(cb).to(cuda)
+    xb = torch.from_numpy(rng.standard_normal((7, K)).astype(np.float32)).bfloat16()
+    xd = xb.to(cuda)
+    out = torch.empty(7, M, dtype=torch.bfloat16, device=cuda)
+    nat.check(lib.ck_linear_bf16(xd.data_ptr(), pd.data_ptr(), cd.data_ptr(), out.data_ptr(), 7,
+                                 M, K, C, bits, nat.stream_ptr(cuda)), "ck_linear_bf16")
+    ref = oracle.fixed_gemv(xb.float().numpy(), pk, cb, M, K, bits, C=C, chunk_rows=None)
+    y = out.float().cpu().numpy()
+    assert rel_l2(y, ref) <= 4e-3, plan
+    assert (y == torch.from_numpy(ref).bfloat16().float().numpy()).mean() >= 0.99
+
+
 def test_bf16_io_two_tokens(cuda, oracle):
     """bf16 x is one exact part: ck_linear_bf16 with 2 and 16 tokens."""
     nat, lib = _nat()
