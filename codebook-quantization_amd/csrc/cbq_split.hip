@@ -440,6 +440,129 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
     }
 }
 
+// Row groups of several chunks (GR > 1 and R = K GR / 4096 > 1: K = 3072,
+// 5120, 6144, 7168), plain x, one matrix.  split_gemv_kernel walks a
+// group's R chunks in one wave, one x tile per chunk, so with few groups per
+// CU (the 1.7B down projection: 1024 groups) it runs one wave per SIMD.
+// Here the whole x is staged once (K <= kRgMaxK, in the tile's swizzled
+// 64-float rows) and the R chunks of a group go to R waves at once: a tile
+// is GPB groups (GPB R <= NW waves in the block), wave w decodes chunk w % R
+// of group w / R, writes its rows' wave sums (at most two rows per chunk,
+// K >= 3072 being a multiple of 1024) to LDS, and after a barrier one thread
+// per output row adds them in chunk order.  That is the order in
+// which split_gemv_kernel adds its chunks' wave sums, over the same per-lane
+// dot products, so the outputs are equal bit for bit.
+constexpr int kRgMaxK = 7168;
+
+template <int NW>
+__global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_rg_kernel(const float *__restrict__ x,
+                                                                      SplitSeg S, int K, int GR,
+                                                                      int R, int GPB)
+{
+    __shared__ __attribute__((aligned(16)))
+        uint32_t s_lds[kSLut + kRgMaxK + NW * kSSlotWords + 2 * NW];
+    float *const s_x = (float *)(s_lds + kSLut);
+    float *const s_part = (float *)(s_lds + kSLut + kRgMaxK + NW * kSSlotWords);   // [NW][2]
+    const int lane = threadIdx.x & (CBQ_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CBQ_WAVE);
+    uint32_t *const s_slot = s_lds + kSLut + kRgMaxK + wave * kSSlotWords;
+    const int lane_addr =
+        __builtin_amdgcn_readfirstlane(4 * (kSLut + kRgMaxK + wave * kSSlotWords)) + 4 * lane;
+    const int nw = GPB * R;                        // waves in the block (blockDim / 64)
+    const int Mg = S.M / GR;
+    const int n_tiles = (Mg + GPB - 1) / GPB;
+    const int gl = wave / R, p = wave - gl * R;    // this wave: group gl of a tile, chunk p
+    // rows of the group that chunk p touches, this lane's row, and the x row
+    // (64 floats) of this lane's sub-block: columns (p 4096 + 64 lane) mod K
+    const int q_lo = p * kSChunk / K, q_hi = (p * kSChunk + kSChunk - 1) / K;
+    const int q_me = (p * kSChunk + lane * kSSub) / K;
+    const int xrow = ((p * kSChunk + lane * kSSub) % K) >> 6;
+    const float *const xr = s_x + xrow * 64;
+    const int xsw = (xrow & 15) << 2;
+    const __attribute__((address_space(4))) uint32_t *const ro =
+        (const __attribute__((address_space(4))) uint32_t *)S.row_off;
+    // chunk of tile t for this wave (a group past the matrix reads chunk 0:
+    // its loads are issued, its sums unused)
+    auto chunk_at = [&](int t, bool &mine) -> int64_t {
+        const int g = t * GPB + gl;
+        mine = g < Mg;
+        return mine ? (int64_t)__builtin_amdgcn_readfirstlane(g * R + p) : 0;
+    };
+
+    // the table, then x in 16-byte pieces (piece c of 64-float row r holds x
+    // piece c ^ (r & 15) of that row), then the first tile's chunk
+    for (int i = wave; i < kSLut / (4 * CBQ_WAVE); i += nw) {
+        __builtin_amdgcn_global_load_lds(S.lut + i * 4 * CBQ_WAVE + 4 * lane,
+                                         (__attribute__((address_space(3))) void *)(s_lds + i * 4 * CBQ_WAVE),
+                                         16, 0, 0);
+    }
+    for (int i = wave; i < (K >> 8); i += nw) {    // 4 rows of 64 floats a load
+        const int r = (i << 2) + (lane >> 4), c = lane & 15;
+        __builtin_amdgcn_global_load_lds(x + (r << 6) + ((c ^ (r & 15)) << 2),
+                                         (__attribute__((address_space(3))) void *)(s_x + (i << 8)),
+                                         16, 0, 0);
+    }
+    SplitItem A, B;
+    bool mineA = false, mineB = false;
+    int64_t c = chunk_at(blockIdx.x, mineA);
+    const uint32_t rA = ro[c];
+    uint32_t hA = ro[c + 1] - rA;
+    hA = hA < (uint32_t)kSRows ? hA : (uint32_t)kSRows;
+    constexpr int kFirstLoads = 4 + (kSRows + 3) / 4;
+    __builtin_amdgcn_sched_barrier(0);
+    split_load_all(A, S, c, rA, hA, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    // every staging load has landed (issued before the chunk's), the chunk's stay in flight
+    __builtin_amdgcn_s_waitcnt((kFirstLoads & 15) | (7 << 4) | (15 << 8) |
+                               ((kFirstLoads >> 4) << 14));
+    lds_barrier();
+
+    for (int t = blockIdx.x; t < n_tiles; t += gridDim.x) {
+        // the next tile's chunk in flight while this one is decoded (every
+        // load issued, so the wait for this chunk leaves them in flight)
+        const bool more = t + (int)gridDim.x < n_tiles;
+        uint32_t hB = 0;
+        if (more) {                                // block-uniform
+            c = chunk_at(t + gridDim.x, mineB);
+            const uint32_t rB = ro[c];
+            hB = ro[c + 1] - rB;
+            hB = hB < (uint32_t)kSRows ? hB : (uint32_t)kSRows;
+            split_load_all(B, S, c, rB, hB, lane);
+        }
+        float part0 = 0.f, part1 = 0.f;
+        if (mineA) {                               // wave-uniform
+            split_stage(A, hA, s_slot, lane);
+            const float acc = split_decode(A.raw, s_lds, lane_addr, xr, xsw);
+            part0 = wave_sum(q_me == q_lo ? acc : 0.f);
+            if (q_hi > q_lo) part1 = wave_sum(q_me == q_hi ? acc : 0.f);
+        }
+        if (lane == 0) {
+            s_part[2 * wave] = part0;
+            s_part[2 * wave + 1] = part1;
+        }
+        __syncthreads();
+        // one thread per row of the tile: its chunks' sums in chunk order
+        if ((int)threadIdx.x < GPB * GR) {
+            const int g2 = (int)threadIdx.x / GR, q = (int)threadIdx.x - g2 * GR;
+            const int g = t * GPB + g2;
+            if (g < Mg) {
+                float res = 0.f;
+                for (int pp = 0; pp < R; pp++) {
+                    const int lo = pp * kSChunk / K, hi = (pp * kSChunk + kSChunk - 1) / K;
+                    if (q >= lo && q <= hi) res += s_part[2 * (g2 * R + pp) + (q - lo)];
+                }
+                S.out[(int64_t)g * GR + q] = res;
+            }
+        }
+        __syncthreads();                           // sums read (and the slot free) before the next tile
+        if (more) {
+            A = B;
+            hA = hB;
+            mineA = mineB;
+        }
+    }
+}
+
 // ---- split format -> fixed-width indices (batched tokens) ------------------
 
 // The 64 weights of this lane's sub-block as bf16 bit patterns, mapped to
@@ -1197,6 +1320,30 @@ int split_linear(const float *x, const float *x1, float *h_out, int mode, float 
         g.lut = m->lut;
         g.out = outs[i];
         g.M = Ms[i];
+    }
+    // Row groups of several chunks, plain x, one matrix: the groups' chunks
+    // to separate waves (split_gemv_rg_kernel), the same outputs bit for bit.
+    // GPB groups per tile, one block per CU: a block's tile takes about as
+    // long as 6 + GPB R chunks' worth of decode work (one wave's decode is
+    // latency-bound; more waves share the SIMDs), so the GPB with the least
+    // tiles per block x (6 + GPB R) (ties to the larger GPB).
+    const int R = K * GR / kSChunk;
+    if (mode == XF_NONE && n == 1 && !arg_v && GR > 1 && R > 1 && R <= 16 && K <= kRgMaxK &&
+        ((uintptr_t)x & 15) == 0) {
+        constexpr int NW = 16;
+        const int Mg = Ms[0] / GR, cus = cbq_num_cus();
+        int GPB = 1;
+        int64_t best = -1;
+        for (int gpb = 1; gpb * R <= NW; gpb++) {
+            const int64_t cost = (int64_t)(((Mg + gpb - 1) / gpb + cus - 1) / cus) * (6 + gpb * R);
+            if (best < 0 || cost <= best) { best = cost; GPB = gpb; }
+        }
+        const int tiles = (Mg + GPB - 1) / GPB;
+        const int blocks = std::max(1, std::min(cus, tiles));
+        hipLaunchKernelGGL(split_gemv_rg_kernel<NW>, dim3(blocks), dim3(GPB * R * CBQ_WAVE), 0,
+                           stream, x, segs.s[0], K, GR, R, GPB);
+        if (n_blocks) *n_blocks = blocks;
+        return cbq_launch_status("split_gemv_rg_kernel");
     }
     // One block per CU in all (a second round of blocks would pay the table
     // staging and the first loads again): each matrix gets blocks in
