@@ -211,11 +211,14 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
 
     const int R = K * GR / kSChunk;                    // chunks per row group
     const int Mg = M / GR;                              // row groups
+    // Wave w of block b is walker w nblocks + b and takes rows (groups)
+    // wid, wid + W, ...: when the rows do not divide evenly, the extra ones
+    // go to the low waves of every block, not to every wave of the low
+    // blocks, so no CU holds more than its share plus one row per wave.
     const int W = S.nblocks * NW;
-    const int wid = bid * NW + wave;
+    const int wid = wave * S.nblocks + bid;
     const int rows = wid < Mg ? (Mg - wid + W - 1) / W : 0;
-    const int b0 = bid * NW;
-    const int rows_max = b0 < Mg ? (Mg - b0 + W - 1) / W : 0;
+    const int rows_max = bid < Mg ? (Mg - bid + W - 1) / W : 0;   // wave 0's
     const int n_seg = (rows_max + 63) >> 6;
     const float *const xr = s_x + lane * 64;
     const int xsw = (lane & 15) << 2;
@@ -1355,14 +1358,32 @@ int split_linear(const float *x, const float *x1, float *h_out, int mode, float 
     const int cus = cbq_num_cus();
     const int64_t per = m_sum / cus;
     const int nw = per >= 16 ? 16 : per >= 8 ? 8 : 4;
+    // Shares rounded down (at least one block), then the CUs left over one
+    // at a time to the matrix with the most rows per block, so the launch
+    // never holds more blocks than CUs unless it has more matrices.
     int blocks = 0;
     for (int i = 0; i < n; i++) {
         SplitSeg &g = segs.s[i];
         const int Mg = g.M / GR;
-        g.block0 = blocks;
-        const int share = (int)std::max<int64_t>(1, (cus * (int64_t)Mg + m_sum / 2) / m_sum);
+        const int share = (int)std::max<int64_t>(1, cus * (int64_t)Mg / m_sum);
         g.nblocks = std::max(1, std::min(share, (Mg + nw - 1) / nw));
         blocks += g.nblocks;
+    }
+    for (; blocks < cus; blocks++) {
+        int best = -1;
+        for (int i = 0; i < n; i++) {
+            const SplitSeg &g = segs.s[i];
+            const int Mg = g.M / GR;
+            if (g.nblocks >= (Mg + nw - 1) / nw) continue;   // every wave holds a row already
+            if (best < 0 || (int64_t)Mg * segs.s[best].nblocks > (int64_t)(segs.s[best].M / GR) * g.nblocks)
+                best = i;
+        }
+        if (best < 0) break;
+        segs.s[best].nblocks++;
+    }
+    for (int i = 0, b0 = 0; i < n; i++) {
+        segs.s[i].block0 = b0;
+        b0 += segs.s[i].nblocks;
     }
 #define CBQ_SPLIT_GR(NWV, MODE, G)                                                                \
     launch_split_gemv<NWV, MODE, G>(blocks, stream, x, segs, K, x1, h_out, eps, arg_v, arg_i)
