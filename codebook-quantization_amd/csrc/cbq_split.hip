@@ -83,10 +83,13 @@ __device__ __forceinline__ void split_load(SplitItem &it, const SplitSeg &S, int
         it.raw[4 * k + 2] = v.z;
         it.raw[4 * k + 3] = v.w;
     }
+    // Piece 0 unconditionally (a chunk holds at least two code rows: 64
+    // codes of at least one bit), so the wait for it, which covers the raw
+    // loads issued before it, is on every path.
     const u4 *wp = (const u4 *)(S.cwords + (size_t)r0 * kSSub) + lane;
 #pragma unroll
     for (int k = 0; k < (kSRows + 3) / 4; k++)
-        if (4 * k < (int)H) it.ew[k] = wp[k * kSSub];
+        if (k == 0 || 4 * k < (int)H) it.ew[k] = wp[k * kSSub];
 }
 
 // split_load with every load issued (4 + (kSRows + 3) / 4 of them): code
@@ -117,7 +120,18 @@ __device__ __forceinline__ void split_stage(const SplitItem &it, uint32_t H, uin
 {
 #pragma unroll
     for (int k = 0; k < (kSRows + 3) / 4; k++)
-        if (4 * k < (int)H) *(u4 *)(s_slot + k * 4 * kSSub + 4 * lane) = it.ew[k];
+        if (k == 0 || 4 * k < (int)H) *(u4 *)(s_slot + k * 4 * kSSub + 4 * lane) = it.ew[k];
+}
+
+// split_stage of an item loaded by split_load_all, every piece written (the
+// slot's rows past the item's last code row hold copies of its last piece,
+// which the decoder reads past the end of a sub-block's codes and never
+// consumes): every load of the item is waited for on every path.
+__device__ __forceinline__ void split_stage_all(const SplitItem &it, uint32_t *s_slot, int lane)
+{
+#pragma unroll
+    for (int k = 0; k < (kSRows + 3) / 4; k++)
+        *(u4 *)(s_slot + k * 4 * kSSub + 4 * lane) = it.ew[k];
 }
 
 // Decodes the 64 weights of this lane's sub-block against the staged x and
@@ -400,24 +414,27 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
                 }
             };
             // The slot is rewritten only after the previous item's reads (LDS
-            // operations of a wave complete in order).
+            // operations of a wave complete in order).  The next item's loads
+            // go out after this one is staged: the wait the staging needs
+            // (for loads issued on some paths only) then comes before them,
+            // and the decode runs with them in flight.
             if (seg_items > 0 && (seg > 0 || p > 0)) {
                 const int64_t c = chunk_of(seg, p, 0, rA, hA);
                 split_load(A, S, c, rA, hA, lane);
             }
             for (int b = 0; b < seg_items; b += 2) {
+                split_stage(A, hA, s_slot, lane);
                 if (b + 1 < seg_items) {
                     const int64_t c = chunk_of(seg, p, b + 1, rB, hB);
                     split_load(B, S, c, rB, hB, lane);
                 }
-                split_stage(A, hA, s_slot, lane);
                 add_rows(split_decode(A.raw, s_lds, lane_addr, xr, xsw), b);
                 if (b + 1 >= seg_items) break;
+                split_stage(B, hB, s_slot, lane);
                 if (b + 2 < seg_items) {
                     const int64_t c = chunk_of(seg, p, b + 2, rA, hA);
                     split_load(A, S, c, rA, hA, lane);
                 }
-                split_stage(B, hB, s_slot, lane);
                 add_rows(split_decode(B.raw, s_lds, lane_addr, xr, xsw), b + 1);
             }
         }
@@ -443,38 +460,46 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
     }
 }
 
-// Row groups of several chunks (GR > 1 and R = K GR / 4096 > 1: K = 3072,
-// 5120, 6144, 7168), plain x, one matrix.  split_gemv_kernel walks a
-// group's R chunks in one wave, one x tile per chunk, so with few groups per
-// CU (the 1.7B down projection: 1024 groups) it runs one wave per SIMD.
-// Here the whole x is staged once (K <= kRgMaxK, in the tile's swizzled
-// 64-float rows) and the R chunks of a group go to R waves at once: a tile
-// is GPB groups (GPB R <= NW waves in the block), wave w decodes chunk w % R
-// of group w / R, writes its rows' wave sums (at most two rows per chunk,
-// K >= 3072 being a multiple of 1024) to LDS, and after a barrier one thread
-// per output row adds them in chunk order.  That is the order in
-// which split_gemv_kernel adds its chunks' wave sums, over the same per-lane
-// dot products, so the outputs are equal bit for bit.
-constexpr int kRgMaxK = 7168;
+// Rows or row groups of several chunks (R = K GR / 4096 > 1: K = 3072,
+// 5120, 6144, 7168 in groups, K = 8192, 12288 as whole rows), plain x, one
+// matrix.  split_gemv_kernel walks a group's R chunks in one wave, one x
+// tile per chunk, with a barrier and the next tile's staging between them.
+// Here the whole x is staged once (K <= rg_max_k(NW), in the tile's
+// swizzled 64-float rows) and the R chunks of a group go to R waves: the
+// block holds GPB R waves (<= NW), and wave (gl, p) = gl R + p decodes chunk
+// p of the block's groups gl, gl + GPB, gl + 2 GPB, ... one after another,
+// the next one's loads in flight while one is decoded.  The wave sums of a
+// chunk's rows (at most two rows: K is a multiple of 1024 and at least
+// 3072) stay in the register of lane (item mod 64).  After every 64 items
+// the waves write them to their slots, and after a barrier one thread per
+// output row adds them in chunk order.  That is the order in which
+// split_gemv_kernel adds its chunks' wave sums, over the same per-lane dot
+// products, so the outputs are equal bit for bit.  Block b owns groups
+// b, b + nblocks, ...  LDS: the table, x and NW slots fill the 160 KiB.
+constexpr int kRgLdsWords = 40960;
+constexpr int rg_max_k(int nw) { return kRgLdsWords - kSLut - nw * kSSlotWords; }
 
 template <int NW>
 __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_rg_kernel(const float *__restrict__ x,
                                                                       SplitSeg S, int K, int GR,
                                                                       int R, int GPB)
 {
-    __shared__ __attribute__((aligned(16)))
-        uint32_t s_lds[kSLut + kRgMaxK + NW * kSSlotWords + 2 * NW];
+    constexpr int kMaxK = rg_max_k(NW);
+    __shared__ __attribute__((aligned(16))) uint32_t s_lds[kRgLdsWords];
     float *const s_x = (float *)(s_lds + kSLut);
-    float *const s_part = (float *)(s_lds + kSLut + kRgMaxK + NW * kSSlotWords);   // [NW][2]
     const int lane = threadIdx.x & (CBQ_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CBQ_WAVE);
-    uint32_t *const s_slot = s_lds + kSLut + kRgMaxK + wave * kSSlotWords;
+    uint32_t *const s_slots = s_lds + kSLut + kMaxK;
+    uint32_t *const s_slot = s_slots + wave * kSSlotWords;
     const int lane_addr =
-        __builtin_amdgcn_readfirstlane(4 * (kSLut + kRgMaxK + wave * kSSlotWords)) + 4 * lane;
+        __builtin_amdgcn_readfirstlane(4 * (kSLut + kMaxK + wave * kSSlotWords)) + 4 * lane;
     const int nw = GPB * R;                        // waves in the block (blockDim / 64)
     const int Mg = S.M / GR;
-    const int n_tiles = (Mg + GPB - 1) / GPB;
-    const int gl = wave / R, p = wave - gl * R;    // this wave: group gl of a tile, chunk p
+    const int nblk = gridDim.x, b = blockIdx.x;
+    const int nb = (Mg - b + nblk - 1) / nblk;     // groups of this block (>= 1: nblk <= Mg)
+    const int gl = wave / R, p = wave - gl * R;    // this wave: chunk p of groups gl + i GPB
+    const int ni = gl < nb ? (nb - gl + GPB - 1) / GPB : 0;
+    const int n_seg = ((nb + GPB - 1) / GPB + 63) >> 6;   // wave gl = 0's items, by 64
     // rows of the group that chunk p touches, this lane's row, and the x row
     // (64 floats) of this lane's sub-block: columns (p 4096 + 64 lane) mod K
     const int q_lo = p * kSChunk / K, q_hi = (p * kSChunk + kSChunk - 1) / K;
@@ -484,16 +509,14 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_rg_kernel(const floa
     const int xsw = (xrow & 15) << 2;
     const __attribute__((address_space(4))) uint32_t *const ro =
         (const __attribute__((address_space(4))) uint32_t *)S.row_off;
-    // chunk of tile t for this wave (a group past the matrix reads chunk 0:
-    // its loads are issued, its sums unused)
-    auto chunk_at = [&](int t, bool &mine) -> int64_t {
-        const int g = t * GPB + gl;
-        mine = g < Mg;
-        return mine ? (int64_t)__builtin_amdgcn_readfirstlane(g * R + p) : 0;
+    // chunk of item i of this wave (group b + (gl + i GPB) nblk)
+    auto chunk_of = [&](int i) -> int64_t {
+        return (int64_t)__builtin_amdgcn_readfirstlane(((gl + i * GPB) * nblk + b) * R + p);
     };
 
     // the table, then x in 16-byte pieces (piece c of 64-float row r holds x
-    // piece c ^ (r & 15) of that row), then the first tile's chunk
+    // piece c ^ (r & 15) of that row), then the first item's chunk (a wave
+    // without items reads chunk 0, unused)
     for (int i = wave; i < kSLut / (4 * CBQ_WAVE); i += nw) {
         __builtin_amdgcn_global_load_lds(S.lut + i * 4 * CBQ_WAVE + 4 * lane,
                                          (__attribute__((address_space(3))) void *)(s_lds + i * 4 * CBQ_WAVE),
@@ -506,8 +529,7 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_rg_kernel(const floa
                                          16, 0, 0);
     }
     SplitItem A, B;
-    bool mineA = false, mineB = false;
-    int64_t c = chunk_at(blockIdx.x, mineA);
+    int64_t c = ni > 0 ? chunk_of(0) : 0;
     const uint32_t rA = ro[c];
     uint32_t hA = ro[c + 1] - rA;
     hA = hA < (uint32_t)kSRows ? hA : (uint32_t)kSRows;
@@ -520,49 +542,67 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_rg_kernel(const floa
                                ((kFirstLoads >> 4) << 14));
     lds_barrier();
 
-    for (int t = blockIdx.x; t < n_tiles; t += gridDim.x) {
-        // the next tile's chunk in flight while this one is decoded (every
-        // load issued, so the wait for this chunk leaves them in flight)
-        const bool more = t + (int)gridDim.x < n_tiles;
-        uint32_t hB = 0;
-        if (more) {                                // block-uniform
-            c = chunk_at(t + gridDim.x, mineB);
-            const uint32_t rB = ro[c];
-            hB = ro[c + 1] - rB;
-            hB = hB < (uint32_t)kSRows ? hB : (uint32_t)kSRows;
-            split_load_all(B, S, c, rB, hB, lane);
-        }
-        float part0 = 0.f, part1 = 0.f;
-        if (mineA) {                               // wave-uniform
-            split_stage(A, hA, s_slot, lane);
-            const float acc = split_decode(A.raw, s_lds, lane_addr, xr, xsw);
-            part0 = wave_sum(q_me == q_lo ? acc : 0.f);
-            if (q_hi > q_lo) part1 = wave_sum(q_me == q_hi ? acc : 0.f);
-        }
-        if (lane == 0) {
-            s_part[2 * wave] = part0;
-            s_part[2 * wave + 1] = part1;
-        }
-        __syncthreads();
-        // one thread per row of the tile: its chunks' sums in chunk order
-        if ((int)threadIdx.x < GPB * GR) {
-            const int g2 = (int)threadIdx.x / GR, q = (int)threadIdx.x - g2 * GR;
-            const int g = t * GPB + g2;
-            if (g < Mg) {
-                float res = 0.f;
-                for (int pp = 0; pp < R; pp++) {
-                    const int lo = pp * kSChunk / K, hi = (pp * kSChunk + kSChunk - 1) / K;
-                    if (q >= lo && q <= hi) res += s_part[2 * (g2 * R + pp) + (q - lo)];
-                }
-                S.out[(int64_t)g * GR + q] = res;
+    // Item k's loads (item ni - 1's again past the last one, so that every
+    // path issues the same loads and the wait for the item being decoded
+    // leaves them in flight); items alternate between A and B.
+    auto load_item = [&](SplitItem &it, uint32_t &h, int k) {
+        const int64_t ck = chunk_of(k < ni ? k : ni - 1);
+        const uint32_t r0 = ro[ck];
+        h = ro[ck + 1] - r0;
+        h = h < (uint32_t)kSRows ? h : (uint32_t)kSRows;
+        split_load_all(it, S, ck, r0, h, lane);
+    };
+    uint32_t hB = 0;
+    int i = 0;
+    for (int seg = 0; seg < n_seg; seg++) {
+        float r0 = 0.f, r1 = 0.f;                  // lane l: item 64 seg + l's row sums
+        const int end = min(ni, 64 * seg + 64);
+        auto take = [&](float acc, int k) {
+            const float s0 = wave_sum(q_me == q_lo ? acc : 0.f);
+            const float s1 = q_hi > q_lo ? wave_sum(q_me == q_hi ? acc : 0.f) : 0.f;
+            if (lane == k - 64 * seg) {
+                r0 = s0;
+                r1 = s1;
             }
+        };
+        // (64 seg is even, so a pair never straddles two segments; an odd
+        // count ends only the last one)
+        for (; i < end; i += 2) {                  // wave-uniform
+            load_item(B, hB, i + 1);
+            split_stage_all(A, s_slot, lane);
+            take(split_decode(A.raw, s_lds, lane_addr, xr, xsw), i);
+            if (i + 1 >= end) {
+                i = end;
+                break;
+            }
+            load_item(A, hA, i + 2);
+            split_stage_all(B, s_slot, lane);
+            take(split_decode(B.raw, s_lds, lane_addr, xr, xsw), i + 1);
         }
-        __syncthreads();                           // sums read (and the slot free) before the next tile
-        if (more) {
-            A = B;
-            hA = hB;
-            mineA = mineB;
+        // the last decode's slot reads are done (its sums used them), so the
+        // slot's first 128 words take the row sums until the next staging
+        s_slot[2 * lane] = __float_as_uint(r0);
+        s_slot[2 * lane + 1] = __float_as_uint(r1);
+        __syncthreads();
+        // one thread per row: its chunks' sums in chunk order
+        const int base = 64 * GPB * seg;
+        for (int t = (int)threadIdx.x; t < 64 * GPB * GR; t += nw * CBQ_WAVE) {
+            const int jl = t / GR, q = t - jl * GR;
+            if (base + jl >= nb) break;            // (t rises with jl)
+            const int g2 = jl % GPB, il = jl / GPB;
+            float res = 0.f;
+            for (int pp = 0; pp < R; pp++) {
+                const int lo = pp * kSChunk / K, hi = (pp * kSChunk + kSChunk - 1) / K;
+                if (q >= lo && q <= hi)
+                    res += __uint_as_float(s_slots[(g2 * R + pp) * kSSlotWords + 2 * il + (q - lo)]);
+            }
+            S.out[((int64_t)(base + jl) * nblk + b) * GR + q] = res;
         }
+        // nothing in flight into the next segment's loop (the next item's
+        // loads, an unused pair half's, the stores): the compiler then keeps
+        // the next item's loads in flight over each decode
+        __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));   // vmcnt(0)
+        __syncthreads();                           // sums read before the next item's staging
     }
 }
 
@@ -1324,27 +1364,32 @@ int split_linear(const float *x, const float *x1, float *h_out, int mode, float 
         g.out = outs[i];
         g.M = Ms[i];
     }
-    // Row groups of several chunks, plain x, one matrix: the groups' chunks
-    // to separate waves (split_gemv_rg_kernel), the same outputs bit for bit.
-    // GPB groups per tile, one block per CU: a block's tile takes about as
+    // Rows or row groups of several chunks, plain x, one matrix: the chunks
+    // of a group to separate waves (split_gemv_rg_kernel), the same outputs
+    // bit for bit.  16 waves a block up to K = 8192, 12 up to K = 12288 (x
+    // and the slots share what the table leaves of the LDS).  One block per
+    // CU, GPB R waves each: a round of one chunk per wave takes about as
     // long as 6 + GPB R chunks' worth of decode work (one wave's decode is
     // latency-bound; more waves share the SIMDs), so the GPB with the least
-    // tiles per block x (6 + GPB R) (ties to the larger GPB).
+    // rounds x (6 + GPB R) (ties to the larger GPB).
     const int R = K * GR / kSChunk;
-    if (mode == XF_NONE && n == 1 && !arg_v && GR > 1 && R > 1 && R <= 16 && K <= kRgMaxK &&
-        ((uintptr_t)x & 15) == 0) {
-        constexpr int NW = 16;
-        const int Mg = Ms[0] / GR, cus = cbq_num_cus();
+    const int rg_nw = K <= rg_max_k(16) ? 16 : K <= rg_max_k(12) ? 12 : 0;
+    if (mode == XF_NONE && n == 1 && !arg_v && R > 1 && R <= rg_nw && ((uintptr_t)x & 15) == 0) {
+        const int Mg = Ms[0] / GR;
+        const int blocks = std::max(1, std::min(cbq_num_cus(), Mg));
+        const int nb = (Mg + blocks - 1) / blocks;   // groups of block 0 (the most)
         int GPB = 1;
         int64_t best = -1;
-        for (int gpb = 1; gpb * R <= NW; gpb++) {
-            const int64_t cost = (int64_t)(((Mg + gpb - 1) / gpb + cus - 1) / cus) * (6 + gpb * R);
+        for (int gpb = 1; gpb * R <= rg_nw; gpb++) {
+            const int64_t cost = (int64_t)((nb + gpb - 1) / gpb) * (6 + gpb * R);
             if (best < 0 || cost <= best) { best = cost; GPB = gpb; }
         }
-        const int tiles = (Mg + GPB - 1) / GPB;
-        const int blocks = std::max(1, std::min(cus, tiles));
-        hipLaunchKernelGGL(split_gemv_rg_kernel<NW>, dim3(blocks), dim3(GPB * R * CBQ_WAVE), 0,
-                           stream, x, segs.s[0], K, GR, R, GPB);
+        if (rg_nw == 16)
+            hipLaunchKernelGGL(split_gemv_rg_kernel<16>, dim3(blocks), dim3(GPB * R * CBQ_WAVE), 0,
+                               stream, x, segs.s[0], K, GR, R, GPB);
+        else
+            hipLaunchKernelGGL(split_gemv_rg_kernel<12>, dim3(blocks), dim3(GPB * R * CBQ_WAVE), 0,
+                               stream, x, segs.s[0], K, GR, R, GPB);
         if (n_blocks) *n_blocks = blocks;
         return cbq_launch_status("split_gemv_rg_kernel");
     }
