@@ -225,14 +225,20 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
 
     const int R = K * GR / kSChunk;                    // chunks per row group
     const int Mg = M / GR;                              // row groups
-    // Wave w of block b is walker w nblocks + b and takes rows (groups)
+    // Wave w of block b is walker w nblocks + pos and takes rows (groups)
     // wid, wid + W, ...: when the rows do not divide evenly, the extra ones
     // go to the low waves of every block, not to every wave of the low
     // blocks, so no CU holds more than its share plus one row per wave.
-    const int W = S.nblocks * NW;
-    const int wid = wave * S.nblocks + bid;
+    // pos numbers the blocks XCD by XCD (blocks b and b + 8 share one), so
+    // neighbouring rows are read and written through one L2: a chunk's code
+    // pieces past its last row and an output line stay in that XCD.
+    const int nbk = S.nblocks;
+    const int xu = bid & 7;
+    const int pos = xu * (nbk >> 3) + min(xu, nbk & 7) + (bid >> 3);
+    const int W = nbk * NW;
+    const int wid = wave * nbk + pos;
     const int rows = wid < Mg ? (Mg - wid + W - 1) / W : 0;
-    const int rows_max = bid < Mg ? (Mg - bid + W - 1) / W : 0;   // wave 0's
+    const int rows_max = pos < Mg ? (Mg - pos + W - 1) / W : 0;   // wave 0's
     const int n_seg = (rows_max + 63) >> 6;
     const float *const xr = s_x + lane * 64;
     const int xsw = (lane & 15) << 2;
@@ -474,8 +480,8 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
 // the waves write them to their slots, and after a barrier one thread per
 // output row adds them in chunk order.  That is the order in which
 // split_gemv_kernel adds its chunks' wave sums, over the same per-lane dot
-// products, so the outputs are equal bit for bit.  Block b owns groups
-// b, b + nblocks, ...  LDS: the table, x and NW slots fill the 160 KiB.
+// products, so the outputs are equal bit for bit.  LDS: the table, x and NW
+// slots fill the 160 KiB.
 constexpr int kRgLdsWords = 40960;
 constexpr int rg_max_k(int nw) { return kRgLdsWords - kSLut - nw * kSSlotWords; }
 
@@ -495,8 +501,12 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_rg_kernel(const floa
         __builtin_amdgcn_readfirstlane(4 * (kSLut + kMaxK + wave * kSSlotWords)) + 4 * lane;
     const int nw = GPB * R;                        // waves in the block (blockDim / 64)
     const int Mg = S.M / GR;
+    // block b owns groups pos, pos + nblk, ... with the blocks numbered XCD
+    // by XCD (b and b + 8 share one), so neighbouring groups go through one
+    // L2 (a chunk's code pieces past its last row, an output line)
     const int nblk = gridDim.x, b = blockIdx.x;
-    const int nb = (Mg - b + nblk - 1) / nblk;     // groups of this block (>= 1: nblk <= Mg)
+    const int pos = (b & 7) * (nblk >> 3) + min(b & 7, nblk & 7) + (b >> 3);
+    const int nb = (Mg - pos + nblk - 1) / nblk;   // groups of this block (>= 1: nblk <= Mg)
     const int gl = wave / R, p = wave - gl * R;    // this wave: chunk p of groups gl + i GPB
     const int ni = gl < nb ? (nb - gl + GPB - 1) / GPB : 0;
     const int n_seg = ((nb + GPB - 1) / GPB + 63) >> 6;   // wave gl = 0's items, by 64
@@ -509,9 +519,9 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_rg_kernel(const floa
     const int xsw = (xrow & 15) << 2;
     const __attribute__((address_space(4))) uint32_t *const ro =
         (const __attribute__((address_space(4))) uint32_t *)S.row_off;
-    // chunk of item i of this wave (group b + (gl + i GPB) nblk)
+    // chunk of item i of this wave (group pos + (gl + i GPB) nblk)
     auto chunk_of = [&](int i) -> int64_t {
-        return (int64_t)__builtin_amdgcn_readfirstlane(((gl + i * GPB) * nblk + b) * R + p);
+        return (int64_t)__builtin_amdgcn_readfirstlane(((gl + i * GPB) * nblk + pos) * R + p);
     };
 
     // the table, then x in 16-byte pieces (piece c of 64-float row r holds x
@@ -596,7 +606,7 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_rg_kernel(const floa
                 if (q >= lo && q <= hi)
                     res += __uint_as_float(s_slots[(g2 * R + pp) * kSSlotWords + 2 * il + (q - lo)]);
             }
-            S.out[((int64_t)(base + jl) * nblk + b) * GR + q] = res;
+            S.out[((int64_t)(base + jl) * nblk + pos) * GR + q] = res;
         }
         // nothing in flight into the next segment's loop (the next item's
         // loads, an unused pair half's, the stores): the compiler then keeps
