@@ -1232,19 +1232,33 @@ int cbq_split_linear_fewtok_f32(const float *x, int T, int n, const cbq_split_ma
         tiles_sum += tiles[i];
     }
     // one block per CU in all: a matrix gets one block per tile when the
-    // tiles fit, else blocks in proportion to its tiles (each block then
-    // walks several tiles, staging the table once)
+    // tiles fit, else blocks in proportion to its tiles, rounded down, and
+    // the CUs left over one at a time to the matrix with the most tiles per
+    // block (each block then walks several tiles, staging the table once)
     const int cus = cbq_num_cus();
     int blocks = 0;
     for (int i = 0; i < n; i++) {
         SplitSeg &g = segs.s[i];
-        g.block0 = blocks;
-        const int share =
-            tiles_sum <= cus ? tiles[i]
-                             : (int)std::max<int64_t>(1, (cus * (int64_t)tiles[i] + tiles_sum / 2) /
-                                                             tiles_sum);
+        const int share = tiles_sum <= cus
+                              ? tiles[i]
+                              : (int)std::max<int64_t>(1, cus * (int64_t)tiles[i] / tiles_sum);
         g.nblocks = std::max(1, std::min(share, tiles[i]));
         blocks += g.nblocks;
+    }
+    for (; blocks < cus; blocks++) {
+        int best = -1;
+        for (int i = 0; i < n; i++) {
+            if (segs.s[i].nblocks >= tiles[i]) continue;
+            if (best < 0 || (int64_t)tiles[i] * segs.s[best].nblocks >
+                                (int64_t)tiles[best] * segs.s[i].nblocks)
+                best = i;
+        }
+        if (best < 0) break;
+        segs.s[best].nblocks++;
+    }
+    for (int i = 0, b0 = 0; i < n; i++) {
+        segs.s[i].block0 = b0;
+        b0 += segs.s[i].nblocks;
     }
     // with a workspace, x's three bf16 parts are written once per 16 tokens
     // in fragment order and the GEMM loads them ready-made
