@@ -182,14 +182,15 @@ def _split_of(cuda, w):
 @pytest.mark.parametrize("Ms,K", [((2048, 1024, 1024), 2048), ((6144,), 2048),
                                   ((2048,), 6144), ((96, 40), 1024), ((64, 128), 3072),
                                   ((512,), 5120), ((8194, 6), 6144), ((36, 4), 7168),
-                                  ((66, 2), 8192), ((2050, 2), 12288)])
+                                  ((66, 2), 8192), ((2050, 2), 12288), ((40, 4), 9216),
+                                  ((22, 2), 10240)])
 def test_row_groups_against_oracle(cuda, oracle, Ms, K):
     """K % 4096 != 0: the split GEMV walks groups of 4096 / gcd(K, 4096) rows
     (2 for K = 2048, 6144; 4 for K = 1024, 3072, 5120).  Each matrix against
     the reference C kernel on the same indices (rel-L2 <= 1e-5), the grouped
     launch equal to one launch per matrix bit for bit.  With several chunks
-    per group or row (K = 3072, 5120, 6144, 7168; 8192 and 12288 as whole
-    rows) one matrix goes to the kernel that puts a group's chunks on
+    per group or row (K = 3072, 5120, 6144, 7168, 9216, 10240; 8192 and 12288
+    as whole rows) one matrix goes to the kernel that puts a group's chunks on
     separate waves and a grouped launch to the row walk, so that equality
     holds between the two kernels; (8194, 6) x 6144 and (2050, 2) x 12288
     give that kernel several tiles per block."""
