@@ -62,6 +62,18 @@ constexpr int kEpiRows = 16;
 constexpr int kLdsEpi = kPWaves * kEpiRows * kEpiRow<true>;
 constexpr int kWtChunks = (6 * kWBuf * 16 > kLdsEpi ? 6 * kWBuf * 16 : kLdsEpi) / 16;
 
+// Diagnostic build (-DCBQ_TIMELINE): wave w of block b (grid index
+// z * gridDim.x + b) records the 100 MHz s_memrealtime clock at entry, after
+// the codebook staging, after the loop's prologue (ring filled, first two
+// W tiles decoded), after the K loop and at exit, plus its K steps, into
+// cbq_pf_timeline (read by cbq_prefill_timeline_read).  The product build
+// has none of it.
+constexpr int kPfTimelineWaves = 4096;
+constexpr int kPfTimelineFields = 6;
+#ifdef CBQ_TIMELINE
+__device__ unsigned long long cbq_pf_timeline[kPfTimelineWaves * kPfTimelineFields];
+#endif
+
 // Word 3 of a raw buffer resource on gfx9 (32-bit data format; no swizzle,
 // no stride): loads past num_records bytes return 0.
 constexpr int kBufRsrcWord3 = 0x00020000;
@@ -126,7 +138,7 @@ __device__ __forceinline__ void prefill_loop(
     __amdgpu_buffer_rsrc_t xb, const uint32_t (&xoff)[kTB], __amdgpu_buffer_rsrc_t wb,
     const uint32_t (&doff)[kRawLoads<BITS>], int G, const uint16_t *s_cb, const uint16_t *s_cblo,
     u32x4 *s_w, u32x4 *s_wlo, uint32_t *s_raw, int wave, int lane, bool active,
-    f32x4 (&acc)[kTB][kNB])
+    f32x4 (&acc)[kTB][kNB], unsigned long long &ts_pro)
 {
     constexpr int NF = 64 / kPWaves;                     // indices a thread decodes
     constexpr int NW = (NF * BITS + 31 + 31) / 32;       // words covering them
@@ -255,6 +267,11 @@ __device__ __forceinline__ void prefill_loop(
             for (int nb = 0; nb < kNB; nb++) read_frag(0, nb, bf[nb], bl);
         }
     }
+#ifdef CBQ_TIMELINE
+    ts_pro = __builtin_amdgcn_s_memrealtime();
+#else
+    (void)ts_pro;
+#endif
     for (int g0 = 0; g0 < G; g0 += kUnroll) {
 #pragma unroll
         for (int u = 0; u < kUnroll; u++) {
@@ -307,6 +324,10 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     const int tid = threadIdx.x;
     const int lane = tid & (CBQ_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / CBQ_WAVE);
+    unsigned long long ts_pro = 0;
+#ifdef CBQ_TIMELINE
+    const unsigned long long ts_entry = __builtin_amdgcn_s_memrealtime();
+#endif
     const int tix = tile0 + (int)blockIdx.x;
     const int t0 = (tix % nT) * kPT;
     const int m0 = (tix / nT) * kPM;
@@ -338,6 +359,9 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
         }
     }
     const bool two = __syncthreads_or(inexact);        // also publishes the codebook
+#ifdef CBQ_TIMELINE
+    const unsigned long long ts_staged = __builtin_amdgcn_s_memrealtime();
+#endif
 
     // x fragments: token block tb, lane -> row lane % 16, k chunk lane / 16.
     // XF: x is in fragment order (prefill_x_frag_kernel), the wave's 1 KiB
@@ -381,7 +405,7 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
     const bool active = t0 + wave * kWT < T;
 #define CBQ_PREFILL_LOOP(TW, H)                                                                 \
     prefill_loop<BITS, TW, H, XF>(xrs, xoff, wrs, doff, G, s_cb, s_cblo, s_w, s_wlo, s_raw, wave, \
-                                  lane, active, acc)
+                                  lane, active, acc, ts_pro)
     static_assert(kPWaves == 8, "the part switch below has kPWaves / 2 cases");
     if (two) {
         switch (wave & 3) {
@@ -399,6 +423,9 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
         }
     }
 #undef CBQ_PREFILL_LOOP
+#ifdef CBQ_TIMELINE
+    const unsigned long long ts_loop = __builtin_amdgcn_s_memrealtime();
+#endif
 
     // acc[tb][nb][r] = out[token t0 + 64 wave + 16 tb + 4 (lane / 16) + r]
     //                     [feature m0 + 16 nb + lane % 16]
@@ -443,6 +470,19 @@ __global__ __launch_bounds__(kPBlock) void fixed_prefill_kernel(
             }
         }
     }
+#ifdef CBQ_TIMELINE
+    const unsigned long long ts_exit = __builtin_amdgcn_s_memrealtime();
+    const int twid = ((int)(blockIdx.z * gridDim.x + blockIdx.x)) * kPWaves + wave;
+    if (lane == 0 && twid < kPfTimelineWaves) {
+        unsigned long long *tl = cbq_pf_timeline + (size_t)twid * kPfTimelineFields;
+        tl[0] = ts_entry;
+        tl[1] = ts_staged;
+        tl[2] = ts_pro;
+        tl[3] = ts_loop;
+        tl[4] = ts_exit;
+        tl[5] = (unsigned long long)G;
+    }
+#endif
 }
 
 // x [T][K] bf16 row-major -> fragment order: piece i (16 bytes) of chunk
@@ -648,4 +688,25 @@ int cbq_prefill_bf16(const uint16_t *x, const uint8_t *packed, const float *cb, 
     case 14: return launch_prefill<14>(x, packed, cb, out, T, M, K, C, p, part, xf, st);
     default: return -1;
     }
+}
+
+// Per-wave timeline of the last bf16 prefill launch (every launch of a call
+// writes it; the last one's waves win), in a -DCBQ_TIMELINE build:
+// kPfTimelineWaves x 6 uint64 (entry, codebook staged, prologue done, loop
+// done, exit in 10 ns ticks; K steps).  CK_ERR_ARG in the product build or
+// when dst_bytes is short.
+extern "C" int cbq_prefill_timeline_read(void *dst, size_t dst_bytes)
+{
+#ifdef CBQ_TIMELINE
+    const size_t n = sizeof(unsigned long long) * kPfTimelineWaves * kPfTimelineFields;
+    if (!dst || dst_bytes < n) return CK_ERR_ARG;
+    if (hipMemcpyFromSymbol(dst, HIP_SYMBOL(cbq_pf_timeline), n, 0, hipMemcpyDeviceToHost) !=
+        hipSuccess)
+        return CK_ERR_HIP;
+    return CK_SUCCESS;
+#else
+    (void)dst;
+    (void)dst_bytes;
+    return CK_ERR_ARG;
+#endif
 }

@@ -4,6 +4,7 @@
 
     python codebook-quantization_amd/build_native.py --timeline   # once, on the build host
     python codebook-quantization_amd/timeline.py [--lib PATH]      # on the GPU
+    python codebook-quantization_amd/timeline.py --prefill          # the bf16 prefill GEMM
 
 Each shape: N(0, 0.02) bf16 weights (synthetic.make_bf16), the tensor's own
 frequency-sorted codebook, 13-bit packed indices, four copies; one second of
@@ -118,5 +119,86 @@ def main(argv=None):
         print(row)
 
 
+PREFILL_SHAPES = (("gate/up, one round of 192 tiles", 1024, 12288, 4096),
+                  ("gate/up, one round, K = 1024", 1024, 12288, 1024),
+                  ("q, 128 tiles, K split 2", 2048, 4096, 4096),
+                  ("q, 32 tiles, K split 8", 512, 4096, 4096),
+                  ("k, 8 tiles, K split 16", 512, 1024, 4096))
+
+
+def prefill(args):
+    """Per-wave timeline of the bf16 prefill GEMM (cbq_linear_bf16_ws) on
+    9B shapes: one timed call per shape after a second of warm-up; the last
+    prefill launch of the call is the one recorded."""
+    import cbq_native as nat
+    import codebook_builder as cbb
+    import synthetic
+    lib = nat.load(args.lib)
+    probe = np.zeros(4096 * 6, np.uint64)
+    if lib.cbq_prefill_timeline_read(probe.ctypes.data, probe.nbytes) == nat.CK_ERR_ARG:
+        raise SystemExit(f"{args.lib} is not a timeline build (build_native.py --timeline)")
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream().cuda_stream
+    print("| shape | T, K->M | call µs (events) | prefill launch span µs | waves | entry skew µs "
+          "(p50/p100) | codebook staged µs | prologue µs | K loop µs (p10/p50/p90) | µs per K "
+          "step | epilogue µs (p50/p90) | loop end -> launch end µs |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|---|")
+    for name, T, M, K in PREFILL_SHAPES:
+        w = synthetic.make_bf16((M, K), f"timeline.prefill.{M}.{K}", device=dev)
+        cb, lut = cbb.codebook_from_counts_torch(cbb.counts_torch(w))
+        idx = lut[cbb.patterns_torch(w).reshape(-1).to(torch.int64)]
+        del w
+        C, bits = cb.numel(), cbb.bits_for(cb.numel())
+        pk = cbb.pack_torch(idx, bits)
+        p = torch.zeros(pk.numel() + 32, dtype=torch.uint8, device=dev)
+        p[:pk.numel()] = pk
+        del idx, pk
+        x = torch.randn(T, K, device=dev).bfloat16()
+        out = torch.empty(T, M, device=dev, dtype=torch.bfloat16)
+        nws = int(lib.cbq_linear_bf16_workspace(T, M, K))
+        ws = torch.empty(max(1, nws // 4), dtype=torch.float32, device=dev)
+
+        def call():
+            nat.check(lib.cbq_linear_bf16_ws(x.data_ptr(), p.data_ptr(), cb.data_ptr(),
+                                             out.data_ptr(), T, M, K, C, bits, ws.data_ptr(), nws,
+                                             st), "cbq_linear_bf16_ws")
+        t0 = time.time()
+        while time.time() - t0 < args.warm:
+            for _ in range(8):
+                call()
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        call()
+        e1.record()
+        torch.cuda.synchronize()
+        ev_us = e0.elapsed_time(e1) * 1e3
+        tl = np.zeros(4096 * 6, np.uint64)
+        nat.check(lib.cbq_prefill_timeline_read(tl.ctypes.data, tl.nbytes),
+                  "cbq_prefill_timeline_read")
+        tl = tl.reshape(4096, 6).astype(np.int64)
+        last = tl[:, 0].max()
+        tl = tl[(tl[:, 0] > 0) & (tl[:, 0] >= last - 100_000)]  # this launch (1 ms window)
+        r = (tl[:, :5] - tl[:, 0].min()) * 0.01                  # µs from the first entry
+        G = tl[:, 5]
+        loop = r[:, 3] - r[:, 2]
+        print(f"| {name} | {T}, {K}->{M} | {ev_us:.1f} | {r[:, 4].max():.1f} | {len(tl)} | "
+              f"{np.median(r[:, 0]):.2f} / {r[:, 0].max():.2f} | {np.median(r[:, 1] - r[:, 0]):.2f} | "
+              f"{np.median(r[:, 2] - r[:, 1]):.2f} | "
+              f"{' / '.join(f'{np.percentile(loop, q):.1f}' for q in (10, 50, 90))} | "
+              f"{np.median(loop / np.maximum(G, 1)):.3f} | "
+              f"{np.median(r[:, 4] - r[:, 3]):.2f} / {np.percentile(r[:, 4] - r[:, 3], 90):.2f} | "
+              f"{r[:, 4].max() - np.median(r[:, 3]):.2f} |", flush=True)
+        del p, x, out, ws
+        torch.cuda.empty_cache()
+
+
 if __name__ == "__main__":
-    main()
+    if "--prefill" in sys.argv:
+        sys.argv.remove("--prefill")
+        ap = argparse.ArgumentParser()
+        ap.add_argument("--lib", default=os.path.join(HERE, "libcbq_hip_timeline.so"))
+        ap.add_argument("--warm", type=float, default=1.0)
+        prefill(ap.parse_args())
+    else:
+        main()

@@ -445,6 +445,15 @@ const char *cbq_version(void);
  * 4096 * 6 * 8.  No counterpart in the reference. */
 int cbq_timeline_read(void *dst, size_t dst_bytes);
 
+/* Diagnostics: in a -DCBQ_TIMELINE library, copies the per-wave timeline of
+ * the last bf16 prefill GEMM launch (ck_linear_bf16 / cbq_linear_bf16_ws with
+ * T >= 64): 4096 waves x 6 uint64 (clock at entry, after the codebook
+ * staging, after the K loop's prologue, after the K loop, at exit, in 10 ns
+ * ticks; then the wave's K steps), wave w of grid block b at index
+ * 8 b + w.  CK_ERR_ARG in the normal build or when dst_bytes <
+ * 4096 * 6 * 8.  No counterpart in the reference. */
+int cbq_prefill_timeline_read(void *dst, size_t dst_bytes);
+
 /* ---- lm_head GEMV with the greedy pick fused ------------------------------
  * The one-token GEMV of the decoder's last matrix (vocabulary rows) and the
  * greedy pick of the next token in two launches: the GEMV's epilogue reduces
