@@ -61,6 +61,7 @@ SIGNATURES = {
     "cbq_version": (ctypes.c_char_p, []),
     "cbq_timeline_read": (_i, [_vp, ctypes.c_size_t]),
     "cbq_prefill_timeline_read": (_i, [_vp, ctypes.c_size_t]),
+    "cbq_split_timeline_read": (_i, [_vp, ctypes.c_size_t]),
     "ck_linear_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "ck_linear_bf16": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "cbq_linear_bf16_workspace": (ctypes.c_size_t, [_i, _i, _i]),

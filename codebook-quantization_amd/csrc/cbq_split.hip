@@ -43,6 +43,18 @@ constexpr int kSSlotRows = 16;
 constexpr int kSSlotWords = kSSlotRows * kSSub;   // one wave's chunk slot
 constexpr int kSMaxSeg = 4;
 
+// Diagnostic build (-DCBQ_TIMELINE): wave w of block b of a split_gemv_kernel
+// launch records the 100 MHz s_memrealtime clock at entry, after the first
+// barrier (table, x tile and the first chunk's offsets staged), after its
+// first chunk is decoded, after its row loop and at exit, plus its rows, in
+// cbq_split_timeline[b * NW + w] (read by cbq_split_timeline_read).  The
+// product build has none of it.
+constexpr int kSplitTimelineWaves = 4096;
+constexpr int kSplitTimelineFields = 6;
+#ifdef CBQ_TIMELINE
+__device__ unsigned long long cbq_split_timeline[kSplitTimelineWaves * kSplitTimelineFields];
+#endif
+
 constexpr int split_lds_words(int nw) { return kSLut + kSChunk + nw * kSSlotWords; }
 
 struct SplitSeg {
@@ -219,6 +231,10 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
     float *const s_x = (float *)(s_lds + kSLut);
     const int lane = threadIdx.x & (CBQ_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CBQ_WAVE);
+#ifdef CBQ_TIMELINE
+    const unsigned long long ts_entry = __builtin_amdgcn_s_memrealtime();
+    unsigned long long ts_staged = 0, ts_first = 0;
+#endif
     uint32_t *const s_slot = s_lds + kSLut + kSChunk + wave * kSSlotWords;
     const int lane_addr =
         __builtin_amdgcn_readfirstlane(4 * (kSLut + kSChunk + wave * kSSlotWords)) + 4 * lane;
@@ -356,6 +372,9 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
                 __builtin_amdgcn_s_waitcnt((kFirstLoads & 15) | (7 << 4) | (15 << 8) |
                                            ((kFirstLoads >> 4) << 14));
                 lds_barrier();
+#ifdef CBQ_TIMELINE
+                ts_staged = __builtin_amdgcn_s_memrealtime();
+#endif
             } else {
                 __syncthreads();
             }
@@ -435,6 +454,9 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
                     split_load(B, S, c, rB, hB, lane);
                 }
                 add_rows(split_decode(A.raw, s_lds, lane_addr, xr, xsw), b);
+#ifdef CBQ_TIMELINE
+                if (seg == 0 && p == 0 && b == 0) ts_first = __builtin_amdgcn_s_memrealtime();
+#endif
                 if (b + 1 >= seg_items) break;
                 split_stage(B, hB, s_slot, lane);
                 if (b + 2 < seg_items) {
@@ -459,11 +481,27 @@ __global__ __launch_bounds__(NW * CBQ_WAVE) void split_gemv_kernel(const float *
             }
         }
     }
+#ifdef CBQ_TIMELINE
+    const unsigned long long ts_loop = __builtin_amdgcn_s_memrealtime();
+#endif
     if (arg_v) {                                   // one matrix per launch (checked on the host)
         __shared__ float s_av[NW];
         __shared__ int s_ai[NW];
         arg_block_store(a_best, a_idx, s_av, s_ai, arg_v, arg_i);
     }
+#ifdef CBQ_TIMELINE
+    const unsigned long long ts_exit = __builtin_amdgcn_s_memrealtime();
+    const int twid = (int)blockIdx.x * NW + wave;
+    if (lane == 0 && twid < kSplitTimelineWaves) {
+        unsigned long long *tl = cbq_split_timeline + (size_t)twid * kSplitTimelineFields;
+        tl[0] = ts_entry;
+        tl[1] = ts_staged;
+        tl[2] = ts_first;
+        tl[3] = ts_loop;
+        tl[4] = ts_exit;
+        tl[5] = (unsigned long long)rows;
+    }
+#endif
 }
 
 // Rows or row groups of several chunks (R = K GR / 4096 > 1: K = 3072,
@@ -1518,3 +1556,23 @@ int cbq_split_linear_argmax_f32(const float *x0, const float *x1, float *h_out, 
 }
 
 }  // extern "C"
+
+// Per-wave timeline of the last split_gemv_kernel launch, in a
+// -DCBQ_TIMELINE build: kSplitTimelineWaves x 6 uint64 (entry, staged, first
+// chunk decoded, row loop done, exit in 10 ns ticks; rows).  CK_ERR_ARG in
+// the product build or when dst_bytes is short.
+extern "C" int cbq_split_timeline_read(void *dst, size_t dst_bytes)
+{
+#ifdef CBQ_TIMELINE
+    const size_t n = sizeof(unsigned long long) * kSplitTimelineWaves * kSplitTimelineFields;
+    if (!dst || dst_bytes < n) return CK_ERR_ARG;
+    if (hipMemcpyFromSymbol(dst, HIP_SYMBOL(cbq_split_timeline), n, 0, hipMemcpyDeviceToHost) !=
+        hipSuccess)
+        return CK_ERR_HIP;
+    return CK_SUCCESS;
+#else
+    (void)dst;
+    (void)dst_bytes;
+    return CK_ERR_ARG;
+#endif
+}

@@ -5,6 +5,7 @@
     python codebook-quantization_amd/build_native.py --timeline   # once, on the build host
     python codebook-quantization_amd/timeline.py [--lib PATH]      # on the GPU
     python codebook-quantization_amd/timeline.py --prefill          # the bf16 prefill GEMM
+    python codebook-quantization_amd/timeline.py --split            # the split-format row walk
 
 Each shape: N(0, 0.02) bf16 weights (synthetic.make_bf16), the tensor's own
 frequency-sorted codebook, 13-bit packed indices, four copies; one second of
@@ -39,6 +40,8 @@ def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--lib", default=os.path.join(HERE, "libcbq_hip_timeline.so"))
     ap.add_argument("--warm", type=float, default=1.0)
+    ap.add_argument("--graph", action="store_true",
+                    help="also time the four copies graph-replayed")
     args = ap.parse_args(argv)
     import cbq_native as nat
     import codebook_builder as cbb
@@ -85,6 +88,29 @@ def main(argv=None):
         ev_us = e0.elapsed_time(e1) * 1e3
         tl = np.zeros(4096 * 6, np.uint64)
         nat.check(lib.cbq_timeline_read(tl.ctypes.data, tl.nbytes), "cbq_timeline_read")
+        if args.graph:
+            # the four copies graph-replayed: time per launch, and the span of
+            # the last launch (its waves overwrite the record)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for p in mats:
+                    nat.check(lib.ck_linear_f32(x.data_ptr(), p.data_ptr(), cb.data_ptr(),
+                                                out.data_ptr(), 1, M, K, C, bits,
+                                                torch.cuda.current_stream().cuda_stream), "graph")
+            g.replay()
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(20):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            tg = np.zeros(4096 * 6, np.uint64)
+            nat.check(lib.cbq_timeline_read(tg.ctypes.data, tg.nbytes), "cbq_timeline_read")
+            tg = tg.reshape(4096, 6).astype(np.int64)
+            tg = tg[(tg[:, 0] > 0) & (tg[:, 0] >= tg[:, 0].max() - 100_000)]
+            print(f"graph {name}: {e0.elapsed_time(e1) * 1e3 / (20 * len(mats)):.1f} us per launch, "
+                  f"last launch span {(tg[:, 4].max() - tg[:, 0].min()) * 0.01:.1f} us", flush=True)
+            del g
         cus = torch.cuda.get_device_properties(dev).multi_processor_count
         W = min(4096, 8 * min(cus, (M + 7) // 8))                # waves of the launch
         tl = tl.reshape(4096, 6)[:W].astype(np.int64)
@@ -193,8 +219,112 @@ def prefill(args):
         torch.cuda.empty_cache()
 
 
+SPLIT_SHAPES = (("stacked gate+up, SiLU product in the epilogue", True, 12288, 4096),
+                ("stacked q/k/v rows as one matrix", False, 6144, 4096),
+                ("o_proj", False, 4096, 4096))
+
+
+def split(args):
+    """Per-wave timeline of the one-token split-format row walk
+    (split_gemv_kernel) on 9B shapes: the split format built from each
+    matrix's indices, one second of warm-up launches, then one launch timed
+    with HIP events."""
+    import ctypes
+    import cbq_native as nat
+    import codebook_builder as cbb
+    import synthetic
+    from gpu_huffman_functions import build_split
+    lib = nat.load(args.lib)
+    probe = np.zeros(4096 * 6, np.uint64)
+    if lib.cbq_split_timeline_read(probe.ctypes.data, probe.nbytes) == nat.CK_ERR_ARG:
+        raise SystemExit(f"{args.lib} is not a timeline build (build_native.py --timeline)")
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream().cuda_stream
+    print("| shape | event µs (one launch) | graph-replayed µs per launch / in-kernel span µs "
+          "of the last | in-kernel span µs | waves | staged after entry µs (p50/p90) | "
+          "first chunk decoded µs after that (p50/p90) | µs per further chunk (p50) | "
+          "loop end µs (p10/p50/p90/p100) | loop end -> exit µs (p50) |")
+    print("|---|---|---|---|---|---|---|---|---|---|")
+    for name, glu, M, K in SPLIT_SHAPES:
+        rows = 2 * M if glu else M
+        w = synthetic.make_bf16((rows, K), f"timeline.split.{rows}.{K}", device=dev)
+        cb, lut = cbb.codebook_from_counts_torch(cbb.counts_torch(w))
+        idx = lut[cbb.patterns_torch(w).reshape(-1).to(torch.int64)].to(torch.int32)
+        del w
+        keep, desc = build_split(idx, cb.cpu().numpy(), dev)
+        del idx
+        x = torch.randn(1, K, device=dev)
+        out = torch.empty(1, M, device=dev)
+        mp = (ctypes.POINTER(nat.SplitMatrix) * 1)(ctypes.pointer(desc))
+        op = (ctypes.c_void_p * 1)(out.data_ptr())
+        mr = (ctypes.c_int * 1)(M)
+
+        def launch():
+            st = torch.cuda.current_stream().cuda_stream     # the capture stream in a graph
+            if glu:
+                nat.check(lib.cbq_split_linear_glu_f32(x.data_ptr(), None, None, 0, 0.0,
+                                                       ctypes.pointer(desc), out.data_ptr(), M, K,
+                                                       st), "cbq_split_linear_glu_f32")
+            else:
+                nat.check(lib.cbq_split_linear_f32(x.data_ptr(), None, None, 0, 0.0, 1, mp, op,
+                                                   mr, K, st), "cbq_split_linear_f32")
+        t0 = time.time()
+        while time.time() - t0 < args.warm:
+            for _ in range(8):
+                launch()
+            torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        launch()
+        e1.record()
+        torch.cuda.synchronize()
+        ev_us = e0.elapsed_time(e1) * 1e3
+        tl = np.zeros(4096 * 6, np.uint64)
+        nat.check(lib.cbq_split_timeline_read(tl.ctypes.data, tl.nbytes), "cbq_split_timeline_read")
+        # the same launch graph-replayed: time per launch, and the span of
+        # the last replay's last launch (its waves overwrite the record)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(8):
+                launch()
+        g.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(10):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        graph_us = e0.elapsed_time(e1) * 1e3 / 80
+        tg = np.zeros(4096 * 6, np.uint64)
+        nat.check(lib.cbq_split_timeline_read(tg.ctypes.data, tg.nbytes), "cbq_split_timeline_read")
+        tg = tg.reshape(4096, 6).astype(np.int64)
+        tg = tg[(tg[:, 0] > 0) & (tg[:, 0] >= tg[:, 0].max() - 100_000) & (tg[:, 5] > 0)]
+        graph_span = float((tg[:, 4].max() - tg[:, 0].min()) * 0.01)
+        del g
+        tl = tl.reshape(4096, 6).astype(np.int64)
+        last = tl[:, 0].max()
+        tl = tl[(tl[:, 0] > 0) & (tl[:, 0] >= last - 100_000) & (tl[:, 5] > 0)]
+        r = (tl[:, :5] - tl[:, 0].min()) * 0.01
+        items = tl[:, 5] * (2 if glu else 1)
+        per = (r[:, 3] - r[:, 2]) / np.maximum(items - 1, 1)
+        p = lambda a, qs: " / ".join(f"{np.percentile(a, q):.2f}" for q in qs)  # noqa: E731
+        print(f"| {name} {K}->{M} | {ev_us:.1f} | {graph_us:.1f} / {graph_span:.1f} | "
+              f"{r[:, 4].max():.1f} | {len(tl)} | "
+              f"{p(r[:, 1] - r[:, 0], (50, 90))} | {p(r[:, 2] - r[:, 1], (50, 90))} | "
+              f"{np.median(per):.2f} | {p(r[:, 3], (10, 50, 90, 100))} | "
+              f"{np.median(r[:, 4] - r[:, 3]):.2f} |", flush=True)
+        del keep, x, out
+        torch.cuda.empty_cache()
+
+
 if __name__ == "__main__":
-    if "--prefill" in sys.argv:
+    if "--split" in sys.argv:
+        sys.argv.remove("--split")
+        ap = argparse.ArgumentParser()
+        ap.add_argument("--lib", default=os.path.join(HERE, "libcbq_hip_timeline.so"))
+        ap.add_argument("--warm", type=float, default=1.0)
+        split(ap.parse_args())
+    elif "--prefill" in sys.argv:
         sys.argv.remove("--prefill")
         ap = argparse.ArgumentParser()
         ap.add_argument("--lib", default=os.path.join(HERE, "libcbq_hip_timeline.so"))

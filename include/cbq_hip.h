@@ -454,6 +454,16 @@ int cbq_timeline_read(void *dst, size_t dst_bytes);
  * 4096 * 6 * 8.  No counterpart in the reference. */
 int cbq_prefill_timeline_read(void *dst, size_t dst_bytes);
 
+/* Diagnostics: in a -DCBQ_TIMELINE library, copies the per-wave timeline of
+ * the last split-format row-walk GEMV launch (one token,
+ * cbq_split_linear_f32 / cbq_split_linear_glu_f32): 4096 waves x 6 uint64
+ * (clock at entry, after the first barrier, after the wave's first chunk,
+ * after its row loop, at exit, in 10 ns ticks; then its rows), wave w of
+ * block b at index 16 b + w for 16-wave blocks.  CK_ERR_ARG in the normal
+ * build or when dst_bytes < 4096 * 6 * 8.  No counterpart in the
+ * reference. */
+int cbq_split_timeline_read(void *dst, size_t dst_bytes);
+
 /* ---- lm_head GEMV with the greedy pick fused ------------------------------
  * The one-token GEMV of the decoder's last matrix (vocabulary rows) and the
  * greedy pick of the next token in two launches: the GEMV's epilogue reduces

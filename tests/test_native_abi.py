@@ -112,6 +112,7 @@ def test_argument_validation_before_launch(lib):
     assert up(__file__.encode(), part, 0, 1 << 20, 2) == 0                      # nothing to copy
     assert lib.cbq_timeline_read(None, 0) == 2               # diagnostics: product build / no buffer
     assert lib.cbq_prefill_timeline_read(None, 0) == 2
+    assert lib.cbq_split_timeline_read(None, 0) == 2
 
 
 def test_build_luts_rejects_overfull(lib):
